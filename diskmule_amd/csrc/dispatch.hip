@@ -1,0 +1,91 @@
+// dispatch.hip -- kernel selection for the matvec, FFN and GEMM operators.
+#include "runtime.h"
+
+#include <math.h>
+
+#include "dm_qmv.h"
+
+namespace dm {
+
+int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, const void *w,
+                   size_t batch, const float *x, float *y) {
+    uint32_t be, bb;
+    type_layout(type, &be, &bb);
+    uint64_t row_bytes;
+    row_byte_len(type, columns, &row_bytes);
+    if (qmv_supported(type, rows, columns, w, batch)) {
+        DM_HIP(launch_qmv(ctx, type, (uint32_t)rows, (uint32_t)columns, w, (uint32_t)batch, x, y,
+                          nullptr));
+        return DMHIP_OK;
+    }
+    DM_HIP(launch_gemv_exact(ctx->stream, type, be, bb, (uint32_t)rows, (uint32_t)columns,
+                             (size_t)row_bytes, (const uint8_t *)w, (uint32_t)batch, x, y));
+    return DMHIP_OK;
+}
+
+int enqueue_matvec_argmax(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
+                          const void *w, const float *x, float *y, uint32_t *index_device) {
+    DM_HIP(launch_argmax_init(ctx->stream, ctx->argmax_state));
+    if (qmv_supported(type, rows, columns, w, 1)) {
+        // The argmax is folded into the matvec's epilogue.
+        DM_HIP(launch_qmv(ctx, type, (uint32_t)rows, (uint32_t)columns, w, 1, x, y,
+                          ctx->argmax_state));
+    } else {
+        DM_CHECK_STATUS(enqueue_matvec(ctx, type, rows, columns, w, 1, x, y));
+        DM_HIP(launch_argmax(ctx->stream, y, rows, ctx->argmax_state, index_device));
+        return DMHIP_OK;
+    }
+    DM_HIP(launch_argmax_finish(ctx->stream, ctx->argmax_state, index_device));
+    return DMHIP_OK;
+}
+
+}  // namespace dm
+
+using namespace dm;
+
+extern "C" {
+
+size_t dmhip_ffn_workspace_bytes(size_t batch, size_t ffn) {
+    // gate, up and activation rows, plus room for a normalized copy of h
+    // (hidden <= 4 * ffn is assumed by the callers on this path).
+    return (7 * batch * ffn + 256) * sizeof(float);
+}
+
+int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn, uint32_t gate_type,
+                     const void *gate, uint32_t up_type, const void *up, uint32_t down_type,
+                     const void *down, float epsilon, const float *h, float *y, void *workspace) {
+    if (!ctx || !gate || !up || !down || !h || !y || !workspace)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "ffn arguments must not be null");
+    if (batch < 1 || batch > 16)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "batch %zu is outside 1..=16", batch);
+    if (hidden == 0 || ffn == 0) return fail(DMHIP_ERR_EMPTY_INPUT, "FFN requires a non-empty input");
+    if (!isfinite(epsilon) || epsilon <= 0.0f)
+        return fail(DMHIP_ERR_INVALID_POSITIVE_PARAMETER, "RMSNorm epsilon requires a finite positive parameter");
+    uint64_t rb;
+    const uint32_t types[3] = {gate_type, up_type, down_type};
+    const size_t cols[3] = {hidden, hidden, ffn};
+    for (int i = 0; i < 3; i++) {
+        uint32_t t = types[i];
+        if (!(t == 0 || t == 1 || t == 6 || t == 8 || t == 12 || t == 14))
+            return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "HIP FFN does not support %s", type_name(t));
+        if (!row_byte_len(t, cols[i], &rb))
+            return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT, "%s row of %zu values is not whole blocks",
+                        type_name(t), cols[i]);
+    }
+    if (hidden > 0xffffffffull || ffn > 0xffffffffull)
+        return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "HIP vector length exceeds the 32-bit kernel limit");
+    DM_CHECK_STATUS(set_device(ctx));
+    float *ws = (float *)workspace;
+    float *normalized = ws;                       // [batch][hidden]
+    float *g = normalized + batch * hidden;       // [batch][ffn]
+    float *u = g + batch * ffn;                   // [batch][ffn]
+    float *a = u + batch * ffn;                   // [batch][ffn]
+    DM_HIP(launch_rms_norm(ctx->stream, h, (uint32_t)batch, (uint32_t)hidden, nullptr, epsilon, normalized));
+    DM_CHECK_STATUS(enqueue_matvec(ctx, gate_type, ffn, hidden, gate, batch, normalized, g));
+    DM_CHECK_STATUS(enqueue_matvec(ctx, up_type, ffn, hidden, up, batch, normalized, u));
+    DM_HIP(launch_silu_mul(ctx->stream, g, u, batch * ffn, a));
+    DM_CHECK_STATUS(enqueue_matvec(ctx, down_type, hidden, ffn, down, batch, a, y));
+    return DMHIP_OK;
+}
+
+}  // extern "C"

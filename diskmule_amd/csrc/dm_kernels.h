@@ -1,0 +1,43 @@
+// dm_kernels.h -- launchers of the gfx950 kernels (host-callable).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace dm {
+
+constexpr uint32_t kMaxTopK = 256;
+
+// Device-side argmax accumulator: packed (ordered value, ~index) key and a
+// non-finite flag.
+struct ArgmaxState {
+    unsigned long long key;
+    uint32_t non_finite;
+    uint32_t pad;
+};
+
+hipError_t launch_dequantize(hipStream_t s, uint32_t type, const uint8_t *enc, uint32_t be,
+                             uint32_t bb, size_t elements, float *out);
+hipError_t launch_gemv_exact(hipStream_t s, uint32_t type, uint32_t be, uint32_t bb, uint32_t rows,
+                             uint32_t columns, size_t row_bytes, const uint8_t *w, uint32_t batch,
+                             const float *x, float *y);
+hipError_t launch_argmax(hipStream_t s, const float *v, size_t n, ArgmaxState *state,
+                         uint32_t *index);
+hipError_t launch_argmax_init(hipStream_t s, ArgmaxState *state);
+hipError_t launch_argmax_finish(hipStream_t s, const ArgmaxState *state, uint32_t *index);
+hipError_t launch_top_k(hipStream_t s, const float *logits, uint32_t rows, uint32_t count,
+                        uint32_t k, uint32_t *ids, float *probabilities, uint32_t *non_finite);
+hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,
+                               uint32_t experts, uint32_t k, uint32_t batch, const float *x,
+                               float *logits, uint32_t *ids, float *probabilities,
+                               uint32_t *non_finite);
+hipError_t launch_rms_norm(hipStream_t s, const float *in, uint32_t batch, uint32_t n,
+                           const float *weight, float eps, float *out);
+hipError_t launch_silu_mul(hipStream_t s, const float *gate, const float *up, size_t n, float *out);
+hipError_t launch_moe_combine(hipStream_t s, const float *expert_out, const float *p, uint32_t batch,
+                              uint32_t k, uint32_t hidden, float *y);
+hipError_t launch_silu_mul_glm_pairs(hipStream_t s, const float *gate_up, uint32_t pairs,
+                                     uint32_t width, float *act);
+
+}  // namespace dm

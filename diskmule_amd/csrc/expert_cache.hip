@@ -1,0 +1,402 @@
+// expert_cache.hip -- routed-expert residency and the MoE decode layer.
+//
+// ExpertCache of src/expert.rs:64-229 with HBM slots: the LRU bookkeeping is
+// the reference's (clock per layer, hit updates last_used, a miss evicts the
+// unpinned slot with the smallest (is_some, last_used, index)), and the
+// positional reads become asynchronous host->HBM copies on the context's
+// upload stream.  Ordering is by events, never by host waits:
+//   * an upload into a slot first waits for the `released` event recorded
+//     after the last compute work that read the slot;
+//   * compute work that uses a freshly loaded slot waits for its `ready`
+//     event (the end of its upload).
+#include "runtime.h"
+
+#include <chrono>
+#include <vector>
+
+#include "dm_qmv.h"
+
+namespace dm {
+
+__global__ void gather_rows_kernel(const float *__restrict__ x, const uint32_t *__restrict__ rows,
+                                   uint32_t count, uint32_t width, float *__restrict__ out) {
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < (size_t)count * width;
+         e += (size_t)gridDim.x * blockDim.x) {
+        uint32_t p = (uint32_t)(e / width), i = (uint32_t)(e - (size_t)p * width);
+        out[e] = x[(size_t)rows[p] * width + i];
+    }
+}
+
+// y[t] = fold over the k selections in order of fma(out[pos[t][j]], p[t][j], y)
+// (src/gemma4/cpu.rs:608-611).
+__global__ void moe_combine_pos_kernel(const float *__restrict__ expert_out,
+                                       const uint32_t *__restrict__ pos, const float *__restrict__ p,
+                                       uint32_t batch, uint32_t k, uint32_t hidden,
+                                       float *__restrict__ y) {
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < (size_t)batch * hidden;
+         e += (size_t)gridDim.x * blockDim.x) {
+        uint32_t t = (uint32_t)(e / hidden), i = (uint32_t)(e - (size_t)t * hidden);
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < k; j++)
+            acc = __builtin_fmaf(expert_out[(size_t)pos[t * k + j] * hidden + i], p[t * k + j], acc);
+        y[e] = acc;
+    }
+}
+
+struct Slot {
+    bool has = false;
+    size_t expert = 0;
+    uint64_t last_used = 0;
+    bool pinned = false;
+    void *gate_up = nullptr;
+    void *down = nullptr;
+    hipEvent_t ready = nullptr;     // end of the last upload into the slot
+    hipEvent_t released = nullptr;  // end of the last compute that read it
+    bool released_recorded = false;
+};
+
+struct Layer {
+    dmhip_expert_layer_layout layout;
+    std::vector<Slot> slots;
+    uint64_t clock = 0;
+};
+
+}  // namespace dm
+
+struct dmhip_expert_cache {
+    dmhip_ctx *ctx = nullptr;
+    const uint8_t *source = nullptr;
+    size_t source_len = 0;
+    std::vector<dm::Layer> layers;
+    dmhip_expert_cache_stats stats = {};
+    // MoE workspace (device): grows on demand.
+    dm::Scratch work;
+    std::vector<uint32_t> host_ids;
+    std::vector<float> host_probs;
+};
+
+using namespace dm;
+
+namespace {
+
+int acquire(dmhip_expert_cache *c, size_t layer_index, size_t expert, size_t *slot_out) {
+    if (layer_index >= c->layers.size())
+        return fail(DMHIP_ERR_INVALID_LAYER, "expert cache layer %zu is outside its %zu layers",
+                    layer_index, c->layers.size());
+    Layer &layer = c->layers[layer_index];
+    if (expert >= layer.layout.expert_count)
+        return fail(DMHIP_ERR_INVALID_EXPERT, "expert %zu is outside layer %zu's %zu experts", expert,
+                    layer_index, layer.layout.expert_count);
+    layer.clock += 1;
+    for (size_t i = 0; i < layer.slots.size(); i++) {
+        Slot &s = layer.slots[i];
+        if (s.has && s.expert == expert) {
+            s.last_used = layer.clock;
+            c->stats.hits += 1;
+            *slot_out = i;
+            return DMHIP_OK;
+        }
+    }
+    c->stats.misses += 1;
+    size_t victim = SIZE_MAX;
+    for (size_t i = 0; i < layer.slots.size(); i++) {
+        const Slot &s = layer.slots[i];
+        if (s.pinned) continue;
+        if (victim == SIZE_MAX) { victim = i; continue; }
+        const Slot &v = layer.slots[victim];
+        if (s.has < v.has || (s.has == v.has && s.last_used < v.last_used)) victim = i;
+    }
+    if (victim == SIZE_MAX)
+        return fail(DMHIP_ERR_ALL_SLOTS_PINNED, "all expert slots in layer %zu are pinned by in-flight work",
+                    layer_index);
+    Slot &s = layer.slots[victim];
+    if (s.has) c->stats.evictions += 1;
+    const auto started = std::chrono::steady_clock::now();
+    const size_t gu_bytes = layer.layout.gate_up_bytes, dn_bytes = layer.layout.down_bytes;
+    const uint8_t *gu_src = c->source + layer.layout.gate_up_offset + expert * gu_bytes;
+    const uint8_t *dn_src = c->source + layer.layout.down_offset + expert * dn_bytes;
+    hipStream_t up = c->ctx->upload;
+    if (s.released_recorded) DM_HIP(hipStreamWaitEvent(up, s.released, 0));
+    DM_HIP(hipMemcpyAsync(s.gate_up, gu_src, gu_bytes, hipMemcpyHostToDevice, up));
+    DM_HIP(hipMemcpyAsync(s.down, dn_src, dn_bytes, hipMemcpyHostToDevice, up));
+    DM_HIP(hipEventRecord(s.ready, up));
+    DM_HIP(hipStreamWaitEvent(c->ctx->stream, s.ready, 0));
+    c->stats.io_wait_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                               std::chrono::steady_clock::now() - started).count();
+    c->stats.reads += 2;
+    c->stats.bytes_read += gu_bytes + dn_bytes;
+    s.has = true;
+    s.expert = expert;
+    s.last_used = layer.clock;
+    *slot_out = victim;
+    return DMHIP_OK;
+}
+
+int release(dmhip_expert_cache *c, size_t layer, size_t slot) {
+    Slot &s = c->layers[layer].slots[slot];
+    DM_HIP(hipEventRecord(s.released, c->ctx->stream));
+    s.released_recorded = true;
+    s.pinned = false;
+    return DMHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len,
+                           const dmhip_expert_layer_layout *layouts, size_t layer_count,
+                           size_t slots_per_layer, dmhip_expert_cache **out) {
+    if (!ctx || !out) return fail(DMHIP_ERR_INVALID_ARGUMENT, "context and out must not be null");
+    *out = nullptr;
+    if (slots_per_layer == 0)
+        return fail(DMHIP_ERR_NO_SLOTS, "expert cache requires at least one slot per layer");
+    if (layer_count && (!layouts || !source))
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "layouts and source must not be null");
+    for (size_t l = 0; l < layer_count; l++) {
+        const dmhip_expert_layer_layout &L = layouts[l];
+        if (L.gate_up_bytes == 0 || L.down_bytes == 0)
+            return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a 0-byte device buffer");
+        unsigned __int128 gu_end = (unsigned __int128)L.gate_up_offset +
+                                   (unsigned __int128)L.expert_count * L.gate_up_bytes;
+        unsigned __int128 dn_end = (unsigned __int128)L.down_offset +
+                                   (unsigned __int128)L.expert_count * L.down_bytes;
+        if (gu_end > source_len || dn_end > source_len)
+            return fail(DMHIP_ERR_INVALID_LAYOUT, "layer %zu expert ranges exceed the %zu-byte source", l,
+                        source_len);
+    }
+    DM_CHECK_STATUS(set_device(ctx));
+    dmhip_expert_cache *c = new dmhip_expert_cache();
+    c->ctx = ctx;
+    c->source = (const uint8_t *)source;
+    c->source_len = source_len;
+    c->layers.resize(layer_count);
+    uint64_t resident = 0;
+    for (size_t l = 0; l < layer_count; l++) {
+        Layer &layer = c->layers[l];
+        layer.layout = layouts[l];
+        layer.slots.resize(slots_per_layer);
+        for (Slot &s : layer.slots) {
+            if (hipMalloc(&s.gate_up, layer.layout.gate_up_bytes + 256) != hipSuccess ||
+                hipMalloc(&s.down, layer.layout.down_bytes + 256) != hipSuccess ||
+                hipMemset(s.gate_up, 0, layer.layout.gate_up_bytes + 256) != hipSuccess ||
+                hipMemset(s.down, 0, layer.layout.down_bytes + 256) != hipSuccess ||
+                hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess ||
+                hipEventCreateWithFlags(&s.released, hipEventDisableTiming) != hipSuccess) {
+                dmhip_expert_cache_free(c);
+                return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate expert slot buffers");
+            }
+            resident += layer.layout.gate_up_bytes + layer.layout.down_bytes;
+        }
+    }
+    c->stats.resident_bytes = resident;
+    *out = c;
+    return DMHIP_OK;
+}
+
+void dmhip_expert_cache_free(dmhip_expert_cache *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->ctx->device);
+    (void)hipStreamSynchronize(c->ctx->upload);
+    (void)hipStreamSynchronize(c->ctx->stream);
+    for (Layer &layer : c->layers)
+        for (Slot &s : layer.slots) {
+            if (s.gate_up) (void)hipFree(s.gate_up);
+            if (s.down) (void)hipFree(s.down);
+            if (s.ready) (void)hipEventDestroy(s.ready);
+            if (s.released) (void)hipEventDestroy(s.released);
+        }
+    c->work.release();
+    delete c;
+}
+
+int dmhip_expert_cache_stats_get(const dmhip_expert_cache *c, dmhip_expert_cache_stats *stats) {
+    if (!c || !stats) return fail(DMHIP_ERR_INVALID_ARGUMENT, "cache and stats must not be null");
+    *stats = c->stats;
+    return DMHIP_OK;
+}
+
+size_t dmhip_expert_cache_slots_per_layer(const dmhip_expert_cache *c) {
+    return (c && !c->layers.empty()) ? c->layers[0].slots.size() : 0;
+}
+
+int dmhip_expert_acquire(dmhip_expert_cache *c, size_t layer, size_t expert,
+                         const volatile int *cancelled, size_t *slot, const void **gate_up,
+                         const void **down) {
+    if (!c || !slot || !gate_up || !down)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "cache and outputs must not be null");
+    if (cancelled && *cancelled) return fail(DMHIP_ERR_CANCELLED, "expert loading was cancelled");
+    DM_CHECK_STATUS(set_device(c->ctx));
+    size_t s;
+    DM_CHECK_STATUS(acquire(c, layer, expert, &s));
+    if (cancelled && *cancelled) return fail(DMHIP_ERR_CANCELLED, "expert loading was cancelled");
+    Slot &slot_ref = c->layers[layer].slots[s];
+    slot_ref.pinned = true;
+    *slot = s;
+    *gate_up = slot_ref.gate_up;
+    *down = slot_ref.down;
+    return DMHIP_OK;
+}
+
+int dmhip_expert_release(dmhip_expert_cache *c, size_t layer, size_t slot) {
+    if (!c) return fail(DMHIP_ERR_INVALID_ARGUMENT, "cache must not be null");
+    if (layer >= c->layers.size() || slot >= c->layers[layer].slots.size())
+        return fail(DMHIP_ERR_INVALID_LAYER, "slot %zu of layer %zu does not exist", slot, layer);
+    DM_CHECK_STATUS(set_device(c->ctx));
+    return release(c, layer, slot);
+}
+
+int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t batch,
+                    size_t hidden, size_t width, size_t experts, size_t k,
+                    const uint16_t *router_bf16, uint32_t gate_up_type, uint32_t down_type,
+                    const float *x, float *y, uint32_t *ids, float *probabilities) {
+    if (!ctx || !c || !router_bf16 || !x || !y || !ids || !probabilities)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "moe_layer arguments must not be null");
+    if (c->ctx != ctx) return fail(DMHIP_ERR_INVALID_ARGUMENT, "the cache belongs to another context");
+    if (batch < 1 || batch > 16) return fail(DMHIP_ERR_INVALID_ARGUMENT, "batch %zu is outside 1..=16", batch);
+    if (k == 0 || k > experts)
+        return fail(DMHIP_ERR_INVALID_TOP_K, "top-k count %zu is outside 1..=%zu", k, experts);
+    if (k > kMaxTopK || experts > 16384)
+        return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "router with %zu experts, top-%zu exceeds the kernel limits",
+                    experts, k);
+    if (hidden == 0 || width == 0) return fail(DMHIP_ERR_EMPTY_INPUT, "MoE layer requires a non-empty input");
+    if (layer >= c->layers.size())
+        return fail(DMHIP_ERR_INVALID_LAYER, "expert cache layer %zu is outside its %zu layers", layer,
+                    c->layers.size());
+    const dmhip_expert_layer_layout &L = c->layers[layer].layout;
+    uint64_t gu_row, dn_row;
+    if (!row_byte_len(gate_up_type, hidden, &gu_row) || !row_byte_len(down_type, width, &dn_row))
+        return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT, "expert rows are not whole blocks");
+    if (L.gate_up_bytes != 2 * width * gu_row || L.down_bytes != hidden * dn_row)
+        return fail(DMHIP_ERR_INVALID_LAYOUT,
+                    "layer %zu slots hold %zu + %zu bytes; the expert shape needs %llu + %llu", layer,
+                    L.gate_up_bytes, L.down_bytes, (unsigned long long)(2 * width * gu_row),
+                    (unsigned long long)(hidden * dn_row));
+    if (L.expert_count < experts)
+        return fail(DMHIP_ERR_INVALID_LAYOUT, "layer %zu holds %zu experts; the router has %zu", layer,
+                    L.expert_count, experts);
+    DM_CHECK_STATUS(set_device(ctx));
+
+    // Workspace: logits | ids | probs | pos | pair tokens | xg | gate_up | act | expert_out
+    const size_t pairs = batch * k;
+    const size_t a_logits = 0;
+    const size_t a_ids = a_logits + ((batch * experts * 4 + 255) & ~(size_t)255);
+    const size_t a_probs = a_ids + ((pairs * 4 + 255) & ~(size_t)255);
+    const size_t a_pos = a_probs + ((pairs * 4 + 255) & ~(size_t)255);
+    const size_t a_tok = a_pos + ((pairs * 4 + 255) & ~(size_t)255);
+    const size_t a_xg = a_tok + ((pairs * 4 + 255) & ~(size_t)255);
+    const size_t a_gu = a_xg + ((pairs * hidden * 4 + 255) & ~(size_t)255);
+    const size_t a_act = a_gu + ((pairs * 2 * width * 4 + 255) & ~(size_t)255);
+    const size_t a_eo = a_act + ((pairs * width * 4 + 255) & ~(size_t)255);
+    const size_t total = a_eo + ((pairs * hidden * 4 + 255) & ~(size_t)255);
+    DM_CHECK_STATUS(c->work.ensure(total));
+    char *w = (char *)c->work.ptr;
+    float *d_logits = (float *)(w + a_logits);
+    uint32_t *d_ids = (uint32_t *)(w + a_ids);
+    float *d_probs = (float *)(w + a_probs);
+    uint32_t *d_pos = (uint32_t *)(w + a_pos);
+    uint32_t *d_tok = (uint32_t *)(w + a_tok);
+    float *d_xg = (float *)(w + a_xg);
+    float *d_gu = (float *)(w + a_gu);
+    float *d_act = (float *)(w + a_act);
+    float *d_eo = (float *)(w + a_eo);
+
+    // 1. Router logits (exact fold) and top-k softmax on the GPU.
+    DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
+                               (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs, ctx->flags));
+    DM_HIP(hipMemcpyAsync(ids, d_ids, pairs * 4, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipMemcpyAsync(probabilities, d_probs, pairs * 4, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+
+    // 2. Acquire in the reference's order (token by token, selection order)
+    //    and cut the pairs into phases: a phase ends before an acquire whose
+    //    slot is already used by the phase (it would overwrite its bytes).
+    std::vector<uint32_t> pos(pairs);
+    std::vector<size_t> slot_of(pairs);
+    size_t begin = 0;
+    // Host sources of the per-phase token lists stay alive until the final
+    // synchronisation below.
+    std::vector<std::vector<uint32_t>> phase_tokens;
+    auto run_phase = [&](size_t p0, size_t p1) -> int {
+        if (p0 == p1) return DMHIP_OK;
+        // Group the phase's pairs by slot: sorted order = pair index order
+        // within each slot, slots in first-use order.
+        std::vector<size_t> order;
+        std::vector<size_t> group_start, group_slot;
+        std::vector<char> done(p1 - p0, 0);
+        for (size_t i = p0; i < p1; i++) {
+            if (done[i - p0]) continue;
+            group_start.push_back(order.size());
+            group_slot.push_back(slot_of[i]);
+            for (size_t j = i; j < p1; j++)
+                if (!done[j - p0] && slot_of[j] == slot_of[i]) {
+                    done[j - p0] = 1;
+                    order.push_back(j);
+                }
+        }
+        group_start.push_back(order.size());
+        phase_tokens.emplace_back(order.size());
+        std::vector<uint32_t> &tokens = phase_tokens.back();
+        for (size_t q = 0; q < order.size(); q++) {
+            tokens[q] = (uint32_t)(order[q] / k);
+            pos[order[q]] = (uint32_t)(p0 + q);  // row in the expert-output buffer
+        }
+        DM_HIP(hipMemcpyAsync(d_tok, tokens.data(), tokens.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+        hipLaunchKernelGGL(gather_rows_kernel, dim3(64), dim3(256), 0, ctx->stream, x, d_tok,
+                           (uint32_t)tokens.size(), (uint32_t)hidden, d_xg + p0 * hidden);
+        DM_HIP(hipGetLastError());
+        for (size_t g = 0; g + 1 < group_start.size(); g++) {
+            const size_t q0 = group_start[g], q1 = group_start[g + 1];
+            const Slot &s = c->layers[layer].slots[group_slot[g]];
+            const size_t cnt = q1 - q0;
+            const float *xin = d_xg + (p0 + q0) * hidden;
+            float *gu = d_gu + (p0 + q0) * 2 * width;
+            DM_CHECK_STATUS(enqueue_matvec(ctx, gate_up_type, 2 * width, hidden, s.gate_up, cnt, xin, gu));
+            DM_HIP(launch_silu_mul_glm_pairs(ctx->stream, gu, (uint32_t)cnt, (uint32_t)width,
+                                             d_act + (p0 + q0) * width));
+            DM_CHECK_STATUS(enqueue_matvec(ctx, down_type, hidden, width, s.down, cnt,
+                                           d_act + (p0 + q0) * width, d_eo + (p0 + q0) * hidden));
+        }
+        for (size_t g = 0; g + 1 < group_start.size(); g++)
+            DM_CHECK_STATUS(release(c, layer, group_slot[g]));
+        return DMHIP_OK;
+    };
+    for (size_t p = 0; p < pairs; p++) {
+        // Would this acquire evict a slot the open phase still needs?  Check
+        // with the reference's victim rule before touching any state.
+        Layer &Ly = c->layers[layer];
+        const size_t e = ids[p];
+        bool hit = false;
+        for (const Slot &s : Ly.slots)
+            if (s.has && s.expert == e) hit = true;
+        if (!hit) {
+            size_t victim = SIZE_MAX;
+            for (size_t i = 0; i < Ly.slots.size(); i++) {
+                const Slot &s = Ly.slots[i];
+                if (s.pinned) continue;
+                if (victim == SIZE_MAX) { victim = i; continue; }
+                const Slot &v = Ly.slots[victim];
+                if (s.has < v.has || (s.has == v.has && s.last_used < v.last_used)) victim = i;
+            }
+            bool used = false;
+            for (size_t q = begin; q < p; q++)
+                if (slot_of[q] == victim) used = true;
+            if (used) {
+                DM_CHECK_STATUS(run_phase(begin, p));
+                begin = p;
+            }
+        }
+        DM_CHECK_STATUS(acquire(c, layer, e, &slot_of[p]));
+    }
+    DM_CHECK_STATUS(run_phase(begin, pairs));
+
+    // 3. Ordered combine and copy out.
+    DM_HIP(hipMemcpyAsync(d_pos, pos.data(), pairs * 4, hipMemcpyHostToDevice, ctx->stream));
+    hipLaunchKernelGGL(moe_combine_pos_kernel, dim3((uint32_t)((batch * hidden + 255) / 256)), dim3(256), 0,
+                       ctx->stream, d_eo, d_pos, d_probs, (uint32_t)batch, (uint32_t)k, (uint32_t)hidden, y);
+    DM_HIP(hipGetLastError());
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+}  // extern "C"

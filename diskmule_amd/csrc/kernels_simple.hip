@@ -1,0 +1,389 @@
+// kernels_simple.hip -- exact per-element kernels for gfx950.
+//
+// These kernels reproduce the reference arithmetic element by element:
+//  * dequantize_kernel: bit-exact cpu::dequantize (src/cpu.rs:546-645);
+//  * gemv_exact_kernel: any supported type and any column count; each weight
+//    is dequantized exactly and folded with fma (one wave per row).  It
+//    serves shapes the MFMA kernels do not take (unaligned rows, columns
+//    that are not whole 256-blocks, F32/F16/BF16 rows);
+//  * reductions for argmax / top-k / RMSNorm, SiLU products, the exact bf16
+//    router fold and the ordered expert combine.
+#include "dm_device.h"
+#include "dm_kernels.h"
+
+namespace dm {
+
+// Exact value of element t (0 <= t < block elements) of one encoded block.
+// Operation order and rounding follow src/cpu.rs:576-645; compiled without
+// contraction, so each product and difference rounds separately.
+__device__ __forceinline__ float dequant_element(uint32_t type, const uint8_t *block, uint32_t t) {
+    switch (type) {
+    case kF32:
+        return __uint_as_float((uint32_t)block[0] | ((uint32_t)block[1] << 8) |
+                               ((uint32_t)block[2] << 16) | ((uint32_t)block[3] << 24));
+    case kF16:
+        return f16_bits_to_f32((uint32_t)block[0] | ((uint32_t)block[1] << 8));
+    case kBF16:
+        return __uint_as_float(((uint32_t)block[0] | ((uint32_t)block[1] << 8)) << 16);
+    case kQ8_0: {
+        float delta = f16_bits_to_f32((uint32_t)block[0] | ((uint32_t)block[1] << 8));
+        return delta * (float)(int8_t)block[2 + t];
+    }
+    case kQ5_0: {
+        // src/cpu.rs:560-574
+        float delta = f16_bits_to_f32((uint32_t)block[0] | ((uint32_t)block[1] << 8));
+        uint32_t high_bits = (uint32_t)block[2] | ((uint32_t)block[3] << 8) |
+                             ((uint32_t)block[4] << 16) | ((uint32_t)block[5] << 24);
+        uint32_t index = t & 15u;
+        uint32_t packed = block[6 + index];
+        int32_t q;
+        if (t < 16)
+            q = (int32_t)((packed & 0x0fu) | (((high_bits >> index) << 4) & 0x10u)) - 16;
+        else
+            q = (int32_t)((packed >> 4) | ((high_bits >> (index + 12)) & 0x10u)) - 16;
+        return delta * (float)q;
+    }
+    case kQ4_K: {
+        float delta = f16_bits_to_f32((uint32_t)block[0] | ((uint32_t)block[1] << 8));
+        float minimum = f16_bits_to_f32((uint32_t)block[2] | ((uint32_t)block[3] << 8));
+        uint32_t group_pair = t >> 6, within = t & 63u, high = within >> 5, i = within & 31u;
+        uint32_t packed = block[16 + 32 * group_pair + i];
+        uint32_t sc, m;
+        scale_min_q4_k((int)(2 * group_pair + high), block + 4, sc, m);
+        uint32_t q = high ? (packed >> 4) : (packed & 0x0fu);
+        return delta * (float)sc * (float)q - minimum * (float)m;
+    }
+    case kQ6_K: {
+        float delta = f16_bits_to_f32((uint32_t)block[208] | ((uint32_t)block[209] << 8));
+        uint32_t half = t >> 7, r = t & 127u, k = r >> 5, i = r & 31u;
+        const uint8_t *low = block + 64 * half;
+        const uint8_t *high = block + 128 + 32 * half;
+        const int8_t *scales = (const int8_t *)(block + 192 + 8 * half);
+        uint32_t scale_pair = i >> 4;
+        uint32_t lo = (k & 1u) ? low[i + 32] : low[i];
+        uint32_t nib = (k & 2u) ? (lo >> 4) : (lo & 0x0fu);
+        uint32_t q = nib | (((high[i] >> (2 * k)) & 3u) << 4);
+        return delta * (float)scales[scale_pair + 2 * k] * ((float)q - 32.0f);
+    }
+    default:
+        return 0.0f;
+    }
+}
+
+__global__ void dequantize_kernel(uint32_t type, const uint8_t *__restrict__ encoded,
+                                  uint32_t block_elements, uint32_t block_bytes, size_t elements,
+                                  float *__restrict__ out) {
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < elements; e += stride) {
+        size_t b = e / block_elements;
+        uint32_t t = (uint32_t)(e - b * block_elements);
+        out[e] = dequant_element(type, encoded + b * block_bytes, t);
+    }
+}
+
+// One wave per (row); lanes stride over columns, each weight dequantized
+// exactly, fma into per-lane sums, then a wave sum.  256 threads = 4 rows.
+__global__ void __launch_bounds__(256) gemv_exact_kernel(
+    uint32_t type, uint32_t block_elements, uint32_t block_bytes, uint32_t rows,
+    uint32_t columns, size_t row_bytes, const uint8_t *__restrict__ weights, uint32_t batch,
+    const float *__restrict__ x, float *__restrict__ y) {
+    uint32_t lane = threadIdx.x & 63u;
+    uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint8_t *w = weights + (size_t)row * row_bytes;
+    for (uint32_t b = 0; b < batch; b++) {
+        const float *xb = x + (size_t)b * columns;
+        float acc = 0.0f;
+        for (uint32_t c = lane; c < columns; c += 64) {
+            uint32_t blk = c / block_elements;
+            float v = dequant_element(type, w + (size_t)blk * block_bytes, c - blk * block_elements);
+            acc = __builtin_fmaf(v, xb[c], acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) y[(size_t)b * rows + row] = acc;
+    }
+}
+
+// ---- argmax over a device vector (src/cpu.rs:275-293) -------------------
+__global__ void argmax_init_kernel(ArgmaxState *state) {
+    state->key = 0;
+    state->non_finite = 0;
+}
+
+__global__ void __launch_bounds__(256) argmax_kernel(const float *__restrict__ v, size_t n,
+                                                     ArgmaxState *state) {
+    uint64_t best = 0;
+    uint32_t bad = 0;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        float value = v[i];
+        if (!__builtin_isfinite(value)) bad = 1;
+        uint64_t key = argmax_key(value, (uint32_t)i);
+        best = key > best ? key : best;
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63u) == 0) {
+        atomicMax((unsigned long long *)&state->key, (unsigned long long)best);
+    }
+    if (bad) atomicOr(&state->non_finite, 1u);
+}
+
+__global__ void argmax_finish_kernel(const ArgmaxState *state, uint32_t *index) {
+    *index = argmax_key_index(state->key);
+}
+
+// ---- top-k softmax (src/cpu.rs:232-260) -------------------------------
+// One workgroup per row of `count` logits.  Selection i is the largest key
+// strictly below selection i-1 (keys are unique: value, then index).
+__device__ void block_top_k(const float *logits, uint32_t count, uint32_t k, uint32_t *ids,
+                            float *probabilities, uint32_t *non_finite) {
+    __shared__ uint64_t partial[16];
+    __shared__ uint64_t chosen[kMaxTopK];
+    __shared__ float values[kMaxTopK];
+    uint32_t tid = threadIdx.x, nthreads = blockDim.x;
+    uint32_t bad = 0;
+    for (uint32_t i = tid; i < count; i += nthreads)
+        if (!__builtin_isfinite(logits[i])) bad = 1;
+    if (bad) atomicOr(non_finite, 1u);
+    uint64_t previous = ~0ull;
+    for (uint32_t s = 0; s < k; s++) {
+        uint64_t best = 0;
+        for (uint32_t i = tid; i < count; i += nthreads) {
+            uint64_t key = argmax_key(logits[i], i);
+            if (key < previous && key > best) best = key;
+        }
+        best = wave_max_u64(best);
+        if ((tid & 63u) == 0) partial[tid >> 6] = best;
+        __syncthreads();
+        if (tid == 0) {
+            uint64_t b = partial[0];
+            for (uint32_t w = 1; w < (nthreads + 63) / 64; w++) b = partial[w] > b ? partial[w] : b;
+            chosen[s] = b;
+        }
+        __syncthreads();
+        previous = chosen[s];
+    }
+    if (tid == 0) {
+        // softmax_in_place over the selected logits (src/cpu.rs:195-230):
+        // maximum, exp(v - max), sequential sum, divide.
+        float maximum = -__builtin_inff();
+        for (uint32_t s = 0; s < k; s++) {
+            uint32_t index = argmax_key_index(chosen[s]);
+            ids[s] = index;
+            values[s] = logits[index];
+            maximum = fmaxf(maximum, values[s]);
+        }
+        float sum = 0.0f;
+        for (uint32_t s = 0; s < k; s++) {
+            values[s] = expf(values[s] - maximum);
+            sum += values[s];
+        }
+        for (uint32_t s = 0; s < k; s++) probabilities[s] = values[s] / sum;
+    }
+}
+
+__global__ void __launch_bounds__(256) top_k_kernel(const float *__restrict__ logits,
+                                                    uint32_t count, uint32_t k, uint32_t *ids,
+                                                    float *probabilities, uint32_t *non_finite) {
+    uint32_t row = blockIdx.x;
+    block_top_k(logits + (size_t)row * count, count, k, ids + (size_t)row * k,
+                probabilities + (size_t)row * k, non_finite);
+}
+
+// Exact bf16 router + top-k, one workgroup per token.  Thread r folds row r
+// sequentially from column 0 with fma (src/cpu.rs:391-394 order), so the
+// logits equal the CPU's bit for bit and the selected ids cannot differ.
+__global__ void __launch_bounds__(256) router_top_k_kernel(
+    const uint16_t *__restrict__ router, uint32_t hidden, uint32_t experts, uint32_t k,
+    const float *__restrict__ x, float *__restrict__ logits, uint32_t *ids,
+    float *probabilities, uint32_t *non_finite) {
+    uint32_t token = blockIdx.x;
+    extern __shared__ float s_logits[];
+    const float *xt = x + (size_t)token * hidden;
+    float *lt = logits + (size_t)token * experts;
+    for (uint32_t r = threadIdx.x; r < experts; r += blockDim.x) {
+        const uint16_t *w = router + (size_t)r * hidden;
+        float sum = 0.0f;
+        uint32_t c = 0;
+        if ((((uintptr_t)w) & 15u) == 0) {
+            for (; c + 8 <= hidden; c += 8) {
+                u32x4 pk = *(const u32x4 *)(w + c);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    sum = __builtin_fmaf(__uint_as_float(pk[j] << 16), xt[c + 2 * j], sum);
+                    sum = __builtin_fmaf(__uint_as_float(pk[j] & 0xffff0000u), xt[c + 2 * j + 1], sum);
+                }
+            }
+        }
+        for (; c < hidden; c++) sum = __builtin_fmaf(__uint_as_float((uint32_t)w[c] << 16), xt[c], sum);
+        lt[r] = sum;
+        s_logits[r] = sum;
+    }
+    __syncthreads();
+    block_top_k(s_logits, experts, k, ids + (size_t)token * k, probabilities + (size_t)token * k,
+                non_finite);
+}
+
+// ---- RMSNorm (src/cpu.rs:98-142) ---------------------------------------
+__global__ void __launch_bounds__(256) rms_norm_kernel(const float *__restrict__ in, uint32_t n,
+                                                       const float *__restrict__ weight, float eps,
+                                                       float *__restrict__ out) {
+    __shared__ float partial[4];
+    const float *row = in + (size_t)blockIdx.x * n;
+    float *orow = out + (size_t)blockIdx.x * n;
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) s = __builtin_fmaf(row[i], row[i], s);
+    s = wave_sum(s);
+    if ((threadIdx.x & 63u) == 0) partial[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float total = 0.0f;
+    for (uint32_t w = 0; w < blockDim.x / 64; w++) total += partial[w];
+    // (sum / n + eps).sqrt().recip(): two correctly rounded steps.
+    float inverse_rms = 1.0f / __builtin_sqrtf(total / (float)n + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
+        orow[i] = weight ? row[i] * weight[i] * inverse_rms : row[i] * inverse_rms;
+}
+
+// silu(g) * u with the stable sigmoid of src/qwen35/cpu.rs:982-993.
+__device__ __forceinline__ float silu_stable(float v) {
+    float sigmoid;
+    if (v >= 0.0f) {
+        sigmoid = 1.0f / (1.0f + expf(-v));
+    } else {
+        float e = expf(v);
+        sigmoid = e / (1.0f + e);
+    }
+    return v * sigmoid;
+}
+
+__global__ void silu_mul_kernel(const float *__restrict__ gate, const float *__restrict__ up,
+                                size_t n, float *__restrict__ out) {
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = silu_stable(gate[i]) * up[i];
+}
+
+// Ordered expert combine (src/gemma4/cpu.rs:608-611): for every token and
+// feature, y = fma(out_j, p_j, y) over the k selections in order.
+__global__ void moe_combine_kernel(const float *__restrict__ expert_out, const float *__restrict__ p,
+                                   uint32_t batch, uint32_t k, uint32_t hidden,
+                                   float *__restrict__ y) {
+    size_t total = (size_t)batch * hidden;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        uint32_t t = (uint32_t)(e / hidden), i = (uint32_t)(e - (size_t)t * hidden);
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < k; j++)
+            acc = __builtin_fmaf(expert_out[((size_t)t * k + j) * hidden + i], p[(size_t)t * k + j], acc);
+        y[e] = acc;
+    }
+}
+
+// (gate / (1 + exp(-gate))) * up, src/glm52/expert.rs:260-267, applied to
+// `pairs` rows of [gate(width) | up(width)] into act[pairs][width].
+__global__ void silu_mul_glm_pairs_kernel(const float *__restrict__ gate_up, uint32_t pairs,
+                                          uint32_t width, float *__restrict__ act) {
+    size_t total = (size_t)pairs * width;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        uint32_t p = (uint32_t)(e / width), i = (uint32_t)(e - (size_t)p * width);
+        float g = gate_up[(size_t)p * 2 * width + i];
+        float u = gate_up[(size_t)p * 2 * width + width + i];
+        act[e] = (g / (1.0f + expf(-g))) * u;
+    }
+}
+
+// ---- host-side launchers -------------------------------------------------
+
+hipError_t launch_dequantize(hipStream_t s, uint32_t type, const uint8_t *enc, uint32_t be,
+                             uint32_t bb, size_t elements, float *out) {
+    size_t blocks = (elements + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(dequantize_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, type, enc, be,
+                       bb, elements, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_exact(hipStream_t s, uint32_t type, uint32_t be, uint32_t bb, uint32_t rows,
+                             uint32_t columns, size_t row_bytes, const uint8_t *w, uint32_t batch,
+                             const float *x, float *y) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(gemv_exact_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, type, be, bb, rows,
+                       columns, row_bytes, w, batch, x, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(hipStream_t s, const float *v, size_t n, ArgmaxState *state,
+                         uint32_t *index) {
+    hipLaunchKernelGGL(argmax_init_kernel, dim3(1), dim3(1), 0, s, state);
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 1024) blocks = 1024;
+    if (blocks == 0) blocks = 1;
+    hipLaunchKernelGGL(argmax_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, v, n, state);
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1), 0, s, state, index);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_init(hipStream_t s, ArgmaxState *state) {
+    hipLaunchKernelGGL(argmax_init_kernel, dim3(1), dim3(1), 0, s, state);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_finish(hipStream_t s, const ArgmaxState *state, uint32_t *index) {
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1), 0, s, state, index);
+    return hipGetLastError();
+}
+
+hipError_t launch_top_k(hipStream_t s, const float *logits, uint32_t rows, uint32_t count,
+                        uint32_t k, uint32_t *ids, float *probabilities, uint32_t *non_finite) {
+    hipLaunchKernelGGL(top_k_kernel, dim3(rows), dim3(256), 0, s, logits, count, k, ids,
+                       probabilities, non_finite);
+    return hipGetLastError();
+}
+
+hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,
+                               uint32_t experts, uint32_t k, uint32_t batch, const float *x,
+                               float *logits, uint32_t *ids, float *probabilities,
+                               uint32_t *non_finite) {
+    hipLaunchKernelGGL(router_top_k_kernel, dim3(batch), dim3(256), experts * sizeof(float), s,
+                       router, hidden, experts,
+                       k, x, logits, ids, probabilities, non_finite);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(hipStream_t s, const float *in, uint32_t batch, uint32_t n,
+                           const float *weight, float eps, float *out) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(batch), dim3(256), 0, s, in, n, weight, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(hipStream_t s, const float *gate, const float *up, size_t n, float *out) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, gate, up, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(hipStream_t s, const float *expert_out, const float *p, uint32_t batch,
+                              uint32_t k, uint32_t hidden, float *y) {
+    size_t total = (size_t)batch * hidden;
+    size_t blocks = (total + 255) / 256;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, expert_out, p,
+                       batch, k, hidden, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_glm_pairs(hipStream_t s, const float *gate_up, uint32_t pairs,
+                                     uint32_t width, float *act) {
+    size_t total = (size_t)pairs * width;
+    size_t blocks = (total + 255) / 256;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(silu_mul_glm_pairs_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, gate_up,
+                       pairs, width, act);
+    return hipGetLastError();
+}
+
+}  // namespace dm

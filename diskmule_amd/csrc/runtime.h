@@ -1,0 +1,76 @@
+// runtime.h -- host-side state behind the dmhip C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/dmhip.h"
+#include "dm_kernels.h"
+
+namespace dm {
+
+// Records `code` with a formatted message as the calling thread's last error.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps a HIP runtime error onto DMHIP_ERR_COMMAND (MetalError::Command).
+int hip_fail(hipError_t e, const char *what);
+
+#define DM_HIP(call)                                      \
+    do {                                                  \
+        hipError_t dm_e_ = (call);                        \
+        if (dm_e_ != hipSuccess) return dm::hip_fail(dm_e_, #call); \
+    } while (0)
+
+#define DM_CHECK_STATUS(expr)               \
+    do {                                    \
+        int dm_s_ = (expr);                 \
+        if (dm_s_ != DMHIP_OK) return dm_s_; \
+    } while (0)
+
+// Device allocation that grows on demand (scratch for the host-slice API).
+struct Scratch {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    int ensure(size_t need);
+    void release();
+};
+
+// (block elements, block bytes) of a ggml type, src/gguf.rs:321-342.
+bool type_layout(uint32_t type, uint32_t *block_elements, uint32_t *block_bytes);
+const char *type_name(uint32_t type);
+// TensorType::row_byte_len (src/gguf.rs:352-358); false when not a whole
+// number of blocks.
+bool row_byte_len(uint32_t type, uint64_t elements, uint64_t *out);
+
+}  // namespace dm
+
+struct dmhip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipStream_t upload = nullptr;
+    char name[256] = {0};
+    int compute_units = 0;
+    dm::Scratch in, out, enc, aux;          // host-slice staging
+    dm::ArgmaxState *argmax_state = nullptr;  // device
+    uint32_t *argmax_index = nullptr;         // device
+    uint32_t *flags = nullptr;                // device: [0] non-finite
+    bool argmax_pending = false;
+    uint32_t *argmax_user_index = nullptr;
+};
+
+struct dmhip_buf {
+    dmhip_ctx *ctx = nullptr;
+    void *dev = nullptr;
+    size_t len = 0;
+};
+
+namespace dm {
+// Enqueue y = W x on the context stream, choosing the fastest kernel that
+// takes the shape.  Arguments are already validated.
+int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, const void *w,
+                   size_t batch, const float *x, float *y);
+int enqueue_matvec_argmax(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
+                          const void *w, const float *x, float *y, uint32_t *index_device);
+int set_device(dmhip_ctx *ctx);
+}  // namespace dm

@@ -1,0 +1,737 @@
+// runtime.hip -- context, buffers and operators behind include/dmhip.h.
+//
+// Host-slice entry points follow src/metal.rs: validate everything first
+// (same checks, same order, same error variants), then copy inputs in, run
+// the kernels on the context's stream, wait and copy results out.
+#include "runtime.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+namespace dm {
+
+static thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buffer[512];
+    va_list args;
+    va_start(args, fmt);
+    vsnprintf(buffer, sizeof buffer, fmt, args);
+    va_end(args);
+    g_last_error = buffer;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(DMHIP_ERR_COMMAND, "HIP command failed: %s: %s", what, hipGetErrorString(e));
+}
+
+int Scratch::ensure(size_t need) {
+    if (need <= bytes) return DMHIP_OK;
+    release();
+    size_t grow = need < 4096 ? 4096 : need;
+    hipError_t e = hipMalloc(&ptr, grow + 256);
+    if (e != hipSuccess) {
+        ptr = nullptr;
+        return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a %zu-byte device buffer", need);
+    }
+    bytes = grow;
+    return DMHIP_OK;
+}
+
+void Scratch::release() {
+    // Work already enqueued may still read the old allocation.
+    if (ptr) (void)hipDeviceSynchronize();
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+}
+
+bool type_layout(uint32_t type, uint32_t *be, uint32_t *bb) {
+    switch (type) {
+    case 0: *be = 1; *bb = 4; return true;      // F32
+    case 1: *be = 1; *bb = 2; return true;      // F16
+    case 30: *be = 1; *bb = 2; return true;     // BF16
+    case 2: *be = 32; *bb = 18; return true;    // Q4_0
+    case 3: *be = 32; *bb = 20; return true;    // Q4_1
+    case 6: *be = 32; *bb = 22; return true;    // Q5_0
+    case 7: *be = 32; *bb = 24; return true;    // Q5_1
+    case 8: *be = 32; *bb = 34; return true;    // Q8_0
+    case 9: *be = 32; *bb = 40; return true;    // Q8_1
+    case 10: *be = 256; *bb = 84; return true;  // Q2_K
+    case 11: *be = 256; *bb = 110; return true; // Q3_K
+    case 12: *be = 256; *bb = 144; return true; // Q4_K
+    case 13: *be = 256; *bb = 176; return true; // Q5_K
+    case 14: *be = 256; *bb = 210; return true; // Q6_K
+    case 15: *be = 256; *bb = 292; return true; // Q8_K
+    case 24: *be = 1; *bb = 1; return true;     // I8
+    case 25: *be = 1; *bb = 2; return true;     // I16
+    case 26: *be = 1; *bb = 4; return true;     // I32
+    case 27: case 28: *be = 1; *bb = 8; return true;  // I64, F64
+    default: return false;
+    }
+}
+
+const char *type_name(uint32_t type) {
+    switch (type) {
+    case 0: return "F32"; case 1: return "F16"; case 2: return "Q4_0"; case 3: return "Q4_1";
+    case 6: return "Q5_0"; case 7: return "Q5_1"; case 8: return "Q8_0"; case 9: return "Q8_1";
+    case 10: return "Q2_K"; case 11: return "Q3_K"; case 12: return "Q4_K"; case 13: return "Q5_K";
+    case 14: return "Q6_K"; case 15: return "Q8_K"; case 24: return "I8"; case 25: return "I16";
+    case 26: return "I32"; case 27: return "I64"; case 28: return "F64"; case 30: return "BF16";
+    default: return "unknown";
+    }
+}
+
+bool row_byte_len(uint32_t type, uint64_t elements, uint64_t *out) {
+    uint32_t be, bb;
+    if (!type_layout(type, &be, &bb)) return false;
+    if (elements % be) return false;
+    uint64_t blocks = elements / be;
+    if (blocks > UINT64_MAX / bb) return false;
+    *out = blocks * bb;
+    return true;
+}
+
+int set_device(dmhip_ctx *ctx) {
+    DM_HIP(hipSetDevice(ctx->device));
+    return DMHIP_OK;
+}
+
+static bool matvec_kind_supported(uint32_t type) {
+    // The pipelines of MetalContext::prepare_matvec (src/metal.rs:1534-1542).
+    return type == 0 || type == 1 || type == 6 || type == 8 || type == 12 || type == 14;
+}
+
+// MetalContext::prepare_matvec (src/metal.rs:1513-1560), same order of checks.
+static int prepare_matvec(uint32_t type, size_t rows, size_t columns, size_t encoded_length,
+                          size_t input_len, size_t output_len, size_t *row_bytes_out) {
+    if (input_len != columns)
+        return fail(DMHIP_ERR_INVALID_INPUT_LENGTH, "matvec input has %zu columns; expected %zu",
+                    input_len, columns);
+    if (output_len != rows)
+        return fail(DMHIP_ERR_INVALID_OUTPUT_LENGTH, "matvec output has %zu rows; expected %zu",
+                    output_len, rows);
+    if (!matvec_kind_supported(type))
+        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE,
+                    "HIP matrix-vector multiplication does not support %s", type_name(type));
+    uint64_t row_bytes;
+    if (!row_byte_len(type, columns, &row_bytes)) {
+        uint32_t be, bb;
+        type_layout(type, &be, &bb);
+        return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT,
+                    "%s output length %zu is not divisible by its %u-element block",
+                    type_name(type), columns, be);
+    }
+    if (rows != 0 && row_bytes > SIZE_MAX / rows)
+        return fail(DMHIP_ERR_OVERFLOW, "matrix dimensions or encoded byte length overflowed");
+    size_t matrix_bytes = rows * (size_t)row_bytes;
+    if (encoded_length != matrix_bytes)
+        return fail(DMHIP_ERR_INVALID_BYTE_LENGTH, "%s requires %zu encoded bytes, got %zu",
+                    type_name(type), matrix_bytes, encoded_length);
+    *row_bytes_out = (size_t)row_bytes;
+    return DMHIP_OK;
+}
+
+static int count_u32(size_t n) {
+    if (n > 0xffffffffull) return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "HIP vector length exceeds the 32-bit kernel limit");
+    return DMHIP_OK;
+}
+
+static int require_nonempty(const char *operation, size_t n) {
+    if (n == 0) return fail(DMHIP_ERR_EMPTY_INPUT, "%s requires a non-empty input", operation);
+    return DMHIP_OK;
+}
+
+static int validate_vector_length(const char *operation, const char *argument, size_t expected,
+                                  size_t actual) {
+    if (actual != expected)
+        return fail(DMHIP_ERR_INVALID_VECTOR_LENGTH, "%s %s has length %zu; expected %zu",
+                    operation, argument, actual, expected);
+    return DMHIP_OK;
+}
+
+static int require_positive(const char *operation, float v) {
+    if (!isfinite(v) || v <= 0.0f)
+        return fail(DMHIP_ERR_INVALID_POSITIVE_PARAMETER, "%s requires a finite positive parameter",
+                    operation);
+    return DMHIP_OK;
+}
+
+static bool all_finite(const float *v, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        if (!isfinite(v[i])) return false;
+    return true;
+}
+
+}  // namespace dm
+
+using namespace dm;
+
+#define DM_CHECK(expr)                    \
+    do {                                  \
+        int dm_s_ = (expr);               \
+        if (dm_s_ != DMHIP_OK) return dm_s_; \
+    } while (0)
+
+#define DM_REQUIRE(ptr)                                                                 \
+    do {                                                                                \
+        if (!(ptr)) return fail(DMHIP_ERR_INVALID_ARGUMENT, "%s must not be null", #ptr); \
+    } while (0)
+
+extern "C" {
+
+const char *dmhip_last_error(void) { return dm::g_last_error.c_str(); }
+
+int dmhip_context_new(int device, dmhip_ctx **out) {
+    DM_REQUIRE(out);
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0 || device < 0 || device >= count)
+        return fail(DMHIP_ERR_NO_DEVICE, "no HIP device %d is available", device);
+    dmhip_ctx *ctx = new dmhip_ctx();
+    ctx->device = device;
+    hipDeviceProp_t prop;
+    if (hipSetDevice(device) != hipSuccess || hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        delete ctx;
+        return fail(DMHIP_ERR_NO_DEVICE, "HIP device %d did not answer", device);
+    }
+    snprintf(ctx->name, sizeof ctx->name, "%s (%s)", prop.name, prop.gcnArchName);
+    ctx->compute_units = prop.multiProcessorCount;
+    // Default-priority streams only.
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->upload, hipStreamNonBlocking) != hipSuccess ||
+        hipMalloc((void **)&ctx->argmax_state, sizeof(ArgmaxState)) != hipSuccess ||
+        hipMalloc((void **)&ctx->argmax_index, 64) != hipSuccess ||
+        hipMalloc((void **)&ctx->flags, 64) != hipSuccess) {
+        dmhip_context_free(ctx);
+        return fail(DMHIP_ERR_COMMAND, "could not create the HIP streams of device %d", device);
+    }
+    *out = ctx;
+    return DMHIP_OK;
+}
+
+void dmhip_context_free(dmhip_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->upload) (void)hipStreamSynchronize(ctx->upload);
+    ctx->in.release();
+    ctx->out.release();
+    ctx->enc.release();
+    ctx->aux.release();
+    if (ctx->argmax_state) (void)hipFree(ctx->argmax_state);
+    if (ctx->argmax_index) (void)hipFree(ctx->argmax_index);
+    if (ctx->flags) (void)hipFree(ctx->flags);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    if (ctx->upload) (void)hipStreamDestroy(ctx->upload);
+    delete ctx;
+}
+
+int dmhip_device_name(dmhip_ctx *ctx, char *buffer, size_t capacity) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(buffer);
+    if (capacity == 0) return fail(DMHIP_ERR_INVALID_ARGUMENT, "capacity must not be zero");
+    snprintf(buffer, capacity, "%s", ctx->name);
+    return DMHIP_OK;
+}
+
+int dmhip_synchronize(dmhip_ctx *ctx) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(hipStreamSynchronize(ctx->upload));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+void *dmhip_stream(dmhip_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+// ---- buffers -------------------------------------------------------------
+
+static int new_buffer(dmhip_ctx *ctx, size_t length, dmhip_buf **out) {
+    dmhip_buf *b = new dmhip_buf();
+    b->ctx = ctx;
+    b->len = length;
+    // 256 spare bytes: vector loads of the last row may read a few bytes past
+    // its end (they are discarded); the spare keeps them inside the allocation.
+    if (hipMalloc(&b->dev, length + 256) != hipSuccess) {
+        delete b;
+        return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a %zu-byte device buffer",
+                    length);
+    }
+    *out = b;
+    return DMHIP_OK;
+}
+
+int dmhip_map_read_only(dmhip_ctx *ctx, const void *host, size_t length, dmhip_buf **out) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(out);
+    *out = nullptr;
+    if (length == 0) return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a 0-byte device buffer");
+    DM_REQUIRE(host);
+    DM_CHECK(set_device(ctx));
+    dmhip_buf *b;
+    DM_CHECK(new_buffer(ctx, length, &b));
+    hipError_t e = hipMemcpyAsync(b->dev, host, length, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync((char *)b->dev + length, 0, 256, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        dmhip_buffer_free(b);
+        return hip_fail(e, "map_read_only upload");
+    }
+    *out = b;
+    return DMHIP_OK;
+}
+
+int dmhip_new_owned_buffer(dmhip_ctx *ctx, size_t length, dmhip_buf **out) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(out);
+    *out = nullptr;
+    if (length == 0) return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a 0-byte device buffer");
+    DM_CHECK(set_device(ctx));
+    dmhip_buf *b;
+    DM_CHECK(new_buffer(ctx, length, &b));
+    hipError_t e = hipMemsetAsync(b->dev, 0, length + 256, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        dmhip_buffer_free(b);
+        return hip_fail(e, "new_owned_buffer clear");
+    }
+    *out = b;
+    return DMHIP_OK;
+}
+
+void dmhip_buffer_free(dmhip_buf *b) {
+    if (!b) return;
+    if (b->ctx) {
+        (void)hipSetDevice(b->ctx->device);
+        (void)hipStreamSynchronize(b->ctx->stream);
+    }
+    if (b->dev) (void)hipFree(b->dev);
+    delete b;
+}
+
+size_t dmhip_buffer_len(const dmhip_buf *b) { return b ? b->len : 0; }
+void *dmhip_buffer_device_ptr(const dmhip_buf *b) { return b ? b->dev : nullptr; }
+
+static int check_range(const dmhip_buf *b, size_t offset, size_t n) {
+    size_t end;
+    if (__builtin_add_overflow(offset, n, &end))
+        return fail(DMHIP_ERR_OVERFLOW, "matrix dimensions or encoded byte length overflowed");
+    if (end > b->len)
+        return fail(DMHIP_ERR_MAPPED_RANGE, "mapped buffer range %zu..%zu exceeds its %zu-byte file mapping",
+                    offset, end, b->len);
+    return DMHIP_OK;
+}
+
+int dmhip_buffer_write(dmhip_ctx *ctx, dmhip_buf *b, size_t offset, const void *src, size_t n) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(b);
+    DM_CHECK(check_range(b, offset, n));
+    if (n == 0) return DMHIP_OK;
+    DM_REQUIRE(src);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(hipMemcpyAsync((char *)b->dev + offset, src, n, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_buffer_read(dmhip_ctx *ctx, const dmhip_buf *b, size_t offset, void *dst, size_t n) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(b);
+    DM_CHECK(check_range(b, offset, n));
+    if (n == 0) return DMHIP_OK;
+    DM_REQUIRE(dst);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(hipMemcpyAsync(dst, (const char *)b->dev + offset, n, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_copy_to_host(dmhip_ctx *ctx, void *dst, const void *device_src, size_t n) {
+    DM_REQUIRE(ctx);
+    if (n == 0) return DMHIP_OK;
+    DM_REQUIRE(dst);
+    DM_REQUIRE(device_src);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(hipMemcpyAsync(dst, device_src, n, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_copy_to_device(dmhip_ctx *ctx, void *device_dst, const void *src, size_t n) {
+    DM_REQUIRE(ctx);
+    if (n == 0) return DMHIP_OK;
+    DM_REQUIRE(device_dst);
+    DM_REQUIRE(src);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(hipMemcpyAsync(device_dst, src, n, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_host_alloc_pinned(size_t bytes, void **out) {
+    DM_REQUIRE(out);
+    *out = nullptr;
+    if (bytes == 0) return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate 0 pinned bytes");
+    if (hipHostMalloc(out, bytes, hipHostMallocDefault) != hipSuccess) {
+        *out = nullptr;
+        return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate %zu pinned host bytes", bytes);
+    }
+    return DMHIP_OK;
+}
+
+void dmhip_host_free_pinned(void *p) {
+    if (p) (void)hipHostFree(p);
+}
+
+// ---- synchronous host-slice operators --------------------------------------
+
+int dmhip_rms_norm(dmhip_ctx *ctx, const float *input, size_t input_len, const float *weight,
+                   size_t weight_len, float epsilon, float *output, size_t output_len) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(require_nonempty("RMSNorm", input_len));
+    DM_CHECK(validate_vector_length("RMSNorm", "output", input_len, output_len));
+    if (weight) DM_CHECK(validate_vector_length("RMSNorm", "weight", input_len, weight_len));
+    DM_CHECK(require_positive("RMSNorm epsilon", epsilon));
+    DM_REQUIRE(input);
+    DM_REQUIRE(output);
+    if (!all_finite(input, input_len))
+        return fail(DMHIP_ERR_NON_FINITE, "RMSNorm received a non-finite value");
+    DM_CHECK(count_u32(input_len));
+    DM_CHECK(set_device(ctx));
+    size_t bytes = input_len * sizeof(float);
+    DM_CHECK(ctx->in.ensure(2 * bytes));
+    DM_CHECK(ctx->out.ensure(bytes));
+    float *din = (float *)ctx->in.ptr;
+    float *dw = weight ? din + input_len : nullptr;
+    DM_HIP(hipMemcpyAsync(din, input, bytes, hipMemcpyHostToDevice, ctx->stream));
+    if (weight) DM_HIP(hipMemcpyAsync(dw, weight, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(launch_rms_norm(ctx->stream, din, 1, (uint32_t)input_len, dw, epsilon, (float *)ctx->out.ptr));
+    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_silu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const float *up,
+                   size_t up_len, float *output, size_t output_len) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(require_nonempty("SiLU multiply", gate_len));
+    DM_CHECK(validate_vector_length("SiLU multiply", "up", gate_len, up_len));
+    DM_CHECK(validate_vector_length("SiLU multiply", "output", gate_len, output_len));
+    DM_REQUIRE(gate);
+    DM_REQUIRE(up);
+    DM_REQUIRE(output);
+    DM_CHECK(count_u32(gate_len));
+    DM_CHECK(set_device(ctx));
+    size_t bytes = gate_len * sizeof(float);
+    DM_CHECK(ctx->in.ensure(2 * bytes));
+    DM_CHECK(ctx->out.ensure(bytes));
+    float *dg = (float *)ctx->in.ptr, *du = dg + gate_len;
+    DM_HIP(hipMemcpyAsync(dg, gate, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(hipMemcpyAsync(du, up, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(launch_silu_mul(ctx->stream, dg, du, gate_len, (float *)ctx->out.ptr));
+    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_argmax(dmhip_ctx *ctx, const float *input, size_t input_len, size_t *index) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(index);
+    DM_CHECK(require_nonempty("argmax", input_len));
+    DM_REQUIRE(input);
+    if (!all_finite(input, input_len))
+        return fail(DMHIP_ERR_NON_FINITE, "argmax received a non-finite value");
+    DM_CHECK(count_u32(input_len));
+    DM_CHECK(set_device(ctx));
+    size_t bytes = input_len * sizeof(float);
+    DM_CHECK(ctx->in.ensure(bytes));
+    DM_HIP(hipMemcpyAsync(ctx->in.ptr, input, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(launch_argmax(ctx->stream, (const float *)ctx->in.ptr, input_len, ctx->argmax_state,
+                         ctx->argmax_index));
+    uint32_t result = 0;
+    DM_HIP(hipMemcpyAsync(&result, ctx->argmax_index, 4, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    *index = result;
+    return DMHIP_OK;
+}
+
+int dmhip_top_k_softmax(dmhip_ctx *ctx, const float *logits, size_t logits_len, size_t k,
+                        size_t *indices, float *probabilities) {
+    DM_REQUIRE(ctx);
+    if (k == 0 || k > logits_len)
+        return fail(DMHIP_ERR_INVALID_TOP_K, "top-k count %zu is outside 1..=%zu", k, logits_len);
+    DM_REQUIRE(logits);
+    DM_REQUIRE(indices);
+    DM_REQUIRE(probabilities);
+    if (!all_finite(logits, logits_len))
+        return fail(DMHIP_ERR_NON_FINITE, "top-k softmax received a non-finite value");
+    DM_CHECK(count_u32(logits_len));
+    if (k > kMaxTopK)
+        return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "top-k count %zu exceeds the kernel limit %u", k, kMaxTopK);
+    DM_CHECK(set_device(ctx));
+    size_t bytes = logits_len * sizeof(float);
+    DM_CHECK(ctx->in.ensure(bytes));
+    DM_CHECK(ctx->out.ensure(k * 8));
+    uint32_t *dids = (uint32_t *)ctx->out.ptr;
+    float *dp = (float *)(dids + k);
+    DM_HIP(hipMemcpyAsync(ctx->in.ptr, logits, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(launch_top_k(ctx->stream, (const float *)ctx->in.ptr, 1, (uint32_t)logits_len,
+                        (uint32_t)k, dids, dp, ctx->flags));
+    uint32_t ids[kMaxTopK];
+    DM_HIP(hipMemcpyAsync(ids, dids, k * 4, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipMemcpyAsync(probabilities, dp, k * 4, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    for (size_t i = 0; i < k; i++) indices[i] = ids[i];
+    return DMHIP_OK;
+}
+
+static int matvec_from_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
+                              const void *w, const float *input, float *output) {
+    if (rows == 0) return DMHIP_OK;
+    DM_CHECK(require_nonempty("matvec", columns));
+    DM_REQUIRE(input);
+    DM_REQUIRE(output);
+    DM_CHECK(count_u32(columns));
+    DM_CHECK(count_u32(rows));
+    DM_CHECK(ctx->in.ensure(columns * sizeof(float)));
+    DM_CHECK(ctx->out.ensure(rows * sizeof(float)));
+    DM_HIP(hipMemcpyAsync(ctx->in.ptr, input, columns * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    DM_CHECK(enqueue_matvec(ctx, type, rows, columns, w, 1, (const float *)ctx->in.ptr,
+                            (float *)ctx->out.ptr));
+    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
+                 const uint8_t *encoded, size_t encoded_len, const float *input, size_t input_len,
+                 float *output, size_t output_len) {
+    DM_REQUIRE(ctx);
+    size_t row_bytes;
+    DM_CHECK(prepare_matvec(type, rows, columns, encoded_len, input_len, output_len, &row_bytes));
+    if (rows == 0) return DMHIP_OK;
+    DM_CHECK(require_nonempty("matvec", input_len));
+    DM_REQUIRE(encoded);
+    DM_CHECK(set_device(ctx));
+    // Like MetalContext::matvec (src/metal.rs:664), the encoded matrix is
+    // copied to the device for this call.
+    DM_CHECK(ctx->enc.ensure(encoded_len + 256));
+    DM_HIP(hipMemcpyAsync(ctx->enc.ptr, encoded, encoded_len, hipMemcpyHostToDevice, ctx->stream));
+    return matvec_from_device(ctx, type, rows, columns, ctx->enc.ptr, input, output);
+}
+
+static int matvec_buffer(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
+                         const dmhip_buf *buf, size_t offset, size_t length, const float *input,
+                         size_t input_len, float *output, size_t output_len) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(buf);
+    size_t row_bytes;
+    DM_CHECK(prepare_matvec(type, rows, columns, length, input_len, output_len, &row_bytes));
+    DM_CHECK(check_range(buf, offset, length));
+    if (rows == 0) return DMHIP_OK;
+    DM_CHECK(require_nonempty("matvec", input_len));
+    DM_CHECK(set_device(ctx));
+    return matvec_from_device(ctx, type, rows, columns, (const char *)buf->dev + offset, input, output);
+}
+
+int dmhip_matvec_mapped(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
+                        const dmhip_buf *mapping, size_t offset, size_t length, const float *input,
+                        size_t input_len, float *output, size_t output_len) {
+    return matvec_buffer(ctx, type, rows, columns, mapping, offset, length, input, input_len,
+                         output, output_len);
+}
+
+int dmhip_matvec_owned(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
+                       const dmhip_buf *encoded, size_t offset, size_t length, const float *input,
+                       size_t input_len, float *output, size_t output_len) {
+    return matvec_buffer(ctx, type, rows, columns, encoded, offset, length, input, input_len,
+                         output, output_len);
+}
+
+int dmhip_dequantize(dmhip_ctx *ctx, uint32_t type, const dmhip_buf *encoded, size_t offset,
+                     size_t length, float *output, size_t elements) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(encoded);
+    // cpu::dequantize validation (src/cpu.rs:313-341).
+    if (!(type == 0 || type == 1 || type == 6 || type == 8 || type == 12 || type == 14))
+        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "HIP dequantization does not support %s",
+                    type_name(type));
+    uint64_t expected;
+    uint32_t be, bb;
+    type_layout(type, &be, &bb);
+    if (!row_byte_len(type, elements, &expected))
+        return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT,
+                    "%s output length %zu is not divisible by its %u-element block",
+                    type_name(type), elements, be);
+    if (length != expected)
+        return fail(DMHIP_ERR_INVALID_BYTE_LENGTH, "%s requires %llu encoded bytes, got %zu",
+                    type_name(type), (unsigned long long)expected, length);
+    DM_CHECK(check_range(encoded, offset, length));
+    if (elements == 0) return DMHIP_OK;
+    DM_REQUIRE(output);
+    DM_CHECK(set_device(ctx));
+    DM_CHECK(ctx->out.ensure(elements * sizeof(float)));
+    DM_HIP(launch_dequantize(ctx->stream, type, (const uint8_t *)encoded->dev + offset, be, bb,
+                             elements, (float *)ctx->out.ptr));
+    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, elements * sizeof(float), hipMemcpyDeviceToHost,
+                          ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+// ---- stream-ordered device operators ---------------------------------------
+
+static int validate_device_matvec(uint32_t type, size_t rows, size_t columns, size_t batch) {
+    if (!(type == 0 || type == 1 || type == 6 || type == 8 || type == 12 || type == 14))
+        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE,
+                    "HIP matrix-vector multiplication does not support %s", type_name(type));
+    uint64_t rb;
+    if (!row_byte_len(type, columns, &rb)) {
+        uint32_t be, bb;
+        type_layout(type, &be, &bb);
+        return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT,
+                    "%s output length %zu is not divisible by its %u-element block",
+                    type_name(type), columns, be);
+    }
+    if (batch < 1 || batch > 16)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "batch %zu is outside 1..=16", batch);
+    DM_CHECK(count_u32(rows));
+    DM_CHECK(count_u32(columns));
+    if (rows != 0 && rb > SIZE_MAX / rows)
+        return fail(DMHIP_ERR_OVERFLOW, "matrix dimensions or encoded byte length overflowed");
+    return DMHIP_OK;
+}
+
+int dmhip_matvec_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
+                        const void *weights, size_t batch, const float *x, float *y) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(validate_device_matvec(type, rows, columns, batch));
+    if (rows == 0) return DMHIP_OK;
+    DM_CHECK(require_nonempty("matvec", columns));
+    DM_REQUIRE(weights);
+    DM_REQUIRE(x);
+    DM_REQUIRE(y);
+    DM_CHECK(set_device(ctx));
+    return enqueue_matvec(ctx, type, rows, columns, weights, batch, x, y);
+}
+
+int dmhip_matvec_argmax_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
+                               const void *weights, const float *x, float *y,
+                               uint32_t *index_device) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(validate_device_matvec(type, rows, columns, 1));
+    DM_CHECK(require_nonempty("argmax", rows));
+    DM_CHECK(require_nonempty("matvec", columns));
+    DM_REQUIRE(weights);
+    DM_REQUIRE(x);
+    DM_REQUIRE(y);
+    DM_REQUIRE(index_device);
+    DM_CHECK(set_device(ctx));
+    DM_CHECK(enqueue_matvec_argmax(ctx, type, rows, columns, weights, x, y, index_device));
+    ctx->argmax_pending = true;
+    ctx->argmax_user_index = index_device;
+    return DMHIP_OK;
+}
+
+int dmhip_argmax_result(dmhip_ctx *ctx, size_t *index) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(index);
+    if (!ctx->argmax_pending)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "no matvec_argmax is pending on this context");
+    DM_CHECK(set_device(ctx));
+    ArgmaxState state;
+    uint32_t result = 0;
+    DM_HIP(hipMemcpyAsync(&state, ctx->argmax_state, sizeof state, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipMemcpyAsync(&result, ctx->argmax_user_index, 4, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    ctx->argmax_pending = false;
+    if (state.non_finite) return fail(DMHIP_ERR_NON_FINITE, "argmax received a non-finite value");
+    *index = result;
+    return DMHIP_OK;
+}
+
+int dmhip_rms_norm_device(dmhip_ctx *ctx, size_t batch, size_t count, const float *input,
+                          const float *weight, float epsilon, float *output) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(require_nonempty("RMSNorm", count));
+    DM_CHECK(require_positive("RMSNorm epsilon", epsilon));
+    DM_REQUIRE(input);
+    DM_REQUIRE(output);
+    DM_CHECK(count_u32(count));
+    DM_CHECK(count_u32(batch));
+    if (batch == 0) return DMHIP_OK;
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_rms_norm(ctx->stream, input, (uint32_t)batch, (uint32_t)count, weight, epsilon, output));
+    return DMHIP_OK;
+}
+
+int dmhip_silu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const float *up,
+                          float *output) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(require_nonempty("SiLU multiply", count));
+    DM_REQUIRE(gate);
+    DM_REQUIRE(up);
+    DM_REQUIRE(output);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_silu_mul(ctx->stream, gate, up, count, output));
+    return DMHIP_OK;
+}
+
+int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t experts,
+                              size_t k, const uint16_t *router_bf16, const float *x,
+                              float *logits, uint32_t *ids, float *probabilities) {
+    DM_REQUIRE(ctx);
+    if (k == 0 || k > experts)
+        return fail(DMHIP_ERR_INVALID_TOP_K, "top-k count %zu is outside 1..=%zu", k, experts);
+    if (k > kMaxTopK || experts > 16384)
+        return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "router with %zu experts, top-%zu exceeds the kernel limits",
+                    experts, k);
+    DM_CHECK(require_nonempty("router", hidden));
+    DM_REQUIRE(router_bf16);
+    DM_REQUIRE(x);
+    DM_REQUIRE(logits);
+    DM_REQUIRE(ids);
+    DM_REQUIRE(probabilities);
+    DM_CHECK(count_u32(hidden));
+    if (batch == 0) return DMHIP_OK;
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
+                               (uint32_t)k, (uint32_t)batch, x, logits, ids, probabilities,
+                               ctx->flags));
+    return DMHIP_OK;
+}
+
+int dmhip_event_record(dmhip_ctx *ctx, void **event) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(event);
+    DM_CHECK(set_device(ctx));
+    hipEvent_t e;
+    DM_HIP(hipEventCreate(&e));
+    hipError_t r = hipEventRecord(e, ctx->stream);
+    if (r != hipSuccess) {
+        (void)hipEventDestroy(e);
+        return hip_fail(r, "hipEventRecord");
+    }
+    *event = (void *)e;
+    return DMHIP_OK;
+}
+
+int dmhip_event_elapsed_ms(void *start, void *stop, float *ms) {
+    DM_REQUIRE(start);
+    DM_REQUIRE(stop);
+    DM_REQUIRE(ms);
+    DM_HIP(hipEventSynchronize((hipEvent_t)stop));
+    DM_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return DMHIP_OK;
+}
+
+void dmhip_event_free(void *event) {
+    if (event) (void)hipEventDestroy((hipEvent_t)event);
+}
+
+}  // extern "C"

@@ -1,0 +1,521 @@
+"""ctypes binding of ``libdmhip.so`` (the C ABI in ``include/dmhip.h``).
+
+Method names, argument meaning and errors mirror the reference's Metal
+backend (``src/metal.rs``: ``MetalContext``, ``MetalOwnedBuffer``,
+``MetalMappedBuffer``) and expert residency (``src/expert.rs``), so callers
+and tests read like the reference's own.  Errors raise :class:`HipError`
+whose ``variant`` is the ``MetalError`` / ``ExpertCacheError`` variant name.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Callable, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = os.path.join(_HERE, "libdmhip.so")
+
+# dmhip_status -> reference error variant
+VARIANTS = {
+    0: "Ok", 1: "NoDevice", 2: "BufferAllocation", 3: "VectorLength", 4: "VectorTooLarge",
+    5: "EmptyInput", 6: "InvalidVectorLength", 7: "InvalidPositiveParameter", 8: "NonFinite",
+    9: "UnsupportedTensorType", 10: "InvalidElementCount", 11: "InvalidByteLength",
+    12: "Overflow", 13: "InvalidInputLength", 14: "InvalidOutputLength", 15: "InvalidTopK",
+    16: "MappedRange", 17: "Command", 18: "NoSlots", 19: "InvalidLayer", 20: "InvalidExpert",
+    21: "AllSlotsPinned", 22: "Cancelled", 23: "InvalidLayout", 24: "InvalidArgument",
+}
+
+# Every function include/dmhip.h declares (checked against the header by tests).
+EXPORTED_SYMBOLS = [
+    "dmhip_last_error", "dmhip_context_new", "dmhip_context_free", "dmhip_device_name",
+    "dmhip_synchronize", "dmhip_stream", "dmhip_map_read_only", "dmhip_new_owned_buffer",
+    "dmhip_buffer_free", "dmhip_buffer_len", "dmhip_buffer_device_ptr", "dmhip_buffer_write",
+    "dmhip_buffer_read", "dmhip_copy_to_host", "dmhip_copy_to_device", "dmhip_host_alloc_pinned", "dmhip_host_free_pinned", "dmhip_rms_norm",
+    "dmhip_silu_mul", "dmhip_argmax", "dmhip_top_k_softmax", "dmhip_matvec",
+    "dmhip_matvec_mapped", "dmhip_matvec_owned", "dmhip_dequantize", "dmhip_matvec_device",
+    "dmhip_matvec_argmax_device", "dmhip_argmax_result", "dmhip_rms_norm_device",
+    "dmhip_silu_mul_device", "dmhip_ffn_workspace_bytes", "dmhip_ffn_device",
+    "dmhip_router_top_k_device", "dmhip_gemm_workspace_bytes", "dmhip_gemm_device",
+    "dmhip_event_record", "dmhip_event_elapsed_ms", "dmhip_event_free",
+    "dmhip_expert_cache_new", "dmhip_expert_cache_free", "dmhip_expert_cache_stats_get",
+    "dmhip_expert_cache_slots_per_layer", "dmhip_expert_acquire", "dmhip_expert_release",
+    "dmhip_moe_layer",
+]
+
+F32, F16, Q5_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 6, 8, 12, 14, 30
+
+
+class HipError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        self.code = code
+        self.variant = VARIANTS.get(code, f"Unknown({code})")
+        super().__init__(f"{self.variant}: {message}")
+
+
+def library_path() -> str:
+    return _LIB
+
+
+_lib = None
+
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_u32 = ctypes.c_uint32
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_szp = ctypes.POINTER(ctypes.c_size_t)
+
+
+class _Layout(ctypes.Structure):
+    _fields_ = [("expert_count", _sz), ("gate_up_offset", ctypes.c_uint64),
+                ("gate_up_bytes", _sz), ("down_offset", ctypes.c_uint64), ("down_bytes", _sz)]
+
+
+class _Stats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in
+                ("hits", "misses", "evictions", "reads", "bytes_read", "io_wait_ns", "resident_bytes")]
+
+
+def load_library() -> ctypes.CDLL:
+    """Load ``libdmhip.so``; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB):
+        raise HipError(1, f"{_LIB} is missing: build it with diskmule_amd/build.py "
+                          "(there is no CPU fallback)")
+    lib = ctypes.CDLL(_LIB)
+    sig = {
+        "dmhip_last_error": ([], ctypes.c_char_p),
+        "dmhip_context_new": ([ctypes.c_int, ctypes.POINTER(_vp)], ctypes.c_int),
+        "dmhip_context_free": ([_vp], None),
+        "dmhip_device_name": ([_vp, ctypes.c_char_p, _sz], ctypes.c_int),
+        "dmhip_synchronize": ([_vp], ctypes.c_int),
+        "dmhip_stream": ([_vp], _vp),
+        "dmhip_map_read_only": ([_vp, _vp, _sz, ctypes.POINTER(_vp)], ctypes.c_int),
+        "dmhip_new_owned_buffer": ([_vp, _sz, ctypes.POINTER(_vp)], ctypes.c_int),
+        "dmhip_buffer_free": ([_vp], None),
+        "dmhip_buffer_len": ([_vp], _sz),
+        "dmhip_buffer_device_ptr": ([_vp], _vp),
+        "dmhip_buffer_write": ([_vp, _vp, _sz, _vp, _sz], ctypes.c_int),
+        "dmhip_buffer_read": ([_vp, _vp, _sz, _vp, _sz], ctypes.c_int),
+        "dmhip_copy_to_host": ([_vp, _vp, _vp, _sz], ctypes.c_int),
+        "dmhip_copy_to_device": ([_vp, _vp, _vp, _sz], ctypes.c_int),
+        "dmhip_host_alloc_pinned": ([_sz, ctypes.POINTER(_vp)], ctypes.c_int),
+        "dmhip_host_free_pinned": ([_vp], None),
+        "dmhip_rms_norm": ([_vp, _f32p, _sz, _f32p, _sz, ctypes.c_float, _f32p, _sz], ctypes.c_int),
+        "dmhip_silu_mul": ([_vp, _f32p, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_argmax": ([_vp, _f32p, _sz, _szp], ctypes.c_int),
+        "dmhip_top_k_softmax": ([_vp, _f32p, _sz, _sz, _szp, _f32p], ctypes.c_int),
+        "dmhip_matvec": ([_vp, _u32, _sz, _sz, _u8p, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_matvec_mapped": ([_vp, _u32, _sz, _sz, _vp, _sz, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_matvec_owned": ([_vp, _u32, _sz, _sz, _vp, _sz, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_dequantize": ([_vp, _u32, _vp, _sz, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_matvec_device": ([_vp, _u32, _sz, _sz, _vp, _sz, _vp, _vp], ctypes.c_int),
+        "dmhip_matvec_argmax_device": ([_vp, _u32, _sz, _sz, _vp, _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_argmax_result": ([_vp, _szp], ctypes.c_int),
+        "dmhip_rms_norm_device": ([_vp, _sz, _sz, _vp, _vp, ctypes.c_float, _vp], ctypes.c_int),
+        "dmhip_silu_mul_device": ([_vp, _sz, _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_ffn_workspace_bytes": ([_sz, _sz], _sz),
+        "dmhip_ffn_device": ([_vp, _sz, _sz, _sz, _u32, _vp, _u32, _vp, _u32, _vp, ctypes.c_float,
+                              _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_router_top_k_device": ([_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_gemm_workspace_bytes": ([_sz, _sz], _sz),
+        "dmhip_gemm_device": ([_vp, _u32, _sz, _sz, _sz, _vp, _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_event_record": ([_vp, ctypes.POINTER(_vp)], ctypes.c_int),
+        "dmhip_event_elapsed_ms": ([_vp, _vp, ctypes.POINTER(ctypes.c_float)], ctypes.c_int),
+        "dmhip_event_free": ([_vp], None),
+        "dmhip_expert_cache_new": ([_vp, _vp, _sz, ctypes.POINTER(_Layout), _sz, _sz, ctypes.POINTER(_vp)],
+                                   ctypes.c_int),
+        "dmhip_expert_cache_free": ([_vp], None),
+        "dmhip_expert_cache_stats_get": ([_vp, ctypes.POINTER(_Stats)], ctypes.c_int),
+        "dmhip_expert_cache_slots_per_layer": ([_vp], _sz),
+        "dmhip_expert_acquire": ([_vp, _sz, _sz, ctypes.POINTER(ctypes.c_int), _szp,
+                                  ctypes.POINTER(_vp), ctypes.POINTER(_vp)], ctypes.c_int),
+        "dmhip_expert_release": ([_vp, _sz, _sz], ctypes.c_int),
+        "dmhip_moe_layer": ([_vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _u32, _u32, _vp, _vp,
+                             ctypes.POINTER(ctypes.c_uint32), _f32p], ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = lib
+    return lib
+
+
+def _check(code: int) -> None:
+    if code != 0:
+        msg = load_library().dmhip_last_error()
+        raise HipError(code, msg.decode() if msg else "")
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(_f32p) if a.size else None
+
+
+class _Buffer:
+    def __init__(self, ctx: "HipContext", handle: int):
+        self._ctx = ctx
+        self._h = _vp(handle)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def __len__(self) -> int:
+        return int(load_library().dmhip_buffer_len(self._h))
+
+    def is_empty(self) -> bool:
+        return len(self) == 0
+
+    @property
+    def device_ptr(self) -> int:
+        return int(load_library().dmhip_buffer_device_ptr(self._h) or 0)
+
+    def write(self, offset: int, data) -> None:
+        arr = np.ascontiguousarray(data)
+        _check(load_library().dmhip_buffer_write(self._ctx.handle, self._h, offset,
+                                                  arr.ctypes.data, arr.nbytes))
+
+    def read(self, offset: int, nbytes: int, dtype=np.uint8) -> np.ndarray:
+        out = np.empty(nbytes, dtype=np.uint8)
+        _check(load_library().dmhip_buffer_read(self._ctx.handle, self._h, offset,
+                                                 out.ctypes.data, nbytes))
+        return out.view(dtype)
+
+    def free(self) -> None:
+        if self._h:
+            load_library().dmhip_buffer_free(self._h)
+            self._h = _vp(None)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class OwnedBuffer(_Buffer):
+    """MetalOwnedBuffer (src/metal.rs:213-243): zero-filled device bytes."""
+
+    def as_bytes(self) -> np.ndarray:
+        return self.read(0, len(self))
+
+
+class MappedBuffer(_Buffer):
+    """MetalMappedBuffer (src/metal.rs:207-211, :280-288): a GGUF mapping
+    uploaded to HBM once, offsets unchanged."""
+
+
+class HipContext:
+    """MetalContext (src/metal.rs:179-1560) on one HIP device."""
+
+    def __init__(self, device: int = 0):
+        lib = load_library()
+        h = _vp()
+        _check(lib.dmhip_context_new(device, ctypes.byref(h)))
+        self._h = h
+
+    @classmethod
+    def new(cls, device: int = 0) -> "HipContext":
+        return cls(device)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load_library().dmhip_context_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- device, buffers ------------------------------------------------------
+    def device_name(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        _check(load_library().dmhip_device_name(self._h, buf, 256))
+        return buf.value.decode()
+
+    def synchronize(self) -> None:
+        _check(load_library().dmhip_synchronize(self._h))
+
+    def map_read_only(self, mapping) -> MappedBuffer:
+        arr = np.ascontiguousarray(np.frombuffer(mapping, dtype=np.uint8) if isinstance(mapping, (bytes, bytearray)) else mapping).view(np.uint8)
+        h = _vp()
+        _check(load_library().dmhip_map_read_only(self._h, arr.ctypes.data if arr.size else None,
+                                                   arr.size, ctypes.byref(h)))
+        return MappedBuffer(self, h.value)
+
+    def new_owned_buffer(self, length: int) -> OwnedBuffer:
+        h = _vp()
+        _check(load_library().dmhip_new_owned_buffer(self._h, length, ctypes.byref(h)))
+        return OwnedBuffer(self, h.value)
+
+    def device_array(self, data) -> OwnedBuffer:
+        """An owned buffer holding a copy of `data` (helper for device APIs)."""
+        arr = np.ascontiguousarray(data)
+        buf = self.new_owned_buffer(max(arr.nbytes, 1))
+        if arr.nbytes:
+            buf.write(0, arr)
+        return buf
+
+    def copy_to_host(self, device_ptr: int, nbytes: int, dtype=np.uint8) -> np.ndarray:
+        out = np.empty(nbytes, dtype=np.uint8)
+        _check(load_library().dmhip_copy_to_host(self._h, out.ctypes.data, device_ptr, nbytes))
+        return out.view(dtype)
+
+    def copy_to_device(self, device_ptr: int, data) -> None:
+        arr = np.ascontiguousarray(data)
+        _check(load_library().dmhip_copy_to_device(self._h, device_ptr, arr.ctypes.data, arr.nbytes))
+
+    # -- host-slice operators --------------------------------------------------
+    def rms_norm(self, input, weight, epsilon: float, output: np.ndarray) -> None:
+        x = _f32(input)
+        w = None if weight is None else _f32(weight)
+        _check(load_library().dmhip_rms_norm(self._h, _fp(x), x.size, None if w is None else _fp(w),
+                                             0 if w is None else w.size, epsilon, _fp(output), output.size))
+
+    def silu_mul(self, gate, up, output: np.ndarray) -> None:
+        g, u = _f32(gate), _f32(up)
+        _check(load_library().dmhip_silu_mul(self._h, _fp(g), g.size, _fp(u), u.size, _fp(output), output.size))
+
+    def argmax(self, input) -> int:
+        x = _f32(input)
+        idx = ctypes.c_size_t()
+        _check(load_library().dmhip_argmax(self._h, _fp(x), x.size, ctypes.byref(idx)))
+        return idx.value
+
+    def top_k_softmax(self, logits, k: int) -> list[tuple[int, float]]:
+        x = _f32(logits)
+        ids = np.zeros(max(k, 1), dtype=np.uintp)
+        probs = np.zeros(max(k, 1), dtype=np.float32)
+        _check(load_library().dmhip_top_k_softmax(self._h, _fp(x), x.size, k, ids.ctypes.data_as(_szp),
+                                                  _fp(probs)))
+        return [(int(ids[i]), float(probs[i])) for i in range(k)]
+
+    def matvec(self, kind: int, rows: int, columns: int, encoded, input, output: np.ndarray) -> None:
+        enc = np.ascontiguousarray(encoded, dtype=np.uint8)
+        x = _f32(input)
+        _check(load_library().dmhip_matvec(self._h, kind, rows, columns,
+                                           enc.ctypes.data_as(_u8p) if enc.size else None, enc.size,
+                                           _fp(x), x.size, _fp(output), output.size))
+
+    def matvec_mapped(self, kind, rows, columns, mapping: MappedBuffer, offset, length, input,
+                      output: np.ndarray) -> None:
+        x = _f32(input)
+        _check(load_library().dmhip_matvec_mapped(self._h, kind, rows, columns, mapping.handle, offset,
+                                                  length, _fp(x), x.size, _fp(output), output.size))
+
+    def matvec_owned(self, kind, rows, columns, encoded: OwnedBuffer, offset, length, input,
+                     output: np.ndarray) -> None:
+        x = _f32(input)
+        _check(load_library().dmhip_matvec_owned(self._h, kind, rows, columns, encoded.handle, offset,
+                                                 length, _fp(x), x.size, _fp(output), output.size))
+
+    def dequantize(self, kind: int, encoded: _Buffer, offset: int, length: int, elements: int) -> np.ndarray:
+        out = np.zeros(max(elements, 1), dtype=np.float32)
+        _check(load_library().dmhip_dequantize(self._h, kind, encoded.handle, offset, length,
+                                               _fp(out), elements))
+        return out[:elements]
+
+    # -- device operators (device addresses as ints) ------------------------
+    def matvec_device(self, kind, rows, columns, w_ptr, batch, x_ptr, y_ptr) -> None:
+        _check(load_library().dmhip_matvec_device(self._h, kind, rows, columns, w_ptr, batch, x_ptr, y_ptr))
+
+    def matvec_argmax_device(self, kind, rows, columns, w_ptr, x_ptr, y_ptr, index_ptr) -> None:
+        _check(load_library().dmhip_matvec_argmax_device(self._h, kind, rows, columns, w_ptr, x_ptr,
+                                                         y_ptr, index_ptr))
+
+    def argmax_result(self) -> int:
+        idx = ctypes.c_size_t()
+        _check(load_library().dmhip_argmax_result(self._h, ctypes.byref(idx)))
+        return idx.value
+
+    def rms_norm_device(self, batch, count, x_ptr, w_ptr, eps, y_ptr) -> None:
+        _check(load_library().dmhip_rms_norm_device(self._h, batch, count, x_ptr, w_ptr, eps, y_ptr))
+
+    def silu_mul_device(self, count, g_ptr, u_ptr, out_ptr) -> None:
+        _check(load_library().dmhip_silu_mul_device(self._h, count, g_ptr, u_ptr, out_ptr))
+
+    def ffn_workspace_bytes(self, batch, ffn) -> int:
+        return int(load_library().dmhip_ffn_workspace_bytes(batch, ffn))
+
+    def ffn_device(self, batch, hidden, ffn, gate_type, gate_ptr, up_type, up_ptr, down_type,
+                   down_ptr, eps, h_ptr, y_ptr, ws_ptr) -> None:
+        _check(load_library().dmhip_ffn_device(self._h, batch, hidden, ffn, gate_type, gate_ptr, up_type,
+                                               up_ptr, down_type, down_ptr, eps, h_ptr, y_ptr, ws_ptr))
+
+    def router_top_k_device(self, batch, hidden, experts, k, router_ptr, x_ptr, logits_ptr, ids_ptr,
+                            probs_ptr) -> None:
+        _check(load_library().dmhip_router_top_k_device(self._h, batch, hidden, experts, k, router_ptr,
+                                                        x_ptr, logits_ptr, ids_ptr, probs_ptr))
+
+    def gemm_workspace_bytes(self, m, k) -> int:
+        return int(load_library().dmhip_gemm_workspace_bytes(m, k))
+
+    def gemm_device(self, kind, m, n, k, a_ptr, w_ptr, c_ptr, ws_ptr) -> None:
+        _check(load_library().dmhip_gemm_device(self._h, kind, m, n, k, a_ptr, w_ptr, c_ptr, ws_ptr))
+
+    def event_record(self) -> int:
+        ev = _vp()
+        _check(load_library().dmhip_event_record(self._h, ctypes.byref(ev)))
+        return ev.value
+
+    @staticmethod
+    def event_elapsed_ms(start: int, stop: int) -> float:
+        ms = ctypes.c_float()
+        _check(load_library().dmhip_event_elapsed_ms(_vp(start), _vp(stop), ctypes.byref(ms)))
+        return ms.value
+
+    @staticmethod
+    def event_free(ev: int) -> None:
+        load_library().dmhip_event_free(_vp(ev))
+
+    # -- routed experts -------------------------------------------------------
+    def moe_layer(self, cache: "ExpertCache", layer, batch, hidden, width, experts, k, router_ptr,
+                  gate_up_type, down_type, x_ptr, y_ptr):
+        ids = np.zeros(batch * k, dtype=np.uint32)
+        probs = np.zeros(batch * k, dtype=np.float32)
+        _check(load_library().dmhip_moe_layer(self._h, cache.handle, layer, batch, hidden, width, experts,
+                                              k, router_ptr, gate_up_type, down_type, x_ptr, y_ptr,
+                                              ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                              _fp(probs)))
+        return ids.reshape(batch, k).astype(np.int64), probs.reshape(batch, k)
+
+
+class PinnedHostBuffer:
+    """Page-locked host memory (hipHostMalloc) exposed as a numpy array."""
+
+    def __init__(self, nbytes: int):
+        p = _vp()
+        _check(load_library().dmhip_host_alloc_pinned(nbytes, ctypes.byref(p)))
+        self._p = p
+        self.nbytes = nbytes
+        self.array = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(p.value))
+
+    @property
+    def address(self) -> int:
+        return self._p.value
+
+    def free(self):
+        if self._p:
+            self.array = None
+            load_library().dmhip_host_free_pinned(self._p)
+            self._p = _vp(None)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass(frozen=True)
+class ExpertLayerLayout:
+    """src/expert.rs:44-51."""
+    expert_count: int
+    gate_up_offset: int
+    gate_up_bytes: int
+    down_offset: int
+    down_bytes: int
+
+
+class ExpertCache:
+    """ExpertCache (src/expert.rs:64-229): per-layer LRU of HBM slots filled
+    from host memory by asynchronous uploads."""
+
+    def __init__(self, ctx: HipContext, source, layouts: Sequence[ExpertLayerLayout], slots_per_layer: int):
+        self._ctx = ctx
+        if isinstance(source, PinnedHostBuffer):
+            self._source = source
+            addr, n = source.address, source.nbytes
+        else:
+            arr = np.ascontiguousarray(source, dtype=np.uint8)
+            self._source = arr
+            addr, n = arr.ctypes.data, arr.size
+        lay = (_Layout * max(len(layouts), 1))()
+        for i, l in enumerate(layouts):
+            lay[i] = _Layout(l.expert_count, l.gate_up_offset, l.gate_up_bytes, l.down_offset, l.down_bytes)
+        h = _vp()
+        _check(load_library().dmhip_expert_cache_new(ctx.handle, addr, n, lay, len(layouts), slots_per_layer,
+                                                     ctypes.byref(h)))
+        self._h = h
+
+    @property
+    def handle(self):
+        return self._h
+
+    def slots_per_layer(self) -> int:
+        return int(load_library().dmhip_expert_cache_slots_per_layer(self._h))
+
+    def stats(self) -> dict:
+        s = _Stats()
+        _check(load_library().dmhip_expert_cache_stats_get(self._h, ctypes.byref(s)))
+        return {n: getattr(s, n) for n, _ in _Stats._fields_}
+
+    def with_expert(self, layer: int, expert: int, cancelled: Callable[[], bool], use_expert):
+        """src/expert.rs:138-164: cancellation checked before and after the
+        acquire; the slot stays pinned while `use_expert(gate_up_ptr,
+        down_ptr, slot)` enqueues its work."""
+        flag = ctypes.c_int(1 if cancelled() else 0)
+        slot = ctypes.c_size_t()
+        gu = _vp()
+        dn = _vp()
+        _check(load_library().dmhip_expert_acquire(self._h, layer, expert, ctypes.byref(flag),
+                                                   ctypes.byref(slot), ctypes.byref(gu), ctypes.byref(dn)))
+        try:
+            if cancelled():
+                raise HipError(22, "expert loading was cancelled")
+            return use_expert(gu.value, dn.value, slot.value)
+        finally:
+            _check(load_library().dmhip_expert_release(self._h, layer, slot.value))
+
+    def free(self):
+        if getattr(self, "_h", None):
+            load_library().dmhip_expert_cache_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class BackendSelection:
+    """BackendSelection::from_environment (src/runtime.rs:152-186) with the
+    `hip` arm this backend adds: DISKMULE_BACKEND=auto|hip|cpu."""
+
+    CPU = "cpu"
+    HIP = "hip"
+
+    @staticmethod
+    def from_environment(env=None) -> str:
+        env = os.environ if env is None else env
+        requested = env.get("DISKMULE_BACKEND", "auto")
+        if requested == "cpu":
+            return BackendSelection.CPU
+        if requested in ("auto", "hip"):
+            if os.path.exists(_LIB) and (requested == "hip" or _device_present()):
+                return BackendSelection.HIP
+            if requested == "hip":
+                raise HipError(24, "DISKMULE_BACKEND=hip requires libdmhip.so and a HIP device")
+            return BackendSelection.CPU
+        raise HipError(24, "DISKMULE_BACKEND must be auto, hip, or cpu")
+
+
+def _device_present() -> bool:
+    return os.path.exists("/dev/kfd")

@@ -1,0 +1,298 @@
+/*
+ * dmhip.h -- C ABI of the MI355X (gfx950) backend for DiskMule's
+ * quantized-matrix path.
+ *
+ * This header is the drop-in boundary.  It replaces the public surface of the
+ * reference's Metal backend (src/metal.rs, re-exported at :2571-2572) and of
+ * its expert residency (src/expert.rs) for the operators on the quantized
+ * path.  A Rust `hip` module binds these symbols 1:1 (the binding is shown in
+ * INTEGRATION.md) so the graph code keeps calling `matvec_mapped`,
+ * `matvec_owned`, `argmax`, `top_k_softmax`, `rms_norm`, `silu_mul` and
+ * `ExpertCache::with_expert` by name.
+ *
+ * Conventions (kept from src/metal.rs):
+ *  - Every entry point validates its arguments before any device work and
+ *    returns a dmhip_status; nothing aborts, no C++ exception crosses the ABI.
+ *    The message of the last failure on the calling thread is returned by
+ *    dmhip_last_error().
+ *  - The "host" entry points take host slices and are synchronous: they
+ *    return after the device work finished, as the Metal backend does
+ *    (src/metal.rs:1595-1596).
+ *  - The "_device" entry points take device addresses and only enqueue work
+ *    on the context's stream (stream-ordered, asynchronous); they exist so a
+ *    graph can keep activations resident in HBM.  dmhip_synchronize() waits.
+ *  - A context is used from one thread at a time, as MetalContext is owned by
+ *    its model-worker thread (src/runtime.rs:741-760).
+ *  - Tensor types are ggml ids (src/gguf.rs:295-318).  Rows are contiguous;
+ *    row r of a matrix starts at r * row_byte_len(columns).
+ */
+#ifndef DMHIP_H
+#define DMHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  Each mirrors a MetalError / ExpertCacheError variant
+   (src/metal.rs:3-126, src/expert.rs:13-42). */
+typedef enum dmhip_status {
+    DMHIP_OK = 0,
+    DMHIP_ERR_NO_DEVICE = 1,             /* MetalError::NoDevice */
+    DMHIP_ERR_BUFFER_ALLOCATION = 2,     /* MetalError::BufferAllocation */
+    DMHIP_ERR_VECTOR_LENGTH = 3,         /* MetalError::VectorLength */
+    DMHIP_ERR_VECTOR_TOO_LARGE = 4,      /* MetalError::VectorTooLarge */
+    DMHIP_ERR_EMPTY_INPUT = 5,           /* MetalError::EmptyInput */
+    DMHIP_ERR_INVALID_VECTOR_LENGTH = 6, /* MetalError::InvalidVectorLength */
+    DMHIP_ERR_INVALID_POSITIVE_PARAMETER = 7, /* MetalError::InvalidPositiveParameter */
+    DMHIP_ERR_NON_FINITE = 8,            /* MetalError::NonFinite */
+    DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE = 9, /* MetalError::UnsupportedTensorType */
+    DMHIP_ERR_INVALID_ELEMENT_COUNT = 10, /* MetalError::InvalidElementCount */
+    DMHIP_ERR_INVALID_BYTE_LENGTH = 11,  /* MetalError::InvalidByteLength */
+    DMHIP_ERR_OVERFLOW = 12,             /* MetalError::Overflow */
+    DMHIP_ERR_INVALID_INPUT_LENGTH = 13, /* MetalError::InvalidInputLength */
+    DMHIP_ERR_INVALID_OUTPUT_LENGTH = 14, /* MetalError::InvalidOutputLength */
+    DMHIP_ERR_INVALID_TOP_K = 15,        /* MetalError::InvalidTopK */
+    DMHIP_ERR_MAPPED_RANGE = 16,         /* MetalError::MappedRange */
+    DMHIP_ERR_COMMAND = 17,              /* MetalError::Command (a HIP runtime error) */
+    DMHIP_ERR_NO_SLOTS = 18,             /* ExpertCacheError::NoSlots */
+    DMHIP_ERR_INVALID_LAYER = 19,        /* ExpertCacheError::InvalidLayer */
+    DMHIP_ERR_INVALID_EXPERT = 20,       /* ExpertCacheError::InvalidExpert */
+    DMHIP_ERR_ALL_SLOTS_PINNED = 21,     /* ExpertCacheError::AllSlotsPinned */
+    DMHIP_ERR_CANCELLED = 22,            /* ExpertCacheError::Cancelled */
+    DMHIP_ERR_INVALID_LAYOUT = 23,       /* ExpertCacheError::InvalidLayout */
+    DMHIP_ERR_INVALID_ARGUMENT = 24      /* a null handle or pointer */
+} dmhip_status;
+
+/* ggml tensor type ids accepted by the matvec entry points. */
+enum {
+    DMHIP_TYPE_F32 = 0,
+    DMHIP_TYPE_F16 = 1,
+    DMHIP_TYPE_Q8_0 = 8,
+    DMHIP_TYPE_Q4_K = 12,
+    DMHIP_TYPE_Q6_K = 14,
+    DMHIP_TYPE_BF16 = 30
+};
+
+typedef struct dmhip_ctx dmhip_ctx;
+typedef struct dmhip_buf dmhip_buf;
+typedef struct dmhip_expert_cache dmhip_expert_cache;
+
+/* ---------------------------------------------------------------------- */
+/* Context, errors, device                                                 */
+/* ---------------------------------------------------------------------- */
+
+/* Last failure message on the calling thread ("" if none). */
+const char *dmhip_last_error(void);
+
+/* MetalContext::new (src/metal.rs:291-346): selects HIP device `device`,
+   creates its compute stream and its upload stream (default priority). */
+int dmhip_context_new(int device, dmhip_ctx **out);
+void dmhip_context_free(dmhip_ctx *ctx);
+
+/* MetalContext::device_name (src/metal.rs:348-350). */
+int dmhip_device_name(dmhip_ctx *ctx, char *buffer, size_t capacity);
+
+/* Waits for all work enqueued on the context's streams. */
+int dmhip_synchronize(dmhip_ctx *ctx);
+
+/* The context's compute stream, as a hipStream_t. */
+void *dmhip_stream(dmhip_ctx *ctx);
+
+/* ---------------------------------------------------------------------- */
+/* Buffers                                                                 */
+/* ---------------------------------------------------------------------- */
+
+/* MetalContext::map_read_only (src/metal.rs:352-392).  Unified memory let the
+   reference wrap the GGUF mmap in place; a discrete GPU cannot, so the whole
+   mapping is uploaded to HBM once and keeps its byte offsets.  A zero length
+   is BufferAllocation, as in the reference. */
+int dmhip_map_read_only(dmhip_ctx *ctx, const void *host, size_t length, dmhip_buf **out);
+
+/* MetalContext::new_owned_buffer (src/metal.rs:394-402): zero-filled device
+   buffer; a zero length is BufferAllocation. */
+int dmhip_new_owned_buffer(dmhip_ctx *ctx, size_t length, dmhip_buf **out);
+void dmhip_buffer_free(dmhip_buf *buffer);
+size_t dmhip_buffer_len(const dmhip_buf *buffer);
+/* Device address of the buffer's first byte. */
+void *dmhip_buffer_device_ptr(const dmhip_buf *buffer);
+/* MetalOwnedBuffer::as_mut_bytes / as_bytes (src/metal.rs:228-243) as copies. */
+int dmhip_buffer_write(dmhip_ctx *ctx, dmhip_buf *buffer, size_t offset, const void *src, size_t n);
+int dmhip_buffer_read(dmhip_ctx *ctx, const dmhip_buf *buffer, size_t offset, void *dst, size_t n);
+
+/* Synchronous copies between host memory and a device address (for callers
+   that hold device addresses from the _device entry points or an expert
+   slot, as MetalOwnedBuffer::as_bytes exposes slot bytes, src/metal.rs:228). */
+int dmhip_copy_to_host(dmhip_ctx *ctx, void *dst, const void *device_src, size_t n);
+int dmhip_copy_to_device(dmhip_ctx *ctx, void *device_dst, const void *src, size_t n);
+
+/* Pinned host memory for upload sources (hipHostMalloc). */
+int dmhip_host_alloc_pinned(size_t bytes, void **out);
+void dmhip_host_free_pinned(void *ptr);
+
+/* ---------------------------------------------------------------------- */
+/* Synchronous host-slice operators (the MetalContext surface)            */
+/* ---------------------------------------------------------------------- */
+
+/* MetalContext::rms_norm (src/metal.rs:435-476); weight may be NULL. */
+int dmhip_rms_norm(dmhip_ctx *ctx, const float *input, size_t input_len, const float *weight,
+                   size_t weight_len, float epsilon, float *output, size_t output_len);
+
+/* MetalContext::silu_mul (src/metal.rs:554-576). */
+int dmhip_silu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const float *up,
+                   size_t up_len, float *output, size_t output_len);
+
+/* MetalContext::argmax (src/metal.rs:624-644): first maximum, lowest index on
+   ties, non-finite input rejected. */
+int dmhip_argmax(dmhip_ctx *ctx, const float *input, size_t input_len, size_t *index);
+
+/* MetalContext::top_k_softmax (src/metal.rs:1392-1434): k ids in selection
+   order (value descending, index ascending on ties) and their softmax. */
+int dmhip_top_k_softmax(dmhip_ctx *ctx, const float *logits, size_t logits_len, size_t k,
+                        size_t *indices, float *probabilities);
+
+/* MetalContext::matvec (src/metal.rs:648-683): encoded matrix from host memory. */
+int dmhip_matvec(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
+                 const uint8_t *encoded, size_t encoded_len, const float *input,
+                 size_t input_len, float *output, size_t output_len);
+
+/* MetalContext::matvec_mapped (src/metal.rs:687-734). */
+int dmhip_matvec_mapped(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
+                        const dmhip_buf *mapping, size_t encoded_offset, size_t encoded_length,
+                        const float *input, size_t input_len, float *output, size_t output_len);
+
+/* MetalContext::matvec_owned (src/metal.rs:1148-1194). */
+int dmhip_matvec_owned(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
+                       const dmhip_buf *encoded, size_t encoded_offset, size_t encoded_length,
+                       const float *input, size_t input_len, float *output, size_t output_len);
+
+/* Dequantize `elements` values of a device-resident encoding into host f32
+   (the GPU counterpart of cpu::dequantize, src/cpu.rs:312-343; bit-exact). */
+int dmhip_dequantize(dmhip_ctx *ctx, uint32_t ggml_type, const dmhip_buf *encoded,
+                     size_t encoded_offset, size_t encoded_length, float *output,
+                     size_t elements);
+
+/* ---------------------------------------------------------------------- */
+/* Stream-ordered device operators (device addresses, asynchronous)        */
+/* ---------------------------------------------------------------------- */
+
+/* y[b][r] = sum_c W[r][c] * x[b][c] for b < batch (1..16); x is
+   [batch][columns] f32, y is [batch][rows] f32, W is `rows` encoded rows. */
+int dmhip_matvec_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
+                        const void *weights, size_t batch, const float *x, float *y);
+
+/* Batch-1 matvec plus greedy argmax over the rows (src/cpu.rs:275-293).
+   *index_device receives the row index as uint32; a non-finite row makes the
+   next dmhip_argmax_result() report NonFinite. */
+int dmhip_matvec_argmax_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows,
+                               size_t columns, const void *weights, const float *x,
+                               float *y, uint32_t *index_device);
+/* Waits for the last dmhip_matvec_argmax_device and returns its index. */
+int dmhip_argmax_result(dmhip_ctx *ctx, size_t *index);
+
+/* RMSNorm of `batch` rows of `count` values (src/cpu.rs:98-142). */
+int dmhip_rms_norm_device(dmhip_ctx *ctx, size_t batch, size_t count, const float *input,
+                          const float *weight, float epsilon, float *output);
+
+/* out = silu(gate) * up, count values (src/qwen35/cpu.rs:422-424). */
+int dmhip_silu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const float *up,
+                          float *output);
+
+/* Dense gated FFN at decode for `batch` tokens (src/qwen35/cpu.rs:415-427):
+   y = down(silu(gate(n)) * up(n)) with n = rms_norm(h, eps), unit weight.
+   `workspace` holds at least dmhip_ffn_workspace_bytes(batch, ffn) bytes. */
+size_t dmhip_ffn_workspace_bytes(size_t batch, size_t ffn);
+int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn,
+                     uint32_t gate_type, const void *gate, uint32_t up_type, const void *up,
+                     uint32_t down_type, const void *down, float epsilon, const float *h,
+                     float *y, void *workspace);
+
+/* Router for `batch` tokens: logits = bf16 router rows . x (exact sequential
+   fold, src/cpu.rs:391-394), then top_k_softmax per token
+   (src/cpu.rs:232-260).  ids [batch][k] uint32, probabilities [batch][k]. */
+int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t experts,
+                              size_t k, const uint16_t *router_bf16, const float *x,
+                              float *logits, uint32_t *ids, float *probabilities);
+
+/* Prefill GEMM: C[m][n] = sum_k A[m][k] * W[n][k], A bf16 [m][k] row-major,
+   W `n` encoded rows of `k` columns, C f32 [m][n]. */
+size_t dmhip_gemm_workspace_bytes(size_t m, size_t k);
+int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t m, size_t n, size_t k,
+                      const uint16_t *a_bf16, const void *weights, float *c, void *workspace);
+
+/* Events on the compute stream, for timing. */
+int dmhip_event_record(dmhip_ctx *ctx, void **event);
+int dmhip_event_elapsed_ms(void *start, void *stop, float *ms);
+void dmhip_event_free(void *event);
+
+/* ---------------------------------------------------------------------- */
+/* Routed-expert residency (src/expert.rs)                                 */
+/* ---------------------------------------------------------------------- */
+
+/* ExpertLayerLayout (src/expert.rs:44-51): byte ranges inside the source. */
+typedef struct dmhip_expert_layer_layout {
+    size_t expert_count;
+    uint64_t gate_up_offset;
+    size_t gate_up_bytes;
+    uint64_t down_offset;
+    size_t down_bytes;
+} dmhip_expert_layer_layout;
+
+/* ExpertCacheStats (src/expert.rs:53-62). io_wait is nanoseconds the host
+   waited for uploads to finish. */
+typedef struct dmhip_expert_cache_stats {
+    uint64_t hits;
+    uint64_t misses;
+    uint64_t evictions;
+    uint64_t reads;
+    uint64_t bytes_read;
+    uint64_t io_wait_ns;
+    uint64_t resident_bytes;
+} dmhip_expert_cache_stats;
+
+/* ExpertCache::new (src/expert.rs:88-128).  The source is host memory holding
+   the expert tensors at the layout offsets (the reference reads them from the
+   GGUF file with pread; here the caller provides the bytes, ideally in pinned
+   memory from dmhip_host_alloc_pinned so uploads are asynchronous DMA).  Each
+   layer gets `slots_per_layer` HBM slots of gate_up_bytes + down_bytes. */
+int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len,
+                           const dmhip_expert_layer_layout *layouts, size_t layer_count,
+                           size_t slots_per_layer, dmhip_expert_cache **out);
+void dmhip_expert_cache_free(dmhip_expert_cache *cache);
+int dmhip_expert_cache_stats_get(const dmhip_expert_cache *cache,
+                                 dmhip_expert_cache_stats *stats);
+size_t dmhip_expert_cache_slots_per_layer(const dmhip_expert_cache *cache);
+
+/* ExpertCache::with_expert, split into acquire/release for a C caller
+   (src/expert.rs:138-164).  acquire: checks `cancelled` (may be NULL) before
+   and after, finds or loads the expert into a slot (LRU of
+   src/expert.rs:166-229; a miss enqueues the upload on the upload stream and
+   makes the compute stream wait for it), pins the slot and returns the device
+   addresses of its gate_up and down bytes.  Work that reads the slot must be
+   enqueued on the compute stream before release.  release: unpins the slot;
+   a later upload into it waits for that work. */
+int dmhip_expert_acquire(dmhip_expert_cache *cache, size_t layer, size_t expert,
+                         const volatile int *cancelled, size_t *slot, const void **gate_up,
+                         const void **down);
+int dmhip_expert_release(dmhip_expert_cache *cache, size_t layer, size_t slot);
+
+/* One routed-expert layer at decode for `batch` tokens (1..16), the
+   structure of src/gemma4/cpu.rs:574-612 with the GLM SiLU expert
+   (src/glm52/expert.rs:260-267): router -> top-k softmax -> for each
+   selected expert (acquired through the cache in token order, then
+   selection order) gate_up, silu*up, down -> y = fma(out, p, y) in selection
+   order.  Expert gate_up rows are [gate; up] (2*width rows of `hidden`
+   columns), down rows are `hidden` rows of `width` columns.  x and y are
+   device [batch][hidden]; ids/probabilities receive host [batch][k].
+   The call returns after the layer finished. */
+int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *cache, size_t layer, size_t batch,
+                    size_t hidden, size_t width, size_t experts, size_t k,
+                    const uint16_t *router_bf16, uint32_t gate_up_type, uint32_t down_type,
+                    const float *x, float *y, uint32_t *ids, float *probabilities);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

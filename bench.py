@@ -1,0 +1,335 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-matrix path (one JSON line on stdout).
+
+A step is one pass of the hot path over one batch of synthetic input.  The
+headline workload is BASELINE configs[1] (C2): the Q6_K output head,
+151936 x 4096, batch 1, GEMV plus the greedy argmax, with weights and
+activation resident in HBM before the timed region.  ``value`` is the
+algorithmic bytes of a step divided by the wall time per step on the
+compute stream (HIP events, all launches of the step included).
+
+``roofline`` describes the dominant kernel (the Q6_K MFMA matvec): its
+average duration comes from HIP events the library records around each of
+its launches inside the timed region; ``traffic`` is the HBM bytes per
+launch from rocprofv3 FETCH_SIZE/WRITE_SIZE runs (profiles/), when present.
+
+``cpu_baseline`` times the CPU port of src/cpu.rs (oracle/dm_oracle.c,
+16 threads) on the same C2 workload, on this machine's host cores.
+
+``details`` holds the other BASELINE configurations (C1, C3, C4, C5), each
+measured the same way.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4_K/Q6_K GEMV achieved HBM GB/s (% peak); prefill GEMM TFLOP/s; decode tok/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+Q4_K, Q6_K = 12, 14
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Timed:
+    """Wall time on the compute stream (events) plus the library's
+    per-launch timing of the dominant kernels."""
+
+    def __init__(self, ctx):
+        self.ctx = ctx
+
+    def __enter__(self):
+        self.ctx.synchronize()
+        self.ctx.kernel_timing_read()  # drop anything recorded before
+        self.ctx.kernel_timing_enable(True)
+        self.start = self.ctx.event_record()
+        return self
+
+    def __exit__(self, *exc):
+        stop = self.ctx.event_record()
+        self.ctx.synchronize()
+        self.wall_ms = self.ctx.event_elapsed_ms(self.start, stop)
+        self.kernel_ms, self.launches = self.ctx.kernel_timing_read()
+        self.ctx.kernel_timing_enable(False)
+        self.ctx.event_free(self.start)
+        self.ctx.event_free(stop)
+
+
+def upload(ctx, arr):
+    return ctx.device_array(np.ascontiguousarray(arr))
+
+
+# ---------------------------------------------------------------------------
+def bench_c2(ctx, synth, steps, warmup):
+    rows, cols = 151936, 4096
+    log("C2: generating weights")
+    w = synth.quantized_matrix(Q6_K, rows, cols, synth.weight_seed(2))
+    x = synth.normal(synth.activation_seed(2), cols)
+    wb, xb = upload(ctx, w), upload(ctx, x)
+    yb, ib = ctx.new_owned_buffer(rows * 4), ctx.new_owned_buffer(4)
+    step_bytes = w.size + cols * 4 + rows * 4  # 511,129,088 B
+    for _ in range(warmup):
+        ctx.matvec_argmax_device(Q6_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr, ib.device_ptr)
+    idx = ctx.argmax_result()
+    with Timed(ctx) as t:
+        for _ in range(steps):
+            ctx.matvec_argmax_device(Q6_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr,
+                                     ib.device_ptr)
+    ms = t.wall_ms / steps
+    kms = t.kernel_ms / max(t.launches, 1)
+    log(f"C2: {ms * 1e3:.1f} us/step, kernel {kms * 1e3:.1f} us, argmax={idx}")
+    return {
+        "rows": rows, "columns": cols, "weight_bytes": int(w.size), "step_bytes": int(step_bytes),
+        "ms_per_step": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9,
+        "kernel_ms": kms, "kernel_gbps": step_bytes / (kms * 1e-3) / 1e9, "argmax": int(idx),
+    }, (w, x)
+
+
+def bench_c1(ctx, synth, steps, warmup):
+    rows = cols = 4096
+    w = synth.quantized_matrix(Q4_K, rows, cols, synth.weight_seed(1))
+    x = synth.normal(synth.activation_seed(1), cols)
+    copies = 40  # 40 x 9.4 MB = 377 MB > 256 MB MALL: each launch reads from HBM
+    wbs = [upload(ctx, w)]
+    for _ in range(copies - 1):
+        b = ctx.new_owned_buffer(w.size)
+        ctx.copy_device(b.device_ptr, wbs[0].device_ptr, w.size)
+        wbs.append(b)
+    xb, yb = upload(ctx, x), ctx.new_owned_buffer(rows * 4)
+    step_bytes = w.size + cols * 4 + rows * 4  # 9,469,952 B
+    out = {"rows": rows, "columns": cols, "step_bytes": step_bytes}
+    for mode, bufs in (("cold", wbs), ("warm", wbs[:1])):
+        n = max(steps, 2 * copies)
+        for i in range(warmup + 1):
+            ctx.matvec_device(Q4_K, rows, cols, bufs[i % len(bufs)].device_ptr, 1, xb.device_ptr, yb.device_ptr)
+        with Timed(ctx) as t:
+            for i in range(n):
+                ctx.matvec_device(Q4_K, rows, cols, bufs[i % len(bufs)].device_ptr, 1, xb.device_ptr,
+                                  yb.device_ptr)
+        ms, kms = t.wall_ms / n, t.kernel_ms / max(t.launches, 1)
+        out[mode] = {"ms_per_step": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9, "kernel_ms": kms,
+                     "kernel_gbps": step_bytes / (kms * 1e-3) / 1e9,
+                     "kernel_frac_of_peak": step_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    log(f"C1: cold kernel {out['cold']['kernel_ms'] * 1e3:.2f} us ({out['cold']['kernel_gbps']:.0f} GB/s)")
+    return out
+
+
+def bench_c3(ctx, synth, steps, warmup):
+    hidden, ffn = 4096, 12288
+    g = synth.quantized_matrix(Q4_K, ffn, hidden, synth.weight_seed(3, 0))
+    u = synth.quantized_matrix(Q4_K, ffn, hidden, synth.weight_seed(3, 1))
+    d = synth.quantized_matrix(Q6_K, hidden, ffn, synth.weight_seed(3, 2))
+    gb, ub, db = upload(ctx, g), upload(ctx, u), upload(ctx, d)
+    weight_bytes = g.size + u.size + d.size  # 97,910,784 B
+    out = {}
+    for batch in (1, 4, 8):
+        h = synth.normal(synth.activation_seed(3, batch), batch * hidden)
+        hb, yb = upload(ctx, h), ctx.new_owned_buffer(batch * hidden * 4)
+        ws = ctx.new_owned_buffer(ctx.ffn_workspace_bytes(batch, ffn))
+        call = lambda: ctx.ffn_device(batch, hidden, ffn, Q4_K, gb.device_ptr, Q4_K, ub.device_ptr, Q6_K,
+                                      db.device_ptr, 1e-6, hb.device_ptr, yb.device_ptr, ws.device_ptr)
+        for _ in range(warmup):
+            call()
+        with Timed(ctx) as t:
+            for _ in range(steps):
+                call()
+        ms = t.wall_ms / steps
+        step_bytes = weight_bytes + 2 * batch * hidden * 4
+        out[f"B{batch}"] = {"layer_ms": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9,
+                            "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                            "tok_per_s": batch / (ms * 1e-3),
+                            "matvec_kernel_ms": t.kernel_ms / steps}
+        log(f"C3 B={batch}: {ms * 1e3:.1f} us/layer")
+    return out
+
+
+def bench_c4(ctx, synth, steps, warmup):
+    from diskmule_amd import ExpertCache, ExpertLayerLayout
+    from diskmule_amd.hip import PinnedHostBuffer
+    hidden, width, experts, k, slots = 2048, 768, 128, 8, 8
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(4, 9), experts * hidden) * np.float32(0.02))
+    gu_bytes = 2 * width * synth.row_bytes(Q4_K, hidden)
+    dn_bytes = hidden * synth.row_bytes(Q6_K, width)
+    src = PinnedHostBuffer(experts * (gu_bytes + dn_bytes))
+    src.array[:experts * gu_bytes] = synth.quantized_matrix(Q4_K, experts * 2 * width, hidden, synth.weight_seed(4, 0))
+    src.array[experts * gu_bytes:] = synth.quantized_matrix(Q6_K, experts * hidden, width, synth.weight_seed(4, 1))
+    layout = ExpertLayerLayout(experts, 0, gu_bytes, experts * gu_bytes, dn_bytes)
+    rb = upload(ctx, router)
+    out = {"expert_bytes": gu_bytes + dn_bytes, "slots_per_layer": slots}
+    for batch in (1, 4, 16):
+        cache = ExpertCache(ctx, src, [layout], slots)
+        xs = [upload(ctx, synth.normal(synth.activation_seed(4, 100 * batch + i), batch * hidden))
+              for i in range(steps + warmup)]
+        yb = ctx.new_owned_buffer(batch * hidden * 4)
+        for i in range(warmup):
+            ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                          xs[i].device_ptr, yb.device_ptr)
+        s0 = cache.stats()
+        t0 = time.perf_counter()
+        uniq = 0
+        with Timed(ctx) as t:
+            for i in range(warmup, warmup + steps):
+                ids, _ = ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K,
+                                       Q6_K, xs[i].device_ptr, yb.device_ptr)
+                uniq += len(set(ids.ravel().tolist()))
+        wall = time.perf_counter() - t0
+        s1 = cache.stats()
+        misses = s1["misses"] - s0["misses"]
+        hits = s1["hits"] - s0["hits"]
+        up_bytes = s1["bytes_read"] - s0["bytes_read"]
+        kernel_bytes = uniq * (gu_bytes + dn_bytes)
+        # Hot-cache kernel rate: the same tokens again, every expert resident.
+        for _ in range(2):
+            ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                          xs[0].device_ptr, yb.device_ptr)
+        with Timed(ctx) as hot:
+            ids, _ = ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                                   xs[0].device_ptr, yb.device_ptr)
+        hot_bytes = len(set(ids.ravel().tolist())) * (gu_bytes + dn_bytes)
+        out[f"B{batch}"] = {
+            "layer_ms": wall / steps * 1e3, "hits": hits, "misses": misses,
+            "evictions": s1["evictions"] - s0["evictions"],
+            "upload_bytes": up_bytes, "upload_gbps_wall": up_bytes / wall / 1e9,
+            "expert_kernel_gbps": kernel_bytes / (t.kernel_ms * 1e-3) / 1e9 if t.kernel_ms else None,
+            "hot_layer_ms": hot.wall_ms, "hot_expert_kernel_gbps":
+                hot_bytes / (hot.kernel_ms * 1e-3) / 1e9 if hot.kernel_ms else None,
+        }
+        log(f"C4 B={batch}: {wall / steps * 1e3:.2f} ms/layer, misses {misses}, hits {hits}")
+        cache.free()
+    # Upload link rate on its own: one expert from pinned memory per copy.
+    dst = ctx.new_owned_buffer(gu_bytes + dn_bytes)
+    n = 32
+    t0 = time.perf_counter()
+    for i in range(n):
+        ctx.copy_to_device(dst.device_ptr, src.array[i * gu_bytes:(i + 1) * gu_bytes])
+    out["pinned_h2d_gbps"] = n * gu_bytes / (time.perf_counter() - t0) / 1e9
+    src.free()
+    return out
+
+
+def bench_c5(ctx, synth, steps, warmup):
+    m, k = 512, 4096
+    a = synth.to_bf16_bits(synth.normal(synth.activation_seed(5), m * k))
+    ab = upload(ctx, a)
+    ws = ctx.new_owned_buffer(ctx.gemm_workspace_bytes(m, k))
+    out = {}
+    for n in (4096, 12288):
+        w = synth.quantized_matrix(Q4_K, n, k, synth.weight_seed(5, n))
+        wb, cb = upload(ctx, w), ctx.new_owned_buffer(m * n * 4)
+        call = lambda: ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr)
+        for _ in range(warmup):
+            call()
+        with Timed(ctx) as t:
+            for _ in range(steps):
+                call()
+        ms = t.wall_ms / steps
+        flops = 2.0 * m * n * k
+        out[f"N{n}"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+                        "frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                        "kernel_ms_per_step": t.kernel_ms / steps}
+        log(f"C5 N={n}: {ms * 1e3:.1f} us, {out[f'N{n}']['tflops']:.1f} TFLOP/s")
+    return out
+
+
+def cpu_baseline(w, x, seconds):
+    """The CPU port of src/cpu.rs:345-399 + :275-293 on the C2 workload."""
+    from oracle import capi
+    threads = min(16, os.cpu_count() or 1)
+    rows, cols = 151936, 4096
+    step_bytes = w.size + cols * 4 + rows * 4
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        y = capi.matvec(Q6_K, rows, cols, w, x, threads=threads)
+        idx = capi.argmax(y)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": step_bytes * reps / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"full C2 step (Q6_K 151936x4096 matvec + argmax) repeated {reps}x in {dt:.1f}s "
+                      f"on {threads} host threads; oracle/dm_oracle.c restating src/cpu.rs (the Rust "
+                      f"reference cannot be built here)",
+            "argmax": int(idx)}
+
+
+def load_traffic():
+    path = os.path.join(ROOT, "profiles", "c2_q6k_gemv_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--only", default=None, help="c1..c5: run one GPU configuration, print its record")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
+              "multi-GPU path; see DESIGN.md for how the path would shard)", file=sys.stderr)
+        return 2
+
+    from diskmule_amd import HipContext, synth
+    ctx = HipContext(0)
+    log("device:", ctx.device_name())
+    if args.only:
+        fn = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.only]
+        res = fn(ctx, synth, args.steps, args.warmup)
+        print(json.dumps(res[0] if isinstance(res, tuple) else res))
+        return 0
+
+    c2, (w2, x2) = bench_c2(ctx, synth, args.steps, args.warmup)
+    details = {"C2": c2}
+    for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5)):
+        details[name] = fn(ctx, synth, max(3, args.steps // 2), args.warmup)
+    log("CPU baseline")
+    cpu = cpu_baseline(w2, x2, args.cpu_seconds)
+    details["argmax_equal_cpu"] = cpu.pop("argmax") == c2["argmax"]
+
+    record = {
+        "metric": METRIC,
+        "value": round(c2["gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": c2["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "C2: Q6_K output head 151936x4096 GEMV + greedy argmax, batch 1 "
+                               "(BASELINE configs[1]); weights resident in HBM",
+                   "weight_type": "Q6_K", "rows": 151936, "columns": 4096, "batch": 1,
+                   "arithmetic": "exact fp16 MFMA operands (weights sc*(q-32), activations hi/lo), "
+                                 "fp32 accumulation"},
+        "roofline": {"bound": "hbm", "achieved": round(c2["kernel_gbps"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(c2["kernel_gbps"] / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic()},
+        "cpu_baseline": cpu,
+        "details": details,
+    }
+    print(json.dumps(record))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -15,9 +15,10 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
     row_byte_len(type, columns, &row_bytes);
     if (qmv_supported(type, rows, columns, w, batch)) {
         DM_HIP(launch_qmv(ctx, type, (uint32_t)rows, (uint32_t)columns, w, (uint32_t)batch, x, y,
-                          nullptr));
+                          nullptr, nullptr));
         return DMHIP_OK;
     }
+    KernelTimer timer(ctx);
     DM_HIP(launch_gemv_exact(ctx->stream, type, be, bb, (uint32_t)rows, (uint32_t)columns,
                              (size_t)row_bytes, (const uint8_t *)w, (uint32_t)batch, x, y));
     return DMHIP_OK;
@@ -25,17 +26,15 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
 
 int enqueue_matvec_argmax(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
                           const void *w, const float *x, float *y, uint32_t *index_device) {
-    DM_HIP(launch_argmax_init(ctx->stream, ctx->argmax_state));
     if (qmv_supported(type, rows, columns, w, 1)) {
-        // The argmax is folded into the matvec's epilogue.
+        // Two launches: the activation pass resets the argmax state and the
+        // matvec folds the argmax into its epilogue and publishes the index.
         DM_HIP(launch_qmv(ctx, type, (uint32_t)rows, (uint32_t)columns, w, 1, x, y,
-                          ctx->argmax_state));
-    } else {
-        DM_CHECK_STATUS(enqueue_matvec(ctx, type, rows, columns, w, 1, x, y));
-        DM_HIP(launch_argmax(ctx->stream, y, rows, ctx->argmax_state, index_device));
+                          ctx->argmax_state, index_device));
         return DMHIP_OK;
     }
-    DM_HIP(launch_argmax_finish(ctx->stream, ctx->argmax_state, index_device));
+    DM_CHECK_STATUS(enqueue_matvec(ctx, type, rows, columns, w, 1, x, y));
+    DM_HIP(launch_argmax(ctx->stream, y, rows, ctx->argmax_state, index_device));
     return DMHIP_OK;
 }
 

@@ -14,9 +14,10 @@ constexpr uint32_t kMaxTopK = 256;
 struct ArgmaxState {
     unsigned long long key;
     uint32_t non_finite;
-    uint32_t pad;
+    uint32_t done;  // waves that have folded their key in (fused argmax)
 };
 
+hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t n);
 hipError_t launch_dequantize(hipStream_t s, uint32_t type, const uint8_t *enc, uint32_t be,
                              uint32_t bb, size_t elements, float *out);
 hipError_t launch_gemv_exact(hipStream_t s, uint32_t type, uint32_t be, uint32_t bb, uint32_t rows,

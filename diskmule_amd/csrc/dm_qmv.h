@@ -10,11 +10,12 @@ namespace dm {
 // and fewer than 4 GiB of weights (one buffer descriptor).
 bool qmv_supported(uint32_t type, size_t rows, size_t columns, const void *w, size_t batch);
 
-// y[b][r] = W[r] . x[b]; when `argmax` is non-null (batch 1) the kernel also
-// folds a greedy argmax over the rows into `argmax`.
+// y[b][r] = W[r] . x[b]; when `argmax` is non-null (batch 1) the kernels
+// also reset `argmax`, fold a greedy argmax over the rows into it and write
+// the winning row to *index_out.
 hipError_t launch_qmv(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns,
                       const void *w, uint32_t batch, const float *x, float *y,
-                      ArgmaxState *argmax);
+                      ArgmaxState *argmax, uint32_t *index_out);
 
 // Two weight matrices of the same shape applied to the same x, writing
 // silu(gate) * up (the dense FFN's gate/up pair, src/qwen35/cpu.rs:420-424),

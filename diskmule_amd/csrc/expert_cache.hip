@@ -65,6 +65,7 @@ struct Layer {
 
 struct dmhip_expert_cache {
     dmhip_ctx *ctx = nullptr;
+    int device = 0;
     const uint8_t *source = nullptr;
     size_t source_len = 0;
     std::vector<dm::Layer> layers;
@@ -168,6 +169,7 @@ int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len
     DM_CHECK_STATUS(set_device(ctx));
     dmhip_expert_cache *c = new dmhip_expert_cache();
     c->ctx = ctx;
+    c->device = ctx->device;
     c->source = (const uint8_t *)source;
     c->source_len = source_len;
     c->layers.resize(layer_count);
@@ -196,9 +198,9 @@ int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len
 
 void dmhip_expert_cache_free(dmhip_expert_cache *c) {
     if (!c) return;
-    (void)hipSetDevice(c->ctx->device);
-    (void)hipStreamSynchronize(c->ctx->upload);
-    (void)hipStreamSynchronize(c->ctx->stream);
+    // The context may already be gone: wait on the device, not its streams.
+    (void)hipSetDevice(c->device);
+    (void)hipDeviceSynchronize();
     for (Layer &layer : c->layers)
         for (Slot &s : layer.slots) {
             if (s.gate_up) (void)hipFree(s.gate_up);

@@ -22,20 +22,38 @@
 // and the A row; kg = lane >> 4 picks which quarter of each 32-column step
 // the lane supplies.  C[m][n] sits in lane n + 16*(m/4), element m%4, so
 // lane (n, g4) accumulates tokens 2*g4 and 2*g4+1 of row n.
+//
+// Data movement: every lane loads its own 16-byte pieces of a block straight
+// into registers with buffer loads (out-of-range rows read zero), one block
+// ahead of the compute (double-buffered).  For batch 1-2 the activation
+// fragments of the whole row are staged once per workgroup in LDS and read
+// with ds_read_b128; for larger batches they come from L2.
 #include "dm_device.h"
 #include "dm_qmv.h"
+
+#include <stdlib.h>
 
 namespace dm {
 
 namespace {
 
-constexpr uint32_t kBias16 = 0x64006400u;  // fp16 pair (1024, 1024)
+constexpr uint32_t kBias16 = 0x64006400u;    // fp16 pair (1024, 1024)
+constexpr uint32_t kBiasBytes = 0x64646464u;  // source of the 0x64 high bytes
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
 __device__ __forceinline__ half2_t h2_fma(half2_t a, half2_t b, half2_t c) {
     return __builtin_elementwise_fma(a, b, c);
+}
+
+// (v, v) as fp16 from a small integer (exact: |v| < 2048).
+__device__ __forceinline__ half2_t h2_int(int v) {
+    const _Float16 h = (_Float16)(short)v;
+    half2_t r;
+    r[0] = h;
+    r[1] = h;
+    return r;
 }
 
 __device__ __forceinline__ half2_t h2_splat(float v) {
@@ -45,6 +63,10 @@ __device__ __forceinline__ half2_t h2_splat(float v) {
     return h;
 }
 
+__device__ __forceinline__ float f16_lo(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
+}
+
 __device__ __forceinline__ floatx4 mfma(half8 a, half8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -52,12 +74,6 @@ __device__ __forceinline__ floatx4 mfma(half8 a, half8 b, floatx4 c) {
 __device__ __forceinline__ half8 frag(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     u32x4 v = {a, b, c, d};
     return __builtin_bit_cast(half8, v);
-}
-
-// Byte i (0..15) of four little-endian words.
-__device__ __forceinline__ uint32_t byte_of(u32x4 w, uint32_t i) {
-    uint32_t word = i < 4 ? w[0] : (i < 8 ? w[1] : (i < 12 ? w[2] : w[3]));
-    return (word >> (8 * (i & 3))) & 0xffu;
 }
 
 // Steps of 32 columns per 256-column block, including Q4_K's min step.
@@ -74,6 +90,50 @@ __device__ __forceinline__ uint32_t fragment_column(uint32_t kg, uint32_t t, uin
     // Q6_K: kg = 2h + c; k = t >> 1; dw = 2 * (t & 1) + (j >> 2).
     const uint32_t h = kg >> 1, c = kg & 1u, k = t >> 1, dw = 2 * (t & 1u) + (j >> 2);
     return 128 * h + 32 * k + 16 * c + 4 * dw + perm;
+}
+
+// Power-of-two exponent e with max|x| * 2^-e in [2^14, 2^15) (0 for an
+// all-zero or non-finite row, whose result is then non-finite anyway).
+__device__ __forceinline__ int token_exponent(float mx) {
+    int e = 0;
+    if (mx > 0.0f && __builtin_isfinite(mx)) {
+        int ex;
+        (void)frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
+        e = ex - 15;
+        if (e < -126) e = -126;
+        if (e > 127) e = 127;
+    }
+    return e;
+}
+
+// The hi/lo fp16 halves of fragment (blk, t, kg) of one token row `xt`
+// scaled by `down` (a power of two).
+template <uint32_t TYPE>
+__device__ __forceinline__ void build_fragment(const float *xt, uint32_t blk, uint32_t t, uint32_t kg,
+                                               float down, half8 &hi, half8 &lo) {
+    const float *xb = xt + (size_t)blk * 256;
+    if (TYPE == kQ4_K && t == 8) {
+        hi = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        lo = half8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const float *sb = xb + 32 * (2 * kg + j);
+            float s = 0.0f;
+            for (int i = 0; i < 32; i++) s += sb[i] * down;
+            s = s * 0.015625f;  // 2^-6 keeps |sum| inside fp16
+            const _Float16 h = (_Float16)s;
+            hi[j] = h;
+            lo[j] = (_Float16)(s - (float)h);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float v = xb[fragment_column<TYPE>(kg, t, j)] * down;
+            const _Float16 h = (_Float16)v;
+            hi[j] = h;
+            lo[j] = (_Float16)(v - (float)h);
+        }
+    }
 }
 
 }  // namespace
@@ -98,7 +158,6 @@ __global__ void __launch_bounds__(256) qmv_prepare_kernel(const float *__restric
     for (uint32_t i = threadIdx.x; i < columns; i += blockDim.x) {
         float v = xt[i];
         mx = fmaxf(mx, fabsf(v));
-        if (fabsf(v) != fabsf(v)) mx = v;  // keep NaN visible
         ss = __builtin_fmaf(v, v, ss);
     }
     mx = wave_max(mx);
@@ -110,14 +169,7 @@ __global__ void __launch_bounds__(256) qmv_prepare_kernel(const float *__restric
     __syncthreads();
     mx = fmaxf(fmaxf(red_max[0], red_max[1]), fmaxf(red_max[2], red_max[3]));
     ss = red_ss[0] + red_ss[1] + red_ss[2] + red_ss[3];
-    int e = 0;
-    if (mx > 0.0f && __builtin_isfinite(mx)) {
-        int ex;
-        (void)frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
-        e = ex - 15;            // mx * 2^-e in [2^14, 2^15)
-        if (e < -126) e = -126;
-        if (e > 127) e = 127;
-    }
+    const int e = token_exponent(mx);
     const float down = ldexpf(1.0f, -e);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         float up = ldexpf(1.0f, e);
@@ -128,57 +180,237 @@ __global__ void __launch_bounds__(256) qmv_prepare_kernel(const float *__restric
     const uint32_t blocks = columns / 256;
     const uint32_t m2 = 2 * batch;
     const uint32_t fragments = blocks * SPB * 4;
+    half8 *dst = (half8 *)xp;
     for (uint32_t f = blockIdx.x * blockDim.x + threadIdx.x; f < fragments;
          f += gridDim.x * blockDim.x) {
         const uint32_t kg = f & 3u, t = (f >> 2) % SPB, blk = (f >> 2) / SPB;
-        const float *xb = xt + (size_t)blk * 256;
-        _Float16 hi[8], lo[8];
-        if (TYPE == kQ4_K && t == 8) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) { hi[j] = (_Float16)0.0f; lo[j] = (_Float16)0.0f; }
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const float *sb = xb + 32 * (2 * kg + j);
-                float s = 0.0f;
-                for (int i = 0; i < 32; i++) s += sb[i] * down;
-                s = s * 0.015625f;  // 2^-6 keeps |sum| inside fp16
-                _Float16 h = (_Float16)s;
-                hi[j] = h;
-                lo[j] = (_Float16)(s - (float)h);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                float v = xb[fragment_column<TYPE>(kg, t, j)] * down;
-                _Float16 h = (_Float16)v;
-                hi[j] = h;
-                lo[j] = (_Float16)(v - (float)h);
-            }
-        }
-        _Float16 *dst = xp + ((size_t)f * m2 + 2 * token) * 8;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            dst[j] = hi[j];
-            dst[8 + j] = lo[j];
-        }
+        half8 hi, lo;
+        build_fragment<TYPE>(xt, blk, t, kg, down, hi, lo);
+        dst[(size_t)f * m2 + 2 * token] = hi;
+        dst[(size_t)f * m2 + 2 * token + 1] = lo;
     }
 }
 
 // ---------------------------------------------------------------------------
+// Raw bytes of one block of one row as a lane holds them, and the block's
+// contribution to the lane's accumulators.
+// ---------------------------------------------------------------------------
+template <uint32_t TYPE> struct Raw;
+template <> struct Raw<kQ4_K> {
+    u32x4 hdr, q0, q1;  // d|dmin|scales, then qs bytes [32kg, 32kg+32)
+};
+template <> struct Raw<kQ6_K> {
+    u32x4 a1, a2, a3, a4;          // aligned dwords under ql/ql+32/qh/scales
+    uint32_t e1, e2, e3, e4, e4b;  // the dword after each (for the byte shift)
+    uint32_t s;                    // block start mod 4
+};
+
+template <uint32_t TYPE>
+__device__ __forceinline__ void load_raw(__amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t kg,
+                                         Raw<TYPE> &raw);
+
+template <>
+__device__ __forceinline__ void load_raw<kQ4_K>(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t kg,
+                                                Raw<kQ4_K> &raw) {
+    raw.hdr = rsrc_load16(rs, off);
+    raw.q0 = rsrc_load16(rs, off + 16 + 32 * kg);
+    raw.q1 = rsrc_load16(rs, off + 32 + 32 * kg);
+}
+
+template <>
+__device__ __forceinline__ void load_raw<kQ6_K>(__amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t kg,
+                                                Raw<kQ6_K> &raw) {
+    const uint32_t s = boff & 3u, base = boff - s;
+    const uint32_t h = kg >> 1, c = kg & 1u;
+    const uint32_t o1 = base + 64 * h + 16 * c, o2 = o1 + 32, o3 = base + 128 + 32 * h + 16 * c,
+                   o4 = base + 192;
+    raw.s = s;
+    raw.a1 = rsrc_load16(rs, o1);
+    raw.a2 = rsrc_load16(rs, o2);
+    raw.a3 = rsrc_load16(rs, o3);
+    raw.a4 = rsrc_load16(rs, o4);
+    raw.e1 = rsrc_load4(rs, o1 + 16);
+    raw.e2 = rsrc_load4(rs, o2 + 16);
+    raw.e3 = rsrc_load4(rs, o3 + 16);
+    raw.e4 = rsrc_load4(rs, o4 + 16);
+    raw.e4b = rsrc_load4(rs, o4 + 20);
+}
+
+template <int NT>
+__device__ __forceinline__ void block_dot(const Raw<kQ4_K> &raw, const half8 (&a)[9][NT], uint32_t kg,
+                                          float (&acc)[NT][2]) {
+    const u32x4 hdr = raw.hdr;
+    const float dscale = f16_lo(hdr[0]);
+    const float mscale = f16_lo(hdr[0] >> 16);
+    // (scale, min) of sub-blocks 2kg and 2kg+1 (src/cpu.rs:607-616): for
+    // sub-block j < 4 the low 6 bits of scales[j], scales[j+4]; for j >= 4
+    // nibbles of scales[j+4] with the top bits of scales[j-4], scales[j].
+    const bool high_half = kg >= 2;
+    uint32_t sc[2], mn[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t sh = 8 * ((2 * kg + j) & 3u);
+        const uint32_t b1 = hdr[1] >> sh, b2 = hdr[2] >> sh, b3 = hdr[3] >> sh;
+        const uint32_t sc_lo = b1 & 63u, mn_lo = b2 & 63u;
+        const uint32_t sc_hi = (b3 & 15u) | ((b1 >> 2) & 0x30u);
+        const uint32_t mn_hi = ((b3 >> 4) & 15u) | ((b2 >> 2) & 0x30u);
+        sc[j] = high_half ? sc_hi : sc_lo;
+        mn[j] = high_half ? mn_hi : mn_lo;
+    }
+    const half2_t sl = h2_int((int)sc[0]);
+    const half2_t bl = sl * h2_splat(-1024.0f);
+    const half2_t shi = h2_int((int)sc[1]);
+    const half2_t sh = shi * h2_splat(0.0625f);
+    const half2_t bh = shi * h2_splat(-64.0f);
+    floatx4 cm[NT];
+#pragma unroll
+    for (int g = 0; g < NT; g++) cm[g] = floatx4{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const uint32_t d = t < 4 ? raw.q0[t] : raw.q1[t - 4];
+        const uint32_t d8 = d >> 8;
+        const uint32_t p0 = as_u(h2_fma(as_h2((d & 0x000f000fu) | kBias16), sl, bl));
+        const uint32_t p1 = as_u(h2_fma(as_h2((d8 & 0x000f000fu) | kBias16), sl, bl));
+        const uint32_t p2 = as_u(h2_fma(as_h2((d & 0x00f000f0u) | kBias16), sh, bh));
+        const uint32_t p3 = as_u(h2_fma(as_h2((d8 & 0x00f000f0u) | kBias16), sh, bh));
+        const half8 b = frag(p0, p1, p2, p3);
+#pragma unroll
+        for (int g = 0; g < NT; g++) cm[g] = mfma(a[t][g], b, cm[g]);
+    }
+    // min step: B = (64 m_lo, 64 m_hi, 0...), A = sub-block sums * 2^-6.
+    const uint32_t mm = (as_u(h2_int((int)(64 * mn[0]))) & 0xffffu) |
+                        (as_u(h2_int((int)(64 * mn[1]))) << 16);
+    const half8 bmin = frag(mm, 0u, 0u, 0u);
+#pragma unroll
+    for (int g = 0; g < NT; g++) {
+        const floatx4 cmin = mfma(a[8][g], bmin, floatx4{0, 0, 0, 0});
+        acc[g][0] = __builtin_fmaf(dscale, cm[g][0] + cm[g][1], acc[g][0]);
+        acc[g][0] = __builtin_fmaf(-mscale, cmin[0] + cmin[1], acc[g][0]);
+        acc[g][1] = __builtin_fmaf(dscale, cm[g][2] + cm[g][3], acc[g][1]);
+        acc[g][1] = __builtin_fmaf(-mscale, cmin[2] + cmin[3], acc[g][1]);
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void block_dot(const Raw<kQ6_K> &raw, const half8 (&a)[8][NT], uint32_t kg,
+                                          float (&acc)[NT][2]) {
+    const uint32_t s = raw.s;
+    uint32_t L1[4], L2[4], H[4], T[5];
+    if (__builtin_amdgcn_ballot_w64(s != 0) == 0) {
+        // every row of the tile starts this block on a dword boundary
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            L1[i] = raw.a1[i];
+            L2[i] = raw.a2[i];
+            H[i] = raw.a3[i];
+            T[i] = raw.a4[i];
+        }
+        T[4] = raw.e4;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            L1[i] = funnel(raw.a1[i], i < 3 ? raw.a1[i + 1] : raw.e1, s);
+            L2[i] = funnel(raw.a2[i], i < 3 ? raw.a2[i + 1] : raw.e2, s);
+            H[i] = funnel(raw.a3[i], i < 3 ? raw.a3[i + 1] : raw.e3, s);
+            T[i] = funnel(raw.a4[i], i < 3 ? raw.a4[i + 1] : raw.e4, s);
+        }
+        T[4] = funnel(raw.e4, raw.e4b, s);
+    }
+    const float dscale = f16_lo(T[4]);
+    // int8 scales sc[8h + 2k + c], k = 0..3: bytes c and c+2 of scale words
+    // 2h (k = 0, 1) and 2h+1 (k = 2, 3).
+    const uint32_t h = kg >> 1, c = kg & 1u;
+    const uint32_t w01 = h ? T[2] : T[0], w23 = h ? T[3] : T[1];
+    int sck[4];
+    sck[0] = (int)(int8_t)(w01 >> (8 * c));
+    sck[1] = (int)(int8_t)(w01 >> (8 * c + 16));
+    sck[2] = (int)(int8_t)(w23 >> (8 * c));
+    sck[3] = (int)(int8_t)(w23 >> (8 * c + 16));
+    bool fast = true;
+#pragma unroll
+    for (int k = 0; k < 4; k++) fast = fast && sck[k] <= 62 && sck[k] >= -62;
+    const bool all_fast = __builtin_amdgcn_ballot_w64(!fast) == 0;
+    floatx4 cm[NT];
+#pragma unroll
+    for (int g = 0; g < NT; g++) cm[g] = floatx4{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const int k = t >> 1;
+        uint32_t pr[4];
+#pragma unroll
+        for (int half_dw = 0; half_dw < 2; half_dw++) {
+            const int dw = 2 * (t & 1) + half_dw;
+            const uint32_t src = (k & 1) ? L2[dw] : L1[dw];
+            const uint32_t nib = (k & 2) ? (src >> 4) : src;
+            // bits 2k..2k+1 of each qh byte moved to bits 4..5
+            const uint32_t hsh = k == 0 ? H[dw] << 4 : (k == 1 ? H[dw] << 2 : (k == 2 ? H[dw] : H[dw] >> 2));
+            const uint32_t q4 = (nib & 0x0f0f0f0fu) | (hsh & 0x30303030u);  // four 6-bit q
+            // fp16 pairs (1024 + q) of bytes (0, 2) and (1, 3)
+            pr[2 * half_dw] = __builtin_amdgcn_perm(q4, kBiasBytes, 0x00060004u);
+            pr[2 * half_dw + 1] = __builtin_amdgcn_perm(q4, kBiasBytes, 0x00070005u);
+        }
+        if (all_fast) {
+            const half2_t scl = h2_int(sck[k]);
+            const half2_t bias = scl * h2_splat(-1056.0f);
+            const half8 b = frag(as_u(h2_fma(as_h2(pr[0]), scl, bias)), as_u(h2_fma(as_h2(pr[1]), scl, bias)),
+                                 as_u(h2_fma(as_h2(pr[2]), scl, bias)), as_u(h2_fma(as_h2(pr[3]), scl, bias)));
+#pragma unroll
+            for (int g = 0; g < NT; g++) cm[g] = mfma(a[t][g], b, cm[g]);
+        } else {
+            // sc = 8*sh + sl, sl in 0..7: both products exact in fp16.
+            const int shi = sck[k] >> 3, slo = sck[k] & 7;
+            const half2_t off = h2_splat(-1056.0f);
+            const half2_t one = h2_splat(1.0f);
+            const half2_t f_hi = h2_int(8 * shi);
+            const half2_t f_lo = h2_int(slo);
+            half2_t qm[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) qm[i] = h2_fma(as_h2(pr[i]), one, off);  // q - 32
+            const half8 b_hi = frag(as_u(qm[0] * f_hi), as_u(qm[1] * f_hi), as_u(qm[2] * f_hi),
+                                    as_u(qm[3] * f_hi));
+            const half8 b_lo = frag(as_u(qm[0] * f_lo), as_u(qm[1] * f_lo), as_u(qm[2] * f_lo),
+                                    as_u(qm[3] * f_lo));
+#pragma unroll
+            for (int g = 0; g < NT; g++) {
+                cm[g] = mfma(a[t][g], b_hi, cm[g]);
+                cm[g] = mfma(a[t][g], b_lo, cm[g]);
+            }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < NT; g++) {
+        acc[g][0] = __builtin_fmaf(dscale, cm[g][0] + cm[g][1], acc[g][0]);
+        acc[g][1] = __builtin_fmaf(dscale, cm[g][2] + cm[g][3], acc[g][1]);
+    }
+}
+
+// Per-wave argmax candidate of the fused epilogue.
+struct ArgmaxPartial {
+    unsigned long long key;
+    uint32_t non_finite;
+    uint32_t pad;
+};
+
+// ---------------------------------------------------------------------------
 // Main kernel.  A workgroup has 4 waves; S waves split one group of R row
 // tiles along K, so a workgroup covers (4/S)*R tiles of 16 rows.
-// MODE 0: y = W x.  MODE 1: argmax epilogue.  MODE 2: gate/up pair,
-// act = silu(gate) * up.
+// MB > 0: the activation fragments (MB = 2*batch rows) live in LDS.
+// MODE 0: y = W x.  MODE 1: also a per-wave argmax candidate.  MODE 2:
+// gate/up pair, act = silu(gate) * up.
 // ---------------------------------------------------------------------------
-template <uint32_t TYPE, int NT, int R, int S, int MODE>
+template <uint32_t TYPE, int NT, int R, int S, int MODE, int MB>
 __global__ void __launch_bounds__(256) qmv_kernel(
     const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows,
-    uint32_t columns, uint32_t row_bytes, uint32_t total_bytes,
-    const _Float16 *__restrict__ xp, const float *__restrict__ yscale, uint32_t batch,
-    float *__restrict__ y, ArgmaxState *argmax) {
+    uint32_t columns, uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x,
+    int normalize, float epsilon, const _Float16 *__restrict__ xp,
+    const float *__restrict__ yscale_global, uint32_t batch, float *__restrict__ y,
+    ArgmaxPartial *__restrict__ partials) {
     constexpr uint32_t SPB = Steps<TYPE>::value;
+    constexpr uint32_t BB = TYPE == kQ4_K ? 144u : 210u;
     constexpr int RR = MODE == 2 ? 2 * R : R;  // gate/up: R tiles of each matrix
     __shared__ float partial[S > 1 ? 4 * RR * NT * 64 * 2 : 1];
+    __shared__ float token_scale[2][4];
+    extern __shared__ half8 lds_a[];
 
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15u, kg = lane >> 4;
@@ -187,10 +419,30 @@ __global__ void __launch_bounds__(256) qmv_kernel(
     const uint32_t blocks = columns / 256;
     const uint32_t b_begin = kpart * blocks / S, b_end = (kpart + 1) * blocks / S;
     const uint32_t m2 = 2 * batch;
+    const float *yscale = yscale_global;
+
+    // Lanes whose A row carries no token read a zeroed copy of one block's
+    // fragments, so every lane runs the same loads.
+    const half8 *a_lane = nullptr;
+    uint32_t a_block_stride = 0;
+    if constexpr (MB > 0) {
+        // Copy every activation fragment of the row (written by the
+        // preparation kernel) into LDS, followed by one zeroed block.
+        const uint32_t count = blocks * SPB * 4 * MB;
+        const half8 *src = (const half8 *)xp;
+        for (uint32_t i = threadIdx.x; i < count; i += 256) lds_a[i] = src[i];
+        for (uint32_t i = threadIdx.x; i < SPB * 4 * MB; i += 256)
+            lds_a[count + i] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (threadIdx.x < MB / 2) token_scale[threadIdx.x][0] = yscale_global[threadIdx.x];
+        __syncthreads();
+        a_lane = n < (uint32_t)MB ? lds_a + kg * MB + n : lds_a + count + kg * MB;
+        a_block_stride = n < (uint32_t)MB ? SPB * 4 * MB : 0;
+    }
 
     // Whole dwords: the last dword of the matrix may extend up to 3 bytes past
     // its end (inside the allocation's granularity); loads beyond it read 0.
     const uint32_t records = (total_bytes + 3u) & ~3u;
+    const uint32_t nowhere = records + 256;  // every load from here reads 0
     const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(w, records);
     const __amdgpu_buffer_rsrc_t rsrc2 = make_rsrc(MODE == 2 ? w2 : w, records);
 
@@ -206,171 +458,48 @@ __global__ void __launch_bounds__(256) qmv_kernel(
     for (int r = 0; r < RR; r++) {
         const uint32_t tile = first_tile + (MODE == 2 ? r % R : r);
         const uint32_t row = tile * 16 + n;
-        row_base[r] = row < rows ? row * row_bytes : records + 256;  // out of range -> zeros
+        row_base[r] = row < rows ? row * row_bytes : nowhere;
     }
 
-    for (uint32_t blk = b_begin; blk < b_end; blk++) {
-        // --- activations: SPB steps x NT token groups ------------------------
+    auto load_block = [&](uint32_t blk, Raw<TYPE>(&raw)[RR]) {
+#pragma unroll
+        for (int r = 0; r < RR; r++) {
+            const uint32_t off = row_base[r] == nowhere ? nowhere : row_base[r] + blk * BB;
+            load_raw<TYPE>((MODE == 2 && r >= R) ? rsrc2 : rsrc, off, kg, raw[r]);
+        }
+    };
+    auto compute_block = [&](uint32_t blk, const Raw<TYPE>(&raw)[RR]) {
         half8 a[SPB][NT];
 #pragma unroll
         for (int t = 0; t < (int)SPB; t++)
 #pragma unroll
             for (int g = 0; g < NT; g++) {
                 const uint32_t m = 16 * g + n;
-                if (m < m2) {
+                if constexpr (MB > 0) {
+                    // one address per block, then immediate offsets per step
+                    a[t][g] = a_lane[blk * a_block_stride + t * 4 * MB];
+                } else if (m < m2) {
                     const size_t f = ((size_t)blk * SPB + t) * 4 + kg;
                     a[t][g] = *(const half8 *)(xp + (f * m2 + m) * 8);
                 } else {
                     a[t][g] = half8{0, 0, 0, 0, 0, 0, 0, 0};
                 }
             }
+#pragma unroll
+        for (int r = 0; r < RR; r++) block_dot<NT>(raw[r], a, kg, acc[r]);
+    };
 
-#pragma unroll
-        for (int r = 0; r < RR; r++) {
-            const __amdgpu_buffer_rsrc_t rs = (MODE == 2 && r >= R) ? rsrc2 : rsrc;
-            floatx4 cm[NT];
-#pragma unroll
-            for (int g = 0; g < NT; g++) cm[g] = floatx4{0, 0, 0, 0};
-            float dscale, mscale = 0.0f;
-            if constexpr (TYPE == kQ4_K) {
-                const uint32_t off = row_base[r] + blk * 144u;
-                const u32x4 hdr = rsrc_load16(rs, off);
-                const u32x4 q0 = rsrc_load16(rs, off + 16 + 32 * kg);
-                const u32x4 q1 = rsrc_load16(rs, off + 32 + 32 * kg);
-                dscale = f16_bits_to_f32(hdr[0] & 0xffffu);
-                mscale = f16_bits_to_f32(hdr[0] >> 16);
-                // (scale, min) of sub-blocks 2kg and 2kg+1 (src/cpu.rs:607-616).
-                uint32_t sc[2], mn[2];
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const uint32_t idx = 2 * kg + j;
-                    if (idx < 4) {
-                        sc[j] = (hdr[1] >> (8 * idx)) & 63u;
-                        mn[j] = (hdr[2] >> (8 * idx)) & 63u;
-                    } else {
-                        const uint32_t b = idx - 4;
-                        const uint32_t s8 = (hdr[3] >> (8 * b)) & 0xffu;
-                        sc[j] = (s8 & 15u) | (((hdr[1] >> (8 * b)) >> 6 & 3u) << 4);
-                        mn[j] = (s8 >> 4) | (((hdr[2] >> (8 * b)) >> 6 & 3u) << 4);
-                    }
-                }
-                const half2_t sl = h2_splat((float)sc[0]);
-                const half2_t bl = h2_splat(-1024.0f * (float)sc[0]);
-                const half2_t sh = h2_splat((float)sc[1] * 0.0625f);
-                const half2_t bh = h2_splat(-64.0f * (float)sc[1]);
-#pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    const uint32_t d = t < 4 ? q0[t] : q1[t - 4];
-                    const uint32_t d8 = d >> 8;
-                    const uint32_t p0 = as_u(h2_fma(as_h2((d & 0x000f000fu) | kBias16), sl, bl));
-                    const uint32_t p1 = as_u(h2_fma(as_h2((d8 & 0x000f000fu) | kBias16), sl, bl));
-                    const uint32_t p2 = as_u(h2_fma(as_h2((d & 0x00f000f0u) | kBias16), sh, bh));
-                    const uint32_t p3 = as_u(h2_fma(as_h2((d8 & 0x00f000f0u) | kBias16), sh, bh));
-                    const half8 b = frag(p0, p1, p2, p3);
-#pragma unroll
-                    for (int g = 0; g < NT; g++) cm[g] = mfma(a[t][g], b, cm[g]);
-                }
-                // min step: B = (64 m_lo, 64 m_hi, 0...), A = sub-block sums * 2^-6.
-                half2_t mm;
-                mm[0] = (_Float16)(64.0f * (float)mn[0]);
-                mm[1] = (_Float16)(64.0f * (float)mn[1]);
-                const half8 bmin = frag(as_u(mm), 0u, 0u, 0u);
-                floatx4 cmin[NT];
-#pragma unroll
-                for (int g = 0; g < NT; g++) cmin[g] = mfma(a[8][g], bmin, floatx4{0, 0, 0, 0});
-#pragma unroll
-                for (int g = 0; g < NT; g++) {
-                    acc[r][g][0] = __builtin_fmaf(dscale, cm[g][0] + cm[g][1], acc[r][g][0]);
-                    acc[r][g][0] = __builtin_fmaf(-mscale, cmin[g][0] + cmin[g][1], acc[r][g][0]);
-                    acc[r][g][1] = __builtin_fmaf(dscale, cm[g][2] + cm[g][3], acc[r][g][1]);
-                    acc[r][g][1] = __builtin_fmaf(-mscale, cmin[g][2] + cmin[g][3], acc[r][g][1]);
-                }
-            } else {  // Q6_K
-                const uint32_t boff = row_base[r] + blk * 210u;
-                const uint32_t s = boff & 3u;
-                const uint32_t base = boff - s;
-                const uint32_t h = kg >> 1, c = kg & 1u;
-                uint32_t L1[4], L2[4], H[4], T[5];
-                {
-                    const uint32_t o1 = base + 64 * h + 16 * c;
-                    const uint32_t o2 = o1 + 32;
-                    const uint32_t o3 = base + 128 + 32 * h + 16 * c;
-                    const uint32_t o4 = base + 192;
-                    const u32x4 a1 = rsrc_load16(rs, o1), a2 = rsrc_load16(rs, o2),
-                                a3 = rsrc_load16(rs, o3), a4 = rsrc_load16(rs, o4);
-                    const uint32_t e1 = rsrc_load4(rs, o1 + 16), e2 = rsrc_load4(rs, o2 + 16),
-                                   e3 = rsrc_load4(rs, o3 + 16), e4 = rsrc_load4(rs, o4 + 16);
-                    const uint32_t e4b = rsrc_load4(rs, o4 + 20);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        L1[i] = funnel(a1[i], i < 3 ? a1[i + 1] : e1, s);
-                        L2[i] = funnel(a2[i], i < 3 ? a2[i + 1] : e2, s);
-                        H[i] = funnel(a3[i], i < 3 ? a3[i + 1] : e3, s);
-                        T[i] = funnel(a4[i], i < 3 ? a4[i + 1] : e4, s);
-                    }
-                    T[4] = funnel(e4, e4b, s);
-                }
-                dscale = f16_bits_to_f32(T[4] & 0xffffu);
-                // int8 scales sc[8h + 2k + c], k = 0..3.
-                int sck[4];
-                bool fast = true;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const uint32_t bi = 8 * h + 2 * k + c;
-                    sck[k] = (int)(int8_t)((T[bi >> 2] >> (8 * (bi & 3u))) & 0xffu);
-                    fast = fast && sck[k] <= 62 && sck[k] >= -62;
-                }
-                const bool all_fast = __builtin_amdgcn_ballot_w64(!fast) == 0;
-#pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    const int k = t >> 1;
-                    uint32_t pr[4];
-#pragma unroll
-                    for (int half_dw = 0; half_dw < 2; half_dw++) {
-                        const int dw = 2 * (t & 1) + half_dw;
-                        const uint32_t src = (k & 1) ? L2[dw] : L1[dw];
-                        const uint32_t nib = (k & 2) ? (src >> 4) : src;
-                        const uint32_t hb = H[dw] >> (2 * k);
-                        pr[2 * half_dw] = (nib & 0x000f000fu) | ((hb << 4) & 0x00300030u) | kBias16;
-                        pr[2 * half_dw + 1] =
-                            ((nib >> 8) & 0x000f000fu) | ((hb >> 4) & 0x00300030u) | kBias16;
-                    }
-                    if (all_fast) {
-                        const half2_t scl = h2_splat((float)sck[k]);
-                        const half2_t bias = h2_splat(-1056.0f * (float)sck[k]);
-                        const half8 b = frag(as_u(h2_fma(as_h2(pr[0]), scl, bias)),
-                                             as_u(h2_fma(as_h2(pr[1]), scl, bias)),
-                                             as_u(h2_fma(as_h2(pr[2]), scl, bias)),
-                                             as_u(h2_fma(as_h2(pr[3]), scl, bias)));
-#pragma unroll
-                        for (int g = 0; g < NT; g++) cm[g] = mfma(a[t][g], b, cm[g]);
-                    } else {
-                        // sc = 8*sh + sl, sl in 0..7: both products exact in fp16.
-                        const int shi = sck[k] >> 3, slo = sck[k] & 7;
-                        const half2_t off = h2_splat(-1056.0f);
-                        const half2_t one = h2_splat(1.0f);
-                        const half2_t f_hi = h2_splat(8.0f * (float)shi);
-                        const half2_t f_lo = h2_splat((float)slo);
-                        half2_t qm[4];
-#pragma unroll
-                        for (int i = 0; i < 4; i++) qm[i] = h2_fma(as_h2(pr[i]), one, off);  // q - 32
-                        const half8 b_hi = frag(as_u(qm[0] * f_hi), as_u(qm[1] * f_hi),
-                                                as_u(qm[2] * f_hi), as_u(qm[3] * f_hi));
-                        const half8 b_lo = frag(as_u(qm[0] * f_lo), as_u(qm[1] * f_lo),
-                                                as_u(qm[2] * f_lo), as_u(qm[3] * f_lo));
-#pragma unroll
-                        for (int g = 0; g < NT; g++) {
-                            cm[g] = mfma(a[t][g], b_hi, cm[g]);
-                            cm[g] = mfma(a[t][g], b_lo, cm[g]);
-                        }
-                    }
-                }
-#pragma unroll
-                for (int g = 0; g < NT; g++) {
-                    acc[r][g][0] = __builtin_fmaf(dscale, cm[g][0] + cm[g][1], acc[r][g][0]);
-                    acc[r][g][1] = __builtin_fmaf(dscale, cm[g][2] + cm[g][3], acc[r][g][1]);
-                }
-            }
+    // Double-buffered: the loads of block b+1 are in flight while block b
+    // is computed.
+    if (b_begin < b_end) {
+        Raw<TYPE> raw0[RR], raw1[RR];
+        load_block(b_begin, raw0);
+        for (uint32_t blk = b_begin; blk < b_end; blk += 2) {
+            if (blk + 1 < b_end) load_block(blk + 1, raw1);
+            compute_block(blk, raw0);
+            if (blk + 1 >= b_end) break;
+            if (blk + 2 < b_end) load_block(blk + 2, raw0);
+            compute_block(blk + 1, raw1);
         }
     }
 
@@ -411,7 +540,7 @@ __global__ void __launch_bounds__(256) qmv_kernel(
             for (int j = 0; j < 2; j++) {
                 const uint32_t token = 8 * g + 2 * kg + j;
                 if (token >= batch) continue;
-                const float sc = yscale[token];
+                const float sc = MB > 0 ? token_scale[token][0] : yscale[token];
                 float v = acc[r][g][j] * sc;
                 if constexpr (MODE == 2) {
                     const float u = acc[R + r][g][j] * sc;
@@ -434,9 +563,52 @@ __global__ void __launch_bounds__(256) qmv_kernel(
             }
     }
     if constexpr (MODE == 1) {
+        // No atomics and no device-wide fence here: each wave writes its own
+        // candidate and a one-workgroup pass reduces them.
         best = wave_max_u64(best);
-        if (lane == 0 && best) atomicMax(&argmax->key, (unsigned long long)best);
-        if (bad) atomicOr(&argmax->non_finite, 1u);
+        bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
+        if (lane == 0) {
+            ArgmaxPartial p;
+            p.key = best;
+            p.non_finite = bad;
+            p.pad = 0;
+            partials[blockIdx.x * (4 / S) + group] = p;
+        }
+    }
+}
+
+// Reduces the per-wave candidates: the largest key wins (value, then lowest
+// row); any non-finite row marks the result.
+__global__ void __launch_bounds__(256) argmax_partials_kernel(const ArgmaxPartial *__restrict__ partials,
+                                                              uint32_t count, ArgmaxState *state,
+                                                              uint32_t *index_out) {
+    __shared__ unsigned long long keys[4];
+    __shared__ uint32_t flags[4];
+    uint64_t best = 0;
+    uint32_t bad = 0;
+    for (uint32_t i = threadIdx.x; i < count; i += 256) {
+        const ArgmaxPartial p = partials[i];
+        best = p.key > best ? p.key : best;
+        bad |= p.non_finite;
+    }
+    best = wave_max_u64(best);
+    bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
+    if ((threadIdx.x & 63u) == 0) {
+        keys[threadIdx.x >> 6] = best;
+        flags[threadIdx.x >> 6] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = keys[0];
+        uint32_t f = flags[0];
+        for (int i = 1; i < 4; i++) {
+            b = keys[i] > b ? keys[i] : b;
+            f |= flags[i];
+        }
+        state->key = b;
+        state->non_finite = f;
+        state->done = count;
+        *index_out = argmax_key_index(b);
     }
 }
 
@@ -457,11 +629,13 @@ bool qmv_supported(uint32_t type, size_t rows, size_t columns, const void *w, si
 
 namespace {
 
+constexpr size_t kMaxLdsA = 56 * 1024;  // staged activation fragments; + split-K scratch <= 64 KiB
+
 struct Plan {
-    int nt, r, s;
+    int nt, r, s, mb;
 };
 
-Plan choose_plan(uint32_t rows, uint32_t blocks, uint32_t batch, int mode) {
+Plan choose_plan(uint32_t type, uint32_t rows, uint32_t blocks, uint32_t batch, int mode) {
     Plan p;
     p.nt = batch > 8 ? 2 : 1;
     const uint32_t tiles = (rows + 15) / 16;
@@ -475,55 +649,66 @@ Plan choose_plan(uint32_t rows, uint32_t blocks, uint32_t batch, int mode) {
     } else {
         p.s = 4;
     }
+    const uint32_t spb = type == kQ4_K ? 9 : 8;
+    const size_t lds = ((size_t)blocks + 1) * spb * 4 * 2 * batch * 16;
+    p.mb = (batch <= 2 && lds <= kMaxLdsA) ? (int)(2 * batch) : 0;
     return p;
 }
 
-template <uint32_t TYPE, int NT, int R, int S, int MODE>
-hipError_t run(hipStream_t stream, const void *w, const void *w2, uint32_t rows, uint32_t columns,
-               uint32_t row_bytes, uint32_t total, const _Float16 *xp, const float *ysc,
-               uint32_t batch, float *y, ArgmaxState *am) {
-    const uint32_t tiles = (rows + 15) / 16;
+struct Args {
+    const void *w, *w2;
+    uint32_t rows, columns, row_bytes, total;
+    const float *x;
+    int normalize;
+    float epsilon;
+    const _Float16 *xp;
+    const float *ysc;
+    uint32_t batch;
+    float *y;
+    ArgmaxPartial *partials;
+};
+
+template <uint32_t TYPE, int NT, int R, int S, int MODE, int MB>
+hipError_t run(dmhip_ctx *ctx, const Args &a, uint32_t *waves_out) {
+    constexpr uint32_t SPB = Steps<TYPE>::value;
+    const uint32_t tiles = (a.rows + 15) / 16;
     const uint32_t per_wg = (4 / S) * R;
     const uint32_t grid = (tiles + per_wg - 1) / per_wg;
-    hipLaunchKernelGGL((qmv_kernel<TYPE, NT, R, S, MODE>), dim3(grid), dim3(256), 0, stream,
-                       (const uint8_t *)w, (const uint8_t *)w2, rows, columns, row_bytes, total,
-                       xp, ysc, batch, y, am);
+    // fragments of every block plus one zeroed block for the idle A rows
+    const size_t lds = MB > 0 ? ((size_t)(a.columns / 256) + 1) * SPB * 4 * MB * 16 : 0;
+    if (waves_out) *waves_out = grid * (4 / S);
+    KernelTimer timer(ctx);
+    hipLaunchKernelGGL((qmv_kernel<TYPE, NT, R, S, MODE, MB>), dim3(grid), dim3(256), lds, ctx->stream,
+                       (const uint8_t *)a.w, (const uint8_t *)a.w2, a.rows, a.columns, a.row_bytes,
+                       a.total, a.x, a.normalize, a.epsilon, a.xp, a.ysc, a.batch, a.y, a.partials);
     return hipGetLastError();
 }
 
-template <uint32_t TYPE, int MODE>
-hipError_t dispatch(hipStream_t stream, const Plan &p, const void *w, const void *w2, uint32_t rows,
-                    uint32_t columns, uint32_t row_bytes, uint32_t total, const _Float16 *xp,
-                    const float *ysc, uint32_t batch, float *y, ArgmaxState *am) {
-#define DM_RUN(NT_, R_, S_) \
-    return run<TYPE, NT_, R_, S_, MODE>(stream, w, w2, rows, columns, row_bytes, total, xp, ysc, batch, y, am)
-    if (p.nt == 1) {
-        if (p.r == 1) {
-            if (p.s == 1) DM_RUN(1, 1, 1);
-            if (p.s == 2) DM_RUN(1, 1, 2);
-            DM_RUN(1, 1, 4);
-        }
-        if (p.s == 1) DM_RUN(1, 2, 1);
-        if (p.s == 2) DM_RUN(1, 2, 2);
-        DM_RUN(1, 2, 4);
-    }
-    if (p.r == 1) {
-        if (p.s == 1) DM_RUN(2, 1, 1);
-        if (p.s == 2) DM_RUN(2, 1, 2);
-        DM_RUN(2, 1, 4);
-    }
-    if (p.s == 1) DM_RUN(2, 2, 1);
-    if (p.s == 2) DM_RUN(2, 2, 2);
-    DM_RUN(2, 2, 4);
-#undef DM_RUN
+template <uint32_t TYPE, int NT, int R, int MODE, int MB>
+hipError_t run_s(dmhip_ctx *ctx, const Plan &p, const Args &a, uint32_t *w) {
+    if (p.s == 1) return run<TYPE, NT, R, 1, MODE, MB>(ctx, a, w);
+    if (p.s == 2) return run<TYPE, NT, R, 2, MODE, MB>(ctx, a, w);
+    return run<TYPE, NT, R, 4, MODE, MB>(ctx, a, w);
 }
 
+template <uint32_t TYPE, int MODE>
+hipError_t dispatch(dmhip_ctx *ctx, const Plan &p, const Args &a, uint32_t *w) {
+    if (p.mb == 2) return run_s<TYPE, 1, 1, MODE, 2>(ctx, p, a, w);
+    if (p.mb == 4) return run_s<TYPE, 1, 1, MODE, 4>(ctx, p, a, w);
+    if (p.nt == 1)
+        return p.r == 1 ? run_s<TYPE, 1, 1, MODE, 0>(ctx, p, a, w) : run_s<TYPE, 1, 2, MODE, 0>(ctx, p, a, w);
+    return p.r == 1 ? run_s<TYPE, 2, 1, MODE, 0>(ctx, p, a, w) : run_s<TYPE, 2, 2, MODE, 0>(ctx, p, a, w);
+}
+
+// Activation fragments for batches above 2 go to the context's aux scratch:
+// [xp | yscale], written by the preparation kernel.
 hipError_t prepare(dmhip_ctx *ctx, uint32_t type, uint32_t columns, uint32_t batch, const float *x,
                    int normalize, float eps, _Float16 **xp_out, float **ysc_out) {
     const uint32_t spb = type == kQ4_K ? 9 : 8;
     const size_t frags = (size_t)(columns / 256) * spb * 4;
     const size_t xp_bytes = frags * 2 * batch * 8 * sizeof(_Float16);
-    if (ctx->aux.ensure(xp_bytes + 64 * sizeof(float)) != DMHIP_OK) return hipErrorOutOfMemory;
+    if (ctx->aux.ensure(((xp_bytes + 255) & ~(size_t)255) + 64 * sizeof(float)) != DMHIP_OK)
+        return hipErrorOutOfMemory;
     _Float16 *xp = (_Float16 *)ctx->aux.ptr;
     float *ysc = (float *)((char *)ctx->aux.ptr + ((xp_bytes + 255) & ~(size_t)255));
     uint32_t gx = (uint32_t)((frags + 255) / 256);
@@ -539,40 +724,60 @@ hipError_t prepare(dmhip_ctx *ctx, uint32_t type, uint32_t columns, uint32_t bat
     return hipGetLastError();
 }
 
+Args make_args(uint32_t type, uint32_t rows, uint32_t columns, const void *w, const void *w2,
+               uint32_t batch, const float *x, int normalize, float epsilon, float *y) {
+    Args a;
+    const uint32_t blocks = columns / 256;
+    a.w = w;
+    a.w2 = w2;
+    a.rows = rows;
+    a.columns = columns;
+    a.row_bytes = blocks * (type == kQ4_K ? 144u : 210u);
+    a.total = a.row_bytes * rows;
+    a.x = x;
+    a.normalize = normalize;
+    a.epsilon = epsilon;
+    a.xp = nullptr;
+    a.ysc = nullptr;
+    a.batch = batch;
+    a.y = y;
+    a.partials = nullptr;
+    return a;
+}
+
 }  // namespace
 
 hipError_t launch_qmv(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
-                      uint32_t batch, const float *x, float *y, ArgmaxState *argmax) {
-    _Float16 *xp;
-    float *ysc;
-    hipError_t e = prepare(ctx, type, columns, batch, x, 0, 0.0f, &xp, &ysc);
+                      uint32_t batch, const float *x, float *y, ArgmaxState *argmax,
+                      uint32_t *index_out) {
+    Args a = make_args(type, rows, columns, w, w, batch, x, 0, 0.0f, y);
+    const Plan p = choose_plan(type, rows, columns / 256, batch, argmax ? 1 : 0);
+    hipError_t pe = prepare(ctx, type, columns, batch, x, 0, 0.0f, (_Float16 **)&a.xp, (float **)&a.ysc);
+    if (pe != hipSuccess) return pe;
+    if (!argmax)
+        return type == kQ4_K ? dispatch<kQ4_K, 0>(ctx, p, a, nullptr) : dispatch<kQ6_K, 0>(ctx, p, a, nullptr);
+    // One candidate per epilogue wave (at most one per 16-row tile), then a
+    // one-workgroup reduction.
+    const size_t candidates = (size_t)(rows + 15) / 16 + 4;
+    if (ctx->partials.ensure(candidates * sizeof(ArgmaxPartial)) != DMHIP_OK) return hipErrorOutOfMemory;
+    a.partials = (ArgmaxPartial *)ctx->partials.ptr;
+    uint32_t count = 0;
+    hipError_t e = type == kQ4_K ? dispatch<kQ4_K, 1>(ctx, p, a, &count) : dispatch<kQ6_K, 1>(ctx, p, a, &count);
     if (e != hipSuccess) return e;
-    const uint32_t blocks = columns / 256;
-    const uint32_t row_bytes = blocks * (type == kQ4_K ? 144u : 210u);
-    const uint32_t total = row_bytes * rows;
-    const Plan p = choose_plan(rows, blocks, batch, argmax ? 1 : 0);
-    if (type == kQ4_K) {
-        if (argmax) return dispatch<kQ4_K, 1>(ctx->stream, p, w, w, rows, columns, row_bytes, total, xp, ysc, batch, y, argmax);
-        return dispatch<kQ4_K, 0>(ctx->stream, p, w, w, rows, columns, row_bytes, total, xp, ysc, batch, y, nullptr);
-    }
-    if (argmax) return dispatch<kQ6_K, 1>(ctx->stream, p, w, w, rows, columns, row_bytes, total, xp, ysc, batch, y, argmax);
-    return dispatch<kQ6_K, 0>(ctx->stream, p, w, w, rows, columns, row_bytes, total, xp, ysc, batch, y, nullptr);
+    hipLaunchKernelGGL(argmax_partials_kernel, dim3(1), dim3(256), 0, ctx->stream, a.partials, count,
+                       argmax, index_out);
+    return hipGetLastError();
 }
 
 hipError_t launch_qmv_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns,
                               const void *gate, const void *up, uint32_t batch, const float *x,
                               float *act, int normalize, float epsilon) {
-    _Float16 *xp;
-    float *ysc;
-    hipError_t e = prepare(ctx, type, columns, batch, x, normalize, epsilon, &xp, &ysc);
+    Args a = make_args(type, rows, columns, gate, up, batch, x, normalize, epsilon, act);
+    const Plan p = choose_plan(type, rows, columns / 256, batch, 2);
+    hipError_t e = prepare(ctx, type, columns, batch, x, normalize, epsilon, (_Float16 **)&a.xp,
+                           (float **)&a.ysc);
     if (e != hipSuccess) return e;
-    const uint32_t blocks = columns / 256;
-    const uint32_t row_bytes = blocks * (type == kQ4_K ? 144u : 210u);
-    const uint32_t total = row_bytes * rows;
-    const Plan p = choose_plan(rows, blocks, batch, 2);
-    if (type == kQ4_K)
-        return dispatch<kQ4_K, 2>(ctx->stream, p, gate, up, rows, columns, row_bytes, total, xp, ysc, batch, act, nullptr);
-    return dispatch<kQ6_K, 2>(ctx->stream, p, gate, up, rows, columns, row_bytes, total, xp, ysc, batch, act, nullptr);
+    return type == kQ4_K ? dispatch<kQ4_K, 2>(ctx, p, a, nullptr) : dispatch<kQ6_K, 2>(ctx, p, a, nullptr);
 }
 
 }  // namespace dm

@@ -108,6 +108,7 @@ __global__ void __launch_bounds__(256) gemv_exact_kernel(
 __global__ void argmax_init_kernel(ArgmaxState *state) {
     state->key = 0;
     state->non_finite = 0;
+    state->done = 0;
 }
 
 __global__ void __launch_bounds__(256) argmax_kernel(const float *__restrict__ v, size_t n,
@@ -293,7 +294,31 @@ __global__ void silu_mul_glm_pairs_kernel(const float *__restrict__ gate_up, uin
     }
 }
 
+// Plain streaming copy: 16-byte vectors where both ends allow, bytes else.
+__global__ void __launch_bounds__(256) copy_bytes_kernel(uint8_t *__restrict__ dst,
+                                                         const uint8_t *__restrict__ src, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if ((((uintptr_t)dst | (uintptr_t)src) & 15u) == 0) {
+        const size_t vec = n / 16;
+        for (size_t i = tid; i < vec; i += stride)
+            ((u32x4 *)dst)[i] = ((const u32x4 *)src)[i];
+        for (size_t i = vec * 16 + tid; i < n; i += stride) dst[i] = src[i];
+    } else {
+        for (size_t i = tid; i < n; i += stride) dst[i] = src[i];
+    }
+}
+
 // ---- host-side launchers -------------------------------------------------
+
+hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t n) {
+    size_t blocks = (n / 16 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks == 0) blocks = 1;
+    hipLaunchKernelGGL(copy_bytes_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, (uint8_t *)dst,
+                       (const uint8_t *)src, n);
+    return hipGetLastError();
+}
 
 hipError_t launch_dequantize(hipStream_t s, uint32_t type, const uint8_t *enc, uint32_t be,
                              uint32_t bb, size_t elements, float *out) {

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <vector>
+
 #include "../../include/dmhip.h"
 #include "dm_kernels.h"
 
@@ -52,15 +54,20 @@ struct dmhip_ctx {
     char name[256] = {0};
     int compute_units = 0;
     dm::Scratch in, out, enc, aux;          // host-slice staging
+    dm::Scratch partials;                    // per-wave argmax candidates
     dm::ArgmaxState *argmax_state = nullptr;  // device
     uint32_t *argmax_index = nullptr;         // device
     uint32_t *flags = nullptr;                // device: [0] non-finite
     bool argmax_pending = false;
     uint32_t *argmax_user_index = nullptr;
+    // Measurement: start/stop event pairs around the dominant kernels.
+    bool kernel_timing = false;
+    std::vector<hipEvent_t> timing_events;
 };
 
 struct dmhip_buf {
     dmhip_ctx *ctx = nullptr;
+    int device = 0;
     void *dev = nullptr;
     size_t len = 0;
 };
@@ -73,4 +80,12 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
 int enqueue_matvec_argmax(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
                           const void *w, const float *x, float *y, uint32_t *index_device);
 int set_device(dmhip_ctx *ctx);
+
+// While ctx->kernel_timing is set, records an event on the compute stream
+// when constructed (before a launch) and another when destroyed (after it).
+struct KernelTimer {
+    dmhip_ctx *ctx;
+    explicit KernelTimer(dmhip_ctx *c);
+    ~KernelTimer();
+};
 }  // namespace dm

@@ -101,6 +101,26 @@ int set_device(dmhip_ctx *ctx) {
     return DMHIP_OK;
 }
 
+static void timing_mark(dmhip_ctx *ctx) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return;
+    if (hipEventRecord(e, ctx->stream) != hipSuccess) {
+        (void)hipEventDestroy(e);
+        return;
+    }
+    ctx->timing_events.push_back(e);
+}
+
+KernelTimer::KernelTimer(dmhip_ctx *c) : ctx(c) {
+    if (ctx->kernel_timing) timing_mark(ctx);
+}
+
+KernelTimer::~KernelTimer() {
+    // Pairs stay aligned: a failed start leaves an odd count, which the
+    // reader drops.
+    if (ctx->kernel_timing && (ctx->timing_events.size() & 1)) timing_mark(ctx);
+}
+
 static bool matvec_kind_supported(uint32_t type) {
     // The pipelines of MetalContext::prepare_matvec (src/metal.rs:1534-1542).
     return type == 0 || type == 1 || type == 6 || type == 8 || type == 12 || type == 14;
@@ -223,6 +243,7 @@ void dmhip_context_free(dmhip_ctx *ctx) {
     ctx->out.release();
     ctx->enc.release();
     ctx->aux.release();
+    ctx->partials.release();
     if (ctx->argmax_state) (void)hipFree(ctx->argmax_state);
     if (ctx->argmax_index) (void)hipFree(ctx->argmax_index);
     if (ctx->flags) (void)hipFree(ctx->flags);
@@ -254,6 +275,7 @@ void *dmhip_stream(dmhip_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr;
 static int new_buffer(dmhip_ctx *ctx, size_t length, dmhip_buf **out) {
     dmhip_buf *b = new dmhip_buf();
     b->ctx = ctx;
+    b->device = ctx->device;
     b->len = length;
     // 256 spare bytes: vector loads of the last row may read a few bytes past
     // its end (they are discarded); the spare keeps them inside the allocation.
@@ -306,10 +328,9 @@ int dmhip_new_owned_buffer(dmhip_ctx *ctx, size_t length, dmhip_buf **out) {
 
 void dmhip_buffer_free(dmhip_buf *b) {
     if (!b) return;
-    if (b->ctx) {
-        (void)hipSetDevice(b->ctx->device);
-        (void)hipStreamSynchronize(b->ctx->stream);
-    }
+    // The context may already be gone; only the device id is needed.  hipFree
+    // waits for work still using the allocation.
+    (void)hipSetDevice(b->device);
     if (b->dev) (void)hipFree(b->dev);
     delete b;
 }
@@ -703,6 +724,45 @@ int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                (uint32_t)k, (uint32_t)batch, x, logits, ids, probabilities,
                                ctx->flags));
+    return DMHIP_OK;
+}
+
+int dmhip_kernel_timing_enable(dmhip_ctx *ctx, int enable) {
+    DM_REQUIRE(ctx);
+    ctx->kernel_timing = enable != 0;
+    return DMHIP_OK;
+}
+
+int dmhip_kernel_timing_read(dmhip_ctx *ctx, double *total_ms, uint64_t *launches) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(total_ms);
+    DM_REQUIRE(launches);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    double total = 0.0;
+    uint64_t count = 0;
+    std::vector<hipEvent_t> &ev = ctx->timing_events;
+    for (size_t i = 0; i + 1 < ev.size(); i += 2) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess) {
+            total += ms;
+            count += 1;
+        }
+    }
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+    ev.clear();
+    *total_ms = total;
+    *launches = count;
+    return DMHIP_OK;
+}
+
+int dmhip_copy_device(dmhip_ctx *ctx, void *dst, const void *src, size_t n) {
+    DM_REQUIRE(ctx);
+    if (n == 0) return DMHIP_OK;
+    DM_REQUIRE(dst);
+    DM_REQUIRE(src);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_copy_bytes(ctx->stream, dst, src, n));
     return DMHIP_OK;
 }
 

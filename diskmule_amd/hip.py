@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 from dataclasses import dataclass
 from typing import Callable, Sequence
 
@@ -40,6 +41,7 @@ EXPORTED_SYMBOLS = [
     "dmhip_silu_mul_device", "dmhip_ffn_workspace_bytes", "dmhip_ffn_device",
     "dmhip_router_top_k_device", "dmhip_gemm_workspace_bytes", "dmhip_gemm_device",
     "dmhip_event_record", "dmhip_event_elapsed_ms", "dmhip_event_free",
+    "dmhip_kernel_timing_enable", "dmhip_kernel_timing_read", "dmhip_copy_device",
     "dmhip_expert_cache_new", "dmhip_expert_cache_free", "dmhip_expert_cache_stats_get",
     "dmhip_expert_cache_slots_per_layer", "dmhip_expert_acquire", "dmhip_expert_release",
     "dmhip_moe_layer",
@@ -128,6 +130,10 @@ def load_library() -> ctypes.CDLL:
         "dmhip_event_record": ([_vp, ctypes.POINTER(_vp)], ctypes.c_int),
         "dmhip_event_elapsed_ms": ([_vp, _vp, ctypes.POINTER(ctypes.c_float)], ctypes.c_int),
         "dmhip_event_free": ([_vp], None),
+        "dmhip_kernel_timing_enable": ([_vp, ctypes.c_int], ctypes.c_int),
+        "dmhip_kernel_timing_read": ([_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint64)],
+                                     ctypes.c_int),
+        "dmhip_copy_device": ([_vp, _vp, _vp, _sz], ctypes.c_int),
         "dmhip_expert_cache_new": ([_vp, _vp, _sz, ctypes.POINTER(_Layout), _sz, _sz, ctypes.POINTER(_vp)],
                                    ctypes.c_int),
         "dmhip_expert_cache_free": ([_vp], None),
@@ -165,6 +171,7 @@ class _Buffer:
     def __init__(self, ctx: "HipContext", handle: int):
         self._ctx = ctx
         self._h = _vp(handle)
+        ctx._children.add(self)
 
     @property
     def handle(self):
@@ -220,6 +227,8 @@ class HipContext:
 
     def __init__(self, device: int = 0):
         lib = load_library()
+        # Buffers and caches made from this context; close() frees them first.
+        self._children = weakref.WeakSet()
         h = _vp()
         _check(lib.dmhip_context_new(device, ctypes.byref(h)))
         self._h = h
@@ -234,6 +243,8 @@ class HipContext:
 
     def close(self) -> None:
         if getattr(self, "_h", None):
+            for child in list(self._children):
+                child.free()
             load_library().dmhip_context_free(self._h)
             self._h = None
 
@@ -380,6 +391,18 @@ class HipContext:
         _check(load_library().dmhip_event_elapsed_ms(_vp(start), _vp(stop), ctypes.byref(ms)))
         return ms.value
 
+    def kernel_timing_enable(self, enable: bool) -> None:
+        _check(load_library().dmhip_kernel_timing_enable(self._h, int(enable)))
+
+    def kernel_timing_read(self) -> tuple[float, int]:
+        ms = ctypes.c_double()
+        n = ctypes.c_uint64()
+        _check(load_library().dmhip_kernel_timing_read(self._h, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
+    def copy_device(self, dst_ptr: int, src_ptr: int, nbytes: int) -> None:
+        _check(load_library().dmhip_copy_device(self._h, dst_ptr, src_ptr, nbytes))
+
     @staticmethod
     def event_free(ev: int) -> None:
         load_library().dmhip_event_free(_vp(ev))
@@ -453,6 +476,7 @@ class ExpertCache:
         _check(load_library().dmhip_expert_cache_new(ctx.handle, addr, n, lay, len(layouts), slots_per_layer,
                                                      ctypes.byref(h)))
         self._h = h
+        ctx._children.add(self)
 
     @property
     def handle(self):

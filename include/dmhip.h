@@ -227,6 +227,18 @@ int dmhip_event_record(dmhip_ctx *ctx, void **event);
 int dmhip_event_elapsed_ms(void *start, void *stop, float *ms);
 void dmhip_event_free(void *event);
 
+/* Measurement hooks (no counterpart in the reference; used by bench.py).
+   While enabled, the library records HIP events on the compute stream
+   around every launch of its dominant kernels (the quantized matvec and GEMM
+   kernels).  _read waits for the stream, returns the summed duration in ms
+   and the number of timed launches since the previous read, and resets. */
+int dmhip_kernel_timing_enable(dmhip_ctx *ctx, int enable);
+int dmhip_kernel_timing_read(dmhip_ctx *ctx, double *total_ms, uint64_t *launches);
+
+/* Stream-ordered device-to-device copy by a plain streaming kernel (also the
+   calibration kernel for HBM byte counters). */
+int dmhip_copy_device(dmhip_ctx *ctx, void *dst, const void *src, size_t n);
+
 /* ---------------------------------------------------------------------- */
 /* Routed-expert residency (src/expert.rs)                                 */
 /* ---------------------------------------------------------------------- */

@@ -384,3 +384,24 @@ def test_prefill_gemm_matches_oracle(ctx, n):
         e, _ = assert_close(got[r], want[r], f"C5 token {r}")
         worst = max(worst, e)
     print(f"  worst rel_err={worst:.2e}", flush=True)
+
+
+def test_objects_outliving_their_context_exit_cleanly():
+    """Regression: device buffers and caches freed after their context was
+    closed (the order Python's collector may pick at exit)."""
+    import subprocess
+    import sys
+    code = (
+        "import numpy as np\n"
+        "from diskmule_amd import HipContext, ExpertCache, ExpertLayerLayout\n"
+        "ctx = HipContext(0)\n"
+        "a = ctx.device_array(np.arange(1000, dtype=np.float32))\n"
+        "m = ctx.map_read_only(np.zeros(4096, np.uint8))\n"
+        "c = ExpertCache(ctx, np.arange(16, dtype=np.uint8), [ExpertLayerLayout(2, 0, 4, 8, 4)], 1)\n"
+        "ctx.close()\n"
+        "del a, m, c\n"
+        "print('clean')\n"
+    )
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120,
+                       cwd=__import__("os").path.dirname(__import__("os").path.dirname(__file__)))
+    assert r.returncode == 0 and "clean" in r.stdout, (r.returncode, r.stderr[-2000:])

@@ -244,6 +244,20 @@ def bench_c5(ctx, synth, steps, warmup):
     return out
 
 
+def bench_copy(ctx, synth, steps, warmup):
+    """A plain device copy of known size (512 MiB read + 512 MiB written):
+    the calibration kernel for the FETCH_SIZE/WRITE_SIZE counter runs."""
+    n = 512 << 20
+    src, dst = ctx.new_owned_buffer(n), ctx.new_owned_buffer(n)
+    for _ in range(warmup):
+        ctx.copy_device(dst.device_ptr, src.device_ptr, n)
+    with Timed(ctx) as t:
+        for _ in range(steps):
+            ctx.copy_device(dst.device_ptr, src.device_ptr, n)
+    ms = t.wall_ms / steps
+    return {"bytes_read": n, "bytes_written": n, "ms": ms, "gbps": 2 * n / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline(w, x, seconds):
     """The CPU port of src/cpu.rs:345-399 + :275-293 on the C2 workload."""
     from oracle import capi
@@ -278,7 +292,9 @@ def main() -> int:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--only", default=None, help="c1..c5: run one GPU configuration, print its record")
+    p.add_argument("--only", default=None,
+                   help="c1..c5: run one GPU configuration, print its record; copy: the counter "
+                        "calibration copy")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     args = p.parse_args()
     if args.gpus != 1:
@@ -290,7 +306,8 @@ def main() -> int:
     ctx = HipContext(0)
     log("device:", ctx.device_name())
     if args.only:
-        fn = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.only]
+        fn = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
+              "copy": bench_copy}[args.only]
         res = fn(ctx, synth, args.steps, args.warmup)
         print(json.dumps(res[0] if isinstance(res, tuple) else res))
         return 0

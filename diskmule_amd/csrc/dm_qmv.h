@@ -5,6 +5,25 @@
 
 namespace dm {
 
+// Per-wave argmax candidate written by the fused epilogues; a one-workgroup
+// pass reduces them.
+struct ArgmaxPartial {
+    unsigned long long key;
+    uint32_t non_finite;
+    uint32_t pad;
+};
+
+// True when the int8-MFMA matvec (decode batches of 1-2 tokens, Q4_K/Q6_K)
+// takes this shape; the caller has already checked qmv_supported.
+bool qmv8_supported(uint32_t type, size_t rows, size_t columns, size_t batch);
+
+// y[b][r] = W[r] . x[b] with the int8-MFMA kernels.  With `partials` the
+// epilogue also writes one ArgmaxPartial per 16-row tile (batch 1) and
+// *count receives the number written.
+hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
+                       uint32_t batch, const float *x, float *y, ArgmaxPartial *partials,
+                       uint32_t *count);
+
 // True when the MFMA matvec takes this shape: Q4_K or Q6_K rows of whole
 // 256-value blocks, a weight base address aligned to 4 bytes (16 for Q4_K),
 // and fewer than 4 GiB of weights (one buffer descriptor).

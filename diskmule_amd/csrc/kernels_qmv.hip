@@ -144,21 +144,38 @@ __device__ __forceinline__ void build_fragment(const float *xt, uint32_t blk, ui
 // and (Q4_K) the 32-column sums.  yscale[t] = 2^e (times the RMSNorm factor
 // when `normalize`).  Grid: (blocks of fragments, tokens).
 // ---------------------------------------------------------------------------
-template <uint32_t TYPE>
+// With STAGED the token row is copied into LDS (columns <= kPrepareLdsColumns)
+// and the fragments are built from there; the row is read from global memory
+// once, sixteen loads in flight per thread.
+constexpr uint32_t kPrepareLdsColumns = 16384;
+
+template <uint32_t TYPE, bool STAGED>
 __global__ void __launch_bounds__(256) qmv_prepare_kernel(const float *__restrict__ x,
                                                           uint32_t columns, uint32_t batch,
                                                           int normalize, float epsilon,
                                                           _Float16 *__restrict__ xp,
                                                           float *__restrict__ yscale) {
     constexpr uint32_t SPB = Steps<TYPE>::value;
+    constexpr uint32_t U = 16;
+    extern __shared__ float s_row[];
     __shared__ float red_max[4], red_ss[4];
     const uint32_t token = blockIdx.y;
     const float *xt = x + (size_t)token * columns;
     float mx = 0.0f, ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < columns; i += blockDim.x) {
-        float v = xt[i];
-        mx = fmaxf(mx, fabsf(v));
-        ss = __builtin_fmaf(v, v, ss);
+    for (uint32_t i0 = 0; i0 < columns; i0 += 256 * U) {
+        float v[U];
+#pragma unroll
+        for (uint32_t j = 0; j < U; j++) {
+            const uint32_t i = i0 + 256 * j + threadIdx.x;
+            v[j] = i < columns ? xt[i] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < U; j++) {
+            const uint32_t i = i0 + 256 * j + threadIdx.x;
+            if (STAGED && i < columns) s_row[i] = v[j];
+            mx = fmaxf(mx, fabsf(v[j]));
+            ss = __builtin_fmaf(v[j], v[j], ss);
+        }
     }
     mx = wave_max(mx);
     ss = wave_sum(ss);
@@ -185,7 +202,7 @@ __global__ void __launch_bounds__(256) qmv_prepare_kernel(const float *__restric
          f += gridDim.x * blockDim.x) {
         const uint32_t kg = f & 3u, t = (f >> 2) % SPB, blk = (f >> 2) / SPB;
         half8 hi, lo;
-        build_fragment<TYPE>(xt, blk, t, kg, down, hi, lo);
+        build_fragment<TYPE>(STAGED ? s_row : xt, blk, t, kg, down, hi, lo);
         dst[(size_t)f * m2 + 2 * token] = hi;
         dst[(size_t)f * m2 + 2 * token + 1] = lo;
     }
@@ -384,13 +401,6 @@ __device__ __forceinline__ void block_dot(const Raw<kQ6_K> &raw, const half8 (&a
     }
 }
 
-// Per-wave argmax candidate of the fused epilogue.
-struct ArgmaxPartial {
-    unsigned long long key;
-    uint32_t non_finite;
-    uint32_t pad;
-};
-
 // ---------------------------------------------------------------------------
 // Main kernel.  A workgroup has 4 waves; S waves split one group of R row
 // tiles along K, so a workgroup covers (4/S)*R tiles of 16 rows.
@@ -579,17 +589,29 @@ __global__ void __launch_bounds__(256) qmv_kernel(
 
 // Reduces the per-wave candidates: the largest key wins (value, then lowest
 // row); any non-finite row marks the result.
-__global__ void __launch_bounds__(256) argmax_partials_kernel(const ArgmaxPartial *__restrict__ partials,
-                                                              uint32_t count, ArgmaxState *state,
-                                                              uint32_t *index_out) {
-    __shared__ unsigned long long keys[4];
-    __shared__ uint32_t flags[4];
+// 1024 threads with eight loads in flight each: a C2-sized candidate list
+// (9496 entries) takes two rounds of memory latency.
+constexpr uint32_t kArgmaxThreads = 1024;
+
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_partials_kernel(
+    const ArgmaxPartial *__restrict__ partials, uint32_t count, ArgmaxState *state, uint32_t *index_out) {
+    constexpr uint32_t U = 8, WAVES = kArgmaxThreads / 64;
+    __shared__ unsigned long long keys[WAVES];
+    __shared__ uint32_t flags[WAVES];
     uint64_t best = 0;
     uint32_t bad = 0;
-    for (uint32_t i = threadIdx.x; i < count; i += 256) {
-        const ArgmaxPartial p = partials[i];
-        best = p.key > best ? p.key : best;
-        bad |= p.non_finite;
+    for (uint32_t i0 = 0; i0 < count; i0 += kArgmaxThreads * U) {
+        ArgmaxPartial p[U];
+#pragma unroll
+        for (uint32_t j = 0; j < U; j++) {
+            const uint32_t i = i0 + kArgmaxThreads * j + threadIdx.x;
+            p[j] = i < count ? partials[i] : ArgmaxPartial{0, 0, 0};
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < U; j++) {
+            best = p[j].key > best ? p[j].key : best;
+            bad |= p[j].non_finite;
+        }
     }
     best = wave_max_u64(best);
     bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
@@ -601,7 +623,7 @@ __global__ void __launch_bounds__(256) argmax_partials_kernel(const ArgmaxPartia
     if (threadIdx.x == 0) {
         uint64_t b = keys[0];
         uint32_t f = flags[0];
-        for (int i = 1; i < 4; i++) {
+        for (uint32_t i = 1; i < WAVES; i++) {
             b = keys[i] > b ? keys[i] : b;
             f |= flags[i];
         }
@@ -713,12 +735,22 @@ hipError_t prepare(dmhip_ctx *ctx, uint32_t type, uint32_t columns, uint32_t bat
     float *ysc = (float *)((char *)ctx->aux.ptr + ((xp_bytes + 255) & ~(size_t)255));
     uint32_t gx = (uint32_t)((frags + 255) / 256);
     if (gx > 64) gx = 64;
-    if (type == kQ4_K)
-        hipLaunchKernelGGL(qmv_prepare_kernel<kQ4_K>, dim3(gx, batch), dim3(256), 0, ctx->stream, x,
+    const dim3 grid(gx, batch);
+    if (columns <= kPrepareLdsColumns) {
+        const size_t lds = (size_t)columns * sizeof(float);
+        if (type == kQ4_K)
+            hipLaunchKernelGGL((qmv_prepare_kernel<kQ4_K, true>), grid, dim3(256), lds, ctx->stream, x,
+                               columns, batch, normalize, eps, xp, ysc);
+        else
+            hipLaunchKernelGGL((qmv_prepare_kernel<kQ6_K, true>), grid, dim3(256), lds, ctx->stream, x,
+                               columns, batch, normalize, eps, xp, ysc);
+    } else if (type == kQ4_K) {
+        hipLaunchKernelGGL((qmv_prepare_kernel<kQ4_K, false>), grid, dim3(256), 0, ctx->stream, x,
                            columns, batch, normalize, eps, xp, ysc);
-    else
-        hipLaunchKernelGGL(qmv_prepare_kernel<kQ6_K>, dim3(gx, batch), dim3(256), 0, ctx->stream, x,
+    } else {
+        hipLaunchKernelGGL((qmv_prepare_kernel<kQ6_K, false>), grid, dim3(256), 0, ctx->stream, x,
                            columns, batch, normalize, eps, xp, ysc);
+    }
     *xp_out = xp;
     *ysc_out = ysc;
     return hipGetLastError();
@@ -750,10 +782,14 @@ Args make_args(uint32_t type, uint32_t rows, uint32_t columns, const void *w, co
 hipError_t launch_qmv(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
                       uint32_t batch, const float *x, float *y, ArgmaxState *argmax,
                       uint32_t *index_out) {
+    const bool int8_path = qmv8_supported(type, rows, columns, batch);
+    if (!argmax && int8_path) return launch_qmv8(ctx, type, rows, columns, w, batch, x, y, nullptr, nullptr);
     Args a = make_args(type, rows, columns, w, w, batch, x, 0, 0.0f, y);
     const Plan p = choose_plan(type, rows, columns / 256, batch, argmax ? 1 : 0);
-    hipError_t pe = prepare(ctx, type, columns, batch, x, 0, 0.0f, (_Float16 **)&a.xp, (float **)&a.ysc);
-    if (pe != hipSuccess) return pe;
+    if (!int8_path) {
+        hipError_t pe = prepare(ctx, type, columns, batch, x, 0, 0.0f, (_Float16 **)&a.xp, (float **)&a.ysc);
+        if (pe != hipSuccess) return pe;
+    }
     if (!argmax)
         return type == kQ4_K ? dispatch<kQ4_K, 0>(ctx, p, a, nullptr) : dispatch<kQ6_K, 0>(ctx, p, a, nullptr);
     // One candidate per epilogue wave (at most one per 16-row tile), then a
@@ -762,9 +798,13 @@ hipError_t launch_qmv(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t col
     if (ctx->partials.ensure(candidates * sizeof(ArgmaxPartial)) != DMHIP_OK) return hipErrorOutOfMemory;
     a.partials = (ArgmaxPartial *)ctx->partials.ptr;
     uint32_t count = 0;
-    hipError_t e = type == kQ4_K ? dispatch<kQ4_K, 1>(ctx, p, a, &count) : dispatch<kQ6_K, 1>(ctx, p, a, &count);
+    hipError_t e;
+    if (int8_path)
+        e = launch_qmv8(ctx, type, rows, columns, w, batch, x, y, a.partials, &count);
+    else
+        e = type == kQ4_K ? dispatch<kQ4_K, 1>(ctx, p, a, &count) : dispatch<kQ6_K, 1>(ctx, p, a, &count);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(argmax_partials_kernel, dim3(1), dim3(256), 0, ctx->stream, a.partials, count,
+    hipLaunchKernelGGL(argmax_partials_kernel, dim3(1), dim3(kArgmaxThreads), 0, ctx->stream, a.partials, count,
                        argmax, index_out);
     return hipGetLastError();
 }

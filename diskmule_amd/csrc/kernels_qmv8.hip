@@ -23,8 +23,10 @@
 //    exact accumulator seed -32 * sum(X) of the group; Q4_K's
 //    "- dmin * m * x" term uses the sub-block sums of X.
 //
-// The activation records (A fragments plus seeds or sums) are written once
-// per call by qmv8_prepare_kernel and staged in LDS by every workgroup.
+// Every workgroup quantizes the tokens into activation records (A fragments
+// plus seeds or sums) in its own LDS, then streams weight tiles.  Weight bytes
+// go through a per-wave LDS staging area so that the global loads are fully
+// coalesced.
 #include "dm_device.h"
 #include "dm_qmv.h"
 
@@ -69,103 +71,115 @@ __device__ __forceinline__ float combine8(i32x4 c) {
 
 }  // namespace
 
-// ---------------------------------------------------------------------------
-// Activation records.  Grid (workgroups per token, tokens); each workgroup
-// reduces max|x| over the whole token row, then quantizes four blocks per
-// pass: thread l of a 64-thread slice handles step t = l >> 4, lane group
-// g = (l >> 2) & 3 and columns 4q .. 4q+3 (q = l & 3) of that group.
-// yscale[token] = 2^e, or NaN when the row holds a non-finite value.
-// ---------------------------------------------------------------------------
-template <uint32_t TYPE>
-__global__ void __launch_bounds__(256) qmv8_prepare_kernel(const float *__restrict__ x, uint32_t columns,
-                                                           uint32_t batch, uint8_t *__restrict__ xq,
-                                                           float *__restrict__ yscale) {
-    constexpr uint32_t REC = Rec8<TYPE>::bytes;
-    constexpr uint32_t U = 16;
-    __shared__ float red_max[4];
-    __shared__ uint32_t red_bad[4];
-    const uint32_t token = blockIdx.y;
-    const float *xt = x + (size_t)token * columns;
-    float mx = 0.0f;
-    uint32_t bad = 0;
-    for (uint32_t i0 = 0; i0 < columns; i0 += 256 * U) {
-        float v[U];
+namespace {
+
+// Activation records of TOK tokens written by the workgroup into LDS at
+// `rec` (record of block b, token t at (b * TOK + t) * REC).  Phase 1: max|x|
+// and a non-finite flag per token (coalesced loads, eight in flight per
+// thread).  Phase 2: wave k quantizes blocks k, k + WAVES, ...; lane l
+// handles step t = l >> 4, lane group g = (l >> 2) & 3 and columns 4q..4q+3
+// (q = l & 3) of that group.  tscale[token] = 2^e, or NaN when the row holds
+// a non-finite value (every output of that token is then NaN).
+template <uint32_t TYPE, int TOK, uint32_t WAVES>
+__device__ __forceinline__ void build_records8(const float *__restrict__ x, uint32_t columns, uint8_t *rec,
+                                               float *red_max, uint32_t *red_bad, float *tscale) {
+    constexpr uint32_t NT = 64 * WAVES, REC = Rec8<TYPE>::bytes, U = 8;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    float mx[TOK];
+    uint32_t bad[TOK];
 #pragma unroll
-        for (uint32_t j = 0; j < U; j++) {
-            const uint32_t i = i0 + 256 * j + threadIdx.x;
-            v[j] = i < columns ? xt[i] : 0.0f;
-        }
+    for (int tok = 0; tok < TOK; tok++) {
+        mx[tok] = 0.0f;
+        bad[tok] = 0;
+    }
+    for (uint32_t i0 = 0; i0 < columns; i0 += NT * U) {
 #pragma unroll
-        for (uint32_t j = 0; j < U; j++) {
-            bad |= !__builtin_isfinite(v[j]);
-            mx = fmaxf(mx, fabsf(v[j]));
+        for (int tok = 0; tok < TOK; tok++) {
+            float v[U];
+#pragma unroll
+            for (uint32_t j = 0; j < U; j++) {
+                const uint32_t i = i0 + NT * j + tid;
+                v[j] = i < columns ? x[(size_t)tok * columns + i] : 0.0f;
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < U; j++) {
+                bad[tok] |= !__builtin_isfinite(v[j]);
+                mx[tok] = fmaxf(mx[tok], fabsf(v[j]));
+            }
         }
     }
-    mx = wave_max(mx);
-    bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
-    if ((threadIdx.x & 63u) == 0) {
-        red_max[threadIdx.x >> 6] = mx;
-        red_bad[threadIdx.x >> 6] = bad;
+#pragma unroll
+    for (int tok = 0; tok < TOK; tok++) {
+        const float m = wave_max(mx[tok]);
+        const uint32_t f = __builtin_amdgcn_ballot_w64(bad[tok] != 0) != 0;
+        if (lane == 0) {
+            red_max[tok * WAVES + wave] = m;
+            red_bad[tok * WAVES + wave] = f;
+        }
     }
     __syncthreads();
-    mx = fmaxf(fmaxf(red_max[0], red_max[1]), fmaxf(red_max[2], red_max[3]));
-    bad = red_bad[0] | red_bad[1] | red_bad[2] | red_bad[3];
-    int e = 0;
-    if (!bad && mx > 0.0f) {
-        int ex;
-        (void)frexpf(mx, &ex);  // mx < 2^ex
-        e = ex - 22;
-        if (e < -126) e = -126;
-        if (e > 127) e = 127;
-    }
-    const float down = ldexpf(1.0f, -e);
-    if (blockIdx.x == 0 && threadIdx.x == 0)
-        yscale[token] = bad ? __builtin_nanf("") : ldexpf(1.0f, e);
-
     const uint32_t blocks = columns / 256;
-    const uint32_t l = threadIdx.x & 63u, t = l >> 4, g = (l >> 2) & 3u, q = l & 3u;
-    for (uint32_t b = blockIdx.x * 4 + (threadIdx.x >> 6); b < blocks; b += gridDim.x * 4) {
-        const float *xb = xt + (size_t)b * 256 + column8<TYPE>(t, g, 4 * q);
-        uint32_t term[3] = {0, 0, 0};
-        int sum[3] = {0, 0, 0}, sx = 0;
+    const uint32_t t = lane >> 4, g = (lane >> 2) & 3u, q = lane & 3u;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int X = bad ? 0 : (int)rintf(xb[j] * down);  // |X| <= 2^22
-            const int lo = (int)(int8_t)(X & 0xff);
-            const int x1 = (X - lo) >> 8;
-            const int mid = (int)(int8_t)(x1 & 0xff);
-            const int hi = (x1 - mid) >> 8;
-            term[0] |= (uint32_t)(hi & 0xff) << (8 * j);
-            term[1] |= (uint32_t)(mid & 0xff) << (8 * j);
-            term[2] |= (uint32_t)(lo & 0xff) << (8 * j);
-            sum[0] += hi;
-            sum[1] += mid;
-            sum[2] += lo;
-            sx += X;
+    for (int tok = 0; tok < TOK; tok++) {
+        float m = 0.0f;
+        uint32_t f = 0;
+        for (uint32_t k = 0; k < WAVES; k++) {
+            m = fmaxf(m, red_max[tok * WAVES + k]);
+            f |= red_bad[tok * WAVES + k];
         }
-        uint8_t *rec = xq + ((size_t)b * batch + token) * REC;
+        int e = 0;
+        if (!f && m > 0.0f) {
+            int ex;
+            (void)frexpf(m, &ex);  // m < 2^ex
+            e = ex - 22;
+            if (e < -126) e = -126;
+            if (e > 127) e = 127;
+        }
+        const float down = ldexpf(1.0f, -e);
+        if (tid == 0) tscale[tok] = f ? __builtin_nanf("") : ldexpf(1.0f, e);
+        for (uint32_t b = wave; b < blocks; b += WAVES) {
+            const float *xb = x + (size_t)tok * columns + (size_t)b * 256 + column8<TYPE>(t, g, 4 * q);
+            uint32_t term[3] = {0, 0, 0};
+            int sum[3] = {0, 0, 0}, sx = 0;
 #pragma unroll
-        for (int k = 0; k < 3; k++) *(uint32_t *)(rec + t * kStep8 + (g * 3 + k) * 16 + 4 * q) = term[k];
-        if (TYPE == kQ6_K) {
-            // group (t, g) = the four adjacent threads q = 0..3
+            for (int j = 0; j < 4; j++) {
+                const int X = f ? 0 : (int)rintf(xb[j] * down);  // |X| <= 2^22
+                const int lo = (int)(int8_t)(X & 0xff);
+                const int x1 = (X - lo) >> 8;
+                const int mid = (int)(int8_t)(x1 & 0xff);
+                const int hi = (x1 - mid) >> 8;
+                term[0] |= (uint32_t)(hi & 0xff) << (8 * j);
+                term[1] |= (uint32_t)(mid & 0xff) << (8 * j);
+                term[2] |= (uint32_t)(lo & 0xff) << (8 * j);
+                sum[0] += hi;
+                sum[1] += mid;
+                sum[2] += lo;
+                sx += X;
+            }
+            uint8_t *r = rec + ((size_t)b * TOK + tok) * REC;
 #pragma unroll
-            for (int k = 0; k < 3; k++) {
-                sum[k] += __shfl_xor(sum[k], 1, 64);
-                sum[k] += __shfl_xor(sum[k], 2, 64);
+            for (int k = 0; k < 3; k++) *(uint32_t *)(r + t * kStep8 + (g * 3 + k) * 16 + 4 * q) = term[k];
+            if (TYPE == kQ6_K) {
+                // group (t, g) = the four adjacent lanes q = 0..3
+#pragma unroll
+                for (int k = 0; k < 3; k++) {
+                    sum[k] += __shfl_xor(sum[k], 1, 64);
+                    sum[k] += __shfl_xor(sum[k], 2, 64);
+                }
+                if (q == 0) *(i32x4 *)(r + 4 * kStep8 + (t * 4 + g) * 16) = i32x4{-32 * sum[0], -32 * sum[1], -32 * sum[2], 0};
+            } else {
+                // sub-block 2g + (t >> 1) = lanes (t, g, q) and (t ^ 1, g, q)
+                sx += __shfl_xor(sx, 1, 64);
+                sx += __shfl_xor(sx, 2, 64);
+                sx += __shfl_xor(sx, 16, 64);
+                if (q == 0 && (t & 1u) == 0) *(float *)(r + 4 * kStep8 + (2 * g + (t >> 1)) * 4) = (float)sx;
             }
-            if (q == 0) {
-                const i32x4 seed = {-32 * sum[0], -32 * sum[1], -32 * sum[2], 0};
-                *(i32x4 *)(rec + 4 * kStep8 + (t * 4 + g) * 16) = seed;
-            }
-        } else {
-            // sub-block 2g + (t >> 1) = threads (t, g, q) and (t ^ 1, g, q)
-            sx += __shfl_xor(sx, 1, 64);
-            sx += __shfl_xor(sx, 2, 64);
-            sx += __shfl_xor(sx, 16, 64);
-            if (q == 0 && (t & 1u) == 0) *(float *)(rec + 4 * kStep8 + (2 * g + (t >> 1)) * 4) = (float)sx;
         }
     }
 }
+
+}  // namespace
 
 namespace {
 
@@ -180,46 +194,42 @@ template <> struct Raw8<kQ6_K> {
     uint32_t s;                // block start mod 4 (0 or 2)
 };
 
-// Staging of one 16-row tile's block in LDS.  Row r of the tile occupies
-// `chunks` 16-byte chunks: the aligned chunks of global memory that cover
-// its block (Q4_K blocks start 16-aligned; a Q6_K block starts s16 = 0..14
-// bytes into its first chunk).  Consecutive lanes load consecutive chunks of
-// a row, so each quad of lanes reads one contiguous 64-byte span; the lanes
-// then read their own pieces of their own row from LDS.
-template <uint32_t TYPE> struct Stage8;
-template <> struct Stage8<kQ4_K> { static constexpr uint32_t chunks = 9; };
-template <> struct Stage8<kQ6_K> { static constexpr uint32_t chunks = 15; };
-template <uint32_t TYPE> constexpr uint32_t stage_loads8() { return (16 * Stage8<TYPE>::chunks + 63) / 64; }
-// One wave's staging area (every lane of every load writes one chunk).
-template <uint32_t TYPE> constexpr uint32_t stage_bytes8() { return stage_loads8<TYPE>() * 64 * 16; }
+// Staging of G consecutive blocks of a 16-row tile in LDS.  Row r of the
+// tile occupies `chunks` 16-byte chunks loaded from the dword-aligned address
+// at or below its first block (Q4_K rows start 16-aligned: 9 chunks per
+// block; a Q6_K run of 210 G bytes starts 0 or 2 bytes into its first dword).
+// Consecutive lanes load consecutive chunks of a row, so each quad of lanes
+// reads one contiguous 64-byte span and each fetch of a row requests whole
+// runs of cache lines; the lanes then read their own pieces of their own row
+// from LDS.
+template <uint32_t TYPE, uint32_t G> struct Stage8 {
+    static constexpr uint32_t chunks = TYPE == kQ4_K ? 9 * G : (210 * G + 2 + 15) / 16;
+    static constexpr uint32_t items = 16 * chunks;        // chunks of one tile
+    static constexpr uint32_t loads = (items + 63) / 64;  // 16-byte loads per lane
+    static constexpr uint32_t bytes = items * 16;         // one wave's staging area
+};
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 16-byte aligned (LDS)
 
 __device__ __forceinline__ u32x4 as_u32x4(v4u v) { return __builtin_bit_cast(u32x4, v); }
 
-// Lane (n, g)'s pieces of row n's block from the staging area.  `start` is
-// the block's global byte offset (its low four bits locate it in the chunk).
-template <uint32_t TYPE>
-__device__ __forceinline__ void take8(const v4u *stage, uint32_t n, uint32_t g, uint32_t start, Raw8<TYPE> &raw);
-
-template <>
-__device__ __forceinline__ void take8<kQ4_K>(const v4u *stage, uint32_t n, uint32_t g, uint32_t,
-                                             Raw8<kQ4_K> &raw) {
-    const v4u *sr = stage + n * Stage8<kQ4_K>::chunks;
+// Lane (n, g)'s pieces of one block of row n from a staging area of CH
+// chunks per row; `off` is the block's byte offset inside the row's run.
+template <uint32_t CH>
+__device__ __forceinline__ void take8(const v4u *stage, uint32_t n, uint32_t g, uint32_t off, Raw8<kQ4_K> &raw) {
+    const v4u *sr = stage + n * CH + off / 16;  // Q4_K blocks stay 16-aligned
     raw.hdr = as_u32x4(sr[0]);
     raw.q0 = as_u32x4(sr[1 + 2 * g]);
     raw.q1 = as_u32x4(sr[2 + 2 * g]);
 }
 
-template <>
-__device__ __forceinline__ void take8<kQ6_K>(const v4u *stage, uint32_t n, uint32_t g, uint32_t start,
-                                             Raw8<kQ6_K> &raw) {
-    const uint32_t s16 = start & 15u;
+template <uint32_t CH>
+__device__ __forceinline__ void take8(const v4u *stage, uint32_t n, uint32_t g, uint32_t off, Raw8<kQ6_K> &raw) {
     // dwords of row n from the one holding the block's first byte
-    const uint32_t *sw = (const uint32_t *)(stage + n * Stage8<kQ6_K>::chunks) + (s16 >> 2);
+    const uint32_t *sw = (const uint32_t *)(stage + n * CH) + (off >> 2);
     const uint32_t h = g >> 1, c = g & 1u;
     const uint32_t o1 = 16 * h + 4 * c, o2 = o1 + 8, o3 = 32 + 8 * h + 4 * c;
-    raw.s = s16 & 3u;
+    raw.s = off & 3u;
     raw.a1 = u32x4{sw[o1], sw[o1 + 1], sw[o1 + 2], sw[o1 + 3]};
     raw.a2 = u32x4{sw[o2], sw[o2 + 1], sw[o2 + 2], sw[o2 + 3]};
     raw.a3 = u32x4{sw[o3], sw[o3 + 1], sw[o3 + 2], sw[o3 + 3]};
@@ -337,132 +347,227 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ6_K> &raw, const i32x4 *
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// Main kernel.  WAVES = max(8, S) waves per workgroup; S waves split the
-// blocks of one 16-row tile, so a workgroup covers WAVES / S tiles.
+// Main kernel.  WAVES = max(8, S) waves per workgroup.
+//  * S == 1 (tall matrices): persistent.  Workgroup b owns an even share
+//    [t0, t1) of the 16-row tiles; each wave takes the next tile from an LDS
+//    counter when it starts the last block group of its current one, so the
+//    first group of the next tile is in flight across the switch.
+//  * S > 1 (short matrices): S waves split the block groups (G consecutive
+//    blocks) of one tile and reduce through LDS; a workgroup covers WAVES / S
+//    tiles once.
 // Dynamic LDS: activation records | zeroed region | per-wave staging.
-// MODE 0: y = W x.  MODE 1 (one token): also one ArgmaxPartial per tile.
+// MODE 0: y = W x.  MODE 1 (one token): also one ArgmaxPartial per
+// workgroup in partials[blockIdx.x].
+// Register budget: 4 waves per SIMD (G <= 2) or 2 (G = 4), about what the
+// workgroup's LDS allows on a C2-sized row; a tighter budget makes the
+// compiler wait for each prefetch right after issuing it.
 // ---------------------------------------------------------------------------
-template <uint32_t TYPE, int S, int MODE, int TOK>
-__global__ void __launch_bounds__(64 * (S > 8 ? S : 8)) qmv8_kernel(
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
+__global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
+    __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2))) qmv8_kernel(
     const uint8_t *__restrict__ w, uint32_t rows, uint32_t columns, uint32_t row_bytes,
-    uint32_t total_bytes, const uint8_t *__restrict__ xq, const float *__restrict__ yscale,
-    float *__restrict__ y, ArgmaxPartial *__restrict__ partials) {
+    uint32_t total_bytes, const float *__restrict__ x, float *__restrict__ y,
+    ArgmaxPartial *__restrict__ partials) {
     constexpr uint32_t WAVES = S > 8 ? S : 8;
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
     constexpr uint32_t BB = TYPE == kQ4_K ? 144u : 210u;
-    constexpr uint32_t CH = Stage8<TYPE>::chunks, NL = stage_loads8<TYPE>();
+    using ST = Stage8<TYPE, G>;
+    constexpr uint32_t CH = ST::chunks, NL = ST::loads, ITEMS = ST::items;
     extern __shared__ i32x4 lds8[];
     __shared__ float red[S > 1 ? WAVES * 64 * TOK : 1];
+    __shared__ float red_max[TOK * WAVES];
+    __shared__ uint32_t red_bad[TOK * WAVES];
     __shared__ float tscale[TOK];
+    __shared__ uint32_t next_tile;
+    __shared__ unsigned long long wg_key[WAVES];
+    __shared__ uint32_t wg_bad[WAVES];
 
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15u, g = lane >> 4;
-    const uint32_t group = wave / S, kpart = wave % S;
-    const uint32_t tile = blockIdx.x * (WAVES / S) + group;
-    const uint32_t blocks = columns / 256;
+    const uint32_t kpart = wave % S;
+    const uint32_t blocks = columns / 256, groups = (blocks + G - 1) / G;
+    const uint32_t tiles = (rows + 15) / 16;
     const uint32_t rec_bytes = blocks * TOK * REC;
-    v4u *stage = (v4u *)((uint8_t *)lds8 + rec_bytes + kZero8) + wave * (NL * 64);
+    v4u *stage = (v4u *)((uint8_t *)lds8 + rec_bytes + kZero8) + wave * ITEMS;
 
     // Whole dwords: the last dword of the matrix may extend up to 3 bytes past
     // its end (inside the allocation's granularity); loads beyond it read 0.
     const uint32_t records = (total_bytes + 3u) & ~3u;
     const uint32_t nowhere = records + 256;  // every load from here reads 0
     const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(w, records);
-    const uint32_t row = tile * 16 + n;
-    const uint32_t row_base = row < rows ? row * row_bytes : nowhere;
 
-    // Chunk j*64 + lane of the staging area: row r, chunk c of the tile.
-    uint32_t src_row[NL], src_chunk[NL];
-#pragma unroll
-    for (uint32_t j = 0; j < NL; j++) {
-        const uint32_t item = j * 64 + lane, r = item / CH, c = item % CH;
-        const uint32_t rr = tile * 16 + r;
-        src_row[j] = (item < 16 * CH && rr < rows) ? rr * row_bytes : nowhere;
-        src_chunk[j] = 16 * c;
+    // Tile schedule.
+    uint32_t tile, t_end;
+    if constexpr (S == 1) {
+        const uint32_t t0 = (uint32_t)((uint64_t)blockIdx.x * tiles / gridDim.x);
+        t_end = (uint32_t)((uint64_t)(blockIdx.x + 1) * tiles / gridDim.x);
+        tile = t0 + wave;
+        if (threadIdx.x == 0) next_tile = t0 + WAVES;
+    } else {
+        tile = blockIdx.x * (WAVES / S) + wave / S;
+        t_end = tile + 1 < tiles ? tile + 1 : tiles;
     }
-    v4u st[NL];
-    auto fetch = [&](uint32_t blk) {
+
+    // Staging chunk j*64 + lane: row r, chunk c of the tile.
+    uint32_t src_row[NL], src_chunk[NL];
+    uint32_t next_row_base = nowhere;
+    auto setup = [&](uint32_t tl) {
 #pragma unroll
         for (uint32_t j = 0; j < NL; j++) {
-            const uint32_t off = src_row[j] == nowhere ? nowhere : ((src_row[j] + blk * BB) & ~15u) + src_chunk[j];
+            const uint32_t item = j * 64 + lane, r = item / CH, c = item % CH;
+            const uint32_t rr = tl * 16 + r;
+            src_row[j] = (item < ITEMS && rr < rows) ? rr * row_bytes : nowhere;
+            src_chunk[j] = 16 * c;
+        }
+        const uint32_t rw = tl * 16 + n;
+        next_row_base = rw < rows ? rw * row_bytes : nowhere;
+    };
+    v4u st[NL];
+    auto fetch = [&](uint32_t grp) {
+#pragma unroll
+        for (uint32_t j = 0; j < NL; j++) {
+            const uint32_t off =
+                src_row[j] == nowhere ? nowhere : ((src_row[j] + grp * G * BB) & ~3u) + src_chunk[j];
             st[j] = __builtin_bit_cast(v4u, rsrc_load16(rsrc, off));
         }
     };
 
-    // Wave kpart takes blocks kpart, kpart + S, ...: the S waves of a tile
-    // read S consecutive blocks of each row at a time.  The first block is
-    // requested before the activation records are staged.
-    const uint32_t b_begin = kpart;
-    if (b_begin < blocks) fetch(b_begin);
-
-    {
-        const i32x4 *src = (const i32x4 *)xq;
-        for (uint32_t i = threadIdx.x; i < rec_bytes / 16; i += 64 * WAVES) lds8[i] = src[i];
-        for (uint32_t i = threadIdx.x; i < kZero8 / 16; i += 64 * WAVES) lds8[rec_bytes / 16 + i] = i32x4{0, 0, 0, 0};
-        if (threadIdx.x < (uint32_t)TOK) tscale[threadIdx.x] = yscale[threadIdx.x];
-        __syncthreads();
+    // The first weights are requested before the records are built.
+    bool active = tile < t_end;
+    if (active) {
+        setup(tile);
+        if (kpart < groups) fetch(kpart);
     }
+    uint32_t row_base = next_row_base;
+
+    build_records8<TYPE, TOK, WAVES>(x, columns, (uint8_t *)lds8, red_max, red_bad, tscale);
+    for (uint32_t i = threadIdx.x; i < kZero8 / 16; i += 64 * WAVES) lds8[rec_bytes / 16 + i] = i32x4{0, 0, 0, 0};
+    __syncthreads();
+
     // A row n of the MFMA: live when it is term n % 4 (< 3) of lane group n / 4.
     const uint32_t term = n & 3u;
     const bool a_live = (n >> 2) == g && term < 3;
     const uint32_t a_base = a_live ? (g * 3 + term) * 16 : rec_bytes;
     const uint32_t a_stride = a_live ? REC : 0;
 
-    float acc[TOK];
-#pragma unroll
-    for (int tok = 0; tok < TOK; tok++) acc[tok] = 0.0f;
-
-    // The chunks of block blk go to the wave's staging area; the loads of
-    // the next block are in flight while this one is read back and computed.
+    // The chunks of a block group go to the wave's staging area; the loads of
+    // the next group are in flight while this one is read back and computed.
     // A wave only reads its own staging area, and its LDS operations run in
     // order, so no barrier is needed.
-    for (uint32_t blk = b_begin; blk < blocks; blk += S) {
+    auto put_stage = [&]() {
 #pragma unroll
-        for (uint32_t j = 0; j < NL; j++) stage[j * 64 + lane] = st[j];
-        if (blk + S < blocks) fetch(blk + S);
-        Raw8<TYPE> raw;
-        take8<TYPE>(stage, n, g, row_base == nowhere ? 0u : row_base + blk * BB, raw);
-        block_dot8<TOK>(raw, lds8, a_base + blk * TOK * a_stride, a_stride, blk * TOK * REC, g, acc);
-    }
-
-    // The four lane groups of row n hold disjoint parts of its dot.
+        for (uint32_t j = 0; j < NL; j++)
+            if (j + 1 < NL || j * 64 + lane < ITEMS) stage[j * 64 + lane] = st[j];
+    };
+    auto compute_group = [&](uint32_t grp, uint32_t rb, float (&acc)[TOK]) {
+        // the run of row n starts 0 or 2 bytes into its first dword (Q6_K)
+        const uint32_t s0 = rb == nowhere ? 0u : ((rb + grp * G * BB) & 3u);
 #pragma unroll
-    for (int tok = 0; tok < TOK; tok++) {
-        acc[tok] += __shfl_xor(acc[tok], 16, 64);
-        acc[tok] += __shfl_xor(acc[tok], 32, 64);
-    }
-    if constexpr (S > 1) {
-#pragma unroll
-        for (int tok = 0; tok < TOK; tok++) red[(wave * 64 + lane) * TOK + tok] = acc[tok];
-        __syncthreads();
-        if (kpart != 0) return;
-#pragma unroll
-        for (int tok = 0; tok < TOK; tok++) {
-            float v = 0.0f;
-            for (int p = 0; p < S; p++) v += red[((wave + p) * 64 + lane) * TOK + tok];
-            acc[tok] = v;
+        for (uint32_t b = 0; b < G; b++) {
+            const uint32_t blk = grp * G + b;
+            if (blk >= blocks) break;
+            Raw8<TYPE> raw;
+            take8<CH>(stage, n, g, s0 + b * BB, raw);
+            block_dot8<TOK>(raw, lds8, a_base + blk * TOK * a_stride, a_stride, blk * TOK * REC, g, acc);
         }
-    }
+    };
 
     uint64_t best = 0;
     uint32_t bad = 0;
-    if (g < (uint32_t)TOK && row < rows) {
-        const float v = (TOK == 1 || g == 0 ? acc[0] : acc[TOK - 1]) * tscale[g];
-        y[(size_t)g * rows + row] = v;
-        if constexpr (MODE == 1) {
-            bad = !__builtin_isfinite(v);
-            best = argmax_key(v, row);
+    auto finish_row = [&](float (&acc)[TOK], uint32_t rb, uint32_t tl) {
+        const uint32_t row = tl * 16 + n;
+        if (g < (uint32_t)TOK && rb != nowhere) {
+            const float v = (TOK == 1 || g == 0 ? acc[0] : acc[TOK - 1]) * tscale[g];
+            y[(size_t)g * rows + row] = v;
+            if constexpr (MODE == 1) {
+                bad |= !__builtin_isfinite(v);
+                const uint64_t key = argmax_key(v, row);
+                best = key > best ? key : best;
+            }
+        }
+    };
+
+    if constexpr (S == 1) {
+        while (active) {
+            float acc[TOK];
+#pragma unroll
+            for (int tok = 0; tok < TOK; tok++) acc[tok] = 0.0f;
+            uint32_t next = t_end;
+            const uint32_t rb = row_base;
+            for (uint32_t grp = 0; grp < groups; grp++) {
+                put_stage();
+                if (grp + 1 < groups) {
+                    fetch(grp + 1);
+                } else {
+                    uint32_t claimed = 0;
+                    if (lane == 0) claimed = atomicAdd(&next_tile, 1u);
+                    next = __builtin_amdgcn_readfirstlane(claimed);
+                    if (next < t_end) {
+                        setup(next);
+                        fetch(0);
+                    }
+                }
+                compute_group(grp, rb, acc);
+            }
+#pragma unroll
+            for (int tok = 0; tok < TOK; tok++) {
+                acc[tok] += __shfl_xor(acc[tok], 16, 64);
+                acc[tok] += __shfl_xor(acc[tok], 32, 64);
+            }
+            finish_row(acc, rb, tile);
+            tile = next;
+            row_base = next_row_base;
+            active = tile < t_end;
+        }
+    } else {
+        float acc[TOK];
+#pragma unroll
+        for (int tok = 0; tok < TOK; tok++) acc[tok] = 0.0f;
+        if (active) {
+            for (uint32_t grp = kpart; grp < groups; grp += S) {
+                put_stage();
+                if (grp + S < groups) fetch(grp + S);
+                compute_group(grp, row_base, acc);
+            }
+        }
+#pragma unroll
+        for (int tok = 0; tok < TOK; tok++) {
+            acc[tok] += __shfl_xor(acc[tok], 16, 64);
+            acc[tok] += __shfl_xor(acc[tok], 32, 64);
+            red[(wave * 64 + lane) * TOK + tok] = acc[tok];
+        }
+        __syncthreads();
+        if (kpart == 0 && active) {
+#pragma unroll
+            for (int tok = 0; tok < TOK; tok++) {
+                float v = 0.0f;
+                for (int p = 0; p < S; p++) v += red[((wave + p) * 64 + lane) * TOK + tok];
+                acc[tok] = v;
+            }
+            finish_row(acc, row_base, tile);
         }
     }
+
     if constexpr (MODE == 1) {
         best = wave_max_u64(best);
         bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
         if (lane == 0) {
+            wg_key[wave] = best;
+            wg_bad[wave] = bad;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t k = wg_key[0];
+            uint32_t f = wg_bad[0];
+            for (uint32_t i = 1; i < WAVES; i++) {
+                k = wg_key[i] > k ? wg_key[i] : k;
+                f |= wg_bad[i];
+            }
             ArgmaxPartial p;
-            p.key = best;
-            p.non_finite = bad;
+            p.key = k;
+            p.non_finite = f;
             p.pad = 0;
-            partials[tile] = p;
+            partials[blockIdx.x] = p;
         }
     }
 }
@@ -473,88 +578,125 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8)) qmv8_kernel(
 
 namespace {
 
-constexpr size_t kMaxLds8 = 64 * 1024;
+constexpr size_t kMaxLds8 = 160 * 1024;  // gfx950 LDS per workgroup
 
-// Dynamic LDS of one workgroup: records, zeroed region, staging per wave.
-size_t lds8_bytes(uint32_t type, uint32_t blocks, uint32_t batch, uint32_t waves) {
-    const size_t rec = type == kQ4_K ? Rec8<kQ4_K>::bytes : Rec8<kQ6_K>::bytes;
-    const size_t stage = type == kQ4_K ? stage_bytes8<kQ4_K>() : stage_bytes8<kQ6_K>();
-    return (size_t)blocks * batch * rec + kZero8 + (size_t)waves * stage;
+size_t stage_bytes8(uint32_t type, uint32_t g) {
+    if (type == kQ4_K) return g == 1 ? Stage8<kQ4_K, 1>::bytes : g == 2 ? Stage8<kQ4_K, 2>::bytes : Stage8<kQ4_K, 4>::bytes;
+    return g == 1 ? Stage8<kQ6_K, 1>::bytes : g == 2 ? Stage8<kQ6_K, 2>::bytes : Stage8<kQ6_K, 4>::bytes;
 }
 
-// Split of each tile's blocks over S waves: enough waves to keep every SIMD
-// busy, at least two blocks per wave, and the workgroup's LDS (dynamic plus
-// the split-K scratch) within 64 KiB.  DMHIP_QMV8_SPLIT (1..16, a power of
-// two) overrides the wave-count rule for tuning.  Returns 0 when no split
-// fits.
-uint32_t plan_split8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch) {
-    static const int forced = [] {
-        const char *v = getenv("DMHIP_QMV8_SPLIT");
-        return v ? atoi(v) : 0;
-    }();
+// Dynamic LDS of one workgroup: records, zeroed region, staging per wave.
+size_t lds8_bytes(uint32_t type, uint32_t blocks, uint32_t batch, uint32_t waves, uint32_t g) {
+    const size_t rec = type == kQ4_K ? Rec8<kQ4_K>::bytes : Rec8<kQ6_K>::bytes;
+    return (size_t)blocks * batch * rec + kZero8 + (size_t)waves * stage_bytes8(type, g);
+}
+
+struct Plan8 {
+    uint32_t s = 0, g = 1;
+};
+
+int env_int(const char *name) {
+    const char *v = getenv(name);
+    return v ? atoi(v) : 0;
+}
+
+// Blocks per fetch (G) and split of each tile's block groups over S waves:
+// enough waves to keep every SIMD busy, at least two groups per wave, and
+// the workgroup's LDS (dynamic plus split-K scratch) within the 160 KiB of
+// a gfx950 workgroup.  DMHIP_QMV8_SPLIT (1..16, a power of two) and
+// DMHIP_QMV8_G (1, 2, 4) override the rules for tuning.  s == 0: no plan.
+Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch) {
+    static const int forced_s = env_int("DMHIP_QMV8_SPLIT");
+    static const int forced_g = env_int("DMHIP_QMV8_G");
+    Plan8 p;
     const uint32_t tiles = (rows + 15) / 16, blocks = columns / 256;
+    // Two blocks per fetch halve the cache lines requested twice (a block's
+    // last line is the next block's first) on tall matrices; short ones
+    // need the parallelism of single-block groups more.
+    p.g = (forced_g == 1 || forced_g == 2 || forced_g == 4) ? (uint32_t)forced_g : (tiles >= 2048 ? 2u : 1u);
+    while (p.g > 1 && blocks < 2 * p.g) p.g /= 2;
+    const uint32_t groups = (blocks + p.g - 1) / p.g;
     uint32_t s = 1;
-    if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) {
-        s = (uint32_t)forced;
+    if (forced_s == 1 || forced_s == 2 || forced_s == 4 || forced_s == 8 || forced_s == 16) {
+        s = (uint32_t)forced_s;
     } else {
-        while (s < kMaxWaves8 && (size_t)tiles * s < 4096 && blocks >= 4 * s) s *= 2;
+        while (s < kMaxWaves8 && (size_t)tiles * s < 4096 && groups >= 4 * s) s *= 2;
     }
     for (; s >= 1; s /= 2) {
         const uint32_t waves = s > 8 ? s : 8;
-        const size_t stat = (s > 1 ? (size_t)waves * 64 * batch * sizeof(float) : 4) + 64;
-        if (lds8_bytes(type, blocks, batch, waves) + stat <= kMaxLds8) return s;
+        // static: split-K scratch, token maxima, argmax candidates, counters
+        const size_t stat = (s > 1 ? (size_t)waves * 64 * batch * sizeof(float) : 4) + 512;
+        if (lds8_bytes(type, blocks, batch, waves, p.g) + stat <= kMaxLds8) {
+            p.s = s;
+            return p;
+        }
     }
-    return 0;
+    p.s = 0;
+    return p;
 }
 
-template <uint32_t TYPE, int S, int MODE, int TOK>
-hipError_t run8(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, const void *w, const uint8_t *xq,
-                const float *ysc, float *y, ArgmaxPartial *partials, uint32_t *count) {
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
+hipError_t run8(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, const void *w, const float *x, float *y,
+                ArgmaxPartial *partials, uint32_t *count) {
     constexpr uint32_t WAVES = S > 8 ? S : 8;
-    const uint32_t tiles = (rows + 15) / 16, per = WAVES / S;
-    const uint32_t grid = (tiles + per - 1) / per;
+    const uint32_t tiles = (rows + 15) / 16;
     const uint32_t blocks = columns / 256;
     const uint32_t row_bytes = blocks * (TYPE == kQ4_K ? 144u : 210u);
-    if (count) *count = grid * per;
+    const size_t lds = lds8_bytes(TYPE, blocks, TOK, WAVES, G);
+    uint32_t grid;
+    if (S == 1) {
+        // persistent: as many workgroups as fit on the device at once
+        const uint32_t by_regs = 4 * (G <= 2 ? 4 : 2) / WAVES;
+        uint32_t by_lds = (uint32_t)(kMaxLds8 / (lds + 4096));
+        uint32_t per_cu = by_regs < by_lds ? by_regs : by_lds;
+        if (per_cu == 0) per_cu = 1;
+        const uint32_t cus = ctx->compute_units > 0 ? (uint32_t)ctx->compute_units : 256u;
+        const uint32_t need = (tiles + WAVES - 1) / WAVES;
+        grid = cus * per_cu < need ? cus * per_cu : need;
+    } else {
+        const uint32_t per = WAVES / S;
+        grid = (tiles + per - 1) / per;
+    }
+    if (count) *count = grid;
+    auto kernel = qmv8_kernel<TYPE, S, MODE, TOK, G>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
     KernelTimer timer(ctx);
-    hipLaunchKernelGGL((qmv8_kernel<TYPE, S, MODE, TOK>), dim3(grid), dim3(64 * WAVES),
-                       lds8_bytes(TYPE, blocks, TOK, WAVES), ctx->stream, (const uint8_t *)w, rows, columns,
-                       row_bytes, row_bytes * rows, xq, ysc, y, partials);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WAVES), lds, ctx->stream, (const uint8_t *)w, rows,
+                       columns, row_bytes, row_bytes * rows, x, y, partials);
     return hipGetLastError();
 }
 
-template <uint32_t TYPE, int MODE, int TOK>
-hipError_t run8_s(dmhip_ctx *ctx, uint32_t s, uint32_t rows, uint32_t columns, const void *w,
-                  const uint8_t *xq, const float *ysc, float *y, ArgmaxPartial *partials, uint32_t *count) {
+template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
+hipError_t run8_s(dmhip_ctx *ctx, uint32_t s, uint32_t rows, uint32_t columns, const void *w, const float *x,
+                  float *y, ArgmaxPartial *partials, uint32_t *count) {
     switch (s) {
-    case 1: return run8<TYPE, 1, MODE, TOK>(ctx, rows, columns, w, xq, ysc, y, partials, count);
-    case 2: return run8<TYPE, 2, MODE, TOK>(ctx, rows, columns, w, xq, ysc, y, partials, count);
-    case 4: return run8<TYPE, 4, MODE, TOK>(ctx, rows, columns, w, xq, ysc, y, partials, count);
-    case 8: return run8<TYPE, 8, MODE, TOK>(ctx, rows, columns, w, xq, ysc, y, partials, count);
-    default: return run8<TYPE, 16, MODE, TOK>(ctx, rows, columns, w, xq, ysc, y, partials, count);
+    case 1: return run8<TYPE, 1, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
+    case 2: return run8<TYPE, 2, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
+    case 4: return run8<TYPE, 4, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
+    case 8: return run8<TYPE, 8, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
+    default: return run8<TYPE, 16, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
     }
+}
+
+template <uint32_t TYPE, int MODE, int TOK>
+hipError_t run8_g(dmhip_ctx *ctx, const Plan8 &p, uint32_t rows, uint32_t columns, const void *w,
+                  const float *x, float *y, ArgmaxPartial *partials, uint32_t *count) {
+    if (p.g == 4) return run8_s<TYPE, MODE, TOK, 4>(ctx, p.s, rows, columns, w, x, y, partials, count);
+    if (p.g == 2) return run8_s<TYPE, MODE, TOK, 2>(ctx, p.s, rows, columns, w, x, y, partials, count);
+    return run8_s<TYPE, MODE, TOK, 1>(ctx, p.s, rows, columns, w, x, y, partials, count);
 }
 
 template <uint32_t TYPE>
 hipError_t launch8(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, const void *w, uint32_t batch,
                    const float *x, float *y, ArgmaxPartial *partials, uint32_t *count) {
-    const uint32_t blocks = columns / 256;
-    const size_t rec_bytes = (size_t)blocks * batch * Rec8<TYPE>::bytes;
-    const size_t xq_bytes = (rec_bytes + 255) & ~(size_t)255;
-    if (ctx->aux.ensure(xq_bytes + 64 * sizeof(float)) != DMHIP_OK) return hipErrorOutOfMemory;
-    uint8_t *xq = (uint8_t *)ctx->aux.ptr;
-    float *ysc = (float *)((char *)ctx->aux.ptr + xq_bytes);
-    uint32_t gx = (blocks + 3) / 4;
-    if (gx > 16) gx = 16;
-    hipLaunchKernelGGL(qmv8_prepare_kernel<TYPE>, dim3(gx, batch), dim3(256), 0, ctx->stream, x, columns,
-                       batch, xq, ysc);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const uint32_t s = plan_split8(TYPE, rows, columns, batch);
-    if (s == 0) return hipErrorInvalidValue;
-    if (partials) return run8_s<TYPE, 1, 1>(ctx, s, rows, columns, w, xq, ysc, y, partials, count);
-    if (batch == 1) return run8_s<TYPE, 0, 1>(ctx, s, rows, columns, w, xq, ysc, y, nullptr, nullptr);
-    return run8_s<TYPE, 0, 2>(ctx, s, rows, columns, w, xq, ysc, y, nullptr, nullptr);
+    const Plan8 p = plan8(TYPE, rows, columns, batch);
+    if (p.s == 0) return hipErrorInvalidValue;
+    if (partials) return run8_g<TYPE, 1, 1>(ctx, p, rows, columns, w, x, y, partials, count);
+    if (batch == 1) return run8_g<TYPE, 0, 1>(ctx, p, rows, columns, w, x, y, nullptr, nullptr);
+    return run8_g<TYPE, 0, 2>(ctx, p, rows, columns, w, x, y, nullptr, nullptr);
 }
 
 }  // namespace
@@ -562,7 +704,7 @@ hipError_t launch8(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, const void *
 bool qmv8_supported(uint32_t type, size_t rows, size_t columns, size_t batch) {
     if (type != kQ4_K && type != kQ6_K) return false;
     if (batch < 1 || batch > 2 || columns % 256 || columns == 0) return false;
-    return plan_split8(type, (uint32_t)rows, (uint32_t)columns, (uint32_t)batch) != 0;
+    return plan8(type, (uint32_t)rows, (uint32_t)columns, (uint32_t)batch).s != 0;
 }
 
 hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,

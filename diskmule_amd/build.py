@@ -19,6 +19,9 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
+# The GEMM rescales its MFMA accumulators every block with VALU FMAs; keeping
+# them in VGPRs (not AGPRs) avoids a copy in and out per element.
+SOURCE_FLAGS = {"kernels_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def build(verbose: bool = False, jobs: int = 6) -> str:
@@ -32,7 +35,7 @@ def build(verbose: bool = False, jobs: int = 6) -> str:
             continue
         obj = os.path.join(objdir, src + ".o")
         objs.append(obj)
-        cmd = [HIPCC, *FLAGS, "-c", path, "-o", obj]
+        cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-c", path, "-o", obj]
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
         if len(procs) >= jobs:
             _drain(procs, verbose)

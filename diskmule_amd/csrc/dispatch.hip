@@ -79,6 +79,19 @@ int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn, ui
     float *g = normalized + batch * hidden;       // [batch][ffn]
     float *u = g + batch * ffn;                   // [batch][ffn]
     float *a = u + batch * ffn;                   // [batch][ffn]
+    // Fused: RMSNorm folded into the gate/up kernel's activation scale and
+    // silu(gate) * up in its epilogue, then the down projection.
+    if (gate_type == up_type && qmv_supported(gate_type, ffn, hidden, gate, batch) &&
+        qmv_supported(up_type, ffn, hidden, up, batch)) {
+        if (qmv8_gate_up_supported(gate_type, ffn, hidden, batch))
+            DM_HIP(launch_qmv8_gate_up(ctx, gate_type, (uint32_t)ffn, (uint32_t)hidden, gate, up,
+                                       (uint32_t)batch, h, a, 1, epsilon));
+        else
+            DM_HIP(launch_qmv_gate_up(ctx, gate_type, (uint32_t)ffn, (uint32_t)hidden, gate, up,
+                                      (uint32_t)batch, h, a, 1, epsilon));
+        DM_CHECK_STATUS(enqueue_matvec(ctx, down_type, hidden, ffn, down, batch, a, y));
+        return DMHIP_OK;
+    }
     DM_HIP(launch_rms_norm(ctx->stream, h, (uint32_t)batch, (uint32_t)hidden, nullptr, epsilon, normalized));
     DM_CHECK_STATUS(enqueue_matvec(ctx, gate_type, ffn, hidden, gate, batch, normalized, g));
     DM_CHECK_STATUS(enqueue_matvec(ctx, up_type, ffn, hidden, up, batch, normalized, u));

@@ -24,6 +24,13 @@ hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t co
                        uint32_t batch, const float *x, float *y, ArgmaxPartial *partials,
                        uint32_t *count);
 
+// The int8-MFMA gate/up pair: act[b][r] = silu(gate[r] . n[b]) * (up[r] . n[b])
+// with n = RMSNorm(x) (unit weight) when `normalize`, else n = x.
+bool qmv8_gate_up_supported(uint32_t type, size_t rows, size_t columns, size_t batch);
+hipError_t launch_qmv8_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns,
+                               const void *gate, const void *up, uint32_t batch, const float *x,
+                               float *act, int normalize, float epsilon);
+
 // True when the MFMA matvec takes this shape: Q4_K or Q6_K rows of whole
 // 256-value blocks, a weight base address aligned to 4 bytes (16 for Q4_K),
 // and fewer than 4 GiB of weights (one buffer descriptor).

@@ -14,10 +14,11 @@
 //
 //  * Weights enter as their raw codes: Q4_K nibbles 0..15, Q6_K 6-bit codes
 //    0..63.  No floating-point conversion and no per-weight scale.
-//  * Each token is scaled by a power of two so max|x| 2^-e < 2^22 and rounded
-//    to integers X = 65536 hi + 256 mid + lo (balanced bytes); A rows
-//    4g + {0, 1, 2} carry hi, mid and lo.  Precision: 22 bits relative to the
-//    token's largest element.
+//  * Each 256-value block of a token is scaled by its own power of two so
+//    max|x| 2^-e < 2^22 over the block and rounded to integers
+//    X = 65536 hi + 256 mid + lo (balanced bytes); A rows 4g + {0, 1, 2} carry
+//    hi, mid and lo.  Precision: 22 bits relative to the block's largest
+//    element; 2^e multiplies the block's result.
 //  * A group dot is v = (C0 * 256 + C1) * 256 + C2 in fp32, scaled by the
 //    group's 6/8-bit scale and the block's d.  Q6_K's "- 32" offset is the
 //    exact accumulator seed -32 * sum(X) of the group; Q4_K's
@@ -44,10 +45,11 @@ constexpr uint32_t kMaxWaves8 = 16;
 
 // Bytes of one block's record for one token: A fragments of the four steps
 // (768), then Q6_K seeds (4 steps x 4 groups x 4 int32) or Q4_K sub-block
-// sums (8 floats).
+// sums (8 floats), then the block's activation scale 2^e (a float, padded to
+// 16 bytes).
 template <uint32_t TYPE> struct Rec8;
-template <> struct Rec8<kQ4_K> { static constexpr uint32_t bytes = 4 * kStep8 + 32; };
-template <> struct Rec8<kQ6_K> { static constexpr uint32_t bytes = 4 * kStep8 + 256; };
+template <> struct Rec8<kQ4_K> { static constexpr uint32_t bytes = 4 * kStep8 + 32 + 16; };
+template <> struct Rec8<kQ6_K> { static constexpr uint32_t bytes = 4 * kStep8 + 256 + 16; };
 
 // Column (0..255) of byte i of lane group g's 16 codes at step t.
 template <uint32_t TYPE>
@@ -74,77 +76,52 @@ __device__ __forceinline__ float combine8(i32x4 c) {
 namespace {
 
 // Activation records of TOK tokens written by the workgroup into LDS at
-// `rec` (record of block b, token t at (b * TOK + t) * REC).  Phase 1: max|x|
-// and a non-finite flag per token (coalesced loads, eight in flight per
-// thread).  Phase 2: wave k quantizes blocks k, k + WAVES, ...; lane l
-// handles step t = l >> 4, lane group g = (l >> 2) & 3 and columns 4q..4q+3
-// (q = l & 3) of that group.  tscale[token] = 2^e, or NaN when the row holds
-// a non-finite value (every output of that token is then NaN).
-template <uint32_t TYPE, int TOK, uint32_t WAVES>
+// `rec` (record of block b, token t at (b * TOK + t) * REC).  Wave k handles
+// blocks k, k + WAVES, ...: lane l loads the four values of step t = l >> 4,
+// lane group g = (l >> 2) & 3, columns 4q .. 4q+3 (q = l & 3) of the block,
+// and the block gets its own power-of-two scale 2^e (max|x| 2^-e < 2^22 over
+// the block; a wave-wide maximum, no barrier).  The scale is stored after the
+// record; it is NaN when the block holds a non-finite value, which makes
+// every output of that token NaN.  With NORM each wave also leaves its part
+// of sum(x^2) per token in red_ss[tok * WAVES + wave].
+template <uint32_t TYPE, int TOK, uint32_t WAVES, bool NORM>
 __device__ __forceinline__ void build_records8(const float *__restrict__ x, uint32_t columns, uint8_t *rec,
-                                               float *red_max, uint32_t *red_bad, float *tscale) {
-    constexpr uint32_t NT = 64 * WAVES, REC = Rec8<TYPE>::bytes, U = 8;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    float mx[TOK];
-    uint32_t bad[TOK];
-#pragma unroll
-    for (int tok = 0; tok < TOK; tok++) {
-        mx[tok] = 0.0f;
-        bad[tok] = 0;
-    }
-    for (uint32_t i0 = 0; i0 < columns; i0 += NT * U) {
-#pragma unroll
-        for (int tok = 0; tok < TOK; tok++) {
-            float v[U];
-#pragma unroll
-            for (uint32_t j = 0; j < U; j++) {
-                const uint32_t i = i0 + NT * j + tid;
-                v[j] = i < columns ? x[(size_t)tok * columns + i] : 0.0f;
-            }
-#pragma unroll
-            for (uint32_t j = 0; j < U; j++) {
-                bad[tok] |= !__builtin_isfinite(v[j]);
-                mx[tok] = fmaxf(mx[tok], fabsf(v[j]));
-            }
-        }
-    }
-#pragma unroll
-    for (int tok = 0; tok < TOK; tok++) {
-        const float m = wave_max(mx[tok]);
-        const uint32_t f = __builtin_amdgcn_ballot_w64(bad[tok] != 0) != 0;
-        if (lane == 0) {
-            red_max[tok * WAVES + wave] = m;
-            red_bad[tok * WAVES + wave] = f;
-        }
-    }
-    __syncthreads();
+                                               float *red_ss) {
+    constexpr uint32_t REC = Rec8<TYPE>::bytes;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t blocks = columns / 256;
     const uint32_t t = lane >> 4, g = (lane >> 2) & 3u, q = lane & 3u;
 #pragma unroll
     for (int tok = 0; tok < TOK; tok++) {
-        float m = 0.0f;
-        uint32_t f = 0;
-        for (uint32_t k = 0; k < WAVES; k++) {
-            m = fmaxf(m, red_max[tok * WAVES + k]);
-            f |= red_bad[tok * WAVES + k];
-        }
-        int e = 0;
-        if (!f && m > 0.0f) {
-            int ex;
-            (void)frexpf(m, &ex);  // m < 2^ex
-            e = ex - 22;
-            if (e < -126) e = -126;
-            if (e > 127) e = 127;
-        }
-        const float down = ldexpf(1.0f, -e);
-        if (tid == 0) tscale[tok] = f ? __builtin_nanf("") : ldexpf(1.0f, e);
+        float ss = 0.0f;
         for (uint32_t b = wave; b < blocks; b += WAVES) {
             const float *xb = x + (size_t)tok * columns + (size_t)b * 256 + column8<TYPE>(t, g, 4 * q);
+            float v[4];
+            float mx = 0.0f;
+            uint32_t bad = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[j] = xb[j];
+                bad |= !__builtin_isfinite(v[j]);
+                mx = fmaxf(mx, fabsf(v[j]));
+                if (NORM) ss = __builtin_fmaf(v[j], v[j], ss);
+            }
+            mx = wave_max(mx);
+            bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
+            int e = 0;
+            if (!bad && mx > 0.0f) {
+                int ex;
+                (void)frexpf(mx, &ex);  // mx < 2^ex
+                e = ex - 22;
+                if (e < -126) e = -126;
+                if (e > 127) e = 127;
+            }
+            const float down = ldexpf(1.0f, -e);
             uint32_t term[3] = {0, 0, 0};
             int sum[3] = {0, 0, 0}, sx = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int X = f ? 0 : (int)rintf(xb[j] * down);  // |X| <= 2^22
+                const int X = bad ? 0 : (int)rintf(v[j] * down);  // |X| <= 2^22
                 const int lo = (int)(int8_t)(X & 0xff);
                 const int x1 = (X - lo) >> 8;
                 const int mid = (int)(int8_t)(x1 & 0xff);
@@ -175,6 +152,11 @@ __device__ __forceinline__ void build_records8(const float *__restrict__ x, uint
                 sx += __shfl_xor(sx, 16, 64);
                 if (q == 0 && (t & 1u) == 0) *(float *)(r + 4 * kStep8 + (2 * g + (t >> 1)) * 4) = (float)sx;
             }
+            if (lane == 0) *(float *)(r + REC - 16) = bad ? __builtin_nanf("") : ldexpf(1.0f, e);
+        }
+        if (NORM) {
+            ss = wave_sum(ss);
+            if (lane == 0) red_ss[tok * WAVES + wave] = ss;
         }
     }
 }
@@ -279,10 +261,11 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ4_K> &raw, const i32x4 *
         i32x4 c_hi = mfma8(lds[a + 2 * kStep8 / 16], b2, zero);
         c_hi = mfma8(lds[a + 3 * kStep8 / 16], b3, c_hi);
         const float *sums = (const float *)lds + (rec + tok * REC + 4 * kStep8) / 4 + 2 * g;
+        const float bs = ((const float *)lds)[(rec + tok * REC + REC - 16) / 4];  // block scale 2^e
         const float part = __builtin_fmaf(sc[1], combine8(c_hi), sc[0] * combine8(c_lo));
         const float mins = __builtin_fmaf(mn[1], sums[1], mn[0] * sums[0]);
-        acc[tok] = __builtin_fmaf(d, part, acc[tok]);
-        acc[tok] = __builtin_fmaf(-dmin, mins, acc[tok]);
+        acc[tok] = __builtin_fmaf(d * bs, part, acc[tok]);
+        acc[tok] = __builtin_fmaf(-dmin * bs, mins, acc[tok]);
     }
 }
 
@@ -340,7 +323,8 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ6_K> &raw, const i32x4 *
             const i32x4 cc = mfma8(lds[a + t * (kStep8 / 16)], b[t], lds[seeds + 4 * t]);
             part = __builtin_fmaf(sc[t], combine8(cc), part);
         }
-        acc[tok] = __builtin_fmaf(d, part, acc[tok]);
+        const float bs = ((const float *)lds)[(rec + tok * REC + REC - 16) / 4];  // block scale 2^e
+        acc[tok] = __builtin_fmaf(d * bs, part, acc[tok]);
     }
 }
 
@@ -357,7 +341,8 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ6_K> &raw, const i32x4 *
 //    tiles once.
 // Dynamic LDS: activation records | zeroed region | per-wave staging.
 // MODE 0: y = W x.  MODE 1 (one token): also one ArgmaxPartial per
-// workgroup in partials[blockIdx.x].
+// workgroup in partials[blockIdx.x].  MODE 2: W (gate) and W2 (up) of the same
+// shape on RMSNorm(x) (unit weight, when `normalize`), y = silu(gate) * up.
 // Register budget: 4 waves per SIMD (G <= 2) or 2 (G = 4), about what the
 // workgroup's LDS allows on a C2-sized row; a tighter budget makes the
 // compiler wait for each prefetch right after issuing it.
@@ -365,19 +350,18 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ6_K> &raw, const i32x4 *
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
 __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2))) qmv8_kernel(
-    const uint8_t *__restrict__ w, uint32_t rows, uint32_t columns, uint32_t row_bytes,
-    uint32_t total_bytes, const float *__restrict__ x, float *__restrict__ y,
-    ArgmaxPartial *__restrict__ partials) {
+    const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows, uint32_t columns,
+    uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x, int normalize, float epsilon,
+    float *__restrict__ y, ArgmaxPartial *__restrict__ partials) {
     constexpr uint32_t WAVES = S > 8 ? S : 8;
+    constexpr int NM = MODE == 2 ? 2 : 1;  // weight matrices streamed
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
     constexpr uint32_t BB = TYPE == kQ4_K ? 144u : 210u;
     using ST = Stage8<TYPE, G>;
     constexpr uint32_t CH = ST::chunks, NL = ST::loads, ITEMS = ST::items;
     extern __shared__ i32x4 lds8[];
-    __shared__ float red[S > 1 ? WAVES * 64 * TOK : 1];
-    __shared__ float red_max[TOK * WAVES];
-    __shared__ uint32_t red_bad[TOK * WAVES];
-    __shared__ float tscale[TOK];
+    __shared__ float red[S > 1 ? WAVES * 64 * TOK * NM : 1];
+    __shared__ float red_ss[TOK * WAVES];
     __shared__ uint32_t next_tile;
     __shared__ unsigned long long wg_key[WAVES];
     __shared__ uint32_t wg_bad[WAVES];
@@ -388,13 +372,15 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     const uint32_t blocks = columns / 256, groups = (blocks + G - 1) / G;
     const uint32_t tiles = (rows + 15) / 16;
     const uint32_t rec_bytes = blocks * TOK * REC;
-    v4u *stage = (v4u *)((uint8_t *)lds8 + rec_bytes + kZero8) + wave * ITEMS;
+    v4u *stage = (v4u *)((uint8_t *)lds8 + rec_bytes + kZero8) + wave * ITEMS * NM;
+    v4u *stage2 = stage + (NM - 1) * ITEMS;
 
     // Whole dwords: the last dword of the matrix may extend up to 3 bytes past
     // its end (inside the allocation's granularity); loads beyond it read 0.
     const uint32_t records = (total_bytes + 3u) & ~3u;
     const uint32_t nowhere = records + 256;  // every load from here reads 0
     const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(w, records);
+    const __amdgpu_buffer_rsrc_t rsrc2 = make_rsrc(MODE == 2 ? w2 : w, records);
 
     // Tile schedule.
     uint32_t tile, t_end;
@@ -422,13 +408,14 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
         const uint32_t rw = tl * 16 + n;
         next_row_base = rw < rows ? rw * row_bytes : nowhere;
     };
-    v4u st[NL];
+    v4u st[NL], st2[MODE == 2 ? NL : 1];
     auto fetch = [&](uint32_t grp) {
 #pragma unroll
         for (uint32_t j = 0; j < NL; j++) {
             const uint32_t off =
                 src_row[j] == nowhere ? nowhere : ((src_row[j] + grp * G * BB) & ~3u) + src_chunk[j];
             st[j] = __builtin_bit_cast(v4u, rsrc_load16(rsrc, off));
+            if constexpr (MODE == 2) st2[j] = __builtin_bit_cast(v4u, rsrc_load16(rsrc2, off));
         }
     };
 
@@ -440,9 +427,25 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     }
     uint32_t row_base = next_row_base;
 
-    build_records8<TYPE, TOK, WAVES>(x, columns, (uint8_t *)lds8, red_max, red_bad, tscale);
+    const bool norm = MODE == 2 && normalize;
+    if (norm)
+        build_records8<TYPE, TOK, WAVES, true>(x, columns, (uint8_t *)lds8, red_ss);
+    else
+        build_records8<TYPE, TOK, WAVES, false>(x, columns, (uint8_t *)lds8, red_ss);
     for (uint32_t i = threadIdx.x; i < kZero8 / 16; i += 64 * WAVES) lds8[rec_bytes / 16 + i] = i32x4{0, 0, 0, 0};
     __syncthreads();
+    // Output scale per token: 1, or the RMSNorm factor (unit weight)
+    // inv = (ss/n + eps).sqrt().recip() (src/cpu.rs:98-142) folded in.
+    float tscale[TOK];
+#pragma unroll
+    for (int tok = 0; tok < TOK; tok++) {
+        tscale[tok] = 1.0f;
+        if (norm) {
+            float q = 0.0f;
+            for (uint32_t k2 = 0; k2 < WAVES; k2++) q += red_ss[tok * WAVES + k2];
+            tscale[tok] = 1.0f / __builtin_sqrtf(q / (float)columns + epsilon);
+        }
+    }
 
     // A row n of the MFMA: live when it is term n % 4 (< 3) of lane group n / 4.
     const uint32_t term = n & 3u;
@@ -457,27 +460,47 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     auto put_stage = [&]() {
 #pragma unroll
         for (uint32_t j = 0; j < NL; j++)
-            if (j + 1 < NL || j * 64 + lane < ITEMS) stage[j * 64 + lane] = st[j];
+            if (j + 1 < NL || j * 64 + lane < ITEMS) {
+                stage[j * 64 + lane] = st[j];
+                if constexpr (MODE == 2) stage2[j * 64 + lane] = st2[j];
+            }
     };
-    auto compute_group = [&](uint32_t grp, uint32_t rb, float (&acc)[TOK]) {
+    // acc[m][tok]: matrix m (gate, up) of token tok
+    auto compute_group = [&](uint32_t grp, uint32_t rb, float (&acc)[NM][TOK]) {
         // the run of row n starts 0 or 2 bytes into its first dword (Q6_K)
         const uint32_t s0 = rb == nowhere ? 0u : ((rb + grp * G * BB) & 3u);
 #pragma unroll
         for (uint32_t b = 0; b < G; b++) {
             const uint32_t blk = grp * G + b;
             if (blk >= blocks) break;
-            Raw8<TYPE> raw;
-            take8<CH>(stage, n, g, s0 + b * BB, raw);
-            block_dot8<TOK>(raw, lds8, a_base + blk * TOK * a_stride, a_stride, blk * TOK * REC, g, acc);
+#pragma unroll
+            for (int mtx = 0; mtx < NM; mtx++) {
+                Raw8<TYPE> raw;
+                take8<CH>(mtx == 0 ? stage : stage2, n, g, s0 + b * BB, raw);
+                block_dot8<TOK>(raw, lds8, a_base + blk * TOK * a_stride, a_stride, blk * TOK * REC, g, acc[mtx]);
+            }
         }
     };
 
     uint64_t best = 0;
     uint32_t bad = 0;
-    auto finish_row = [&](float (&acc)[TOK], uint32_t rb, uint32_t tl) {
+    auto finish_row = [&](float (&acc)[NM][TOK], uint32_t rb, uint32_t tl) {
         const uint32_t row = tl * 16 + n;
         if (g < (uint32_t)TOK && rb != nowhere) {
-            const float v = (TOK == 1 || g == 0 ? acc[0] : acc[TOK - 1]) * tscale[g];
+            const float ts = TOK == 1 || g == 0 ? tscale[0] : tscale[TOK - 1];
+            float v = (TOK == 1 || g == 0 ? acc[0][0] : acc[0][TOK - 1]) * ts;
+            if constexpr (MODE == 2) {
+                const float u = (TOK == 1 || g == 0 ? acc[NM - 1][0] : acc[NM - 1][TOK - 1]) * ts;
+                // silu(gate) * up, stable sigmoid (src/qwen35/cpu.rs:982-993)
+                float sig;
+                if (v >= 0.0f) {
+                    sig = 1.0f / (1.0f + expf(-v));
+                } else {
+                    const float ex = expf(v);
+                    sig = ex / (1.0f + ex);
+                }
+                v = v * sig * u;
+            }
             y[(size_t)g * rows + row] = v;
             if constexpr (MODE == 1) {
                 bad |= !__builtin_isfinite(v);
@@ -489,9 +512,11 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
 
     if constexpr (S == 1) {
         while (active) {
-            float acc[TOK];
+            float acc[NM][TOK];
 #pragma unroll
-            for (int tok = 0; tok < TOK; tok++) acc[tok] = 0.0f;
+            for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+                for (int tok = 0; tok < TOK; tok++) acc[mtx][tok] = 0.0f;
             uint32_t next = t_end;
             const uint32_t rb = row_base;
             for (uint32_t grp = 0; grp < groups; grp++) {
@@ -510,19 +535,23 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
                 compute_group(grp, rb, acc);
             }
 #pragma unroll
-            for (int tok = 0; tok < TOK; tok++) {
-                acc[tok] += __shfl_xor(acc[tok], 16, 64);
-                acc[tok] += __shfl_xor(acc[tok], 32, 64);
-            }
+            for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+                for (int tok = 0; tok < TOK; tok++) {
+                    acc[mtx][tok] += __shfl_xor(acc[mtx][tok], 16, 64);
+                    acc[mtx][tok] += __shfl_xor(acc[mtx][tok], 32, 64);
+                }
             finish_row(acc, rb, tile);
             tile = next;
             row_base = next_row_base;
             active = tile < t_end;
         }
     } else {
-        float acc[TOK];
+        float acc[NM][TOK];
 #pragma unroll
-        for (int tok = 0; tok < TOK; tok++) acc[tok] = 0.0f;
+        for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+            for (int tok = 0; tok < TOK; tok++) acc[mtx][tok] = 0.0f;
         if (active) {
             for (uint32_t grp = kpart; grp < groups; grp += S) {
                 put_stage();
@@ -531,19 +560,23 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
             }
         }
 #pragma unroll
-        for (int tok = 0; tok < TOK; tok++) {
-            acc[tok] += __shfl_xor(acc[tok], 16, 64);
-            acc[tok] += __shfl_xor(acc[tok], 32, 64);
-            red[(wave * 64 + lane) * TOK + tok] = acc[tok];
-        }
+        for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+            for (int tok = 0; tok < TOK; tok++) {
+                acc[mtx][tok] += __shfl_xor(acc[mtx][tok], 16, 64);
+                acc[mtx][tok] += __shfl_xor(acc[mtx][tok], 32, 64);
+                red[((wave * 64 + lane) * TOK + tok) * NM + mtx] = acc[mtx][tok];
+            }
         __syncthreads();
         if (kpart == 0 && active) {
 #pragma unroll
-            for (int tok = 0; tok < TOK; tok++) {
-                float v = 0.0f;
-                for (int p = 0; p < S; p++) v += red[((wave + p) * 64 + lane) * TOK + tok];
-                acc[tok] = v;
-            }
+            for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+                for (int tok = 0; tok < TOK; tok++) {
+                    float v = 0.0f;
+                    for (int p = 0; p < S; p++) v += red[(((wave + p) * 64 + lane) * TOK + tok) * NM + mtx];
+                    acc[mtx][tok] = v;
+                }
             finish_row(acc, row_base, tile);
         }
     }
@@ -585,10 +618,11 @@ size_t stage_bytes8(uint32_t type, uint32_t g) {
     return g == 1 ? Stage8<kQ6_K, 1>::bytes : g == 2 ? Stage8<kQ6_K, 2>::bytes : Stage8<kQ6_K, 4>::bytes;
 }
 
-// Dynamic LDS of one workgroup: records, zeroed region, staging per wave.
-size_t lds8_bytes(uint32_t type, uint32_t blocks, uint32_t batch, uint32_t waves, uint32_t g) {
+// Dynamic LDS of one workgroup: records, zeroed region, staging per wave
+// (one area per streamed matrix).
+size_t lds8_bytes(uint32_t type, uint32_t blocks, uint32_t batch, uint32_t waves, uint32_t g, uint32_t mats) {
     const size_t rec = type == kQ4_K ? Rec8<kQ4_K>::bytes : Rec8<kQ6_K>::bytes;
-    return (size_t)blocks * batch * rec + kZero8 + (size_t)waves * stage_bytes8(type, g);
+    return (size_t)blocks * batch * rec + kZero8 + (size_t)waves * mats * stage_bytes8(type, g);
 }
 
 struct Plan8 {
@@ -605,7 +639,7 @@ int env_int(const char *name) {
 // the workgroup's LDS (dynamic plus split-K scratch) within the 160 KiB of
 // a gfx950 workgroup.  DMHIP_QMV8_SPLIT (1..16, a power of two) and
 // DMHIP_QMV8_G (1, 2, 4) override the rules for tuning.  s == 0: no plan.
-Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch) {
+Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t mats) {
     static const int forced_s = env_int("DMHIP_QMV8_SPLIT");
     static const int forced_g = env_int("DMHIP_QMV8_G");
     Plan8 p;
@@ -625,8 +659,8 @@ Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch) {
     for (; s >= 1; s /= 2) {
         const uint32_t waves = s > 8 ? s : 8;
         // static: split-K scratch, token maxima, argmax candidates, counters
-        const size_t stat = (s > 1 ? (size_t)waves * 64 * batch * sizeof(float) : 4) + 512;
-        if (lds8_bytes(type, blocks, batch, waves, p.g) + stat <= kMaxLds8) {
+        const size_t stat = (s > 1 ? (size_t)waves * 64 * batch * mats * sizeof(float) : 4) + 768;
+        if (lds8_bytes(type, blocks, batch, waves, p.g, mats) + stat <= kMaxLds8) {
             p.s = s;
             return p;
         }
@@ -635,14 +669,26 @@ Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch) {
     return p;
 }
 
+// Launch arguments shared by every instantiation.
+struct Args8 {
+    uint32_t rows, columns;
+    const void *w, *w2;
+    const float *x;
+    int normalize;
+    float epsilon;
+    float *y;
+    ArgmaxPartial *partials;
+    uint32_t *count;
+};
+
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
-hipError_t run8(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, const void *w, const float *x, float *y,
-                ArgmaxPartial *partials, uint32_t *count) {
+hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
     constexpr uint32_t WAVES = S > 8 ? S : 8;
+    const uint32_t rows = a.rows, columns = a.columns;
     const uint32_t tiles = (rows + 15) / 16;
     const uint32_t blocks = columns / 256;
     const uint32_t row_bytes = blocks * (TYPE == kQ4_K ? 144u : 210u);
-    const size_t lds = lds8_bytes(TYPE, blocks, TOK, WAVES, G);
+    const size_t lds = lds8_bytes(TYPE, blocks, TOK, WAVES, G, MODE == 2 ? 2u : 1u);
     uint32_t grid;
     if (S == 1) {
         // persistent: as many workgroups as fit on the device at once
@@ -657,46 +703,44 @@ hipError_t run8(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, const void *w, 
         const uint32_t per = WAVES / S;
         grid = (tiles + per - 1) / per;
     }
-    if (count) *count = grid;
+    if (a.count) *a.count = grid;
     auto kernel = qmv8_kernel<TYPE, S, MODE, TOK, G>;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
     KernelTimer timer(ctx);
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WAVES), lds, ctx->stream, (const uint8_t *)w, rows,
-                       columns, row_bytes, row_bytes * rows, x, y, partials);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WAVES), lds, ctx->stream, (const uint8_t *)a.w,
+                       (const uint8_t *)a.w2, rows, columns, row_bytes, row_bytes * rows, a.x, a.normalize,
+                       a.epsilon, a.y, a.partials);
     return hipGetLastError();
 }
 
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
-hipError_t run8_s(dmhip_ctx *ctx, uint32_t s, uint32_t rows, uint32_t columns, const void *w, const float *x,
-                  float *y, ArgmaxPartial *partials, uint32_t *count) {
+hipError_t run8_s(dmhip_ctx *ctx, uint32_t s, const Args8 &a) {
     switch (s) {
-    case 1: return run8<TYPE, 1, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
-    case 2: return run8<TYPE, 2, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
-    case 4: return run8<TYPE, 4, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
-    case 8: return run8<TYPE, 8, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
-    default: return run8<TYPE, 16, MODE, TOK, G>(ctx, rows, columns, w, x, y, partials, count);
+    case 1: return run8<TYPE, 1, MODE, TOK, G>(ctx, a);
+    case 2: return run8<TYPE, 2, MODE, TOK, G>(ctx, a);
+    case 4: return run8<TYPE, 4, MODE, TOK, G>(ctx, a);
+    case 8: return run8<TYPE, 8, MODE, TOK, G>(ctx, a);
+    default: return run8<TYPE, 16, MODE, TOK, G>(ctx, a);
     }
 }
 
 template <uint32_t TYPE, int MODE, int TOK>
-hipError_t run8_g(dmhip_ctx *ctx, const Plan8 &p, uint32_t rows, uint32_t columns, const void *w,
-                  const float *x, float *y, ArgmaxPartial *partials, uint32_t *count) {
-    if (p.g == 4) return run8_s<TYPE, MODE, TOK, 4>(ctx, p.s, rows, columns, w, x, y, partials, count);
-    if (p.g == 2) return run8_s<TYPE, MODE, TOK, 2>(ctx, p.s, rows, columns, w, x, y, partials, count);
-    return run8_s<TYPE, MODE, TOK, 1>(ctx, p.s, rows, columns, w, x, y, partials, count);
+hipError_t run8_g(dmhip_ctx *ctx, const Plan8 &p, const Args8 &a) {
+    if (p.g == 4) return run8_s<TYPE, MODE, TOK, 4>(ctx, p.s, a);
+    if (p.g == 2) return run8_s<TYPE, MODE, TOK, 2>(ctx, p.s, a);
+    return run8_s<TYPE, MODE, TOK, 1>(ctx, p.s, a);
 }
 
 template <uint32_t TYPE>
-hipError_t launch8(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, const void *w, uint32_t batch,
-                   const float *x, float *y, ArgmaxPartial *partials, uint32_t *count) {
-    const Plan8 p = plan8(TYPE, rows, columns, batch);
+hipError_t launch8(dmhip_ctx *ctx, uint32_t batch, int mode, const Args8 &a) {
+    const Plan8 p = plan8(TYPE, a.rows, a.columns, batch, mode == 2 ? 2u : 1u);
     if (p.s == 0) return hipErrorInvalidValue;
-    if (partials) return run8_g<TYPE, 1, 1>(ctx, p, rows, columns, w, x, y, partials, count);
-    if (batch == 1) return run8_g<TYPE, 0, 1>(ctx, p, rows, columns, w, x, y, nullptr, nullptr);
-    return run8_g<TYPE, 0, 2>(ctx, p, rows, columns, w, x, y, nullptr, nullptr);
+    if (mode == 1) return run8_g<TYPE, 1, 1>(ctx, p, a);
+    if (mode == 2) return batch == 1 ? run8_g<TYPE, 2, 1>(ctx, p, a) : run8_g<TYPE, 2, 2>(ctx, p, a);
+    return batch == 1 ? run8_g<TYPE, 0, 1>(ctx, p, a) : run8_g<TYPE, 0, 2>(ctx, p, a);
 }
 
 }  // namespace
@@ -704,13 +748,29 @@ hipError_t launch8(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, const void *
 bool qmv8_supported(uint32_t type, size_t rows, size_t columns, size_t batch) {
     if (type != kQ4_K && type != kQ6_K) return false;
     if (batch < 1 || batch > 2 || columns % 256 || columns == 0) return false;
-    return plan8(type, (uint32_t)rows, (uint32_t)columns, (uint32_t)batch).s != 0;
+    return plan8(type, (uint32_t)rows, (uint32_t)columns, (uint32_t)batch, 1).s != 0;
+}
+
+bool qmv8_gate_up_supported(uint32_t type, size_t rows, size_t columns, size_t batch) {
+    if (type != kQ4_K && type != kQ6_K) return false;
+    if (batch < 1 || batch > 2 || columns % 256 || columns == 0) return false;
+    return plan8(type, (uint32_t)rows, (uint32_t)columns, (uint32_t)batch, 2).s != 0;
 }
 
 hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
                        uint32_t batch, const float *x, float *y, ArgmaxPartial *partials, uint32_t *count) {
-    if (type == kQ4_K) return launch8<kQ4_K>(ctx, rows, columns, w, batch, x, y, partials, count);
-    return launch8<kQ6_K>(ctx, rows, columns, w, batch, x, y, partials, count);
+    const Args8 a{rows, columns, w, w, x, 0, 0.0f, y, partials, count};
+    const int mode = partials ? 1 : 0;
+    if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, mode, a);
+    return launch8<kQ6_K>(ctx, batch, mode, a);
+}
+
+hipError_t launch_qmv8_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns,
+                               const void *gate, const void *up, uint32_t batch, const float *x, float *act,
+                               int normalize, float epsilon) {
+    const Args8 a{rows, columns, gate, up, x, normalize, epsilon, act, nullptr, nullptr};
+    if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, 2, a);
+    return launch8<kQ6_K>(ctx, batch, 2, a);
 }
 
 }  // namespace dm

@@ -270,8 +270,10 @@ def test_argmax_top_k_rms_norm_silu(ctx, golden):
 
 # ---- config 3: dense FFN at decode ----------------------------------------
 
-@pytest.mark.parametrize("batch", [1, 4, 8])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
 def test_dense_ffn_matches_oracle(ctx, batch):
+    """Config 3.  Batch 1-2 runs the int8 gate/up kernel with RMSNorm folded
+    into its activation scale; batch 4 and 8 the fp16 one."""
     hidden, ffn = 4096, 12288
     print(f"C3 batch={batch}", flush=True)
     g = synth.quantized_matrix(Q4_K, ffn, hidden, synth.weight_seed(3, 0))

@@ -31,6 +31,28 @@ hipError_t launch_qmv8_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uin
                                const void *gate, const void *up, uint32_t batch, const float *x,
                                float *act, int normalize, float epsilon);
 
+// One job of a grouped routed-expert launch: the matrix at `w` (in gate/up
+// form the gate rows, the up rows following at up_offset bytes) applied to
+// `tokens` (1 or 2) activation rows x + x_off + t * x_stride, writing
+// y + y_off + t * y_stride (offsets and strides in floats).
+struct QmvJob {
+    const void *w;
+    uint32_t tokens;
+    uint32_t x_off, y_off;
+    int32_t x_stride, y_stride;
+};
+
+// True when the grouped int8-MFMA launch takes jobs of this shape (`mats`
+// 2 for the gate/up form).  Slot buffers must be 4-byte aligned (16 for
+// Q4_K) and hold whole rows.
+bool qmv8_grouped_supported(uint32_t type, size_t rows, size_t columns, uint32_t mats);
+
+// All jobs in one or a few launches.  gate_up == 0: y = W x.  gate_up == 1:
+// y = (g / (1 + exp(-g))) * u with g = gate . x, u = up . x, the routed-expert
+// activation of src/glm52/expert.rs:260-267.
+hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, int gate_up,
+                               uint64_t up_offset, const QmvJob *jobs, size_t count, const float *x, float *y);
+
 // True when the MFMA matvec takes this shape: Q4_K or Q6_K rows of whole
 // 256-value blocks, a weight base address aligned to 4 bytes (16 for Q4_K),
 // and fewer than 4 GiB of weights (one buffer descriptor).

@@ -11,6 +11,8 @@
 //     event (the end of its upload).
 #include "runtime.h"
 
+#include <string.h>
+
 #include <chrono>
 #include <vector>
 
@@ -28,7 +30,8 @@ __global__ void gather_rows_kernel(const float *__restrict__ x, const uint32_t *
 }
 
 // y[t] = fold over the k selections in order of fma(out[pos[t][j]], p[t][j], y)
-// (src/gemma4/cpu.rs:608-611).
+// (src/gemma4/cpu.rs:608-611); without `pos` selection t * k + j is row
+// t * k + j of expert_out.
 __global__ void moe_combine_pos_kernel(const float *__restrict__ expert_out,
                                        const uint32_t *__restrict__ pos, const float *__restrict__ p,
                                        uint32_t batch, uint32_t k, uint32_t hidden,
@@ -37,8 +40,10 @@ __global__ void moe_combine_pos_kernel(const float *__restrict__ expert_out,
          e += (size_t)gridDim.x * blockDim.x) {
         uint32_t t = (uint32_t)(e / hidden), i = (uint32_t)(e - (size_t)t * hidden);
         float acc = 0.0f;
-        for (uint32_t j = 0; j < k; j++)
-            acc = __builtin_fmaf(expert_out[(size_t)pos[t * k + j] * hidden + i], p[t * k + j], acc);
+        for (uint32_t j = 0; j < k; j++) {
+            const size_t row = pos ? pos[t * k + j] : t * k + j;
+            acc = __builtin_fmaf(expert_out[row * hidden + i], p[t * k + j], acc);
+        }
         y[e] = acc;
     }
 }
@@ -51,7 +56,11 @@ struct Slot {
     void *gate_up = nullptr;
     void *down = nullptr;
     hipEvent_t ready = nullptr;     // end of the last upload into the slot
-    hipEvent_t released = nullptr;  // end of the last compute that read it
+    // End of the last compute that read it: an event of the cache's ring,
+    // shared by the slots released together.  Once the ring wraps the event
+    // may be recorded again later on the same stream, which only makes a
+    // wait on it later, never earlier.
+    hipEvent_t released = nullptr;
     bool released_recorded = false;
 };
 
@@ -72,9 +81,18 @@ struct dmhip_expert_cache {
     dmhip_expert_cache_stats stats = {};
     // MoE workspace (device): grows on demand.
     dm::Scratch work;
-    std::vector<uint32_t> host_ids;
-    std::vector<float> host_probs;
+    // Pinned host copy of the router's selection (ids, then probabilities;
+    // kSelectionPairs pairs), written by the router kernel itself.
+    uint8_t *host_selection = nullptr;
+    // Release events, used round-robin: one record per released group.
+    std::vector<hipEvent_t> release_events;
+    size_t next_release = 0;
 };
+
+namespace {
+constexpr size_t kSelectionPairs = 16 * dm::kMaxTopK;  // batch <= 16
+constexpr size_t kReleaseEvents = 64;
+}
 
 using namespace dm;
 
@@ -133,13 +151,21 @@ int acquire(dmhip_expert_cache *c, size_t layer_index, size_t expert, size_t *sl
     return DMHIP_OK;
 }
 
-int release(dmhip_expert_cache *c, size_t layer, size_t slot) {
-    Slot &s = c->layers[layer].slots[slot];
-    DM_HIP(hipEventRecord(s.released, c->ctx->stream));
-    s.released_recorded = true;
-    s.pinned = false;
+// Unpins `count` slots of a layer after the compute work enqueued so far,
+// with one event record for all of them.
+int release_slots(dmhip_expert_cache *c, size_t layer, const size_t *slots, size_t count) {
+    hipEvent_t ev = c->release_events[c->next_release++ % kReleaseEvents];
+    DM_HIP(hipEventRecord(ev, c->ctx->stream));
+    for (size_t i = 0; i < count; i++) {
+        Slot &s = c->layers[layer].slots[slots[i]];
+        s.released = ev;
+        s.released_recorded = true;
+        s.pinned = false;
+    }
     return DMHIP_OK;
 }
+
+int release(dmhip_expert_cache *c, size_t layer, size_t slot) { return release_slots(c, layer, &slot, 1); }
 
 }  // namespace
 
@@ -183,8 +209,7 @@ int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len
                 hipMalloc(&s.down, layer.layout.down_bytes + 256) != hipSuccess ||
                 hipMemset(s.gate_up, 0, layer.layout.gate_up_bytes + 256) != hipSuccess ||
                 hipMemset(s.down, 0, layer.layout.down_bytes + 256) != hipSuccess ||
-                hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess ||
-                hipEventCreateWithFlags(&s.released, hipEventDisableTiming) != hipSuccess) {
+                hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess) {
                 dmhip_expert_cache_free(c);
                 return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate expert slot buffers");
             }
@@ -192,6 +217,18 @@ int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len
         }
     }
     c->stats.resident_bytes = resident;
+    c->release_events.assign(kReleaseEvents, nullptr);
+    for (hipEvent_t &ev : c->release_events)
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+            ev = nullptr;
+            dmhip_expert_cache_free(c);
+            return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not create the slot release events");
+        }
+    if (hipHostMalloc((void **)&c->host_selection, kSelectionPairs * 8, hipHostMallocDefault) != hipSuccess) {
+        c->host_selection = nullptr;
+        dmhip_expert_cache_free(c);
+        return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate the pinned router selection buffer");
+    }
     *out = c;
     return DMHIP_OK;
 }
@@ -206,9 +243,11 @@ void dmhip_expert_cache_free(dmhip_expert_cache *c) {
             if (s.gate_up) (void)hipFree(s.gate_up);
             if (s.down) (void)hipFree(s.down);
             if (s.ready) (void)hipEventDestroy(s.ready);
-            if (s.released) (void)hipEventDestroy(s.released);
         }
+    for (hipEvent_t ev : c->release_events)
+        if (ev) (void)hipEventDestroy(ev);
     c->work.release();
+    if (c->host_selection) (void)hipHostFree(c->host_selection);
     delete c;
 }
 
@@ -304,11 +343,14 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     float *d_eo = (float *)(w + a_eo);
 
     // 1. Router logits (exact fold) and top-k softmax on the GPU.
+    uint32_t *sel_ids = (uint32_t *)c->host_selection;
+    float *sel_probs = (float *)(c->host_selection + kSelectionPairs * 4);
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
-                               (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs, ctx->flags));
-    DM_HIP(hipMemcpyAsync(ids, d_ids, pairs * 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipMemcpyAsync(probabilities, d_probs, pairs * 4, hipMemcpyDeviceToHost, ctx->stream));
+                               (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs, ctx->flags, sel_ids,
+                               sel_probs));
     DM_HIP(hipStreamSynchronize(ctx->stream));
+    memcpy(ids, sel_ids, pairs * 4);
+    memcpy(probabilities, sel_probs, pairs * 4);
 
     // 2. Acquire in the reference's order (token by token, selection order)
     //    and cut the pairs into phases: a phase ends before an acquire whose
@@ -319,6 +361,15 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     // Host sources of the per-phase token lists stay alive until the final
     // synchronisation below.
     std::vector<std::vector<uint32_t>> phase_tokens;
+    // Grouped int8 path: one launch applies every slot of a phase, with the
+    // gate/up activation in its epilogue; act and expert-output rows are
+    // indexed by pair.  Slot buffers come from hipMalloc (256-byte aligned).
+    const uint64_t up_offset = (uint64_t)width * gu_row;
+    const bool grouped = qmv8_grouped_supported(gate_up_type, width, hidden, 2) &&
+                         qmv8_grouped_supported(down_type, hidden, width, 1) &&
+                         up_offset % (gate_up_type == 12 ? 16 : 4) == 0 &&  // 12: Q4_K
+                         (uint64_t)pairs * (hidden > width ? hidden : width) < (1ull << 31);
+    std::vector<QmvJob> gu_jobs, dn_jobs;
     auto run_phase = [&](size_t p0, size_t p1) -> int {
         if (p0 == p1) return DMHIP_OK;
         // Group the phase's pairs by slot: sorted order = pair index order
@@ -337,6 +388,31 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
                 }
         }
         group_start.push_back(order.size());
+        if (grouped) {
+            // One job per one or two pairs of a slot (two tokens share the
+            // slot's weight stream).
+            gu_jobs.clear();
+            dn_jobs.clear();
+            for (size_t g = 0; g + 1 < group_start.size(); g++) {
+                const Slot &s = c->layers[layer].slots[group_slot[g]];
+                for (size_t q = group_start[g]; q < group_start[g + 1]; q += 2) {
+                    const size_t a = order[q];
+                    const bool two = q + 1 < group_start[g + 1];
+                    const size_t b = two ? order[q + 1] : a;
+                    const int32_t tok_step = (int32_t)(b / k - a / k), pair_step = (int32_t)(b - a);
+                    gu_jobs.push_back(QmvJob{s.gate_up, two ? 2u : 1u, (uint32_t)((a / k) * hidden),
+                                             (uint32_t)(a * width), tok_step * (int32_t)hidden,
+                                             pair_step * (int32_t)width});
+                    dn_jobs.push_back(QmvJob{s.down, two ? 2u : 1u, (uint32_t)(a * width), (uint32_t)(a * hidden),
+                                             pair_step * (int32_t)width, pair_step * (int32_t)hidden});
+                }
+            }
+            DM_HIP(launch_qmv8_grouped(ctx, gate_up_type, (uint32_t)width, (uint32_t)hidden, 1, up_offset,
+                                       gu_jobs.data(), gu_jobs.size(), x, d_act));
+            DM_HIP(launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(),
+                                       dn_jobs.size(), d_act, d_eo));
+            return release_slots(c, layer, group_slot.data(), group_slot.size());
+        }
         phase_tokens.emplace_back(order.size());
         std::vector<uint32_t> &tokens = phase_tokens.back();
         for (size_t q = 0; q < order.size(); q++) {
@@ -359,9 +435,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
             DM_CHECK_STATUS(enqueue_matvec(ctx, down_type, hidden, width, s.down, cnt,
                                            d_act + (p0 + q0) * width, d_eo + (p0 + q0) * hidden));
         }
-        for (size_t g = 0; g + 1 < group_start.size(); g++)
-            DM_CHECK_STATUS(release(c, layer, group_slot[g]));
-        return DMHIP_OK;
+        return release_slots(c, layer, group_slot.data(), group_slot.size());
     };
     for (size_t p = 0; p < pairs; p++) {
         // Would this acquire evict a slot the open phase still needs?  Check
@@ -393,9 +467,10 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     DM_CHECK_STATUS(run_phase(begin, pairs));
 
     // 3. Ordered combine and copy out.
-    DM_HIP(hipMemcpyAsync(d_pos, pos.data(), pairs * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (!grouped) DM_HIP(hipMemcpyAsync(d_pos, pos.data(), pairs * 4, hipMemcpyHostToDevice, ctx->stream));
     hipLaunchKernelGGL(moe_combine_pos_kernel, dim3((uint32_t)((batch * hidden + 255) / 256)), dim3(256), 0,
-                       ctx->stream, d_eo, d_pos, d_probs, (uint32_t)batch, (uint32_t)k, (uint32_t)hidden, y);
+                       ctx->stream, d_eo, grouped ? nullptr : d_pos, d_probs, (uint32_t)batch, (uint32_t)k,
+                       (uint32_t)hidden, y);
     DM_HIP(hipGetLastError());
     DM_HIP(hipStreamSynchronize(ctx->stream));
     return DMHIP_OK;

@@ -75,8 +75,9 @@ __device__ __forceinline__ float combine8(i32x4 c) {
 
 namespace {
 
-// Activation records of TOK tokens written by the workgroup into LDS at
-// `rec` (record of block b, token t at (b * TOK + t) * REC).  Wave k handles
+// Activation records of TOK tokens (token t at x + t * x_stride) written by
+// the workgroup into LDS at `rec` (record of block b, token t at
+// (b * TOK + t) * REC).  Wave k handles
 // blocks k, k + WAVES, ...: lane l loads the four values of step t = l >> 4,
 // lane group g = (l >> 2) & 3, columns 4q .. 4q+3 (q = l & 3) of the block,
 // and the block gets its own power-of-two scale 2^e (max|x| 2^-e < 2^22 over
@@ -85,8 +86,8 @@ namespace {
 // every output of that token NaN.  With NORM each wave also leaves its part
 // of sum(x^2) per token in red_ss[tok * WAVES + wave].
 template <uint32_t TYPE, int TOK, uint32_t WAVES, bool NORM>
-__device__ __forceinline__ void build_records8(const float *__restrict__ x, uint32_t columns, uint8_t *rec,
-                                               float *red_ss) {
+__device__ __forceinline__ void build_records8(const float *__restrict__ x, int x_stride, uint32_t columns,
+                                               uint8_t *rec, float *red_ss) {
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t blocks = columns / 256;
@@ -95,7 +96,7 @@ __device__ __forceinline__ void build_records8(const float *__restrict__ x, uint
     for (int tok = 0; tok < TOK; tok++) {
         float ss = 0.0f;
         for (uint32_t b = wave; b < blocks; b += WAVES) {
-            const float *xb = x + (size_t)tok * columns + (size_t)b * 256 + column8<TYPE>(t, g, 4 * q);
+            const float *xb = x + (ptrdiff_t)tok * x_stride + (size_t)b * 256 + column8<TYPE>(t, g, 4 * q);
             float v[4];
             float mx = 0.0f;
             uint32_t bad = 0;
@@ -342,17 +343,20 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ6_K> &raw, const i32x4 *
 // Dynamic LDS: activation records | zeroed region | per-wave staging.
 // MODE 0: y = W x.  MODE 1 (one token): also one ArgmaxPartial per
 // workgroup in partials[blockIdx.x].  MODE 2: W (gate) and W2 (up) of the same
-// shape on RMSNorm(x) (unit weight, when `normalize`), y = silu(gate) * up.
+// shape on RMSNorm(x) (unit weight, when `normalize`), y = silu(gate) * up
+// with the stable sigmoid, or with `glm` the routed-expert form
+// gate / (1 + exp(-gate)) * up.
+// Token t reads x + t * x_stride and writes y + t * y_stride.
 // Register budget: 4 waves per SIMD (G <= 2) or 2 (G = 4), about what the
 // workgroup's LDS allows on a C2-sized row; a tighter budget makes the
 // compiler wait for each prefetch right after issuing it.
 // ---------------------------------------------------------------------------
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
-__global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
-    __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2))) qmv8_kernel(
-    const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows, uint32_t columns,
-    uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x, int normalize, float epsilon,
-    float *__restrict__ y, ArgmaxPartial *__restrict__ partials) {
+__device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
+                                          uint32_t rows, uint32_t columns, uint32_t row_bytes,
+                                          uint32_t total_bytes, const float *__restrict__ x, int x_stride,
+                                          int normalize, float epsilon, int glm, float *__restrict__ y,
+                                          int y_stride, ArgmaxPartial *__restrict__ partials) {
     constexpr uint32_t WAVES = S > 8 ? S : 8;
     constexpr int NM = MODE == 2 ? 2 : 1;  // weight matrices streamed
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
@@ -429,9 +433,9 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
 
     const bool norm = MODE == 2 && normalize;
     if (norm)
-        build_records8<TYPE, TOK, WAVES, true>(x, columns, (uint8_t *)lds8, red_ss);
+        build_records8<TYPE, TOK, WAVES, true>(x, x_stride, columns, (uint8_t *)lds8, red_ss);
     else
-        build_records8<TYPE, TOK, WAVES, false>(x, columns, (uint8_t *)lds8, red_ss);
+        build_records8<TYPE, TOK, WAVES, false>(x, x_stride, columns, (uint8_t *)lds8, red_ss);
     for (uint32_t i = threadIdx.x; i < kZero8 / 16; i += 64 * WAVES) lds8[rec_bytes / 16 + i] = i32x4{0, 0, 0, 0};
     __syncthreads();
     // Output scale per token: 1, or the RMSNorm factor (unit weight)
@@ -491,17 +495,22 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
             float v = (TOK == 1 || g == 0 ? acc[0][0] : acc[0][TOK - 1]) * ts;
             if constexpr (MODE == 2) {
                 const float u = (TOK == 1 || g == 0 ? acc[NM - 1][0] : acc[NM - 1][TOK - 1]) * ts;
-                // silu(gate) * up, stable sigmoid (src/qwen35/cpu.rs:982-993)
-                float sig;
-                if (v >= 0.0f) {
-                    sig = 1.0f / (1.0f + expf(-v));
+                if (glm) {
+                    // routed-expert activation (src/glm52/expert.rs:260-267)
+                    v = (v / (1.0f + expf(-v))) * u;
                 } else {
-                    const float ex = expf(v);
-                    sig = ex / (1.0f + ex);
+                    // silu(gate) * up, stable sigmoid (src/qwen35/cpu.rs:982-993)
+                    float sig;
+                    if (v >= 0.0f) {
+                        sig = 1.0f / (1.0f + expf(-v));
+                    } else {
+                        const float ex = expf(v);
+                        sig = ex / (1.0f + ex);
+                    }
+                    v = v * sig * u;
                 }
-                v = v * sig * u;
             }
-            y[(size_t)g * rows + row] = v;
+            y[(ptrdiff_t)g * y_stride + row] = v;
             if constexpr (MODE == 1) {
                 bad |= !__builtin_isfinite(v);
                 const uint64_t key = argmax_key(v, row);
@@ -603,6 +612,41 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
             partials[blockIdx.x] = p;
         }
     }
+}
+
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
+__global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
+    __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2))) qmv8_kernel(
+    const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows, uint32_t columns,
+    uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x, int normalize, float epsilon,
+    float *__restrict__ y, ArgmaxPartial *__restrict__ partials) {
+    qmv8_body<TYPE, S, MODE, TOK, G>(w, w2, rows, columns, row_bytes, total_bytes, x, (int)columns, normalize,
+                                     epsilon, 0, y, (int)rows, partials);
+}
+
+// Grouped launch over the routed-expert jobs of a MoE layer: job
+// blockIdx.y applies the matrix at jobs.job[j].w (and, in MODE 2, the up
+// matrix w2_offset bytes further) to TOK tokens at x + x_off, x_stride apart,
+// writing y + y_off, y_stride apart.  Every job has the same shape.
+struct Job8 {
+    uint64_t w;
+    uint32_t x_off, y_off;
+    int32_t x_stride, y_stride;
+};
+constexpr uint32_t kMaxJobs8 = 64;
+struct JobTable8 {
+    Job8 job[kMaxJobs8];
+};
+
+template <uint32_t TYPE, int S, int MODE, int TOK>
+__global__ void __launch_bounds__(64 * (S > 8 ? S : 8)) __attribute__((amdgpu_waves_per_eu(4)))
+    qmv8_grouped_kernel(JobTable8 jobs, uint32_t rows, uint32_t columns, uint32_t row_bytes,
+                        uint32_t total_bytes, uint64_t w2_offset, const float *__restrict__ x,
+                        float *__restrict__ y, int glm) {
+    const Job8 j = jobs.job[blockIdx.y];
+    const uint8_t *w = (const uint8_t *)j.w;
+    qmv8_body<TYPE, S, MODE, TOK, 1>(w, w + w2_offset, rows, columns, row_bytes, total_bytes, x + j.x_off,
+                                     j.x_stride, 0, 0.0f, glm, y + j.y_off, j.y_stride, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -734,6 +778,65 @@ hipError_t run8_g(dmhip_ctx *ctx, const Plan8 &p, const Args8 &a) {
     return run8_s<TYPE, MODE, TOK, 1>(ctx, p.s, a);
 }
 
+// Grouped jobs: one block per fetch (expert rows are short), and a split of
+// each tile's block groups that gives the whole launch about 4096 wave-tiles
+// with at least one group per wave.
+Plan8 plan8_grouped(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t mats,
+                    uint32_t jobs) {
+    static const int forced_s = env_int("DMHIP_QMV8_GROUPED_SPLIT");
+    Plan8 p;
+    p.g = 1;
+    const uint32_t tiles = (rows + 15) / 16, groups = columns / 256;
+    uint32_t s = 1;
+    if (forced_s == 1 || forced_s == 2 || forced_s == 4 || forced_s == 8) {
+        s = (uint32_t)forced_s;
+    } else {
+        while (s < 8 && (size_t)tiles * jobs * s < 4096 && groups >= 2 * s) s *= 2;
+    }
+    for (; s >= 1; s /= 2) {
+        const size_t stat = (s > 1 ? (size_t)8 * 64 * batch * mats * sizeof(float) : 4) + 768;
+        if (lds8_bytes(type, groups, batch, 8, 1, mats) + stat <= kMaxLds8) {
+            p.s = s;
+            return p;
+        }
+    }
+    p.s = 0;
+    return p;
+}
+
+template <uint32_t TYPE, int S, int MODE, int TOK>
+hipError_t run8_grouped(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, uint64_t up_offset,
+                        const JobTable8 &table, uint32_t count, const float *x, float *y) {
+    constexpr uint32_t WAVES = 8;
+    const uint32_t tiles = (rows + 15) / 16;
+    const uint32_t blocks = columns / 256;
+    const uint32_t row_bytes = blocks * (TYPE == kQ4_K ? 144u : 210u);
+    const size_t lds = lds8_bytes(TYPE, blocks, TOK, WAVES, 1, MODE == 2 ? 2u : 1u);
+    // S == 1: one tile per wave; S > 1: WAVES / S tiles per workgroup.
+    const uint32_t per = S == 1 ? WAVES : WAVES / S;
+    const uint32_t grid = (tiles + per - 1) / per;
+    auto kernel = qmv8_grouped_kernel<TYPE, S, MODE, TOK>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    KernelTimer timer(ctx);
+    hipLaunchKernelGGL(kernel, dim3(grid, count), dim3(64 * WAVES), lds, ctx->stream, table, rows, columns,
+                       row_bytes, row_bytes * rows, up_offset, x, y, MODE == 2 ? 1 : 0);
+    return hipGetLastError();
+}
+
+template <uint32_t TYPE, int MODE, int TOK>
+hipError_t run8_grouped_s(dmhip_ctx *ctx, uint32_t s, uint32_t rows, uint32_t columns, uint64_t up_offset,
+                          const JobTable8 &table, uint32_t count, const float *x, float *y) {
+    switch (s) {
+    case 1: return run8_grouped<TYPE, 1, MODE, TOK>(ctx, rows, columns, up_offset, table, count, x, y);
+    case 2: return run8_grouped<TYPE, 2, MODE, TOK>(ctx, rows, columns, up_offset, table, count, x, y);
+    case 4: return run8_grouped<TYPE, 4, MODE, TOK>(ctx, rows, columns, up_offset, table, count, x, y);
+    default: return run8_grouped<TYPE, 8, MODE, TOK>(ctx, rows, columns, up_offset, table, count, x, y);
+    }
+}
+
 template <uint32_t TYPE>
 hipError_t launch8(dmhip_ctx *ctx, uint32_t batch, int mode, const Args8 &a) {
     const Plan8 p = plan8(TYPE, a.rows, a.columns, batch, mode == 2 ? 2u : 1u);
@@ -771,6 +874,51 @@ hipError_t launch_qmv8_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uin
     const Args8 a{rows, columns, gate, up, x, normalize, epsilon, act, nullptr, nullptr};
     if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, 2, a);
     return launch8<kQ6_K>(ctx, batch, 2, a);
+}
+
+bool qmv8_grouped_supported(uint32_t type, size_t rows, size_t columns, uint32_t mats) {
+    if (type != kQ4_K && type != kQ6_K) return false;
+    if (columns % 256 || columns == 0 || rows == 0 || columns > 0xffffffffull || rows > 0xffffffffull)
+        return false;
+    const uint64_t bytes = (uint64_t)rows * (columns / 256) * (type == kQ4_K ? 144u : 210u);
+    if (bytes * mats >= (1ull << 32)) return false;
+    return plan8_grouped(type, (uint32_t)rows, (uint32_t)columns, 2, mats, 1).s != 0;
+}
+
+hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, int gate_up,
+                               uint64_t up_offset, const QmvJob *jobs, size_t count, const float *x, float *y) {
+    const uint32_t mats = gate_up ? 2u : 1u;
+    // Jobs of one and of two tokens go to separate launches, kMaxJobs8 each.
+    for (uint32_t tok = 1; tok <= 2; tok++) {
+        size_t i = 0;
+        while (i < count) {
+            JobTable8 table;
+            uint32_t n = 0;
+            for (; i < count && n < kMaxJobs8; i++) {
+                const QmvJob &j = jobs[i];
+                if (j.tokens != tok) continue;
+                table.job[n++] = Job8{(uint64_t)(uintptr_t)j.w, j.x_off, j.y_off, j.x_stride, j.y_stride};
+            }
+            if (n == 0) continue;
+            // the split is planned for the jobs of this launch
+            const Plan8 p = plan8_grouped(type, rows, columns, tok, mats, n);
+            if (p.s == 0) return hipErrorInvalidValue;
+            hipError_t e;
+            if (type == kQ4_K) {
+                e = gate_up ? (tok == 1 ? run8_grouped_s<kQ4_K, 2, 1>(ctx, p.s, rows, columns, up_offset, table, n, x, y)
+                                        : run8_grouped_s<kQ4_K, 2, 2>(ctx, p.s, rows, columns, up_offset, table, n, x, y))
+                            : (tok == 1 ? run8_grouped_s<kQ4_K, 0, 1>(ctx, p.s, rows, columns, 0, table, n, x, y)
+                                        : run8_grouped_s<kQ4_K, 0, 2>(ctx, p.s, rows, columns, 0, table, n, x, y));
+            } else {
+                e = gate_up ? (tok == 1 ? run8_grouped_s<kQ6_K, 2, 1>(ctx, p.s, rows, columns, up_offset, table, n, x, y)
+                                        : run8_grouped_s<kQ6_K, 2, 2>(ctx, p.s, rows, columns, up_offset, table, n, x, y))
+                            : (tok == 1 ? run8_grouped_s<kQ6_K, 0, 1>(ctx, p.s, rows, columns, 0, table, n, x, y)
+                                        : run8_grouped_s<kQ6_K, 0, 2>(ctx, p.s, rows, columns, 0, table, n, x, y));
+            }
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
 }
 
 }  // namespace dm

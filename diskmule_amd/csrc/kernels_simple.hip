@@ -225,6 +225,135 @@ __global__ void __launch_bounds__(256) router_top_k_kernel(
                 non_finite);
 }
 
+// The same router with the rows staged through LDS (at most 256 experts,
+// hidden % 8 == 0, 16-byte aligned router and x).  Lane r still folds row r
+// sequentially from column 0, so the logits are those of the kernel above;
+// what changes is the memory path.  The columns go in chunks of CC: every
+// thread loads 16-byte pieces of the chunk (rows of the workgroup's experts,
+// then the chunk's x values) into registers and stores them to one of two
+// LDS slots; three chunks are in flight while one is folded.  A
+// row occupies CC * 2 + 16 bytes of its slot, so the 16-byte reads of
+// consecutive lanes fall in distinct banks.  With host_ids/host_probs the
+// selection is also written to (pinned) host memory.
+typedef uint32_t v4a __attribute__((ext_vector_type(4)));  // 16-byte aligned
+
+template <uint32_t CC>
+__global__ void __launch_bounds__(256) router_staged_kernel(
+    const uint16_t *__restrict__ router, uint32_t hidden, uint32_t experts, uint32_t k,
+    const float *__restrict__ x, float *__restrict__ logits, uint32_t *ids, float *probabilities,
+    uint32_t *non_finite, uint32_t *host_ids, float *host_probs) {
+    constexpr uint32_t ROW = CC * 2 + 16;  // LDS bytes per expert row
+    constexpr uint32_t PR = CC * 2 / 16;   // 16-byte pieces of a row per chunk
+    constexpr uint32_t XP = CC * 4 / 16;   // 16-byte pieces of x per chunk
+    constexpr uint32_t NP = 8;             // pieces per thread: rows of up to 2048 / PR experts
+    extern __shared__ v4a r_stage[];
+    __shared__ float s_logits[256];
+    const uint32_t token = blockIdx.x, tid = threadIdx.x;
+    const uint32_t E = experts;
+    const uint32_t slot_bytes = (E * ROW + CC * 4 + 15) & ~15u;
+    const uint32_t chunks = (hidden + CC - 1) / CC;
+    const float *xt = x + (size_t)token * hidden;
+
+    // Buffer loads: a piece past the router or past x reads zeros, so every
+    // thread issues the same loads for every chunk (no branches around them,
+    // which lets the compiler wait for one register set while the next two
+    // stay in flight).  Pieces of rows >= E start at `nowhere`.
+    constexpr uint32_t nowhere = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(router, E * hidden * 2);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xt, hidden * 4);
+    uint32_t woff[NP];
+#pragma unroll
+    for (uint32_t j = 0; j < NP; j++) {
+        const uint32_t item = j * 256 + tid, row = item / PR, p = item % PR;
+        woff[j] = row < E ? row * hidden * 2 + 16 * p : nowhere;
+    }
+    const uint32_t xoff = 16 * (tid % XP);
+    auto load = [&](v4a (&wr)[NP], v4a &xr, uint32_t chunk) {
+        const uint32_t c0 = chunk * CC;
+#pragma unroll
+        for (uint32_t j = 0; j < NP; j++)
+            wr[j] = __builtin_bit_cast(v4a, rsrc_load16(rw, woff[j] + 2 * c0));
+        xr = __builtin_bit_cast(v4a, rsrc_load16(rx, xoff + 4 * c0));
+    };
+    auto store = [&](const v4a (&wr)[NP], const v4a &xr, uint32_t slot) {
+        uint8_t *s = (uint8_t *)r_stage + slot * slot_bytes;
+#pragma unroll
+        for (uint32_t j = 0; j < NP; j++) {
+            const uint32_t item = j * 256 + tid, row = item / PR, p = item % PR;
+            if (row < E) *(v4a *)(s + row * ROW + 16 * p) = wr[j];
+        }
+        if (tid < XP) *(v4a *)(s + E * ROW + 16 * tid) = xr;
+    };
+
+    float acc = 0.0f;
+    auto fold = [&](uint32_t slot, uint32_t chunk) {
+        const uint8_t *s = (const uint8_t *)r_stage + slot * slot_bytes;
+        const v4a *wrow = (const v4a *)(s + tid * ROW);
+        const float *xs = (const float *)(s + E * ROW);
+        const uint32_t n = hidden - chunk * CC < CC ? hidden - chunk * CC : CC;
+        if (n == CC) {
+            // The whole chunk of the row and of x first (one LDS wait per
+            // chunk), then the dependent chain of CC fmas.
+            v4a wv[PR], xv[2 * PR];
+#pragma unroll
+            for (uint32_t q = 0; q < PR; q++) wv[q] = wrow[q];
+#pragma unroll
+            for (uint32_t q = 0; q < 2 * PR; q++) xv[q] = *(const v4a *)(xs + 4 * q);
+#pragma unroll
+            for (uint32_t q = 0; q < PR; q++) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const v4a xq = xv[2 * q + (j >> 1)];
+                    const float xa = __uint_as_float(xq[2 * (j & 1)]);
+                    const float xb = __uint_as_float(xq[2 * (j & 1) + 1]);
+                    acc = __builtin_fmaf(__uint_as_float(wv[q][j] << 16), xa, acc);
+                    acc = __builtin_fmaf(__uint_as_float(wv[q][j] & 0xffff0000u), xb, acc);
+                }
+            }
+        } else {
+            const uint16_t *wh = (const uint16_t *)wrow;
+            for (uint32_t c = 0; c < n; c++) acc = __builtin_fmaf(__uint_as_float((uint32_t)wh[c] << 16), xs[c], acc);
+        }
+    };
+
+    // Three register sets rotate: while chunk c is folded from LDS slot c % 2,
+    // chunks c + 1 .. c + 3 are in flight.  After the fold, chunk c + 1 goes
+    // to the other slot (last read by the fold of chunk c - 1, before the
+    // previous barrier) and its registers take chunk c + 4.
+    v4a ra[NP], rb[NP], rc[NP], xa, xb, xc;
+    load(ra, xa, 0);
+    load(rb, xb, 1);
+    load(rc, xc, 2);
+    store(ra, xa, 0);
+    __syncthreads();
+    load(ra, xa, 3);
+    auto step = [&](uint32_t c, v4a (&wr)[NP], v4a &xr) {
+        if (c < chunks && tid < E) fold(c & 1u, c);
+        store(wr, xr, (c + 1) & 1u);
+        __syncthreads();
+        load(wr, xr, c + 4);
+    };
+    for (uint32_t i = 0; i < chunks; i += 3) {
+        step(i, rb, xb);
+        step(i + 1, rc, xc);
+        step(i + 2, ra, xa);
+    }
+    if (tid < E) {
+        logits[(size_t)token * E + tid] = acc;
+        s_logits[tid] = acc;
+    }
+    __syncthreads();
+    uint32_t *ti = ids + (size_t)token * k;
+    float *tp = probabilities + (size_t)token * k;
+    block_top_k(s_logits, E, k, ti, tp, non_finite);
+    if (host_ids && tid == 0) {
+        for (uint32_t s = 0; s < k; s++) {
+            host_ids[(size_t)token * k + s] = ti[s];
+            host_probs[(size_t)token * k + s] = tp[s];
+        }
+    }
+}
+
 // ---- RMSNorm (src/cpu.rs:98-142) ---------------------------------------
 __global__ void __launch_bounds__(256) rms_norm_kernel(const float *__restrict__ in, uint32_t n,
                                                        const float *__restrict__ weight, float eps,
@@ -367,14 +496,45 @@ hipError_t launch_top_k(hipStream_t s, const float *logits, uint32_t rows, uint3
     return hipGetLastError();
 }
 
+template <uint32_t CC>
+static hipError_t launch_router_staged(hipStream_t s, const uint16_t *router, uint32_t hidden,
+                                       uint32_t experts, uint32_t k, uint32_t batch, const float *x,
+                                       float *logits, uint32_t *ids, float *probabilities,
+                                       uint32_t *non_finite, uint32_t *host_ids, float *host_probs) {
+    const size_t lds = 2 * (((size_t)experts * (CC * 2 + 16) + CC * 4 + 15) & ~(size_t)15);
+    static bool attribute_set = false;  // the largest slot ring, set once
+    if (!attribute_set) {
+        const size_t most = 2 * (((size_t)(2048 / (CC / 8)) * (CC * 2 + 16) + CC * 4 + 15) & ~(size_t)15);
+        hipError_t e = hipFuncSetAttribute((const void *)router_staged_kernel<CC>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)most);
+        if (e != hipSuccess) return e;
+        attribute_set = true;
+    }
+    hipLaunchKernelGGL(router_staged_kernel<CC>, dim3(batch), dim3(256), lds, s, router, hidden, experts, k, x,
+                       logits, ids, probabilities, non_finite, host_ids, host_probs);
+    return hipGetLastError();
+}
+
 hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
-                               uint32_t *non_finite) {
+                               uint32_t *non_finite, uint32_t *host_ids, float *host_probs) {
+    const bool staged = experts <= 256 && hidden % 8 == 0 && (uint64_t)experts * hidden * 2 < (1ull << 30) && ((uintptr_t)router & 15u) == 0 &&
+                        ((uintptr_t)x & 15u) == 0;
+    if (staged && experts <= 128)
+        return launch_router_staged<128>(s, router, hidden, experts, k, batch, x, logits, ids, probabilities,
+                                         non_finite, host_ids, host_probs);
+    if (staged)
+        return launch_router_staged<64>(s, router, hidden, experts, k, batch, x, logits, ids, probabilities,
+                                        non_finite, host_ids, host_probs);
     hipLaunchKernelGGL(router_top_k_kernel, dim3(batch), dim3(256), experts * sizeof(float), s,
                        router, hidden, experts,
                        k, x, logits, ids, probabilities, non_finite);
-    return hipGetLastError();
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !host_ids) return e;
+    e = hipMemcpyAsync(host_ids, ids, (size_t)batch * k * 4, hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) return e;
+    return hipMemcpyAsync(host_probs, probabilities, (size_t)batch * k * 4, hipMemcpyDeviceToHost, s);
 }
 
 hipError_t launch_rms_norm(hipStream_t s, const float *in, uint32_t batch, uint32_t n,

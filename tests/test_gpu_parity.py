@@ -303,6 +303,32 @@ def _moe_setup(hidden=2048, width=768, experts=128):
     return router, gu, dn, gu_bytes, dn_bytes
 
 
+@pytest.mark.parametrize("batch,hidden,experts,k", [(1, 2048, 128, 8), (5, 2048, 128, 8), (2, 1000, 60, 4),
+                                                    (3, 2824, 128, 8), (2, 4096, 256, 8), (2, 1016, 200, 6),
+                                                    (1, 2050, 128, 8), (1, 512, 300, 8)])
+def test_router_top_k_is_bit_exact(ctx, batch, hidden, experts, k):
+    """The bf16 router fold (src/cpu.rs:384-397 order) and top-k: logits bit
+    for bit, ids exact.  Covers the LDS-staged kernel's 128- and 64-column
+    chunks, partial last chunks, expert counts below a wave, and the
+    unstaged kernel (hidden % 8 != 0, more than 256 experts)."""
+    print(f"router batch={batch} hidden={hidden} experts={experts} k={k}", flush=True)
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(6, hidden), experts * hidden) * np.float32(0.02))
+    x = synth.normal(synth.activation_seed(6, experts), batch * hidden).reshape(batch, hidden)
+    rb, xb = dev(ctx, router), dev(ctx, x)
+    lb, ib, pb = dev_out(ctx, batch * experts * 4), dev_out(ctx, batch * k * 4), dev_out(ctx, batch * k * 4)
+    ctx.router_top_k_device(batch, hidden, experts, k, rb.device_ptr, xb.device_ptr, lb.device_ptr,
+                            ib.device_ptr, pb.device_ptr)
+    logits = lb.read(0, batch * experts * 4, np.float32).reshape(batch, experts)
+    ids = ib.read(0, batch * k * 4, np.uint32).reshape(batch, k)
+    probs = pb.read(0, batch * k * 4, np.float32).reshape(batch, k)
+    for t in range(batch):
+        want = capi.matvec_bf16(experts, hidden, router, x[t])
+        assert np.array_equal(bits(logits[t]), bits(want)), f"token {t} logits"
+        top = capi.top_k_softmax(want, k)
+        assert ids[t].tolist() == [e for e, _ in top]
+        assert np.allclose(probs[t], [p for _, p in top], rtol=1e-6)
+
+
 def test_expert_cache_known_answer(ctx, golden):
     """src/expert.rs:266-325 through the HIP slots."""
     c = golden[0]["expert_lru"]

@@ -19,9 +19,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
-# The GEMM rescales its MFMA accumulators every block with VALU FMAs; keeping
-# them in VGPRs (not AGPRs) avoids a copy in and out per element.
-SOURCE_FLAGS = {"kernels_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Extra hipcc flags per source file (none at present).
+SOURCE_FLAGS: dict = {}
 
 
 def build(verbose: bool = False, jobs: int = 6) -> str:

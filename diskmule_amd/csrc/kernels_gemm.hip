@@ -3,66 +3,110 @@
 // A is bf16 activations [m][k]; W is n encoded rows of k columns.  The
 // reference has no batched prefill: it runs one matvec per token
 // (src/gemma4/metal.rs:514-536), so the result for token m must match
-// cpu::matvec(W, widen(A[m])) (src/cpu.rs:345-399) within fp32 tolerance.
+// cpu::matvec(W, widen(A[m])) (src/cpu.rs:345-399) within the GEMM tolerance
+// (max |c - r| <= 1e-3 max |r|, cosine >= 0.99999).
 //
-// Q4_K weights run on v_mfma_f32_32x32x16_f16 with exact fp16 operands and
-// fp32 accumulation:
+// Q4_K weights run on v_mfma_f32_32x32x16_f16 with fp32 accumulation after
+// an on-the-fly dequantization to fp16:
 //  * A: each row is scaled by a power of two 2^-e (max|a| 2^-e in
 //    [2^14, 2^15)) and converted to fp16.  bf16 carries 8 significant bits, so
-//    the conversion is exact for every value above 2^-17 of the row maximum.
-//  * W: each weight enters as the fp16 integer sc*q (0..945), built from the
-//    nibble with the "1024 + q" exponent trick and one packed fp16 FMA.  The
-//    fp32 partial of every 256-column block is then multiplied by d.
-//  * Q4_K's "- dmin * m * sum(a)" term: one extra MFMA per block whose B
-//    holds 64 m of the 8 sub-blocks (twice: hi and lo) and whose A holds the
-//    sub-block sums of the scaled row times 2^-6 as fp16 hi/lo pairs; the
-//    result is multiplied by dmin.
+//    the conversion is exact for every value above 2^-17 of the row maximum;
+//    the output is multiplied back by 2^e.
+//  * W: weight q of sub-block j is fma(q, fp16(d sc_j), fp16(-dmin m_j)) in
+//    fp16 (src/cpu.rs:585-605 computes the same value in fp32).  The nibble q
+//    is read as an fp8 e4m3 code (codes 0..15 are q * 2^-9 exactly) by
+//    v_cvt_scalef32_pk_f16_fp8 with scale 2^9; one packed fp16 FMA then
+//    gives two weights.  The roundings of d sc_j, dmin m_j and of the weight
+//    to fp16 leave a few 1e-4 of max |r| on seeded Q4_K data.
+// The sum over K is order-free, so K is permuted once for both operands: in
+// MFMA step s of a block, lane half h holds the low and high nibbles of qs
+// bytes 64h + 4s .. 64h + 4s + 3, and A is stored in that order.
 // Other weight types take the decode-GEMV path in chunks of 16 tokens.
 //
-// Tiling: a workgroup (8 waves) owns a 64 x 128 tile of C; each group of 4
-// waves forms a 2 x 2 grid of 32 x 64 sub-tiles (two 32x32 MFMA tiles each)
-// and takes every other K-step.  K advances in
-// stages of 128 columns (half a Q4_K block): the stage's A rows and
-// dequantized W rows go to padded LDS rows (272 B: the 16 lanes of a 128-bit
-// read hit 64 distinct banks), double-buffered so that dequantizing the next
-// stage overlaps the MFMAs of this one.  Workgroups that work on the same 64
-// rows of A run on the same XCD.
+// Tiling: a workgroup (4 waves, one per SIMD) owns a 64 x 128 tile of C and
+// each wave computes the whole tile over every fourth Q4_K block, so every
+// element of A and W is read by exactly one wave and no operand is shared
+// through LDS.  A comes from global memory already in MFMA fragment order
+// (one 1 KiB load per 32 rows and step); a wave stages its W block (128 rows
+// x 144 bytes, contiguous 16-byte loads) in its own LDS area and
+// dequantizes from there, with the next block's W in flight in registers.
+// The accumulators stay in AGPRs for the whole K loop; the four partial
+// tiles are added through LDS at the end.  Workgroups that work on the same
+// 64 rows of A run on the same XCD.
 #include "dm_device.h"
 #include "dm_qmv.h"
 #include "runtime.h"
-
-#include <type_traits>
 
 namespace dm {
 
 namespace {
 
-constexpr uint32_t kBM = 64, kBN = 128, kStage = 128;
-constexpr uint32_t kLd = kStage + 8;  // halves per LDS row (272 B)
+constexpr uint32_t kBM = 64, kBN = 128;
+constexpr uint32_t kKSplit = 4, kNHalves = 2, kWaves = kKSplit * kNHalves;  // two waves per SIMD
+constexpr uint32_t kWN = kBN / kNHalves;  // columns of a wave's tile
+// MFMA steps between the load of an A fragment and its use.  Loads complete
+// in order, so this is also the time every W load has to arrive.
+constexpr uint32_t kADist = 4;
+static_assert(16 % kADist == 0, "the A ring repeats every block");
+constexpr uint32_t kStageBytes = kWN * 144;              // one Q4_K block of a wave's W rows
+constexpr uint32_t kStageLoads = kStageBytes / 16 / 64;  // 16-byte loads per lane
+constexpr uint32_t kRedLd = kWN + 4;                     // floats per row of a partial tile in LDS
+constexpr uint32_t kLdsBytes = kWaves * kBM * kRedLd * 4;  // partial tiles of the final sum
+static_assert(kWaves * kStageBytes <= kLdsBytes, "the W staging areas fit in the reduction area");
+static_assert(kStageBytes % 1024 == 0, "whole staging loads");
 
-__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
-__device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 16-byte aligned
 
 __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// First column (within its block) of the 8 columns of MFMA step s, lane half
+// h: columns base .. base + 3 and base + 32 .. base + 35.
+__device__ __forceinline__ uint32_t frag_base(uint32_t s, uint32_t h) { return 64 * (2 * h + s / 8) + 4 * (s % 8); }
+
+// Per sub-block fp16 pairs (d sc, d sc) and (-dmin m, -dmin m).
+struct SubScale {
+    half2_t mul, add;
+};
+
+__device__ __forceinline__ SubScale sub_scale(float d, float dmin, uint32_t sc, uint32_t mn) {
+    const _Float16 a = (_Float16)(d * (float)sc), b = (_Float16)(-dmin * (float)mn);
+    return SubScale{half2_t{a, a}, half2_t{b, b}};
+}
+
+// The 8 weights of one qs dword: low nibbles of its 4 bytes (sub-block
+// scale lo), then high nibbles (hi).
+template <bool HIGH_WORD>
+__device__ __forceinline__ half2_t q_pair(uint32_t v) {
+    return __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v, 512.0f, HIGH_WORD));
+}
+
+__device__ __forceinline__ half8 dequant8(uint32_t dw, const SubScale &lo, const SubScale &hi) {
+    const uint32_t l4 = dw & 0x0f0f0f0fu, h4 = (dw >> 4) & 0x0f0f0f0fu;
+    const half2_t a0 = __builtin_elementwise_fma(q_pair<false>(l4), lo.mul, lo.add);
+    const half2_t a1 = __builtin_elementwise_fma(q_pair<true>(l4), lo.mul, lo.add);
+    const half2_t a2 = __builtin_elementwise_fma(q_pair<false>(h4), hi.mul, hi.add);
+    const half2_t a3 = __builtin_elementwise_fma(q_pair<true>(h4), hi.mul, hi.add);
+    return half8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// A preparation: one workgroup per row of the padded workspace.
-//   a16[m][k]      fp16 of A[m][k] * 2^-e_m (zero rows beyond M)
-//   sums[m][b][16] sub-block sums of the scaled row * 2^-6 as (hi, lo) fp16
-//   rowscale[m]    2^e_m
+// A preparation: one workgroup per row of the padded workspace (rows beyond
+// M are zero).  For the 32-row tile T = m / 32 and lane l = m % 32 + 32 h:
+//   a16[((T * blocks + b) * 16 + s) * 64 + l]  half8: A[m][k] * 2^-e_m at
+//       the 8 columns of step s, half h of block b (frag_base)
+//   rowscale[m]                                2^e_m
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) gemm_prep_kernel(const uint16_t *__restrict__ a, uint32_t m_rows,
-                                                        uint32_t k, _Float16 *__restrict__ a16,
-                                                        _Float16 *__restrict__ sums, float *__restrict__ rowscale) {
+                                                        uint32_t k, half8 *__restrict__ a16,
+                                                        float *__restrict__ rowscale) {
     __shared__ float red[4];
     const uint32_t m = blockIdx.x, tid = threadIdx.x;
     const bool live = m < m_rows;
     const uint16_t *row = a + (size_t)m * k;
-    // chunk c (8 consecutive values) = tid + 256 r
     float mx = 0.0f;
     for (uint32_t c = tid; c < k / 8; c += 256) {
         if (!live) break;
@@ -87,299 +131,243 @@ __global__ void __launch_bounds__(256) gemm_prep_kernel(const uint16_t *__restri
     }
     const float down = ldexpf(1.0f, -e);
     if (tid == 0) rowscale[m] = live ? ldexpf(1.0f, e) : 0.0f;
-    const uint32_t blocks = k / 256;
-    for (uint32_t c = tid; c < k / 8; c += 256) {
-        float v[8];
+    const uint32_t blocks = k / 256, tile = m / 32, l0 = m % 32;
+    // fragment f = (2 b + h) * 16 + s
+    for (uint32_t f = tid; f < blocks * 32; f += 256) {
+        const uint32_t b = f / 32, h = (f / 16) & 1u, s = f & 15u;
+        half8 v;
         if (live) {
-            const u32x4 raw = *(const u32x4 *)(row + 8 * c);
+            const uint16_t *p = row + b * 256 + frag_base(s, h);
+            const u32x2 x0 = *(const u32x2 *)p, x1 = *(const u32x2 *)(p + 32);
+            const uint32_t u[4] = {x0[0], x0[1], x1[0], x1[1]};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                v[2 * i] = __uint_as_float(raw[i] << 16) * down;
-                v[2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u) * down;
+                v[2 * i] = (_Float16)(__uint_as_float(u[i] << 16) * down);
+                v[2 * i + 1] = (_Float16)(__uint_as_float(u[i] & 0xffff0000u) * down);
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = 0.0f;
+            for (int i = 0; i < 8; i++) v[i] = (_Float16)0.0f;
         }
-        half8 h;
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            h[i] = (_Float16)v[i];
-            s += v[i];
-        }
-        *(half8 *)(a16 + (size_t)m * k + 8 * c) = h;
-        // a 32-value sub-block is four consecutive chunks (threads 4j .. 4j+3)
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        if ((tid & 3u) == 0) {
-            const uint32_t sb = c / 4, b = sb / 8, j = sb % 8;
-            const float scaled = s * 0.015625f;  // 2^-6 keeps |sum| inside fp16
-            const _Float16 hi = (_Float16)scaled;
-            const _Float16 lo = (_Float16)(scaled - (float)hi);
-            _Float16 *dst = sums + ((size_t)m * blocks + b) * 16 + 2 * j;
-            dst[0] = hi;
-            dst[1] = lo;
-        }
+        a16[((size_t)(tile * blocks + b) * 16 + s) * 64 + l0 + 32 * h] = v;
     }
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K GEMM main kernel.  Grid: one workgroup (8 waves) per 64 x 128 tile of
-// C.  Waves 0-3 and 4-7 form two groups with the same 2 x 2 layout of 32 x 64
-// sub-tiles; group g takes the K-steps of parity g of every stage, and the
-// two partial tiles are added at the end (two waves per SIMD, half the
-// dequantization per thread).  LDS is double-buffered by stage: while the
-// MFMAs of stage s read buffer s & 1, the waves dequantize stage s + 1 from
-// registers into the other buffer, and the loads of stage s + 3 are in
-// flight.  One barrier per stage.
+// Q4_K GEMM main kernel.  Grid: one workgroup (8 waves, two per SIMD) per
+// 64 x 128 tile of C.  Wave w owns the 64 x 64 half w / 4 of the tile over
+// blocks w % 4, w % 4 + 4, ...  A lone wave issues VALU work at half the
+// SIMD's rate, and the dequantization is VALU work: the second wave of each
+// SIMD supplies the other half while the MFMAs run.  Per block and wave: 16
+// MFMA steps of 4 MFMAs (2 row x 2 column 32 x 32 tiles), the A fragments of
+// step s + kADist in flight during step s, the W block read from the wave's
+// LDS area (the next block's W arrives in registers meanwhile).
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(512) gemm_q4k_kernel(const _Float16 *__restrict__ a16,
-                                                       const _Float16 *__restrict__ sums,
-                                                       const float *__restrict__ rowscale,
-                                                       const uint8_t *__restrict__ w, uint32_t m_rows,
-                                                       uint32_t n_rows, uint32_t k, uint32_t w_bytes,
-                                                       uint32_t m_tiles, float *__restrict__ c) {
-    __shared__ __attribute__((aligned(16))) _Float16 sA[2][kBM * kLd];
-    __shared__ __attribute__((aligned(16))) _Float16 sW[2][kBN * kLd];
-    // per block (double-buffered by block parity): sub-block sums (hi, lo),
-    // 64 m duplicated for hi and lo, d and dmin
-    __shared__ __attribute__((aligned(16))) _Float16 sA2[2][kBM * 16];
-    __shared__ __attribute__((aligned(16))) _Float16 sB2[2][kBN * 16];
-    __shared__ float sD[2][kBN], sDmin[2][kBN];
-
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t grp = wave >> 2, wm = wave & 1u, wn = (wave >> 1) & 1u;
-    // Tile order: the 8 XCDs take workgroups round-robin, so with m-tile =
-    // id % m_tiles and 8 m-tiles (M = 512) each XCD keeps one 64-row slice of
-    // A (512 KB) in its L2 while W streams past it.
-    const uint32_t id = blockIdx.x;
-    const uint32_t mt = id % m_tiles, nt = id / m_tiles;
-    const uint32_t m0 = mt * kBM, n0 = nt * kBN;
-    const uint32_t blocks = k / 256, stages = 2 * blocks;
-    const uint32_t row_bytes = blocks * 144;
-
-    const uint32_t records = (w_bytes + 3u) & ~3u;
-    const uint32_t nowhere = records + 256;
-    const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(w, records);
-
-    // loader roles (per stage of 128 columns)
-    const uint32_t a_row = tid >> 3, a_part = tid & 7u;  // 64 rows x 8 parts of 16 halves
-    const uint32_t w_row = tid >> 2, w_q = tid & 3u;     // 128 rows x 4 quarters of the stage's qs
-    const uint32_t w_base = n0 + w_row < n_rows ? (n0 + w_row) * row_bytes : nowhere;
-    const _Float16 *a_src = a16 + (size_t)(m0 + a_row) * k + 16 * a_part;
-
-    struct Regs {
-        u32x4 a[2];  // 16 halves of A
-        u32x4 q;     // 16 qs bytes: 64 hb + 16 w_q .. + 16
-        u32x4 hdr;   // d | dmin | scales
-        u32x4 s;     // 8 halves of the block's sub-block sums
-    };
-    auto fetch = [&](uint32_t s, Regs &r) {
-        const uint32_t b = s >> 1, hb = s & 1u;
-        const u32x4 *ap = (const u32x4 *)(a_src + b * 256 + hb * 128);
-        r.a[0] = ap[0];
-        r.a[1] = ap[1];
-        const uint32_t off = w_base == nowhere ? nowhere : w_base + b * 144;
-        r.hdr = rsrc_load16(rsrc, off);
-        r.q = rsrc_load16(rsrc, off == nowhere ? nowhere : off + 16 + 64 * hb + 16 * w_q);
-        // every thread loads (threads >= 128 duplicate threads 0..127), so the
-        // loop has no divergent branch around a load
-        r.s = *(const u32x4 *)(sums + ((size_t)(m0 + ((tid & 127u) >> 1)) * blocks + b) * 16 + 8 * (tid & 1u));
-    };
-
-    // Branch-free 6-bit (scale, min) of sub-block sb of a Q4_K block
-    // (src/cpu.rs:607-616): for sb < 4 the low 6 bits of scales[sb] and
-    // scales[sb+4]; for sb >= 4 nibbles of scales[sb+4] with the top bits of
-    // scales[sb-4] and scales[sb].
-    auto scale_min = [](const u32x4 &hdr, uint32_t sb, uint32_t &sc, uint32_t &mn) {
-        const uint32_t sh = 8 * (sb & 3u);
-        const uint32_t b1 = hdr[1] >> sh, b2 = hdr[2] >> sh, b3 = hdr[3] >> sh;
-        const uint32_t hi_mask = 0u - (uint32_t)(sb >= 4);
-        const uint32_t sc_lo = b1 & 63u, sc_hi = (b3 & 15u) | ((b1 >> 2) & 0x30u);
-        const uint32_t mn_lo = b2 & 63u, mn_hi = ((b3 >> 4) & 15u) | ((b2 >> 2) & 0x30u);
-        sc = sc_lo ^ ((sc_lo ^ sc_hi) & hi_mask);
-        mn = mn_lo ^ ((mn_lo ^ mn_hi) & hi_mask);
-    };
-
-    constexpr uint32_t kBias = 0x64646464u;  // source of the 0x64 high bytes ("1024 + q")
-    // The thread's 16 qs bytes belong to sub-block pair j = 2 hb + (w_q >> 1):
-    // low nibbles are sub-block 2j at stage columns 64 (w_q >> 1) + 16 (w_q & 1)
-    // + i, high nibbles sub-block 2j + 1 at the same columns + 32.
-    struct Scales {
-        half2_t scl[2], bias[2];
-    };
-    auto scales = [&](auto hb_c, const Regs &r) {
-        constexpr uint32_t hb = decltype(hb_c)::value;
-        const uint32_t j = 2 * hb + (w_q >> 1);
-        Scales out;
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-            uint32_t sc, mn;
-            scale_min(r.hdr, 2 * j + t, sc, mn);
-            const _Float16 f = (_Float16)(short)sc;
-            out.scl[t] = half2_t{f, f};
-            out.bias[t] = out.scl[t] * half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
-        }
-        return out;
-    };
-    // Piece p (0, 1) dequantizes qs dwords 2p, 2p + 1 (16 weights); piece 1
-    // also copies A and, at the first stage of a block, the block data.
-    auto store_piece = [&](auto hb_c, auto p_c, uint32_t s, const Regs &r, const Scales &sv) {
-        constexpr uint32_t hb = decltype(hb_c)::value;
-        constexpr int p = decltype(p_c)::value;
-        const uint32_t buf = hb, bb = (s >> 1) & 1u;
-        _Float16 *wd = sW[buf] + w_row * kLd + 64 * (w_q >> 1) + 16 * (w_q & 1u) + 8 * p;
-        uint32_t lo[4], hi[4];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const uint32_t d = r.q[2 * p + u];
-            const uint32_t l4 = d & 0x0f0f0f0fu, h4 = (d >> 4) & 0x0f0f0f0fu;
-            lo[2 * u] = as_u(__builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(l4, kBias, 0x00050004u)), sv.scl[0], sv.bias[0]));
-            lo[2 * u + 1] = as_u(__builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(l4, kBias, 0x00070006u)), sv.scl[0], sv.bias[0]));
-            hi[2 * u] = as_u(__builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(h4, kBias, 0x00050004u)), sv.scl[1], sv.bias[1]));
-            hi[2 * u + 1] = as_u(__builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(h4, kBias, 0x00070006u)), sv.scl[1], sv.bias[1]));
-        }
-        *(u32x4 *)wd = u32x4{lo[0], lo[1], lo[2], lo[3]};
-        *(u32x4 *)(wd + 32) = u32x4{hi[0], hi[1], hi[2], hi[3]};
-        if constexpr (p == 1) {
-            u32x4 *ad = (u32x4 *)(sA[buf] + a_row * kLd + 16 * a_part);
-            ad[0] = r.a[0];
-            ad[1] = r.a[1];
-            if constexpr (hb == 0) {
-                // per block: d, dmin, the 64 m row of the min step, the sums
-                sD[bb][w_row] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.hdr[0] & 0xffffu));
-                sDmin[bb][w_row] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.hdr[0] >> 16));
-                uint32_t mm[2];
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    uint32_t sc, mn;
-                    scale_min(r.hdr, 2 * w_q + t, sc, mn);
-                    const _Float16 f = (_Float16)(short)(64 * mn);
-                    mm[t] = as_u(half2_t{f, f});
-                }
-                *(u32x2 *)(sB2[bb] + w_row * 16 + 4 * w_q) = u32x2{mm[0], mm[1]};
-                // threads >= 128 write the same bytes as thread tid - 128
-                *(u32x4 *)(sA2[bb] + ((tid & 127u) >> 1) * 16 + 8 * (tid & 1u)) = r.s;
-            }
-        }
-    };
-
-    floatx16 acc[2], part[2];
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int j = 0; j < 16; j++) acc[t][j] = part[t][j] = 0.0f;
-
-    const uint32_t lr = lane & 31u, lk = 8 * (lane >> 5);
-    // The group's MFMAs of stage s (parity ODD): K-steps grp, grp + 2, ...,
-    // with the store of stage s + 1 spread between them when STORE.
-    auto compute_and_store = [&](auto odd_c, auto store_c, uint32_t s, const Regs &next) {
-        constexpr uint32_t ODD = decltype(odd_c)::value;
-        constexpr bool STORE = decltype(store_c)::value;
-        using NextHb = std::integral_constant<uint32_t, ODD ^ 1u>;
-        const _Float16 *pa = sA[ODD] + (wm * 32 + lr) * kLd + lk + 16 * grp;
-        const _Float16 *pb = sW[ODD] + (wn * 64 + lr) * kLd + lk + 16 * grp;
-        Scales sv;
-        if constexpr (STORE) sv = scales(NextHb{}, next);
-        // fragments of the next K-step are read while this one runs
-        half8 av[2], b0[2], b1[2];
-        auto frags = [&](uint32_t i, int slot) {
-            av[slot] = *(const half8 *)(pa + i * 32);
-            b0[slot] = *(const half8 *)(pb + i * 32);
-            b1[slot] = *(const half8 *)(pb + 32 * kLd + i * 32);
-        };
-        frags(0, 0);
-#pragma unroll
-        for (uint32_t i = 0; i < kStage / 32; i++) {
-            if (i + 1 < kStage / 32) frags(i + 1, (int)((i + 1) & 1u));
-            part[0] = mfma32(av[i & 1u], b0[i & 1u], part[0]);
-            part[1] = mfma32(av[i & 1u], b1[i & 1u], part[1]);
-            if constexpr (STORE) {
-                if (i == 1) store_piece(NextHb{}, std::integral_constant<int, 0>{}, s + 1, next, sv);
-                if (i == 3) store_piece(NextHb{}, std::integral_constant<int, 1>{}, s + 1, next, sv);
-            }
-        }
-        if constexpr (ODD == 1) {
-            // end of the block: scale by d; group 0 subtracts dmin * (m . sums)
-            const uint32_t bb = (s >> 1) & 1u;
-            const half8 av2 = *(const half8 *)(sA2[bb] + (wm * 32 + lr) * 16 + lk);
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const uint32_t col = wn * 64 + t * 32 + lr;
-                const float d = sD[bb][col];
-#pragma unroll
-                for (int j = 0; j < 16; j++) acc[t][j] = __builtin_fmaf(d, part[t][j], acc[t][j]);
-                if (grp == 0) {
-                    const half8 bv = *(const half8 *)(sB2[bb] + col * 16 + lk);
-                    floatx16 zero;
-#pragma unroll
-                    for (int j = 0; j < 16; j++) zero[j] = 0.0f;
-                    const floatx16 mins = mfma32(av2, bv, zero);
-                    const float dmin = sDmin[bb][col];
-#pragma unroll
-                    for (int j = 0; j < 16; j++) acc[t][j] = __builtin_fmaf(-dmin, mins[j], acc[t][j]);
-                }
-#pragma unroll
-                for (int j = 0; j < 16; j++) part[t][j] = 0.0f;
-            }
-        }
-    };
-    using Even = std::integral_constant<uint32_t, 0>;
-    using Odd = std::integral_constant<uint32_t, 1>;
-    using Yes = std::true_type;
-    using No = std::false_type;
-    auto last = [&](uint32_t t) { return t < stages ? t : stages - 1; };  // clamped prefetch
-
-    // Prologue: stage 0 stored, stages 1 and 2 in flight.
-    Regs r0, r1;
-    fetch(0, r0);
-    fetch(last(1), r1);
-    {
-        const Scales sv0 = scales(Even{}, r0);
-        store_piece(Even{}, std::integral_constant<int, 0>{}, 0, r0, sv0);
-        store_piece(Even{}, std::integral_constant<int, 1>{}, 0, r0, sv0);
+__global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__restrict__ a16,
+                                                               const float *__restrict__ rowscale,
+                                                               const uint8_t *__restrict__ w, uint32_t m_rows,
+                                                               uint32_t n_rows, uint32_t k, uint32_t w_bytes,
+                                                               uint32_t m_tiles, float *__restrict__ c) {
+    extern __shared__ v4u gsm[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar offsets
+    const uint32_t kpart = wave % kKSplit, nh = wave / kKSplit;
+    const uint32_t ln = lane & 31u, h = lane >> 5;
+    // Tile order.  The 8 XCDs take workgroups round-robin (XCD = id % 8) and
+    // each has its own L2.  When the tiles split evenly, XCD x works on M half
+    // x % 2 and N quarter x / 2: its half of A (2 MiB at M = 512) stays in
+    // its L2, and the workgroups that share a W tile (the M half's m-tiles)
+    // run there back to back, so W crosses from HBM twice rather than once
+    // per m-tile.  Otherwise m-tile = id % m_tiles.
+    const uint32_t id = blockIdx.x, n_tiles = gridDim.x / m_tiles;
+    uint32_t mt, nt;
+    if (m_tiles % 2 == 0 && n_tiles % 4 == 0) {
+        const uint32_t xcd = id % 8, j = id / 8, mh = m_tiles / 2;
+        mt = (xcd & 1u) * mh + j % mh;
+        nt = (xcd >> 1) * (n_tiles / 4) + j / mh;
+    } else {
+        mt = id % m_tiles;
+        nt = id / m_tiles;
     }
-    fetch(last(2), r0);
-    __syncthreads();
-    // Iteration pair s, s + 1: compute s (buffer 0) storing s + 1 from r1 and
-    // refilling r1 with s + 3; compute s + 1 (buffer 1) storing s + 2 from r0
-    // and refilling r0 with s + 4.  The last pair stores nothing beyond the
-    // final stage.
-    uint32_t s = 0;
-    for (; s + 2 < stages; s += 2) {
-        compute_and_store(Even{}, Yes{}, s, r1);
-        fetch(last(s + 3), r1);
-        __syncthreads();
-        compute_and_store(Odd{}, Yes{}, s + 1, r0);
-        fetch(last(s + 4), r0);
-        __syncthreads();
-    }
-    compute_and_store(Even{}, Yes{}, s, r1);
-    __syncthreads();
-    compute_and_store(Odd{}, No{}, s + 1, r0);
-    __syncthreads();
+    const uint32_t m0 = mt * kBM, n0 = nt * kBN, wn0 = n0 + nh * kWN;
+    const uint32_t blocks = k / 256, row_bytes = blocks * 144;
+    const uint32_t mine = kpart < blocks ? (blocks - kpart + kKSplit - 1) / kKSplit : 0;
 
-    // Group 1 hands its partial tile to group 0 through LDS (the A buffers).
-    float *red = (float *)&sA[0][0];
-    const uint32_t slot = ((wave & 3u) * 64 + lane) * 32;
-    if (grp == 1) {
+    // Buffer loads: the per-lane part of every address is computed once; the
+    // per-block and per-step parts are wave-uniform offsets.  W rows past
+    // n_rows start at kNowhere (>= 2^31 > every W offset): they read zeros.
+    constexpr uint32_t kNowhere = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, w_bytes);
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(a16 + (size_t)2 * mt * blocks * 1024, 2 * blocks * 1024 * 16);
+    v4u *stage = gsm + wave * (kStageBytes / 16);
+
+    // W staging: chunk j * 64 + lane of the block's kWN rows x 9 chunks,
+    // which is also its 16-byte slot in the staging area.
+    uint32_t wbase[kStageLoads];
+#pragma unroll
+    for (uint32_t j = 0; j < kStageLoads; j++) {
+        const uint32_t chunk = j * 64 + lane, r = chunk / 9, p = chunk % 9;
+        wbase[j] = wn0 + r < n_rows ? (wn0 + r) * row_bytes + 16 * p : kNowhere;
+    }
+    v4u wreg[kStageLoads];
+    auto fetch_w = [&](uint32_t b) {
+#pragma unroll
+        for (uint32_t j = 0; j < kStageLoads; j++)
+            wreg[j] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(wrs, wbase[j], b * 144, 0));
+    };
+    auto put_w = [&]() {
+#pragma unroll
+        for (uint32_t j = 0; j < kStageLoads; j++) stage[j * 64 + lane] = wreg[j];
+    };
+    // A fragment of row tile r (32 rows), block b, step s.
+    auto a_frag = [&](uint32_t r, uint32_t b, uint32_t s) {
+        return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
+                                             ars, 16 * lane, (r * blocks * 1024 + (b * 16 + s) * 64) * 16, 0));
+    };
+    // LDS slots of the lane's header (column tile t) and of qs group g.
+    const v4u *hdr_slot = stage + ln * 9;
+    const v4u *q_slot = stage + ln * 9 + 1 + 4 * h;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; r++)
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int j = 0; j < 16; j++) red[slot + 16 * t + j] = acc[t][j];
+            for (int j = 0; j < 16; j++) acc[r][t][j] = 0.0f;
+
+    if (mine > 0) {
+        uint32_t b = kpart;
+        fetch_w(b);
+        put_w();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        fetch_w(mine > 1 ? b + kKSplit : b);
+        half8 afr[2][kADist];
+#pragma unroll
+        for (uint32_t s = 0; s < kADist; s++) {
+            afr[0][s] = a_frag(0, b, s);
+            afr[1][s] = a_frag(1, b, s);
+        }
+        for (uint32_t i = 0; i < mine; i++, b += kKSplit) {
+            const uint32_t bn = i + 1 < mine ? b + kKSplit : b;  // next block (clamped)
+            const uint32_t bnn = i + 2 < mine ? b + 2 * kKSplit : bn;
+            // Per column tile t (the lane's column 32 t + ln of the wave's
+            // half): the scales of the lane's sub-blocks 4 h .. 4 h + 3
+            // (src/cpu.rs:607-616).
+            v4u hd[2], q[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                hd[t] = hdr_slot[32 * 9 * t];
+                q[t] = q_slot[32 * 9 * t];
+            }
+            SubScale ss[2][4];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd[t][0] & 0xffffu));
+                const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd[t][0] >> 16));
+                // 6-bit scales and mins of sub-blocks 0-3 and 4-7, as bytes
+                const uint32_t sc03 = hd[t][1] & 0x3f3f3f3fu, mn03 = hd[t][2] & 0x3f3f3f3fu;
+                const uint32_t sc47 = (hd[t][3] & 0x0f0f0f0fu) | ((hd[t][1] >> 2) & 0x30303030u);
+                const uint32_t mn47 = ((hd[t][3] >> 4) & 0x0f0f0f0fu) | ((hd[t][2] >> 2) & 0x30303030u);
+                const uint32_t scs = h ? sc47 : sc03, mns = h ? mn47 : mn03;
+#pragma unroll
+                for (int x = 0; x < 4; x++) ss[t][x] = sub_scale(d, dmin, (scs >> (8 * x)) & 0xffu, (mns >> (8 * x)) & 0xffu);
+            }
+            // Weights of step 0; then each step issues the A loads of step
+            // s + kADist, its 4 MFMAs, and the weights of step s + 1.  The
+            // scheduling barriers keep every step's loads where they are
+            // written, so each A fragment (and every older load) has kADist
+            // steps to arrive.
+            half8 bv[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) bv[t] = dequant8(q[t][0], ss[t][0], ss[t][1]);
+            v4u qn[2];
+#pragma unroll
+            for (uint32_t s = 0; s < 16; s++) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (s % 4 == 0 && s < 12) {
+                    // qs group s / 4 + 1 while group s / 4 is used
+#pragma unroll
+                    for (int t = 0; t < 2; t++) qn[t] = q_slot[32 * 9 * t + s / 4 + 1];
+                }
+                // The A fragments of step s + kADist (the next block's first
+                // steps at the end) and the weights of step s + 1 are produced
+                // before this step's MFMAs consume the current ones, so they
+                // live in other registers.
+                const uint32_t pb = s + kADist < 16 ? b : bn, ps = (s + kADist) % 16;
+                const half8 an0 = a_frag(0, pb, ps), an1 = a_frag(1, pb, ps);
+                half8 bn_[2];
+                if (s + 1 < 16) {
+                    const uint32_t s1 = s + 1;
+                    if (s1 % 4 == 0) {
+#pragma unroll
+                        for (int t = 0; t < 2; t++) q[t] = qn[t];
+                    }
+#pragma unroll
+                    for (int t = 0; t < 2; t++) bn_[t] = dequant8(q[t][s1 % 4], ss[t][2 * (s1 / 8)], ss[t][2 * (s1 / 8) + 1]);
+                }
+                const half8 a0 = afr[0][s % kADist], a1 = afr[1][s % kADist];
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    acc[0][t] = mfma32(a0, bv[t], acc[0][t]);
+                    acc[1][t] = mfma32(a1, bv[t], acc[1][t]);
+                }
+                afr[0][s % kADist] = an0;
+                afr[1][s % kADist] = an1;
+                if (s + 1 < 16) {
+#pragma unroll
+                    for (int t = 0; t < 2; t++) bv[t] = bn_[t];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // Other lanes read what a lane stores: every LDS read of this
+            // block precedes the stores of the next one, which precede its
+            // reads (wavefront-scope fences order them for the compiler; the
+            // wave's LDS operations execute in order).
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            put_w();
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            fetch_w(bnn);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
+
+    // Partial tiles -> LDS as [wave][row][column] (row stride kRedLd), after
+    // every wave has left its staging area; then each thread adds the four
+    // K-split partials of 16 consecutive columns of one row and stores them.
     __syncthreads();
-    if (grp == 1) return;
-    // C[m][n] = acc * rowscale[m]; lane holds column lr, rows 8(j/4) + 4(lane/32) + j%4.
+    float *red = (float *)gsm;
 #pragma unroll
-    for (int t = 0; t < 2; t++) {
-        const uint32_t n = n0 + wn * 64 + t * 32 + lr;
+    for (int r = 0; r < 2; r++)
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const float v = acc[t][j] + red[slot + 16 * t + j];
-            const uint32_t m = m0 + wm * 32 + 8 * (j / 4) + 4 * (lane >> 5) + (j % 4);
-            if (n < n_rows && m < m_rows) c[(size_t)m * n_rows + n] = v * rowscale[m];
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const uint32_t row = 32 * r + 8 * (j / 4) + 4 * h + (j % 4), col = 32 * t + ln;
+                red[(wave * kBM + row) * kRedLd + col] = acc[r][t][j];
+            }
+    __syncthreads();
+    const uint32_t row = tid >> 3, col0 = 16 * (tid & 7u);  // 64 rows x 8 chunks of 16 columns
+    const uint32_t half = col0 / kWN, hcol = col0 % kWN;
+    const uint32_t m = m0 + row;
+    if (m < m_rows) {
+        const float scale = rowscale[m];
+        const float *src = red + ((half * kKSplit) * kBM + row) * kRedLd + hcol;
+        float *dst = c + (size_t)m * n_rows + n0 + col0;
+        const bool whole = n0 + col0 + 16 <= n_rows && (n_rows & 3u) == 0 && ((uintptr_t)c & 15u) == 0;
+#pragma unroll
+        for (uint32_t v = 0; v < 4; v++) {
+            floatx4 sum = *(const floatx4 *)(src + 4 * v);
+#pragma unroll
+            for (uint32_t kp = 1; kp < kKSplit; kp++) sum += *(const floatx4 *)(src + kp * kBM * kRedLd + 4 * v);
+            sum *= scale;
+            if (whole) {
+                *(floatx4 *)(dst + 4 * v) = sum;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (n0 + col0 + 4 * v + e < n_rows) dst[4 * v + e] = sum[e];
+            }
         }
     }
 }
@@ -394,10 +382,10 @@ namespace {
 
 size_t padded_rows(size_t m) { return (m + kBM - 1) / kBM * kBM; }
 
-// Workspace of the Q4_K path: a16 | sums | rowscale.
+// Workspace of the Q4_K path: a16 | rowscale.
 size_t q4k_workspace(size_t m, size_t k) {
     const size_t mp = padded_rows(m);
-    return mp * k * 2 + mp * (k / 256) * 16 * 2 + mp * 4 + 3 * 256;
+    return mp * k * 2 + mp * 4 + 2 * 256;
 }
 
 }  // namespace
@@ -435,19 +423,23 @@ int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t type, size_t m, size_t n, size_t 
         ((uintptr_t)a_bf16 & 15u) == 0) {
         const size_t mp = padded_rows(m);
         char *ws = (char *)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-        _Float16 *a16 = (_Float16 *)ws;
-        _Float16 *sums = (_Float16 *)(ws + ((mp * k * 2 + 255) & ~(size_t)255));
-        float *rowscale =
-            (float *)((char *)sums + ((mp * (k / 256) * 32 + 255) & ~(size_t)255));
+        half8 *a16 = (half8 *)ws;
+        float *rowscale = (float *)(ws + ((mp * k * 2 + 255) & ~(size_t)255));
         hipLaunchKernelGGL(gemm_prep_kernel, dim3((uint32_t)mp), dim3(256), 0, ctx->stream, a_bf16,
-                           (uint32_t)m, (uint32_t)k, a16, sums, rowscale);
+                           (uint32_t)m, (uint32_t)k, a16, rowscale);
         DM_HIP(hipGetLastError());
         const uint32_t n_tiles = (uint32_t)((n + kBN - 1) / kBN), m_tiles = (uint32_t)(mp / kBM);
+        static bool lds_set = false;  // 128 KiB of dynamic LDS, allowed once per process
+        if (!lds_set) {
+            DM_HIP(hipFuncSetAttribute((const void *)gemm_q4k_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kLdsBytes));
+            lds_set = true;
+        }
         {
             KernelTimer timer(ctx);
-            hipLaunchKernelGGL(gemm_q4k_kernel, dim3(n_tiles * m_tiles), dim3(512), 0, ctx->stream, a16, sums,
-                               rowscale, (const uint8_t *)weights, (uint32_t)m, (uint32_t)n, (uint32_t)k,
-                               (uint32_t)w_bytes, m_tiles, c);
+            hipLaunchKernelGGL(gemm_q4k_kernel, dim3(n_tiles * m_tiles), dim3(64 * kWaves), kLdsBytes, ctx->stream,
+                               a16, rowscale, (const uint8_t *)weights, (uint32_t)m, (uint32_t)n,
+                               (uint32_t)k, (uint32_t)w_bytes, m_tiles, c);
         }
         DM_HIP(hipGetLastError());
         return DMHIP_OK;

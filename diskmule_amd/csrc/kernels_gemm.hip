@@ -23,16 +23,16 @@
 // bytes 64h + 4s .. 64h + 4s + 3, and A is stored in that order.
 // Other weight types take the decode-GEMV path in chunks of 16 tokens.
 //
-// Tiling: a workgroup (4 waves, one per SIMD) owns a 64 x 128 tile of C and
-// each wave computes the whole tile over every fourth Q4_K block, so every
-// element of A and W is read by exactly one wave and no operand is shared
-// through LDS.  A comes from global memory already in MFMA fragment order
-// (one 1 KiB load per 32 rows and step); a wave stages its W block (128 rows
-// x 144 bytes, contiguous 16-byte loads) in its own LDS area and
-// dequantizes from there, with the next block's W in flight in registers.
-// The accumulators stay in AGPRs for the whole K loop; the four partial
-// tiles are added through LDS at the end.  Workgroups that work on the same
-// 64 rows of A run on the same XCD.
+// Tiling: a workgroup (8 waves, two per SIMD) owns a 64 x 128 tile of C;
+// wave w computes the 64 x 64 half w / 4 over every fourth Q4_K block
+// (w % 4, w % 4 + 4, ...), so every W element is dequantized by exactly one
+// wave and no operand is shared through LDS.  A comes from global memory
+// already in MFMA fragment order (one 1 KiB load per 32 rows and step); a
+// wave stages its W block (64 rows x 144 bytes, contiguous 16-byte loads) in
+// its own LDS area and dequantizes from there, with the next block's W in
+// flight in registers.  The accumulators stay in AGPRs for the whole K loop;
+// the partial tiles are added through LDS at the end.  Workgroups are
+// ordered so that each XCD keeps half of A in its L2.
 #include "dm_device.h"
 #include "dm_qmv.h"
 #include "runtime.h"
@@ -436,10 +436,9 @@ int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t type, size_t m, size_t n, size_t 
             lds_set = true;
         }
         {
-            KernelTimer timer(ctx);
-            hipLaunchKernelGGL(gemm_q4k_kernel, dim3(n_tiles * m_tiles), dim3(64 * kWaves), kLdsBytes, ctx->stream,
-                               a16, rowscale, (const uint8_t *)weights, (uint32_t)m, (uint32_t)n,
-                               (uint32_t)k, (uint32_t)w_bytes, m_tiles, c);
+            DM_HIP(launch_kernel(ctx, gemm_q4k_kernel, dim3(n_tiles * m_tiles), dim3(64 * kWaves), kLdsBytes,
+                                 (const half8 *)a16, (const float *)rowscale, (const uint8_t *)weights, (uint32_t)m,
+                                 (uint32_t)n, (uint32_t)k, (uint32_t)w_bytes, m_tiles, c));
         }
         DM_HIP(hipGetLastError());
         return DMHIP_OK;

@@ -699,11 +699,9 @@ hipError_t run(dmhip_ctx *ctx, const Args &a, uint32_t *waves_out) {
     // fragments of every block plus one zeroed block for the idle A rows
     const size_t lds = MB > 0 ? ((size_t)(a.columns / 256) + 1) * SPB * 4 * MB * 16 : 0;
     if (waves_out) *waves_out = grid * (4 / S);
-    KernelTimer timer(ctx);
-    hipLaunchKernelGGL((qmv_kernel<TYPE, NT, R, S, MODE, MB>), dim3(grid), dim3(256), lds, ctx->stream,
-                       (const uint8_t *)a.w, (const uint8_t *)a.w2, a.rows, a.columns, a.row_bytes,
-                       a.total, a.x, a.normalize, a.epsilon, a.xp, a.ysc, a.batch, a.y, a.partials);
-    return hipGetLastError();
+    return launch_kernel(ctx, qmv_kernel<TYPE, NT, R, S, MODE, MB>, dim3(grid), dim3(256), lds,
+                         (const uint8_t *)a.w, (const uint8_t *)a.w2, a.rows, a.columns, a.row_bytes, a.total, a.x,
+                         a.normalize, a.epsilon, a.xp, a.ysc, a.batch, a.y, a.partials);
 }
 
 template <uint32_t TYPE, int NT, int R, int MODE, int MB>

@@ -753,11 +753,9 @@ hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
         hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    KernelTimer timer(ctx);
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WAVES), lds, ctx->stream, (const uint8_t *)a.w,
-                       (const uint8_t *)a.w2, rows, columns, row_bytes, row_bytes * rows, a.x, a.normalize,
-                       a.epsilon, a.y, a.partials);
-    return hipGetLastError();
+    return launch_kernel(ctx, kernel, dim3(grid), dim3(64 * WAVES), lds, (const uint8_t *)a.w,
+                         (const uint8_t *)a.w2, rows, columns, row_bytes, row_bytes * rows, a.x, a.normalize,
+                         a.epsilon, a.y, a.partials);
 }
 
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
@@ -820,10 +818,8 @@ hipError_t run8_grouped(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, uint64_
         hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    KernelTimer timer(ctx);
-    hipLaunchKernelGGL(kernel, dim3(grid, count), dim3(64 * WAVES), lds, ctx->stream, table, rows, columns,
-                       row_bytes, row_bytes * rows, up_offset, x, y, MODE == 2 ? 1 : 0);
-    return hipGetLastError();
+    return launch_kernel(ctx, kernel, dim3(grid, count), dim3(64 * WAVES), lds, table, rows, columns, row_bytes,
+                         row_bytes * rows, up_offset, x, y, MODE == 2 ? 1 : 0);
 }
 
 template <uint32_t TYPE, int MODE, int TOK>

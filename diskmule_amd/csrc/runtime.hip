@@ -102,10 +102,10 @@ int set_device(dmhip_ctx *ctx) {
 }
 
 static void timing_mark(dmhip_ctx *ctx) {
-    hipEvent_t e;
-    if (hipEventCreate(&e) != hipSuccess) return;
+    hipEvent_t e = timing_event(ctx);
+    if (!e) return;
     if (hipEventRecord(e, ctx->stream) != hipSuccess) {
-        (void)hipEventDestroy(e);
+        ctx->timing_pool.push_back(e);
         return;
     }
     ctx->timing_events.push_back(e);
@@ -247,6 +247,8 @@ void dmhip_context_free(dmhip_ctx *ctx) {
     if (ctx->argmax_state) (void)hipFree(ctx->argmax_state);
     if (ctx->argmax_index) (void)hipFree(ctx->argmax_index);
     if (ctx->flags) (void)hipFree(ctx->flags);
+    for (hipEvent_t e : ctx->timing_events) (void)hipEventDestroy(e);
+    for (hipEvent_t e : ctx->timing_pool) (void)hipEventDestroy(e);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     if (ctx->upload) (void)hipStreamDestroy(ctx->upload);
     delete ctx;
@@ -749,7 +751,7 @@ int dmhip_kernel_timing_read(dmhip_ctx *ctx, double *total_ms, uint64_t *launche
             count += 1;
         }
     }
-    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+    ctx->timing_pool.insert(ctx->timing_pool.end(), ev.begin(), ev.end());
     ev.clear();
     *total_ms = total;
     *launches = count;

@@ -460,14 +460,17 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     // The chunks of a block group go to the wave's staging area; the loads of
     // the next group are in flight while this one is read back and computed.
     // A wave only reads its own staging area, and its LDS operations run in
-    // order, so no barrier is needed.
+    // order, so no barrier is needed; the wavefront-scope fences keep the
+    // compiler from moving another lane's reads across these writes.
     auto put_stage = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
         for (uint32_t j = 0; j < NL; j++)
             if (j + 1 < NL || j * 64 + lane < ITEMS) {
                 stage[j * 64 + lane] = st[j];
                 if constexpr (MODE == 2) stage2[j * 64 + lane] = st2[j];
             }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     };
     // acc[m][tok]: matrix m (gate, up) of token tok
     auto compute_group = [&](uint32_t grp, uint32_t rb, float (&acc)[NM][TOK]) {

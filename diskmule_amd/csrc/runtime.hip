@@ -4,6 +4,7 @@
 // (same checks, same order, same error variants), then copy inputs in, run
 // the kernels on the context's stream, wait and copy results out.
 #include "runtime.h"
+#include "dm_qmv.h"
 
 #include <math.h>
 #include <stdio.h>
@@ -641,6 +642,39 @@ int dmhip_matvec_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t colum
     DM_REQUIRE(y);
     DM_CHECK(set_device(ctx));
     return enqueue_matvec(ctx, type, rows, columns, weights, batch, x, y);
+}
+
+int dmhip_matvec_batch_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, size_t count,
+                              const void *const *weights, const float *x, size_t x_stride, float *y,
+                              size_t y_stride) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(validate_device_matvec(type, rows, columns, 1));
+    if (rows == 0 || count == 0) return DMHIP_OK;
+    DM_CHECK(require_nonempty("matvec", columns));
+    DM_REQUIRE(weights);
+    DM_REQUIRE(x);
+    DM_REQUIRE(y);
+    for (size_t i = 0; i < count; i++)
+        if (!weights[i]) return fail(DMHIP_ERR_INVALID_ARGUMENT, "weights[%zu] must not be null", i);
+    DM_CHECK(set_device(ctx));
+    // One grouped launch when every matrix suits the int8 kernel and the
+    // offsets fit its 32-bit job table; otherwise one matvec per matrix.
+    const size_t lim = 0x80000000ull;
+    bool grouped = qmv8_grouped_supported(type, rows, columns, 1) && count < lim && x_stride < lim &&
+                   y_stride < lim && (count - 1) * x_stride + columns < lim &&
+                   (count - 1) * y_stride + rows < lim;
+    for (size_t i = 0; grouped && i < count; i++)
+        grouped = ((uintptr_t)weights[i] & (type == 12u ? 15u : 3u)) == 0;  // 12 = Q4_K
+    if (!grouped) {
+        for (size_t i = 0; i < count; i++)
+            DM_CHECK(enqueue_matvec(ctx, type, rows, columns, weights[i], 1, x + i * x_stride, y + i * y_stride));
+        return DMHIP_OK;
+    }
+    std::vector<QmvJob> jobs(count);
+    for (size_t i = 0; i < count; i++)
+        jobs[i] = QmvJob{weights[i], 1u, (uint32_t)(i * x_stride), (uint32_t)(i * y_stride), 0, 0};
+    DM_HIP(launch_qmv8_grouped(ctx, type, (uint32_t)rows, (uint32_t)columns, 0, 0, jobs.data(), count, x, y));
+    return DMHIP_OK;
 }
 
 int dmhip_matvec_argmax_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,

@@ -37,7 +37,7 @@ EXPORTED_SYMBOLS = [
     "dmhip_buffer_read", "dmhip_copy_to_host", "dmhip_copy_to_device", "dmhip_host_alloc_pinned", "dmhip_host_free_pinned", "dmhip_rms_norm",
     "dmhip_silu_mul", "dmhip_argmax", "dmhip_top_k_softmax", "dmhip_matvec",
     "dmhip_matvec_mapped", "dmhip_matvec_owned", "dmhip_dequantize", "dmhip_matvec_device",
-    "dmhip_matvec_argmax_device", "dmhip_argmax_result", "dmhip_rms_norm_device",
+    "dmhip_matvec_batch_device", "dmhip_matvec_argmax_device", "dmhip_argmax_result", "dmhip_rms_norm_device",
     "dmhip_silu_mul_device", "dmhip_ffn_workspace_bytes", "dmhip_ffn_device",
     "dmhip_router_top_k_device", "dmhip_gemm_workspace_bytes", "dmhip_gemm_device",
     "dmhip_event_record", "dmhip_event_elapsed_ms", "dmhip_event_free",
@@ -117,6 +117,8 @@ def load_library() -> ctypes.CDLL:
         "dmhip_matvec_owned": ([_vp, _u32, _sz, _sz, _vp, _sz, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
         "dmhip_dequantize": ([_vp, _u32, _vp, _sz, _sz, _f32p, _sz], ctypes.c_int),
         "dmhip_matvec_device": ([_vp, _u32, _sz, _sz, _vp, _sz, _vp, _vp], ctypes.c_int),
+        "dmhip_matvec_batch_device": ([_vp, _u32, _sz, _sz, _sz, ctypes.POINTER(_vp), _vp, _sz, _vp, _sz],
+                                      ctypes.c_int),
         "dmhip_matvec_argmax_device": ([_vp, _u32, _sz, _sz, _vp, _vp, _vp, _vp], ctypes.c_int),
         "dmhip_argmax_result": ([_vp, _szp], ctypes.c_int),
         "dmhip_rms_norm_device": ([_vp, _sz, _sz, _vp, _vp, ctypes.c_float, _vp], ctypes.c_int),
@@ -345,6 +347,12 @@ class HipContext:
     # -- device operators (device addresses as ints) ------------------------
     def matvec_device(self, kind, rows, columns, w_ptr, batch, x_ptr, y_ptr) -> None:
         _check(load_library().dmhip_matvec_device(self._h, kind, rows, columns, w_ptr, batch, x_ptr, y_ptr))
+
+    def matvec_batch_device(self, kind, rows, columns, w_ptrs, x_ptr, x_stride, y_ptr, y_stride) -> None:
+        """y + i*y_stride = W_i . (x + i*x_stride) for each device address in w_ptrs."""
+        arr = (_vp * max(len(w_ptrs), 1))(*w_ptrs)
+        _check(load_library().dmhip_matvec_batch_device(self._h, kind, rows, columns, len(w_ptrs), arr, x_ptr,
+                                                        x_stride, y_ptr, y_stride))
 
     def matvec_argmax_device(self, kind, rows, columns, w_ptr, x_ptr, y_ptr, index_ptr) -> None:
         _check(load_library().dmhip_matvec_argmax_device(self._h, kind, rows, columns, w_ptr, x_ptr,

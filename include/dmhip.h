@@ -192,6 +192,17 @@ int dmhip_matvec_argmax_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows,
 /* Waits for the last dmhip_matvec_argmax_device and returns its index. */
 int dmhip_argmax_result(dmhip_ctx *ctx, size_t *index);
 
+/* `count` independent batch-1 matvecs of one shape in one dispatch:
+   y + i*y_stride = W_i . (x + i*x_stride) for i < count, W_i = weights[i]
+   (`rows` encoded rows of `columns` values; strides in floats, 0 allowed for
+   x).  The work of `count` consecutive MetalContext::matvec_mapped calls
+   (src/metal.rs:687-760), e.g. the projections of one layer that read the
+   same activation; Q4_K/Q6_K run as one grouped int8 launch, other types
+   as one matvec per matrix. */
+int dmhip_matvec_batch_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
+                              size_t count, const void *const *weights, const float *x, size_t x_stride,
+                              float *y, size_t y_stride);
+
 /* RMSNorm of `batch` rows of `count` values (src/cpu.rs:98-142). */
 int dmhip_rms_norm_device(dmhip_ctx *ctx, size_t batch, size_t count, const float *input,
                           const float *weight, float epsilon, float *output);

@@ -181,6 +181,36 @@ def test_batched_gemv_matches_oracle(ctx, batch):
             assert_close(got[b], want[b], f"type {kind} batch {batch} token {b}")
 
 
+@pytest.mark.parametrize("kind,rows,cols,x_stride", [(Q4_K, 1000, 2048, 0), (Q6_K, 1000, 2048, 2048),
+                                                     (Q4_K, 4096, 4096, 0), (Q8_0, 300, 512, 512)])
+def test_matvec_batch_matches_one_matvec_per_matrix(ctx, kind, rows, cols, x_stride):
+    """One grouped launch over 5 matrices (shared or per-matrix x, strided y)
+    against the oracle per matrix; Q8_0 takes the per-matrix fallback."""
+    count, y_stride = 5, rows + 24
+    print(f"matvec batch type={kind} {rows}x{cols} x_stride={x_stride}", flush=True)
+    ws = [synth.quantized_matrix(kind, rows, cols, synth.weight_seed(70 + i)) for i in range(count)]
+    xs = synth.normal(synth.activation_seed(70), max(x_stride * (count - 1), 0) + cols)
+    bufs = [dev(ctx, w) for w in ws]
+    xb, yb = dev(ctx, xs), dev_out(ctx, count * y_stride * 4)
+    yb.write(0, np.full(count * y_stride, -7.0, np.float32))
+    ctx.matvec_batch_device(kind, rows, cols, [b.device_ptr for b in bufs], xb.device_ptr, x_stride,
+                            yb.device_ptr, y_stride)
+    got = yb.read(0, count * y_stride * 4, np.float32).reshape(count, y_stride)
+    for i in range(count):
+        x = xs[i * x_stride:i * x_stride + cols]
+        assert_close(got[i, :rows], capi.matvec(kind, rows, cols, ws[i], x), f"matrix {i}")
+        assert (got[i, rows:] == -7.0).all(), f"matrix {i} wrote past its rows"
+
+
+def test_matvec_batch_validation(ctx):
+    wb, xb, yb = dev_out(ctx, 144 * 8), dev_out(ctx, 1024), dev_out(ctx, 64)
+    ctx.matvec_batch_device(Q4_K, 8, 256, [], xb.device_ptr, 0, yb.device_ptr, 8)  # no matrices: no-op
+    with pytest.raises(HipError, match="InvalidArgument"):
+        ctx.matvec_batch_device(Q4_K, 8, 256, [wb.device_ptr, 0], xb.device_ptr, 0, yb.device_ptr, 8)
+    with pytest.raises(HipError, match="InvalidElementCount"):
+        ctx.matvec_batch_device(Q4_K, 8, 100, [wb.device_ptr], xb.device_ptr, 0, yb.device_ptr, 8)
+
+
 def test_q6_k_large_scales_take_the_exact_split_path(ctx):
     rows, cols = 64, 1024
     w = synth.quantized_matrix(Q6_K, rows, cols, synth.weight_seed(55)).reshape(-1, 210).copy()

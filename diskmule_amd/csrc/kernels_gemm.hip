@@ -94,62 +94,120 @@ __device__ __forceinline__ half8 dequant8(uint32_t dw, const SubScale &lo, const
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// A preparation: one workgroup per row of the padded workspace (rows beyond
-// M are zero).  For the 32-row tile T = m / 32 and lane l = m % 32 + 32 h:
+// A preparation, two kernels over the padded workspace (rows beyond M are
+// zero).  For the 32-row tile T = m / 32 and lane l = m % 32 + 32 h:
 //   a16[((T * blocks + b) * 16 + s) * 64 + l]  half8: A[m][k] * 2^-e_m at
 //       the 8 columns of step s, half h of block b (frag_base)
 //   rowscale[m]                                2^e_m
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) gemm_prep_kernel(const uint16_t *__restrict__ a, uint32_t m_rows,
+// Workgroup (g, p) takes rows 8 g .. 8 g + 7 and blocks 4 p .. 4 p + 3.  Wave w
+// first finds max|A[m]| of row m = 8 g + w over all of K (every workgroup of
+// the row group does; they share an XCD, so the repeats hit its L2) and
+// writes rowscale[m] = 2^e_m with max|A[m]| 2^-e_m in [2^14, 2^15) (1 for an
+// all-zero or non-finite row, 0 for the padding rows m >= M).  The 8 rows'
+// fragments of one (block, step, half) are consecutive in a16, so after a
+// pass through LDS the 16-byte stores of 8 neighbouring threads form one
+// 128-byte line.
+constexpr uint32_t kPackBlocks = 4;
+constexpr uint32_t kPackLd = kPackBlocks * 128 + 4;  // dwords per staged row
+
+__global__ void __launch_bounds__(512) gemm_prep_kernel(const uint16_t *__restrict__ a, uint32_t m_rows,
                                                         uint32_t k, half8 *__restrict__ a16,
                                                         float *__restrict__ rowscale) {
-    __shared__ float red[4];
-    const uint32_t m = blockIdx.x, tid = threadIdx.x;
-    const bool live = m < m_rows;
-    const uint16_t *row = a + (size_t)m * k;
-    float mx = 0.0f;
-    for (uint32_t c = tid; c < k / 8; c += 256) {
-        if (!live) break;
-        const u32x4 v = *(const u32x4 *)(row + 8 * c);
+    __shared__ uint32_t tile[8][kPackLd];
+    __shared__ float sdown[8];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+    const uint32_t r0 = blockIdx.x * 8, blocks = k / 256, b0 = blockIdx.y * kPackBlocks;
+    {
+        const uint32_t m = r0 + wave;
+        const bool live = m < m_rows;
+        float mx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const uint32_t chunks = k / 8;
+        if (live && chunks == 64 * 8) {
+            // K = 4096: the whole row in registers, the workgroup's blocks
+            // staged from them (chunk lane + 64 j holds columns 8 (lane + 64 j) ..)
+            const u32x4 *row = (const u32x4 *)(a + (size_t)m * k);
+            u32x4 v[8];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            mx = fmaxf(mx, fabsf(__uint_as_float(v[i] << 16)));
-            mx = fmaxf(mx, fabsf(__uint_as_float(v[i] & 0xffff0000u)));
-        }
-    }
-    mx = wave_max(mx);
-    if ((tid & 63u) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    int e = 0;
-    if (mx > 0.0f && __builtin_isfinite(mx)) {
-        int ex;
-        (void)frexpf(mx, &ex);
-        e = ex - 15;
-        if (e < -126) e = -126;
-        if (e > 127) e = 127;
-    }
-    const float down = ldexpf(1.0f, -e);
-    if (tid == 0) rowscale[m] = live ? ldexpf(1.0f, e) : 0.0f;
-    const uint32_t blocks = k / 256, tile = m / 32, l0 = m % 32;
-    // fragment f = (2 b + h) * 16 + s
-    for (uint32_t f = tid; f < blocks * 32; f += 256) {
-        const uint32_t b = f / 32, h = (f / 16) & 1u, s = f & 15u;
-        half8 v;
-        if (live) {
-            const uint16_t *p = row + b * 256 + frag_base(s, h);
-            const u32x2 x0 = *(const u32x2 *)p, x1 = *(const u32x2 *)(p + 32);
-            const uint32_t u[4] = {x0[0], x0[1], x1[0], x1[1]};
+            for (int j = 0; j < 8; j++) v[j] = row[lane + 64 * j];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[2 * i] = (_Float16)(__uint_as_float(u[i] << 16) * down);
-                v[2 * i + 1] = (_Float16)(__uint_as_float(u[i] & 0xffff0000u) * down);
+            for (int j = 0; j < 8; j++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    mx[i] = fmaxf(mx[i], fabsf(__uint_as_float(v[j][i] << 16)));
+                    mx[i] = fmaxf(mx[i], fabsf(__uint_as_float(v[j][i] & 0xffff0000u)));
+                }
+                const uint32_t q = lane + 64 * j - b0 * 32;
+                if (q < kPackBlocks * 32) *(u32x4 *)&tile[wave][q * 4] = v[j];
             }
-        } else {
+        } else if (live) {
+            const u32x4 *row = (const u32x4 *)(a + (size_t)m * k);
+            uint32_t c = lane;
+            for (; c + 64 * 7 < chunks; c += 64 * 8) {
+                u32x4 v[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = (_Float16)0.0f;
+                for (int j = 0; j < 8; j++) v[j] = row[c + 64 * j];
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        mx[i] = fmaxf(mx[i], fabsf(__uint_as_float(v[j][i] << 16)));
+                        mx[i] = fmaxf(mx[i], fabsf(__uint_as_float(v[j][i] & 0xffff0000u)));
+                    }
+            }
+            for (; c < chunks; c += 64) {
+                const u32x4 v = row[c];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    mx[i] = fmaxf(mx[i], fabsf(__uint_as_float(v[i] << 16)));
+                    mx[i] = fmaxf(mx[i], fabsf(__uint_as_float(v[i] & 0xffff0000u)));
+                }
+            }
         }
-        a16[((size_t)(tile * blocks + b) * 16 + s) * 64 + l0 + 32 * h] = v;
+        float x = wave_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
+        int e = 0;
+        if (x > 0.0f && __builtin_isfinite(x)) {
+            int ex;
+            (void)frexpf(x, &ex);
+            e = ex - 15;
+            if (e < -126) e = -126;
+            if (e > 127) e = 127;
+        }
+        if (lane == 0) {
+            sdown[wave] = live ? ldexpf(1.0f, -e) : 0.0f;
+            if (blockIdx.y == 0) rowscale[m] = live ? ldexpf(1.0f, e) : 0.0f;
+        }
+    }
+    if (k / 8 != 64 * 8 || r0 + wave >= m_rows) {
+        // the workgroup's blocks: thread (row tid >> 6, 16-byte chunk q) of 128 per row
+        const uint32_t rr = tid >> 6;
+#pragma unroll
+        for (uint32_t j = 0; j < kPackBlocks / 2; j++) {
+            const uint32_t q = lane + 64 * j, b = b0 + q / 32;
+            u32x4 v = {0, 0, 0, 0};
+            if (b < blocks && r0 + rr < m_rows) v = *(const u32x4 *)(a + (size_t)(r0 + rr) * k + b0 * 256 + q * 8);
+            *(u32x4 *)&tile[rr][q * 4] = v;
+        }
+    }
+    __syncthreads();
+    // thread: row i = tid & 7, fragment f = (tid >> 3) & 31 (half h = f / 16,
+    // step s = f % 16) of blocks b0 + (tid >> 8) + 2 j
+    const uint32_t i = tid & 7u, f = (tid >> 3) & 31u, h = f >> 4, st = f & 15u;
+    const float down = sdown[i];
+    const uint32_t fb = frag_base(st, h), tl = r0 / 32, l0 = r0 % 32;
+#pragma unroll
+    for (uint32_t j = 0; j < kPackBlocks / 2; j++) {
+        const uint32_t bq = (tid >> 8) + 2 * j, b = b0 + bq;
+        if (b >= blocks) continue;
+        const uint32_t *t = &tile[i][bq * 128];
+        const uint32_t u[4] = {t[fb / 2], t[fb / 2 + 1], t[(fb + 32) / 2], t[(fb + 32) / 2 + 1]};
+        half8 v;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            v[2 * q] = (_Float16)(__uint_as_float(u[q] << 16) * down);
+            v[2 * q + 1] = (_Float16)(__uint_as_float(u[q] & 0xffff0000u) * down);
+        }
+        a16[((size_t)(tl * blocks + b) * 16 + st) * 64 + l0 + i + 32 * h] = v;
     }
 }
 
@@ -425,8 +483,10 @@ int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t type, size_t m, size_t n, size_t 
         char *ws = (char *)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
         half8 *a16 = (half8 *)ws;
         float *rowscale = (float *)(ws + ((mp * k * 2 + 255) & ~(size_t)255));
-        hipLaunchKernelGGL(gemm_prep_kernel, dim3((uint32_t)mp), dim3(256), 0, ctx->stream, a_bf16,
-                           (uint32_t)m, (uint32_t)k, a16, rowscale);
+        // row groups along x: a row group's workgroups are x + (mp / 8) y, one XCD
+        hipLaunchKernelGGL(gemm_prep_kernel,
+                           dim3((uint32_t)(mp / 8), (uint32_t)((k / 256 + kPackBlocks - 1) / kPackBlocks)), dim3(512),
+                           0, ctx->stream, a_bf16, (uint32_t)m, (uint32_t)k, a16, rowscale);
         DM_HIP(hipGetLastError());
         const uint32_t n_tiles = (uint32_t)((n + kBN - 1) / kBN), m_tiles = (uint32_t)(mp / kBM);
         static bool lds_set = false;  // 128 KiB of dynamic LDS, allowed once per process

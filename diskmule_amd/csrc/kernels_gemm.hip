@@ -94,14 +94,14 @@ __device__ __forceinline__ half8 dequant8(uint32_t dw, const SubScale &lo, const
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// A preparation, two kernels over the padded workspace (rows beyond M are
-// zero).  For the 32-row tile T = m / 32 and lane l = m % 32 + 32 h:
+// A preparation over the padded workspace (rows beyond M are zero).  For
+// the 32-row tile T = m / 32 and lane l = m % 32 + 32 h:
 //   a16[((T * blocks + b) * 16 + s) * 64 + l]  half8: A[m][k] * 2^-e_m at
 //       the 8 columns of step s, half h of block b (frag_base)
 //   rowscale[m]                                2^e_m
 // ---------------------------------------------------------------------------
-// Workgroup (g, p) takes rows 8 g .. 8 g + 7 and blocks 4 p .. 4 p + 3.  Wave w
-// first finds max|A[m]| of row m = 8 g + w over all of K (every workgroup of
+// Workgroup (g, p) takes rows 8 g .. 8 g + 7 and blocks 4 p .. 4 p + 3 (for
+// K = 4096 a wave keeps its whole row in registers).  Wave w first finds max|A[m]| of row m = 8 g + w over all of K (every workgroup of
 // the row group does; they share an XCD, so the repeats hit its L2) and
 // writes rowscale[m] = 2^e_m with max|A[m]| 2^-e_m in [2^14, 2^15) (1 for an
 // all-zero or non-finite row, 0 for the padding rows m >= M).  The 8 rows'

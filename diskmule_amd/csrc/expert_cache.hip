@@ -4,7 +4,8 @@
 // the reference's (clock per layer, hit updates last_used, a miss evicts the
 // unpinned slot with the smallest (is_some, last_used, index)), and the
 // positional reads become asynchronous host->HBM copies on the context's
-// upload stream.  Ordering is by events, never by host waits:
+// two upload streams (alternating by expert).  Ordering is by events, never
+// by host waits:
 //   * an upload into a slot first waits for the `released` event recorded
 //     after the last compute work that read the slot;
 //   * compute work that uses a freshly loaded slot waits for its `ready`
@@ -134,7 +135,8 @@ int acquire(dmhip_expert_cache *c, size_t layer_index, size_t expert, size_t *sl
     const size_t gu_bytes = layer.layout.gate_up_bytes, dn_bytes = layer.layout.down_bytes;
     const uint8_t *gu_src = c->source + layer.layout.gate_up_offset + expert * gu_bytes;
     const uint8_t *dn_src = c->source + layer.layout.down_offset + expert * dn_bytes;
-    hipStream_t up = c->ctx->upload;
+    // experts alternate between the two upload streams
+    hipStream_t up = (c->ctx->upload_next++ & 1u) ? c->ctx->upload2 : c->ctx->upload;
     if (s.released_recorded) DM_HIP(hipStreamWaitEvent(up, s.released, 0));
     DM_HIP(hipMemcpyAsync(s.gate_up, gu_src, gu_bytes, hipMemcpyHostToDevice, up));
     DM_HIP(hipMemcpyAsync(s.down, dn_src, dn_bytes, hipMemcpyHostToDevice, up));

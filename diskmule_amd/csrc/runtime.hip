@@ -225,6 +225,7 @@ int dmhip_context_new(int device, dmhip_ctx **out) {
     // Default-priority streams only.
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&ctx->upload, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->upload2, hipStreamNonBlocking) != hipSuccess ||
         hipMalloc((void **)&ctx->argmax_state, sizeof(ArgmaxState)) != hipSuccess ||
         hipMalloc((void **)&ctx->argmax_index, 64) != hipSuccess ||
         hipMalloc((void **)&ctx->flags, 64) != hipSuccess) {
@@ -240,6 +241,7 @@ void dmhip_context_free(dmhip_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->upload) (void)hipStreamSynchronize(ctx->upload);
+    if (ctx->upload2) (void)hipStreamSynchronize(ctx->upload2);
     ctx->in.release();
     ctx->out.release();
     ctx->enc.release();
@@ -252,6 +254,7 @@ void dmhip_context_free(dmhip_ctx *ctx) {
     for (hipEvent_t e : ctx->timing_pool) (void)hipEventDestroy(e);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     if (ctx->upload) (void)hipStreamDestroy(ctx->upload);
+    if (ctx->upload2) (void)hipStreamDestroy(ctx->upload2);
     delete ctx;
 }
 
@@ -267,6 +270,7 @@ int dmhip_synchronize(dmhip_ctx *ctx) {
     DM_REQUIRE(ctx);
     DM_CHECK(set_device(ctx));
     DM_HIP(hipStreamSynchronize(ctx->upload));
+    DM_HIP(hipStreamSynchronize(ctx->upload2));
     DM_HIP(hipStreamSynchronize(ctx->stream));
     return DMHIP_OK;
 }

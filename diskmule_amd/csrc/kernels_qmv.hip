@@ -402,14 +402,58 @@ __device__ __forceinline__ void block_dot(const Raw<kQ6_K> &raw, const half8 (&a
 }
 
 // ---------------------------------------------------------------------------
+// Weight staging.  A wave fetches G consecutive blocks of each of its 16-row
+// tiles as whole 16-byte chunks (row r of the tile: `chunks` chunks from the
+// dword at or below its first block; Q4_K runs start 16-aligned), consecutive
+// lanes on consecutive chunks of a row, and parks them in its own LDS area;
+// each lane then takes its operand pieces from there.  Every load
+// instruction covers a few long runs of rows instead of 16 rows' separate
+// 16-byte pieces.
+// ---------------------------------------------------------------------------
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 16-byte aligned (LDS)
+
+template <uint32_t TYPE, uint32_t G> struct StageQ {
+    static constexpr uint32_t chunks = TYPE == kQ4_K ? 9 * G : (210 * G + 2 + 15) / 16;
+    static constexpr uint32_t items = 16 * chunks;        // chunks of one tile
+    static constexpr uint32_t loads = (items + 63) / 64;  // 16-byte loads per lane
+};
+
+// Lane (n, kg)'s raw bytes of the block at byte `off` of row n's run.
+__device__ __forceinline__ void take_raw(const v4u *stage, uint32_t ch, uint32_t n, uint32_t kg, uint32_t off,
+                                         Raw<kQ4_K> &raw) {
+    const v4u *sr = stage + n * ch + off / 16;
+    raw.hdr = __builtin_bit_cast(u32x4, sr[0]);
+    raw.q0 = __builtin_bit_cast(u32x4, sr[1 + 2 * kg]);
+    raw.q1 = __builtin_bit_cast(u32x4, sr[2 + 2 * kg]);
+}
+
+__device__ __forceinline__ void take_raw(const v4u *stage, uint32_t ch, uint32_t n, uint32_t kg, uint32_t off,
+                                         Raw<kQ6_K> &raw) {
+    // dwords of row n from the one holding the block's first byte
+    const uint32_t *sw = (const uint32_t *)(stage + n * ch) + (off >> 2);
+    const uint32_t h = kg >> 1, c = kg & 1u;
+    const uint32_t o1 = 16 * h + 4 * c, o2 = o1 + 8, o3 = 32 + 8 * h + 4 * c;
+    raw.s = off & 3u;
+    raw.a1 = u32x4{sw[o1], sw[o1 + 1], sw[o1 + 2], sw[o1 + 3]};
+    raw.a2 = u32x4{sw[o2], sw[o2 + 1], sw[o2 + 2], sw[o2 + 3]};
+    raw.a3 = u32x4{sw[o3], sw[o3 + 1], sw[o3 + 2], sw[o3 + 3]};
+    raw.a4 = u32x4{sw[48], sw[49], sw[50], sw[51]};
+    raw.e1 = sw[o1 + 4];
+    raw.e2 = sw[o2 + 4];
+    raw.e3 = sw[o3 + 4];
+    raw.e4 = sw[52];
+    raw.e4b = sw[53];
+}
+
+// ---------------------------------------------------------------------------
 // Main kernel.  A workgroup has 4 waves; S waves split one group of R row
 // tiles along K, so a workgroup covers (4/S)*R tiles of 16 rows.
 // MB > 0: the activation fragments (MB = 2*batch rows) live in LDS.
 // MODE 0: y = W x.  MODE 1: also a per-wave argmax candidate.  MODE 2:
 // gate/up pair, act = silu(gate) * up.
 // ---------------------------------------------------------------------------
-template <uint32_t TYPE, int NT, int R, int S, int MODE, int MB>
-__global__ void __launch_bounds__(256) qmv_kernel(
+template <uint32_t TYPE, int NT, int R, int S, int MODE, int MB, uint32_t G>
+__global__ void __launch_bounds__(64 * (S > 4 ? S : 4)) qmv_kernel(
     const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows,
     uint32_t columns, uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x,
     int normalize, float epsilon, const _Float16 *__restrict__ xp,
@@ -418,16 +462,18 @@ __global__ void __launch_bounds__(256) qmv_kernel(
     constexpr uint32_t SPB = Steps<TYPE>::value;
     constexpr uint32_t BB = TYPE == kQ4_K ? 144u : 210u;
     constexpr int RR = MODE == 2 ? 2 * R : R;  // gate/up: R tiles of each matrix
-    __shared__ float partial[S > 1 ? 4 * RR * NT * 64 * 2 : 1];
+    constexpr uint32_t WAVES = S > 4 ? S : 4;
+    __shared__ float partial[S > 1 ? WAVES * RR * NT * 64 * 2 : 1];
     __shared__ float token_scale[2][4];
     extern __shared__ half8 lds_a[];
 
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15u, kg = lane >> 4;
     const uint32_t group = wave / S, kpart = wave % S;
-    const uint32_t first_tile = (blockIdx.x * (4 / S) + group) * R;
+    const uint32_t first_tile = (blockIdx.x * (WAVES / S) + group) * R;
     const uint32_t blocks = columns / 256;
-    const uint32_t b_begin = kpart * blocks / S, b_end = (kpart + 1) * blocks / S;
+    const uint32_t groups = (blocks + G - 1) / G;
+    const uint32_t g_begin = kpart * groups / S, g_end = (kpart + 1) * groups / S;
     const uint32_t m2 = 2 * batch;
     const float *yscale = yscale_global;
 
@@ -440,8 +486,8 @@ __global__ void __launch_bounds__(256) qmv_kernel(
         // preparation kernel) into LDS, followed by one zeroed block.
         const uint32_t count = blocks * SPB * 4 * MB;
         const half8 *src = (const half8 *)xp;
-        for (uint32_t i = threadIdx.x; i < count; i += 256) lds_a[i] = src[i];
-        for (uint32_t i = threadIdx.x; i < SPB * 4 * MB; i += 256)
+        for (uint32_t i = threadIdx.x; i < count; i += 64 * WAVES) lds_a[i] = src[i];
+        for (uint32_t i = threadIdx.x; i < SPB * 4 * MB; i += 64 * WAVES)
             lds_a[count + i] = half8{0, 0, 0, 0, 0, 0, 0, 0};
         if (threadIdx.x < MB / 2) token_scale[threadIdx.x][0] = yscale_global[threadIdx.x];
         __syncthreads();
@@ -471,15 +517,49 @@ __global__ void __launch_bounds__(256) qmv_kernel(
         row_base[r] = row < rows ? row * row_bytes : nowhere;
     }
 
-    auto load_block = [&](uint32_t blk, Raw<TYPE>(&raw)[RR]) {
+    // Staging: the wave's area holds RR tiles of ITEMS chunks; load j of
+    // this lane is chunk src_chunk[j] of row (item / CH) of each tile.
+    using ST = StageQ<TYPE, G>;
+    constexpr uint32_t CH = ST::chunks, NL = ST::loads, ITEMS = ST::items;
+    const size_t a_bytes = MB > 0 ? ((size_t)blocks + 1) * SPB * 4 * MB * 16 : 0;
+    v4u *stage = (v4u *)((uint8_t *)lds_a + a_bytes) + (size_t)wave * RR * ITEMS;
+    uint32_t src_row[RR][NL], src_chunk[NL];
+#pragma unroll
+    for (uint32_t j = 0; j < NL; j++) {
+        const uint32_t item = j * 64 + lane, ri = item / CH;
+        src_chunk[j] = 16 * (item - ri * CH);
 #pragma unroll
         for (int r = 0; r < RR; r++) {
-            const uint32_t off = row_base[r] == nowhere ? nowhere : row_base[r] + blk * BB;
-            load_raw<TYPE>((MODE == 2 && r >= R) ? rsrc2 : rsrc, off, kg, raw[r]);
+            const uint32_t row = (first_tile + (MODE == 2 ? r % R : r)) * 16 + ri;
+            src_row[r][j] = (item < ITEMS && row < rows) ? row * row_bytes : nowhere;
         }
+    }
+    v4u st[RR][NL];
+    auto fetch = [&](uint32_t grp) {
+#pragma unroll
+        for (int r = 0; r < RR; r++)
+#pragma unroll
+            for (uint32_t j = 0; j < NL; j++) {
+                const uint32_t off =
+                    src_row[r][j] == nowhere ? nowhere : ((src_row[r][j] + grp * G * BB) & ~3u) + src_chunk[j];
+                st[r][j] = __builtin_bit_cast(v4u, rsrc_load16((MODE == 2 && r >= R) ? rsrc2 : rsrc, off));
+            }
     };
-    auto compute_block = [&](uint32_t blk, const Raw<TYPE>(&raw)[RR]) {
-        half8 a[SPB][NT];
+    // A wave reads only its own area and its LDS operations run in order; the
+    // wavefront-scope fences keep the compiler from moving another lane's
+    // reads across these writes.
+    auto put = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int r = 0; r < RR; r++)
+#pragma unroll
+            for (uint32_t j = 0; j < NL; j++)
+                if (j + 1 < NL || j * 64 + lane < ITEMS) stage[r * ITEMS + j * 64 + lane] = st[r][j];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    };
+    // Activation fragments of block blk (from LDS, or from the prepared
+    // fragments in global memory one block ahead of their use).
+    auto load_a = [&](uint32_t blk, half8 (&a)[SPB][NT]) {
 #pragma unroll
         for (int t = 0; t < (int)SPB; t++)
 #pragma unroll
@@ -495,21 +575,40 @@ __global__ void __launch_bounds__(256) qmv_kernel(
                     a[t][g] = half8{0, 0, 0, 0, 0, 0, 0, 0};
                 }
             }
-#pragma unroll
-        for (int r = 0; r < RR; r++) block_dot<NT>(raw[r], a, kg, acc[r]);
     };
 
-    // Double-buffered: the loads of block b+1 are in flight while block b
-    // is computed.
-    if (b_begin < b_end) {
-        Raw<TYPE> raw0[RR], raw1[RR];
-        load_block(b_begin, raw0);
-        for (uint32_t blk = b_begin; blk < b_end; blk += 2) {
-            if (blk + 1 < b_end) load_block(blk + 1, raw1);
-            compute_block(blk, raw0);
-            if (blk + 1 >= b_end) break;
-            if (blk + 2 < b_end) load_block(blk + 2, raw0);
-            compute_block(blk + 1, raw1);
+    // The loads of group g+1 are in flight while group g is computed, and
+    // the activation fragments of the next block while a block is computed.
+    if (g_begin < g_end) {
+        const uint32_t blk_end = g_end * G < blocks ? g_end * G : blocks;
+        half8 a[SPB][NT];
+        load_a(g_begin * G, a);
+        fetch(g_begin);
+        for (uint32_t grp = g_begin; grp < g_end; grp++) {
+            put();
+            if (grp + 1 < g_end) fetch(grp + 1);
+#pragma unroll
+            for (uint32_t b = 0; b < G; b++) {
+                const uint32_t blk = grp * G + b;
+                if (blk >= blk_end) break;
+                half8 a_next[SPB][NT];
+                if (blk + 1 < blk_end) load_a(blk + 1, a_next);
+                Raw<TYPE> raw[RR];
+#pragma unroll
+                for (int r = 0; r < RR; r++) {
+                    // the run of row n starts 0 or 2 bytes into its first dword (Q6_K)
+                    const uint32_t s0 = row_base[r] == nowhere ? 0u : ((row_base[r] + grp * G * BB) & 3u);
+                    take_raw(stage + r * ITEMS, CH, n, kg, s0 + b * BB, raw[r]);
+                }
+#pragma unroll
+                for (int r = 0; r < RR; r++) block_dot<NT>(raw[r], a, kg, acc[r]);
+                if (blk + 1 < blk_end) {
+#pragma unroll
+                    for (int t = 0; t < (int)SPB; t++)
+#pragma unroll
+                        for (int g = 0; g < NT; g++) a[t][g] = a_next[t][g];
+                }
+            }
         }
     }
 
@@ -582,7 +681,7 @@ __global__ void __launch_bounds__(256) qmv_kernel(
             p.key = best;
             p.non_finite = bad;
             p.pad = 0;
-            partials[blockIdx.x * (4 / S) + group] = p;
+            partials[blockIdx.x * (WAVES / S) + group] = p;
         }
     }
 }
@@ -654,26 +753,58 @@ namespace {
 constexpr size_t kMaxLdsA = 56 * 1024;  // staged activation fragments; + split-K scratch <= 64 KiB
 
 struct Plan {
-    int nt, r, s, mb;
+    int nt, r, s, mb, g;
 };
 
+int env_int(const char *name) {
+    const char *v = getenv(name);
+    return v ? atoi(v) : 0;
+}
+
 Plan choose_plan(uint32_t type, uint32_t rows, uint32_t blocks, uint32_t batch, int mode) {
+    static const int forced_g = env_int("DMHIP_QMV_G");
+    static const int forced_s = env_int("DMHIP_QMV_SPLIT");
     Plan p;
     p.nt = batch > 8 ? 2 : 1;
     const uint32_t tiles = (rows + 15) / 16;
-    p.r = (batch > 2 && mode != 2) ? 2 : 1;
-    // Enough waves to fill 256 CUs several times over; otherwise split K.
-    const uint32_t waves = (tiles + p.r - 1) / p.r;
-    if (waves >= 2048 || blocks < 2) {
-        p.s = 1;
-    } else if (waves >= 1024 || blocks < 4) {
-        p.s = 2;
-    } else {
-        p.s = 4;
-    }
     const uint32_t spb = type == kQ4_K ? 9 : 8;
-    const size_t lds = ((size_t)blocks + 1) * spb * 4 * 2 * batch * 16;
-    p.mb = (batch <= 2 && lds <= kMaxLdsA) ? (int)(2 * batch) : 0;
+    const size_t a_lds = ((size_t)blocks + 1) * spb * 4 * 2 * batch * 16;
+    p.mb = (batch <= 2 && a_lds <= kMaxLdsA) ? (int)(2 * batch) : 0;
+    // Two tiles per wave share each activation fragment load (batches above
+    // 2, one matrix, tall matrices); short matrices need the waves more.
+    p.r = (batch > 2 && mode != 2 && tiles >= 2048) ? 2 : 1;
+    const uint32_t rr = mode == 2 ? 2 * p.r : p.r;
+    // Blocks per staged group: 2 (runs of 2 blocks stream faster), or 1 when
+    // the row has a single block or LDS is short; DMHIP_QMV_G (1, 2) overrides.
+    p.g = (forced_g == 1 || forced_g == 2) ? forced_g : (blocks >= 2 ? 2 : 1);
+    // Split each tile's block groups over S waves of a workgroup until the
+    // launch has about 4096 waves, with at least two groups per wave (S = 8
+    // only for prepared activations of up to 8 tokens, else S <= 4);
+    // DMHIP_QMV_SPLIT (1, 2, 4, 8) overrides.
+    const uint32_t waves = (tiles + p.r - 1) / p.r;
+    const uint32_t s_max = (p.mb == 0 && p.nt == 1) ? 8 : 4;
+    uint32_t s = 1;
+    if (forced_s == 1 || forced_s == 2 || forced_s == 4 || (forced_s == 8 && s_max == 8)) {
+        s = (uint32_t)forced_s;
+    } else {
+        while (s < s_max && (size_t)waves * s < 4096 && (blocks + p.g - 1) / p.g >= 4 * s) s *= 2;
+    }
+    // Dynamic (activations, staging) plus static (split-K partials) LDS
+    // within the 160 KiB of a workgroup: first one block per group, then a
+    // narrower split.
+    for (;;) {
+        const uint32_t wv = s > 4 ? s : 4;
+        const size_t items = 16 * (type == kQ4_K ? 9 * p.g : (210 * p.g + 2 + 15) / 16);
+        const size_t lds = (p.mb > 0 ? a_lds : 0) + (size_t)wv * rr * items * 16 +
+                           (s > 1 ? (size_t)wv * rr * p.nt * 64 * 2 * 4 : 4) + 256;
+        if (lds <= 160 * 1024 || s == 1) break;
+        if (p.g == 2) {
+            p.g = 1;
+        } else {
+            s /= 2;
+        }
+    }
+    p.s = (int)s;
     return p;
 }
 
@@ -690,25 +821,46 @@ struct Args {
     ArgmaxPartial *partials;
 };
 
-template <uint32_t TYPE, int NT, int R, int S, int MODE, int MB>
+template <uint32_t TYPE, int NT, int R, int S, int MODE, int MB, uint32_t G>
 hipError_t run(dmhip_ctx *ctx, const Args &a, uint32_t *waves_out) {
     constexpr uint32_t SPB = Steps<TYPE>::value;
+    constexpr int RR = MODE == 2 ? 2 * R : R;
+    constexpr uint32_t WAVES = S > 4 ? S : 4;
     const uint32_t tiles = (a.rows + 15) / 16;
-    const uint32_t per_wg = (4 / S) * R;
+    const uint32_t per_wg = (WAVES / S) * R;
     const uint32_t grid = (tiles + per_wg - 1) / per_wg;
-    // fragments of every block plus one zeroed block for the idle A rows
-    const size_t lds = MB > 0 ? ((size_t)(a.columns / 256) + 1) * SPB * 4 * MB * 16 : 0;
-    if (waves_out) *waves_out = grid * (4 / S);
-    return launch_kernel(ctx, qmv_kernel<TYPE, NT, R, S, MODE, MB>, dim3(grid), dim3(256), lds,
-                         (const uint8_t *)a.w, (const uint8_t *)a.w2, a.rows, a.columns, a.row_bytes, a.total, a.x,
-                         a.normalize, a.epsilon, a.xp, a.ysc, a.batch, a.y, a.partials);
+    // fragments of every block plus one zeroed block for the idle A rows,
+    // then each wave's weight staging area
+    const size_t lds = (MB > 0 ? ((size_t)(a.columns / 256) + 1) * SPB * 4 * MB * 16 : 0) +
+                       (size_t)WAVES * RR * StageQ<TYPE, G>::items * 16;
+    if (waves_out) *waves_out = grid * (WAVES / S);
+    auto kernel = qmv_kernel<TYPE, NT, R, S, MODE, MB, G>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    return launch_kernel(ctx, kernel, dim3(grid), dim3(64 * WAVES), (uint32_t)lds, (const uint8_t *)a.w,
+                         (const uint8_t *)a.w2, a.rows, a.columns, a.row_bytes, a.total, a.x, a.normalize, a.epsilon,
+                         a.xp, a.ysc, a.batch, a.y, a.partials);
+}
+
+template <uint32_t TYPE, int NT, int R, int MODE, int MB, uint32_t G>
+hipError_t run_sg(dmhip_ctx *ctx, const Plan &p, const Args &a, uint32_t *w) {
+    if (p.s == 1) return run<TYPE, NT, R, 1, MODE, MB, G>(ctx, a, w);
+    if (p.s == 2) return run<TYPE, NT, R, 2, MODE, MB, G>(ctx, a, w);
+    if constexpr (MB == 0 && NT == 1) {
+        // the 8-wave split serves short matrices with prepared activations of
+        // up to 8 tokens (wider splits or two token groups outgrow the
+        // registers of the larger workgroup)
+        if (p.s == 8) return run<TYPE, NT, R, 8, MODE, MB, G>(ctx, a, w);
+    }
+    return run<TYPE, NT, R, 4, MODE, MB, G>(ctx, a, w);
 }
 
 template <uint32_t TYPE, int NT, int R, int MODE, int MB>
 hipError_t run_s(dmhip_ctx *ctx, const Plan &p, const Args &a, uint32_t *w) {
-    if (p.s == 1) return run<TYPE, NT, R, 1, MODE, MB>(ctx, a, w);
-    if (p.s == 2) return run<TYPE, NT, R, 2, MODE, MB>(ctx, a, w);
-    return run<TYPE, NT, R, 4, MODE, MB>(ctx, a, w);
+    if (p.g == 2) return run_sg<TYPE, NT, R, MODE, MB, 2>(ctx, p, a, w);
+    return run_sg<TYPE, NT, R, MODE, MB, 1>(ctx, p, a, w);
 }
 
 template <uint32_t TYPE, int MODE>

@@ -783,7 +783,7 @@ hipError_t run8_g(dmhip_ctx *ctx, const Plan8 &p, const Args8 &a) {
 // runs of 2 blocks stream about 60% faster than single blocks; G = 1
 // otherwise; DMHIP_QMV8_GROUPED_G forces 1 or 2), and a split of each tile's
 // block groups that gives the whole launch about 4096 wave-tiles with at
-// least two groups per wave.
+// least one group per wave.
 Plan8 plan8_grouped(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t mats,
                     uint32_t jobs) {
     static const int forced_s = env_int("DMHIP_QMV8_GROUPED_SPLIT");

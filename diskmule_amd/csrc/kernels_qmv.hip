@@ -23,11 +23,14 @@
 // the lane supplies.  C[m][n] sits in lane n + 16*(m/4), element m%4, so
 // lane (n, g4) accumulates tokens 2*g4 and 2*g4+1 of row n.
 //
-// Data movement: every lane loads its own 16-byte pieces of a block straight
-// into registers with buffer loads (out-of-range rows read zero), one block
-// ahead of the compute (double-buffered).  For batch 1-2 the activation
+// Data movement: a wave stages G = 2 consecutive blocks of each of its row
+// tiles in its own LDS area with contiguous 16-byte loads (out-of-range rows
+// read zero), the next group in flight while the current one is computed,
+// and every lane takes its pieces from there.  For batch 1-2 the activation
 // fragments of the whole row are staged once per workgroup in LDS and read
-// with ds_read_b128; for larger batches they come from L2.
+// with ds_read_b128; for larger batches they come from L2, the next block's
+// while a block is computed.  Short matrices split K over up to 8 waves of a
+// workgroup.
 #include "dm_device.h"
 #include "dm_qmv.h"
 
@@ -221,37 +224,6 @@ template <> struct Raw<kQ6_K> {
     uint32_t e1, e2, e3, e4, e4b;  // the dword after each (for the byte shift)
     uint32_t s;                    // block start mod 4
 };
-
-template <uint32_t TYPE>
-__device__ __forceinline__ void load_raw(__amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t kg,
-                                         Raw<TYPE> &raw);
-
-template <>
-__device__ __forceinline__ void load_raw<kQ4_K>(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t kg,
-                                                Raw<kQ4_K> &raw) {
-    raw.hdr = rsrc_load16(rs, off);
-    raw.q0 = rsrc_load16(rs, off + 16 + 32 * kg);
-    raw.q1 = rsrc_load16(rs, off + 32 + 32 * kg);
-}
-
-template <>
-__device__ __forceinline__ void load_raw<kQ6_K>(__amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t kg,
-                                                Raw<kQ6_K> &raw) {
-    const uint32_t s = boff & 3u, base = boff - s;
-    const uint32_t h = kg >> 1, c = kg & 1u;
-    const uint32_t o1 = base + 64 * h + 16 * c, o2 = o1 + 32, o3 = base + 128 + 32 * h + 16 * c,
-                   o4 = base + 192;
-    raw.s = s;
-    raw.a1 = rsrc_load16(rs, o1);
-    raw.a2 = rsrc_load16(rs, o2);
-    raw.a3 = rsrc_load16(rs, o3);
-    raw.a4 = rsrc_load16(rs, o4);
-    raw.e1 = rsrc_load4(rs, o1 + 16);
-    raw.e2 = rsrc_load4(rs, o2 + 16);
-    raw.e3 = rsrc_load4(rs, o3 + 16);
-    raw.e4 = rsrc_load4(rs, o4 + 16);
-    raw.e4b = rsrc_load4(rs, o4 + 20);
-}
 
 template <int NT>
 __device__ __forceinline__ void block_dot(const Raw<kQ4_K> &raw, const half8 (&a)[9][NT], uint32_t kg,

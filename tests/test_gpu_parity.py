@@ -181,6 +181,27 @@ def test_batched_gemv_matches_oracle(ctx, batch):
             assert_close(got[b], want[b], f"type {kind} batch {batch} token {b}")
 
 
+@pytest.mark.parametrize("kind,rows,cols,batch", [
+    (Q6_K, 2048, 768, 4),    # 630-byte rows (every other row 2 bytes off a dword), odd block count
+    (Q6_K, 300, 12288, 8),   # short and wide: K split over 8 waves, partial last tile
+    (Q4_K, 100, 12288, 12),  # two token groups, partial tile
+    (Q4_K, 4096, 12288, 3),
+    (Q6_K, 1000, 2560, 5),   # 10 blocks: partial last pair of a split
+])
+def test_batched_gemv_short_and_misaligned_shapes(ctx, kind, rows, cols, batch):
+    """Batches above 2 on shapes that take the fp16 kernel's wide K split,
+    its partial block pairs and misaligned Q6_K rows."""
+    print(f"batched gemv type={kind} {rows}x{cols} batch={batch}", flush=True)
+    w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(90 + batch))
+    x = synth.normal(synth.activation_seed(90 + batch), batch * cols).reshape(batch, cols)
+    want = np.stack([capi.matvec(kind, rows, cols, w, x[b]) for b in range(batch)])
+    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, batch * rows * 4)
+    ctx.matvec_device(kind, rows, cols, wb.device_ptr, batch, xb.device_ptr, yb.device_ptr)
+    got = yb.read(0, batch * rows * 4, np.float32).reshape(batch, rows)
+    for b in range(batch):
+        assert_close(got[b], want[b], f"type {kind} {rows}x{cols} batch {batch} token {b}")
+
+
 @pytest.mark.parametrize("kind,rows,cols,x_stride", [(Q4_K, 1000, 2048, 0), (Q6_K, 1000, 2048, 2048),
                                                      (Q4_K, 4096, 4096, 0), (Q8_0, 300, 512, 512)])
 def test_matvec_batch_matches_one_matvec_per_matrix(ctx, kind, rows, cols, x_stride):

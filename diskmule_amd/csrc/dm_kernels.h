@@ -5,9 +5,32 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace dm {
 
 constexpr uint32_t kMaxTopK = 256;
+
+// A kernel's dynamic-LDS limit per device: raised to the size a launch asks
+// for when that exceeds what was set on the device before (the attribute
+// belongs to each device's copy of the code object).  Safe to share between
+// threads (one instance per kernel, as a function-local static).
+struct LdsLimit {
+    std::atomic<uint32_t> set[64] = {};  // bytes allowed on device d (0..63)
+    hipError_t ensure(const void *kernel, size_t bytes) {
+        int device = 0;
+        hipError_t e = hipGetDevice(&device);
+        if (e != hipSuccess) return e;
+        const bool cached = device >= 0 && device < 64;
+        if (cached && set[device].load(std::memory_order_acquire) >= bytes) return hipSuccess;
+        e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+        if (e != hipSuccess || !cached) return e;
+        uint32_t have = set[device].load(std::memory_order_relaxed);
+        while (have < bytes && !set[device].compare_exchange_weak(have, (uint32_t)bytes, std::memory_order_acq_rel)) {
+        }
+        return hipSuccess;
+    }
+};
 
 // Device-side argmax accumulator: packed (ordered value, ~index) key and a
 // non-finite flag.

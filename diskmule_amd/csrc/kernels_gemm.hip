@@ -489,12 +489,8 @@ int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t type, size_t m, size_t n, size_t 
                            0, ctx->stream, a_bf16, (uint32_t)m, (uint32_t)k, a16, rowscale);
         DM_HIP(hipGetLastError());
         const uint32_t n_tiles = (uint32_t)((n + kBN - 1) / kBN), m_tiles = (uint32_t)(mp / kBM);
-        static bool lds_set = false;  // 128 KiB of dynamic LDS, allowed once per process
-        if (!lds_set) {
-            DM_HIP(hipFuncSetAttribute((const void *)gemm_q4k_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kLdsBytes));
-            lds_set = true;
-        }
+        static LdsLimit limit;  // 136 KiB of dynamic LDS
+        DM_HIP(limit.ensure((const void *)gemm_q4k_kernel, kLdsBytes));
         {
             DM_HIP(launch_kernel(ctx, gemm_q4k_kernel, dim3(n_tiles * m_tiles), dim3(64 * kWaves), kLdsBytes,
                                  (const half8 *)a16, (const float *)rowscale, (const uint8_t *)weights, (uint32_t)m,

@@ -808,7 +808,8 @@ hipError_t run(dmhip_ctx *ctx, const Args &a, uint32_t *waves_out) {
     if (waves_out) *waves_out = grid * (WAVES / S);
     auto kernel = qmv_kernel<TYPE, NT, R, S, MODE, MB, G>;
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        static LdsLimit limit;
+        hipError_t e = limit.ensure((const void *)kernel, lds);
         if (e != hipSuccess) return e;
     }
     return launch_kernel(ctx, kernel, dim3(grid), dim3(64 * WAVES), (uint32_t)lds, (const uint8_t *)a.w,

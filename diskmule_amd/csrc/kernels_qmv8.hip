@@ -753,7 +753,8 @@ hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
     if (a.count) *a.count = grid;
     auto kernel = qmv8_kernel<TYPE, S, MODE, TOK, G>;
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        static LdsLimit limit;
+        hipError_t e = limit.ensure((const void *)kernel, lds);
         if (e != hipSuccess) return e;
     }
     return launch_kernel(ctx, kernel, dim3(grid), dim3(64 * WAVES), lds, (const uint8_t *)a.w,
@@ -826,7 +827,8 @@ hipError_t run8_grouped(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, uint64_
     const uint32_t grid = (tiles + per - 1) / per;
     auto kernel = qmv8_grouped_kernel<TYPE, S, MODE, TOK, G>;
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        static LdsLimit limit;
+        hipError_t e = limit.ensure((const void *)kernel, lds);
         if (e != hipSuccess) return e;
     }
     return launch_kernel(ctx, kernel, dim3(grid, count), dim3(64 * WAVES), lds, table, rows, columns, row_bytes,

@@ -502,14 +502,11 @@ static hipError_t launch_router_staged(hipStream_t s, const uint16_t *router, ui
                                        float *logits, uint32_t *ids, float *probabilities,
                                        uint32_t *non_finite, uint32_t *host_ids, float *host_probs) {
     const size_t lds = 2 * (((size_t)experts * (CC * 2 + 16) + CC * 4 + 15) & ~(size_t)15);
-    static bool attribute_set = false;  // the largest slot ring, set once
-    if (!attribute_set) {
-        const size_t most = 2 * (((size_t)(2048 / (CC / 8)) * (CC * 2 + 16) + CC * 4 + 15) & ~(size_t)15);
-        hipError_t e = hipFuncSetAttribute((const void *)router_staged_kernel<CC>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)most);
-        if (e != hipSuccess) return e;
-        attribute_set = true;
-    }
+    // the largest slot ring, once per device
+    static LdsLimit limit;
+    const size_t most = 2 * (((size_t)(2048 / (CC / 8)) * (CC * 2 + 16) + CC * 4 + 15) & ~(size_t)15);
+    hipError_t e = limit.ensure((const void *)router_staged_kernel<CC>, most);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(router_staged_kernel<CC>, dim3(batch), dim3(256), lds, s, router, hidden, experts, k, x,
                        logits, ids, probabilities, non_finite, host_ids, host_probs);
     return hipGetLastError();

@@ -17,9 +17,10 @@ launch from rocprofv3 FETCH_SIZE/WRITE_SIZE runs (profiles/), when present.
 16 threads) on the same C2 workload, on this machine's host cores.
 
 ``details`` holds the other BASELINE configurations (C1, C3, C4, C5), each
-measured the same way.
+measured the same way, and a Q8_0 GEMV entry (the third k-quant of the north
+star, which no configuration uses).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|copy]
 """
 from __future__ import annotations
 
@@ -173,6 +174,30 @@ def bench_c1(ctx, synth, steps, warmup):
                         "gbps": per / (ms * 1e-3) / 1e9, "frac_of_peak": per / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     log(f"C1: cold kernel {out['cold']['kernel_ms'] * 1e3:.2f} us ({out['cold']['kernel_gbps']:.0f} GB/s); "
         f"sustained {ms * 1e3:.2f} us per matrix ({out['sustained']['gbps']:.0f} GB/s)")
+    return out
+
+
+def bench_q8(ctx, synth, steps, warmup):
+    """Q8_0 (named in the north star; no BASELINE config): batch-1 GEMV at the
+    C2 and C1 shapes, weights resident, back-to-back launches."""
+    Q8_0 = 8
+    out = {}
+    for rows, cols in ((151936, 4096), (4096, 4096)):
+        w = synth.quantized_matrix(Q8_0, rows, cols, synth.weight_seed(8, rows))
+        x = synth.normal(synth.activation_seed(8), cols)
+        wb, xb, yb = upload(ctx, w), upload(ctx, x), ctx.new_owned_buffer(rows * 4)
+        for _ in range(warmup):
+            ctx.matvec_device(Q8_0, rows, cols, wb.device_ptr, 1, xb.device_ptr, yb.device_ptr)
+        ctx.synchronize()
+        time.sleep(0.2)
+        with Timed(ctx, kernels=False) as t:
+            for _ in range(steps):
+                ctx.matvec_device(Q8_0, rows, cols, wb.device_ptr, 1, xb.device_ptr, yb.device_ptr)
+        ms = t.wall_ms / steps
+        step_bytes = w.size + 4 * cols + 4 * rows
+        out[f"{rows}x{cols}"] = {"ms": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9,
+                                 "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        log(f"Q8_0 {rows}x{cols}: {ms * 1e3:.1f} us per launch ({out[f'{rows}x{cols}']['gbps']:.0f} GB/s)")
     return out
 
 
@@ -382,14 +407,14 @@ def main() -> int:
     log("device:", ctx.device_name())
     if args.only:
         fn = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-              "copy": bench_copy}[args.only]
+              "q8": bench_q8, "copy": bench_copy}[args.only]
         res = fn(ctx, synth, args.steps, args.warmup)
         print(json.dumps(res[0] if isinstance(res, tuple) else res))
         return 0
 
     c2, (w2, x2) = bench_c2(ctx, synth, args.steps, args.warmup)
     details = {"C2": c2}
-    for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5)):
+    for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5), ("Q8_0", bench_q8)):
         details[name] = fn(ctx, synth, max(3, args.steps // 2), args.warmup)
     log("CPU baseline")
     cpu = cpu_baseline(w2, x2, args.cpu_seconds)

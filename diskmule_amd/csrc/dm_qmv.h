@@ -13,8 +13,8 @@ struct ArgmaxPartial {
     uint32_t pad;
 };
 
-// True when the int8-MFMA matvec (decode batches of 1-2 tokens, Q4_K/Q6_K)
-// takes this shape; the caller has already checked qmv_supported.
+// True when the int8-MFMA matvec (decode batches of 1-2 tokens, Q4_K/Q6_K/
+// Q8_0) takes this shape; the caller has already checked qmv_supported.
 bool qmv8_supported(uint32_t type, size_t rows, size_t columns, size_t batch);
 
 // y[b][r] = W[r] . x[b] with the int8-MFMA kernels.  With `partials` the
@@ -55,7 +55,8 @@ hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uin
 
 // True when the MFMA matvec takes this shape: Q4_K or Q6_K rows of whole
 // 256-value blocks, a weight base address aligned to 4 bytes (16 for Q4_K),
-// and fewer than 4 GiB of weights (one buffer descriptor).
+// and fewer than 4 GiB of weights (one buffer descriptor); or Q8_0 rows of
+// whole 256-value super-blocks at a 16-byte aligned base, batch 1-2.
 bool qmv_supported(uint32_t type, size_t rows, size_t columns, const void *w, size_t batch);
 
 // y[b][r] = W[r] . x[b]; when `argmax` is non-null (batch 1) the kernels

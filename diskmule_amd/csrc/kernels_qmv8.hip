@@ -1,5 +1,5 @@
 // kernels_qmv8.hip -- int8-MFMA quantized matvec for gfx950: decode batches
-// of one or two tokens over Q4_K / Q6_K rows.
+// of one or two tokens over Q4_K / Q6_K / Q8_0 rows.
 //
 // y[b][r] = sum_c W[r][c] * x[b][c] (src/cpu.rs:345-399 semantics; the group
 // dots are exact integers, the blocks accumulate in fp32).
@@ -13,7 +13,10 @@
 // of its own code group with up to four activation rows.
 //
 //  * Weights enter as their raw codes: Q4_K nibbles 0..15, Q6_K 6-bit codes
-//    0..63.  No floating-point conversion and no per-weight scale.
+//    0..63, Q8_0 signed bytes.  No floating-point conversion and no
+//    per-weight scale.  A Q8_0 row is handled in 256-value super-blocks of 8
+//    blocks (272 bytes); lane group g holds blocks 2g and 2g + 1, each step
+//    within one block, whose d scales that step's dot.
 //  * Each 256-value block of a token is scaled by its own power of two so
 //    max|x| 2^-e < 2^22 over the block and rounded to integers
 //    X = 65536 hi + 256 mid + lo (balanced bytes); A rows 4g + {0, 1, 2} carry
@@ -50,11 +53,16 @@ constexpr uint32_t kMaxWaves8 = 16;
 template <uint32_t TYPE> struct Rec8;
 template <> struct Rec8<kQ4_K> { static constexpr uint32_t bytes = 4 * kStep8 + 32 + 16; };
 template <> struct Rec8<kQ6_K> { static constexpr uint32_t bytes = 4 * kStep8 + 256 + 16; };
+template <> struct Rec8<kQ8_0> { static constexpr uint32_t bytes = 4 * kStep8 + 16; };
+
+// Bytes of one 256-value block (Q8_0: 8 blocks of 34).
+template <uint32_t TYPE> constexpr uint32_t kBlock8 = TYPE == kQ4_K ? 144u : TYPE == kQ6_K ? 210u : 272u;
 
 // Column (0..255) of byte i of lane group g's 16 codes at step t.
 template <uint32_t TYPE>
 __device__ __forceinline__ uint32_t column8(uint32_t t, uint32_t g, uint32_t i) {
     if (TYPE == kQ4_K) return 64 * g + 16 * t + i;  // qs[32g + 16(t&1) + i], nibble t >> 1
+    if (TYPE == kQ8_0) return 64 * g + 16 * t + i;  // block 2g + t/2, codes 16(t&1) + i
     return 128 * (g >> 1) + 32 * t + 16 * (g & 1u) + i;
 }
 
@@ -138,7 +146,9 @@ __device__ __forceinline__ void build_records8(const float *__restrict__ x, int 
             uint8_t *r = rec + ((size_t)b * TOK + tok) * REC;
 #pragma unroll
             for (int k = 0; k < 3; k++) *(uint32_t *)(r + t * kStep8 + (g * 3 + k) * 16 + 4 * q) = term[k];
-            if (TYPE == kQ6_K) {
+            if constexpr (TYPE == kQ8_0) {
+                // signed codes, no offset: nothing besides the A fragments
+            } else if (TYPE == kQ6_K) {
                 // group (t, g) = the four adjacent lanes q = 0..3
 #pragma unroll
                 for (int k = 0; k < 3; k++) {
@@ -171,6 +181,13 @@ template <uint32_t TYPE> struct Raw8;
 template <> struct Raw8<kQ4_K> {
     u32x4 hdr, q0, q1;  // d|dmin|scales; qs bytes [32g, 32g+16) and [32g+16, 32g+32)
 };
+template <> struct Raw8<kQ8_0> {
+    // bytes [68g, 68g + 68) of the super-block: blocks 2g (d, 32 codes from
+    // byte 2) and 2g + 1 (d at 34, codes from 36, dword-aligned)
+    u32x4 w0, w1;  // dwords 0..7
+    uint32_t w8;   // dword 8: last two codes of block 2g, d of block 2g + 1
+    u32x4 c2, c3;  // dwords 9..16: codes of block 2g + 1
+};
 template <> struct Raw8<kQ6_K> {
     u32x4 a1, a2, a3, a4;      // aligned dwords under ql[64h+16c], ql[64h+32+16c], qh[32h+16c], scales
     uint32_t e1, e2, e3, e4;   // the dword after each (e4 also holds d)
@@ -186,7 +203,7 @@ template <> struct Raw8<kQ6_K> {
 // runs of cache lines; the lanes then read their own pieces of their own row
 // from LDS.
 template <uint32_t TYPE, uint32_t G> struct Stage8 {
-    static constexpr uint32_t chunks = TYPE == kQ4_K ? 9 * G : (210 * G + 2 + 15) / 16;
+    static constexpr uint32_t chunks = TYPE == kQ4_K ? 9 * G : TYPE == kQ8_0 ? 17 * G : (210 * G + 2 + 15) / 16;
     static constexpr uint32_t items = 16 * chunks;        // chunks of one tile
     static constexpr uint32_t loads = (items + 63) / 64;  // 16-byte loads per lane
     static constexpr uint32_t bytes = items * 16;         // one wave's staging area
@@ -204,6 +221,16 @@ __device__ __forceinline__ void take8(const v4u *stage, uint32_t n, uint32_t g, 
     raw.hdr = as_u32x4(sr[0]);
     raw.q0 = as_u32x4(sr[1 + 2 * g]);
     raw.q1 = as_u32x4(sr[2 + 2 * g]);
+}
+
+template <uint32_t CH>
+__device__ __forceinline__ void take8(const v4u *stage, uint32_t n, uint32_t g, uint32_t off, Raw8<kQ8_0> &raw) {
+    const uint32_t *sw = (const uint32_t *)(stage + n * CH) + off / 4 + 17 * g;  // super-blocks stay 16-aligned
+    raw.w0 = u32x4{sw[0], sw[1], sw[2], sw[3]};
+    raw.w1 = u32x4{sw[4], sw[5], sw[6], sw[7]};
+    raw.w8 = sw[8];
+    raw.c2 = u32x4{sw[9], sw[10], sw[11], sw[12]};
+    raw.c3 = u32x4{sw[13], sw[14], sw[15], sw[16]};
 }
 
 template <uint32_t CH>
@@ -267,6 +294,36 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ4_K> &raw, const i32x4 *
         const float mins = __builtin_fmaf(mn[1], sums[1], mn[0] * sums[0]);
         acc[tok] = __builtin_fmaf(d * bs, part, acc[tok]);
         acc[tok] = __builtin_fmaf(-dmin * bs, mins, acc[tok]);
+    }
+}
+
+// Q8_0 (src/cpu.rs:576-583, value = d * q): the codes of block 2g start two
+// bytes into dword 0, so steps 0 and 1 take dwords shifted by two bytes;
+// block 2g + 1's codes are dword-aligned.
+template <int TOK>
+__device__ __forceinline__ void block_dot8(const Raw8<kQ8_0> &raw, const i32x4 *lds, uint32_t a_off,
+                                           uint32_t a_stride, uint32_t rec, uint32_t g, float (&acc)[TOK]) {
+    constexpr uint32_t REC = Rec8<kQ8_0>::bytes;
+    const uint32_t w[9] = {raw.w0[0], raw.w0[1], raw.w0[2], raw.w0[3], raw.w1[0],
+                           raw.w1[1], raw.w1[2], raw.w1[3], raw.w8};
+    i32x4 b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        b[0][i] = (int)funnel(w[i], w[i + 1], 2);
+        b[1][i] = (int)funnel(w[i + 4], w[i + 5], 2);
+    }
+    b[2] = __builtin_bit_cast(i32x4, raw.c2);
+    b[3] = __builtin_bit_cast(i32x4, raw.c3);
+    const float d0 = f16_lo(raw.w0[0]), d1 = f16_lo(raw.w8 >> 16);
+    const i32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int tok = 0; tok < TOK; tok++) {
+        const uint32_t a = (a_off + tok * a_stride) / 16;
+        const float p0 = combine8(mfma8(lds[a], b[0], zero)) + combine8(mfma8(lds[a + kStep8 / 16], b[1], zero));
+        const float p1 =
+            combine8(mfma8(lds[a + 2 * kStep8 / 16], b[2], zero)) + combine8(mfma8(lds[a + 3 * kStep8 / 16], b[3], zero));
+        const float bs = ((const float *)lds)[(rec + tok * REC + REC - 16) / 4];  // block scale 2^e
+        acc[tok] = __builtin_fmaf(bs, __builtin_fmaf(d1, p1, d0 * p0), acc[tok]);
     }
 }
 
@@ -360,7 +417,7 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     constexpr uint32_t WAVES = S > 8 ? S : 8;
     constexpr int NM = MODE == 2 ? 2 : 1;  // weight matrices streamed
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
-    constexpr uint32_t BB = TYPE == kQ4_K ? 144u : 210u;
+    constexpr uint32_t BB = kBlock8<TYPE>;
     using ST = Stage8<TYPE, G>;
     constexpr uint32_t CH = ST::chunks, NL = ST::loads, ITEMS = ST::items;
     extern __shared__ i32x4 lds8[];
@@ -662,13 +719,14 @@ constexpr size_t kMaxLds8 = 160 * 1024;  // gfx950 LDS per workgroup
 
 size_t stage_bytes8(uint32_t type, uint32_t g) {
     if (type == kQ4_K) return g == 1 ? Stage8<kQ4_K, 1>::bytes : g == 2 ? Stage8<kQ4_K, 2>::bytes : Stage8<kQ4_K, 4>::bytes;
+    if (type == kQ8_0) return g == 1 ? Stage8<kQ8_0, 1>::bytes : g == 2 ? Stage8<kQ8_0, 2>::bytes : Stage8<kQ8_0, 4>::bytes;
     return g == 1 ? Stage8<kQ6_K, 1>::bytes : g == 2 ? Stage8<kQ6_K, 2>::bytes : Stage8<kQ6_K, 4>::bytes;
 }
 
 // Dynamic LDS of one workgroup: records, zeroed region, staging per wave
 // (one area per streamed matrix).
 size_t lds8_bytes(uint32_t type, uint32_t blocks, uint32_t batch, uint32_t waves, uint32_t g, uint32_t mats) {
-    const size_t rec = type == kQ4_K ? Rec8<kQ4_K>::bytes : Rec8<kQ6_K>::bytes;
+    const size_t rec = type == kQ4_K ? Rec8<kQ4_K>::bytes : type == kQ8_0 ? Rec8<kQ8_0>::bytes : Rec8<kQ6_K>::bytes;
     return (size_t)blocks * batch * rec + kZero8 + (size_t)waves * mats * stage_bytes8(type, g);
 }
 
@@ -734,7 +792,7 @@ hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
     const uint32_t rows = a.rows, columns = a.columns;
     const uint32_t tiles = (rows + 15) / 16;
     const uint32_t blocks = columns / 256;
-    const uint32_t row_bytes = blocks * (TYPE == kQ4_K ? 144u : 210u);
+    const uint32_t row_bytes = blocks * kBlock8<TYPE>;
     const size_t lds = lds8_bytes(TYPE, blocks, TOK, WAVES, G, MODE == 2 ? 2u : 1u);
     uint32_t grid;
     if (S == 1) {
@@ -820,7 +878,7 @@ hipError_t run8_grouped(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, uint64_
     constexpr uint32_t WAVES = 8;
     const uint32_t tiles = (rows + 15) / 16;
     const uint32_t blocks = columns / 256;
-    const uint32_t row_bytes = blocks * (TYPE == kQ4_K ? 144u : 210u);
+    const uint32_t row_bytes = blocks * kBlock8<TYPE>;
     const size_t lds = lds8_bytes(TYPE, blocks, TOK, WAVES, G, MODE == 2 ? 2u : 1u);
     // S == 1: one tile per wave; S > 1: WAVES / S tiles per workgroup.
     const uint32_t per = S == 1 ? WAVES : WAVES / S;
@@ -858,14 +916,20 @@ hipError_t launch8(dmhip_ctx *ctx, uint32_t batch, int mode, const Args8 &a) {
     const Plan8 p = plan8(TYPE, a.rows, a.columns, batch, mode == 2 ? 2u : 1u);
     if (p.s == 0) return hipErrorInvalidValue;
     if (mode == 1) return run8_g<TYPE, 1, 1>(ctx, p, a);
-    if (mode == 2) return batch == 1 ? run8_g<TYPE, 2, 1>(ctx, p, a) : run8_g<TYPE, 2, 2>(ctx, p, a);
+    if (mode == 2) {
+        if constexpr (TYPE == kQ8_0) {
+            return hipErrorInvalidValue;  // gate/up pairs are Q4_K or Q6_K
+        } else {
+            return batch == 1 ? run8_g<TYPE, 2, 1>(ctx, p, a) : run8_g<TYPE, 2, 2>(ctx, p, a);
+        }
+    }
     return batch == 1 ? run8_g<TYPE, 0, 1>(ctx, p, a) : run8_g<TYPE, 0, 2>(ctx, p, a);
 }
 
 }  // namespace
 
 bool qmv8_supported(uint32_t type, size_t rows, size_t columns, size_t batch) {
-    if (type != kQ4_K && type != kQ6_K) return false;
+    if (type != kQ4_K && type != kQ6_K && type != kQ8_0) return false;
     if (batch < 1 || batch > 2 || columns % 256 || columns == 0) return false;
     return plan8(type, (uint32_t)rows, (uint32_t)columns, (uint32_t)batch, 1).s != 0;
 }
@@ -881,6 +945,7 @@ hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t co
     const Args8 a{rows, columns, w, w, x, 0, 0.0f, y, partials, count};
     const int mode = partials ? 1 : 0;
     if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, mode, a);
+    if (type == kQ8_0) return launch8<kQ8_0>(ctx, batch, mode, a);
     return launch8<kQ6_K>(ctx, batch, mode, a);
 }
 

@@ -265,6 +265,37 @@ def test_output_head_q6_k_with_argmax(ctx):
     assert idx == want_idx
 
 
+@pytest.mark.parametrize("rows,cols,batch", [(1000, 2048, 1), (4096, 4096, 2), (300, 12288, 1), (40000, 4096, 1),
+                                             (513, 4128, 1)])
+def test_q8_0_gemv_matches_oracle(ctx, rows, cols, batch):
+    """Q8_0 on the int8 kernel (whole 8-block super-blocks, batch 1-2); 4128
+    columns (129 blocks) take the exact per-element kernel."""
+    print(f"Q8_0 gemv {rows}x{cols} batch={batch}", flush=True)
+    w = synth.quantized_matrix(Q8_0, rows, cols, synth.weight_seed(80 + batch))
+    x = synth.normal(synth.activation_seed(80 + batch), batch * cols).reshape(batch, cols)
+    want = np.stack([capi.matvec(Q8_0, rows, cols, w, x[b]) for b in range(batch)])
+    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, batch * rows * 4)
+    ctx.matvec_device(Q8_0, rows, cols, wb.device_ptr, batch, xb.device_ptr, yb.device_ptr)
+    got = yb.read(0, batch * rows * 4, np.float32).reshape(batch, rows)
+    for b in range(batch):
+        assert_close(got[b], want[b], f"Q8_0 {rows}x{cols} token {b}")
+
+
+def test_q8_0_argmax_is_exact(ctx):
+    rows, cols = 50000, 4096
+    w = synth.quantized_matrix(Q8_0, rows, cols, synth.weight_seed(88))
+    x = synth.normal(synth.activation_seed(88), cols)
+    want = capi.matvec(Q8_0, rows, cols, w, x)
+    wb, xb, yb, ib = dev(ctx, w), dev(ctx, x), dev_out(ctx, rows * 4), dev_out(ctx, 4)
+    ctx.matvec_argmax_device(Q8_0, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr, ib.device_ptr)
+    idx = ctx.argmax_result()
+    got = yb.read(0, rows * 4, np.float32)
+    assert_close(got, want, "Q8_0 logits")
+    assert idx == capi.argmax(got)
+    print(f"  argmax gpu={idx} cpu={capi.argmax(want)} top2 gap={top2_gap(want):.4g}", flush=True)
+    assert idx == capi.argmax(want)
+
+
 def test_argmax_fused_rejects_non_finite(ctx):
     rows, cols = 300, 256
     w = synth.quantized_matrix(Q6_K, rows, cols, 3)

@@ -18,6 +18,17 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
                           nullptr, nullptr));
         return DMHIP_OK;
     }
+    if (type == 8 && batch > 2 && qmv_supported(type, rows, columns, w, 2)) {
+        // Q8_0 (8) has only the int8 kernel (1-2 tokens): one launch per pair
+        // of tokens, each streaming the matrix at HBM rate, beats the exact
+        // per-element kernel by an order of magnitude.
+        for (size_t t = 0; t < batch; t += 2) {
+            const uint32_t n = batch - t < 2 ? (uint32_t)(batch - t) : 2u;
+            DM_HIP(launch_qmv(ctx, type, (uint32_t)rows, (uint32_t)columns, w, n, x + t * columns, y + t * rows,
+                              nullptr, nullptr));
+        }
+        return DMHIP_OK;
+    }
     KernelTimer timer(ctx);
     DM_HIP(launch_gemv_exact(ctx->stream, type, be, bb, (uint32_t)rows, (uint32_t)columns,
                              (size_t)row_bytes, (const uint8_t *)w, (uint32_t)batch, x, y));

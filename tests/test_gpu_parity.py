@@ -266,10 +266,11 @@ def test_output_head_q6_k_with_argmax(ctx):
 
 
 @pytest.mark.parametrize("rows,cols,batch", [(1000, 2048, 1), (4096, 4096, 2), (300, 12288, 1), (40000, 4096, 1),
-                                             (513, 4128, 1)])
+                                             (513, 4128, 1), (700, 2048, 5), (513, 4128, 3)])
 def test_q8_0_gemv_matches_oracle(ctx, rows, cols, batch):
-    """Q8_0 on the int8 kernel (whole 8-block super-blocks, batch 1-2); 4128
-    columns (129 blocks) take the exact per-element kernel."""
+    """Q8_0 on the int8 kernel (whole 8-block super-blocks; batches above 2
+    as launches of token pairs); 4128 columns (129 blocks) take the exact
+    per-element kernel."""
     print(f"Q8_0 gemv {rows}x{cols} batch={batch}", flush=True)
     w = synth.quantized_matrix(Q8_0, rows, cols, synth.weight_seed(80 + batch))
     x = synth.normal(synth.activation_seed(80 + batch), batch * cols).reshape(batch, cols)

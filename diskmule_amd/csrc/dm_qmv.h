@@ -13,16 +13,29 @@ struct ArgmaxPartial {
     uint32_t pad;
 };
 
+// Fused argmax finish of the int8 kernel: every workgroup folds its
+// candidate into *best with a device-scope atomic maximum and then takes a
+// ticket; the one that draws the last ticket writes `state` and `index` and
+// resets *best and *ticket to zero (their value before every launch).  All
+// null: the candidates go to `partials` for a separate pass.
+struct ArgmaxFinish {
+    ArgmaxState *state;
+    uint32_t *index;
+    uint32_t *ticket;
+    unsigned long long *best;
+};
+
 // True when the int8-MFMA matvec (decode batches of 1-2 tokens, Q4_K/Q6_K/
 // Q8_0) takes this shape; the caller has already checked qmv_supported.
 bool qmv8_supported(uint32_t type, size_t rows, size_t columns, size_t batch);
 
 // y[b][r] = W[r] . x[b] with the int8-MFMA kernels.  With `partials` the
-// epilogue also writes one ArgmaxPartial per 16-row tile (batch 1) and
-// *count receives the number written.
+// epilogue also writes one ArgmaxPartial per workgroup (batch 1) and *count
+// receives the number written; with a `finish` ticket the kernel reduces
+// them itself into finish.state / finish.index.
 hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
                        uint32_t batch, const float *x, float *y, ArgmaxPartial *partials,
-                       uint32_t *count);
+                       uint32_t *count, ArgmaxFinish finish = ArgmaxFinish{nullptr, nullptr, nullptr, nullptr});
 
 // The int8-MFMA gate/up pair: act[b][r] = silu(gate[r] . n[b]) * (up[r] . n[b])
 // with n = RMSNorm(x) (unit weight) when `normalize`, else n = x.

@@ -930,10 +930,13 @@ hipError_t launch_qmv(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t col
     a.partials = (ArgmaxPartial *)ctx->partials.ptr;
     uint32_t count = 0;
     hipError_t e;
-    if (int8_path)
-        e = launch_qmv8(ctx, type, rows, columns, w, batch, x, y, a.partials, &count);
-    else
-        e = type == kQ4_K ? dispatch<kQ4_K, 1>(ctx, p, a, &count) : dispatch<kQ6_K, 1>(ctx, p, a, &count);
+    if (int8_path) {
+        // the int8 kernel's last workgroup publishes the argmax itself
+        return launch_qmv8(ctx, type, rows, columns, w, batch, x, y, a.partials, &count,
+                           ArgmaxFinish{argmax, index_out, ctx->argmax_ticket,
+                                        (unsigned long long *)(ctx->argmax_ticket + 2)});
+    }
+    e = type == kQ4_K ? dispatch<kQ4_K, 1>(ctx, p, a, &count) : dispatch<kQ6_K, 1>(ctx, p, a, &count);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(argmax_partials_kernel, dim3(1), dim3(kArgmaxThreads), 0, ctx->stream, a.partials, count,
                        argmax, index_out);

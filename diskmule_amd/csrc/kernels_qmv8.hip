@@ -413,7 +413,8 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
                                           uint32_t rows, uint32_t columns, uint32_t row_bytes,
                                           uint32_t total_bytes, const float *__restrict__ x, int x_stride,
                                           int normalize, float epsilon, int glm, float *__restrict__ y,
-                                          int y_stride, ArgmaxPartial *__restrict__ partials) {
+                                          int y_stride, ArgmaxPartial *__restrict__ partials,
+                                          const ArgmaxFinish finish) {
     constexpr uint32_t WAVES = S > 8 ? S : 8;
     constexpr int NM = MODE == 2 ? 2 : 1;  // weight matrices streamed
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
@@ -665,11 +666,32 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
                 k = wg_key[i] > k ? wg_key[i] : k;
                 f |= wg_bad[i];
             }
-            ArgmaxPartial p;
-            p.key = k;
-            p.non_finite = f;
-            p.pad = 0;
-            partials[blockIdx.x] = p;
+            if (finish.ticket) {
+                // Fold the candidate into the device-wide maximum (a
+                // non-finite row contributes the all-ones key, above every
+                // finite key), wait for the atomic to complete, then take a
+                // ticket: the workgroup that draws the last one reads the
+                // final maximum.  No cache-wide release fence is needed.
+                const unsigned long long packed = f ? ~0ull : k;
+                const unsigned long long prev = atomicMax(finish.best, packed);
+                asm volatile("" ::"v"(prev) : "memory");
+                if (atomicAdd(finish.ticket, 1u) == gridDim.x - 1) {
+                    const uint64_t kb = __hip_atomic_load(finish.best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const uint32_t nf = kb == ~0ull ? 1u : 0u;
+                    finish.state->key = nf ? 0ull : kb;
+                    finish.state->non_finite = nf;
+                    finish.state->done = gridDim.x;
+                    *finish.index = argmax_key_index(kb);
+                    __hip_atomic_store(finish.best, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(finish.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            } else {
+                ArgmaxPartial p;
+                p.key = k;
+                p.non_finite = f;
+                p.pad = 0;
+                partials[blockIdx.x] = p;
+            }
         }
     }
 }
@@ -679,9 +701,9 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2))) qmv8_kernel(
     const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows, uint32_t columns,
     uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x, int normalize, float epsilon,
-    float *__restrict__ y, ArgmaxPartial *__restrict__ partials) {
+    float *__restrict__ y, ArgmaxPartial *__restrict__ partials, ArgmaxFinish finish) {
     qmv8_body<TYPE, S, MODE, TOK, G>(w, w2, rows, columns, row_bytes, total_bytes, x, (int)columns, normalize,
-                                     epsilon, 0, y, (int)rows, partials);
+                                     epsilon, 0, y, (int)rows, partials, finish);
 }
 
 // Grouped launch over the routed-expert jobs of a MoE layer: job
@@ -706,7 +728,8 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8)) __attribute__((amdgpu_wa
     const Job8 j = jobs.job[blockIdx.y];
     const uint8_t *w = (const uint8_t *)j.w;
     qmv8_body<TYPE, S, MODE, TOK, G>(w, w + w2_offset, rows, columns, row_bytes, total_bytes, x + j.x_off,
-                                     j.x_stride, 0, 0.0f, glm, y + j.y_off, j.y_stride, nullptr);
+                                     j.x_stride, 0, 0.0f, glm, y + j.y_off, j.y_stride, nullptr,
+                                     ArgmaxFinish{nullptr, nullptr, nullptr, nullptr});
 }
 
 // ---------------------------------------------------------------------------
@@ -784,6 +807,7 @@ struct Args8 {
     float *y;
     ArgmaxPartial *partials;
     uint32_t *count;
+    ArgmaxFinish finish;
 };
 
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
@@ -817,7 +841,7 @@ hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
     }
     return launch_kernel(ctx, kernel, dim3(grid), dim3(64 * WAVES), lds, (const uint8_t *)a.w,
                          (const uint8_t *)a.w2, rows, columns, row_bytes, row_bytes * rows, a.x, a.normalize,
-                         a.epsilon, a.y, a.partials);
+                         a.epsilon, a.y, a.partials, a.finish);
 }
 
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
@@ -941,8 +965,9 @@ bool qmv8_gate_up_supported(uint32_t type, size_t rows, size_t columns, size_t b
 }
 
 hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
-                       uint32_t batch, const float *x, float *y, ArgmaxPartial *partials, uint32_t *count) {
-    const Args8 a{rows, columns, w, w, x, 0, 0.0f, y, partials, count};
+                       uint32_t batch, const float *x, float *y, ArgmaxPartial *partials, uint32_t *count,
+                       ArgmaxFinish finish) {
+    const Args8 a{rows, columns, w, w, x, 0, 0.0f, y, partials, count, finish};
     const int mode = partials ? 1 : 0;
     if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, mode, a);
     if (type == kQ8_0) return launch8<kQ8_0>(ctx, batch, mode, a);
@@ -952,7 +977,8 @@ hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t co
 hipError_t launch_qmv8_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns,
                                const void *gate, const void *up, uint32_t batch, const float *x, float *act,
                                int normalize, float epsilon) {
-    const Args8 a{rows, columns, gate, up, x, normalize, epsilon, act, nullptr, nullptr};
+    const Args8 a{rows, columns, gate, up, x, normalize, epsilon, act, nullptr, nullptr,
+                  ArgmaxFinish{nullptr, nullptr, nullptr, nullptr}};
     if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, 2, a);
     return launch8<kQ6_K>(ctx, batch, 2, a);
 }

@@ -228,7 +228,9 @@ int dmhip_context_new(int device, dmhip_ctx **out) {
         hipStreamCreateWithFlags(&ctx->upload2, hipStreamNonBlocking) != hipSuccess ||
         hipMalloc((void **)&ctx->argmax_state, sizeof(ArgmaxState)) != hipSuccess ||
         hipMalloc((void **)&ctx->argmax_index, 64) != hipSuccess ||
-        hipMalloc((void **)&ctx->flags, 64) != hipSuccess) {
+        hipMalloc((void **)&ctx->flags, 64) != hipSuccess ||
+        hipMalloc((void **)&ctx->argmax_ticket, 64) != hipSuccess ||
+        hipMemsetAsync(ctx->argmax_ticket, 0, 64, ctx->stream) != hipSuccess) {
         dmhip_context_free(ctx);
         return fail(DMHIP_ERR_COMMAND, "could not create the HIP streams of device %d", device);
     }
@@ -248,6 +250,7 @@ void dmhip_context_free(dmhip_ctx *ctx) {
     ctx->aux.release();
     ctx->partials.release();
     if (ctx->argmax_state) (void)hipFree(ctx->argmax_state);
+    if (ctx->argmax_ticket) (void)hipFree(ctx->argmax_ticket);
     if (ctx->argmax_index) (void)hipFree(ctx->argmax_index);
     if (ctx->flags) (void)hipFree(ctx->flags);
     for (hipEvent_t e : ctx->timing_events) (void)hipEventDestroy(e);

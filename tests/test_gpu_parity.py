@@ -307,6 +307,15 @@ def test_argmax_fused_rejects_non_finite(ctx):
     with pytest.raises(HipError) as e:
         ctx.argmax_result()
     assert e.value.variant == "NonFinite"
+    # The fused finish leaves its device-wide maximum and ticket reset: the
+    # next calls on the context see only their own rows.
+    for seed in (5, 6):
+        x = synth.normal(seed, cols)
+        xb = dev(ctx, x)
+        ctx.matvec_argmax_device(Q6_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr, ib.device_ptr)
+        idx = ctx.argmax_result()
+        assert idx == capi.argmax(yb.read(0, rows * 4, np.float32))
+        assert idx == capi.argmax(capi.matvec(Q6_K, rows, cols, w, x))
 
 
 # ---- reductions and activations ------------------------------------------
@@ -495,6 +504,23 @@ def test_prefill_gemm_matches_oracle(ctx, n):
         e, _ = assert_close(got[r], want[r], f"C5 token {r}")
         worst = max(worst, e)
     print(f"  worst rel_err={worst:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("m,n,k", [(100, 200, 2048), (9, 136, 4608), (65, 264, 12288), (8, 128, 256)])
+def test_prefill_gemm_ragged_shapes(ctx, m, n, k):
+    """M not a multiple of the 64-row tile (padding rows), N not a multiple of
+    the 128-column tile, and K other than 4096 (the preparation's general
+    path: the row maximum in a loop, several workgroups per row group)."""
+    print(f"C5 ragged m={m} n={n} k={k}", flush=True)
+    a = synth.to_bf16_bits(synth.normal(synth.activation_seed(7), m * k))
+    w = synth.quantized_matrix(Q4_K, n, k, synth.weight_seed(7, n))
+    want = capi.gemm_tokenwise(Q4_K, m, n, k, a, w)
+    ab, wb, cb = dev(ctx, a), dev(ctx, w), dev_out(ctx, m * n * 4)
+    ws = dev_out(ctx, ctx.gemm_workspace_bytes(m, k))
+    ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr)
+    got = cb.read(0, m * n * 4, np.float32).reshape(m, n)
+    for r in range(m):
+        assert_close(got[r], want[r], f"C5 ragged token {r}")
 
 
 def test_objects_outliving_their_context_exit_cleanly():

@@ -56,7 +56,9 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
                                uint32_t *non_finite, uint32_t *host_ids = nullptr,
-                               float *host_probs = nullptr);
+                               float *host_probs = nullptr, uint32_t *tickets = nullptr);
+// Per-token counters of the fused router selection (zero between launches).
+constexpr uint32_t kRouterTickets = 4096;
 hipError_t launch_rms_norm(hipStream_t s, const float *in, uint32_t batch, uint32_t n,
                            const float *weight, float eps, float *out);
 hipError_t launch_silu_mul(hipStream_t s, const float *gate, const float *up, size_t n, float *out);

@@ -349,7 +349,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     float *sel_probs = (float *)(c->host_selection + kSelectionPairs * 4);
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs, ctx->flags, sel_ids,
-                               sel_probs));
+                               sel_probs, batch <= kRouterTickets ? ctx->router_tickets : nullptr));
     DM_HIP(hipStreamSynchronize(ctx->stream));
     memcpy(ids, sel_ids, pairs * 4);
     memcpy(probabilities, sel_probs, pairs * 4);

@@ -354,6 +354,168 @@ __global__ void __launch_bounds__(256) router_staged_kernel(
     }
 }
 
+// Expert-parallel form of the exact router for decode: workgroup (g, t) is
+// one wave that folds the RF_EXPERTS rows g * RF_EXPERTS .. of token t.
+// Lane e < RF_EXPERTS still folds its row sequentially from column 0 with
+// fma, so the logits are bit-identical to the kernels above; what changes is
+// that the router's rows stream through E / RF_EXPERTS compute units per
+// token instead of one, and the dependent fma chain reads fp32 operands from
+// LDS (two 16-byte reads per four fmas, no unpacking on the chain).  Columns
+// go in chunks of RF_CHUNK through two LDS buffers: every lane loads 16-byte
+// pieces of the next chunk's rows and x while the chain runs, then widens
+// the bf16 pieces to fp32 into the other buffer.
+constexpr uint32_t RF_EXPERTS = 8, RF_CHUNK = 512;
+constexpr uint32_t RF_ROW = RF_CHUNK + 4;                        // floats per staged row (bank skew)
+constexpr uint32_t RF_BUF = RF_EXPERTS * RF_ROW + RF_CHUNK;      // floats per buffer: rows, then x
+constexpr uint32_t RF_WPIECES = RF_EXPERTS * RF_CHUNK * 2 / 16;  // 16-byte bf16 pieces of the rows
+constexpr uint32_t RF_XPIECES = RF_CHUNK * 4 / 16;               // 16-byte pieces of x
+constexpr uint32_t RF_LOADS = (RF_WPIECES + RF_XPIECES) / 64;    // per lane and chunk
+static_assert((RF_WPIECES + RF_XPIECES) % 64 == 0, "whole loads per lane");
+
+__global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restrict__ router, uint32_t hidden,
+                                                         uint32_t experts, uint32_t k, const float *__restrict__ x,
+                                                         float *logits, uint32_t *tickets, uint32_t *ids,
+                                                         float *probabilities, uint32_t *non_finite,
+                                                         uint32_t *host_ids, float *host_probs) {
+    __shared__ v4a rf_lds[2 * RF_BUF / 4];
+    const uint32_t lane = threadIdx.x, e0 = blockIdx.x * RF_EXPERTS, token = blockIdx.y;
+    const uint32_t chunks = (hidden + RF_CHUNK - 1) / RF_CHUNK;
+    // Piece j of a chunk: row piece (row j / 64, column 8 (j % 64)) for
+    // j < RF_WPIECES, else x piece j - RF_WPIECES.  Rows past `experts`
+    // and columns past `hidden` read zeros (buffer loads past the end).
+    constexpr uint32_t nowhere = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(router, experts * hidden * 2);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)token * hidden, hidden * 4);
+    uint32_t off[RF_LOADS];
+#pragma unroll
+    for (uint32_t i = 0; i < RF_LOADS; i++) {
+        const uint32_t j = i * 64 + lane;
+        if (j < RF_WPIECES) {
+            const uint32_t row = e0 + j / (RF_CHUNK / 8);
+            off[i] = row < experts ? row * hidden * 2 + 16 * (j % (RF_CHUNK / 8)) : nowhere;
+        } else {
+            off[i] = 16 * (j - RF_WPIECES);
+        }
+    }
+    v4a r[RF_LOADS];
+    auto load = [&](uint32_t c) {
+        const uint32_t c0 = c * RF_CHUNK;
+#pragma unroll
+        for (uint32_t i = 0; i < RF_LOADS; i++) {
+            const uint32_t j = i * 64 + lane;
+            // the last chunk of a row may run past `hidden`: those columns are
+            // never folded, so whatever they read is harmless
+            if (j < RF_WPIECES)
+                r[i] = __builtin_bit_cast(v4a, rsrc_load16(rw, off[i] == nowhere ? nowhere : off[i] + 2 * c0));
+            else
+                r[i] = __builtin_bit_cast(v4a, rsrc_load16(rx, off[i] + 4 * c0));
+        }
+    };
+    auto store = [&](uint32_t b) {
+        float *buf = (float *)rf_lds + b * RF_BUF;
+#pragma unroll
+        for (uint32_t i = 0; i < RF_LOADS; i++) {
+            const uint32_t j = i * 64 + lane;
+            if (j < RF_WPIECES) {
+                float *dst = buf + (j / (RF_CHUNK / 8)) * RF_ROW + 8 * (j % (RF_CHUNK / 8));
+                v4a lo, hi;
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    lo[2 * q] = r[i][q] << 16;
+                    lo[2 * q + 1] = r[i][q] & 0xffff0000u;
+                    hi[2 * q] = r[i][q + 2] << 16;
+                    hi[2 * q + 1] = r[i][q + 2] & 0xffff0000u;
+                }
+                *(v4a *)dst = lo;
+                *(v4a *)(dst + 4) = hi;
+            } else {
+                *(v4a *)(buf + RF_EXPERTS * RF_ROW + 4 * (j - RF_WPIECES)) = r[i];
+            }
+        }
+    };
+    float acc = 0.0f;
+    const uint32_t my = lane < RF_EXPERTS ? lane : 0;
+    load(0);
+    store(0);
+    for (uint32_t c = 0; c < chunks; c++) {
+        if (c + 1 < chunks) load(c + 1);
+        // One wave: its LDS operations run in order; the fences keep the
+        // compiler from moving other lanes' reads across the stores.
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        const float *buf = (const float *)rf_lds + (c & 1u) * RF_BUF;
+        const float *wr = buf + my * RF_ROW, *xr = buf + RF_EXPERTS * RF_ROW;
+        const uint32_t n = hidden - c * RF_CHUNK < RF_CHUNK ? hidden - c * RF_CHUNK : RF_CHUNK;
+        if (lane < RF_EXPERTS) {
+            if (n == RF_CHUNK) {
+#pragma unroll 8
+                for (uint32_t q = 0; q < RF_CHUNK; q += 4) {
+                    const v4a wv = *(const v4a *)(wr + q), xv = *(const v4a *)(xr + q);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc = __builtin_fmaf(__uint_as_float(wv[i]), __uint_as_float(xv[i]), acc);
+                }
+            } else {
+                for (uint32_t q = 0; q < n; q++) acc = __builtin_fmaf(wr[q], xr[q], acc);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (c + 1 < chunks) store((c + 1) & 1u);
+    }
+    if (!tickets) {
+        if (lane < RF_EXPERTS && e0 + lane < experts) logits[(size_t)token * experts + e0 + lane] = acc;
+        return;
+    }
+    // Fused selection: publish the logits with device-scope exchanges, wait
+    // for them to complete, then take the token's ticket; the workgroup that
+    // draws the last one reads every logit of the token back and selects.
+    float old = 0.0f;
+    if (lane < RF_EXPERTS && e0 + lane < experts)
+        old = __hip_atomic_exchange(&logits[(size_t)token * experts + e0 + lane], acc, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"(old) : "memory");
+    uint32_t drawn = 0;
+    if (lane == 0) drawn = atomicAdd(&tickets[token], 1u);
+    if (__builtin_amdgcn_readfirstlane(drawn) != gridDim.x - 1) return;
+    __shared__ float s_row[256];
+    for (uint32_t i = lane; i < experts; i += 64)
+        s_row[i] = __hip_atomic_load(&logits[(size_t)token * experts + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    uint32_t *ti = ids + (size_t)token * k;
+    float *tp = probabilities + (size_t)token * k;
+    block_top_k(s_row, experts, k, ti, tp, non_finite);
+    if (lane == 0) {
+        if (host_ids) {
+            for (uint32_t s = 0; s < k; s++) {
+                host_ids[(size_t)token * k + s] = ti[s];
+                host_probs[(size_t)token * k + s] = tp[s];
+            }
+        }
+        __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Top-k softmax over the router logits (at most 256) of one token per
+// workgroup, with the selection also written to (pinned) host memory when
+// host_ids is set.
+__global__ void __launch_bounds__(256) top_k_host_kernel(const float *__restrict__ logits, uint32_t count,
+                                                         uint32_t k, uint32_t *ids, float *probabilities,
+                                                         uint32_t *non_finite, uint32_t *host_ids,
+                                                         float *host_probs) {
+    __shared__ float s_row[256];
+    const uint32_t row = blockIdx.x;
+    uint32_t *ti = ids + (size_t)row * k;
+    float *tp = probabilities + (size_t)row * k;
+    // the row once into LDS (count <= 256), where the k selection rounds read it
+    if (threadIdx.x < count) s_row[threadIdx.x] = logits[(size_t)row * count + threadIdx.x];
+    __syncthreads();
+    block_top_k(s_row, count, k, ti, tp, non_finite);
+    if (host_ids && threadIdx.x == 0) {
+        for (uint32_t s = 0; s < k; s++) {
+            host_ids[(size_t)row * k + s] = ti[s];
+            host_probs[(size_t)row * k + s] = tp[s];
+        }
+    }
+}
+
 // ---- RMSNorm (src/cpu.rs:98-142) ---------------------------------------
 __global__ void __launch_bounds__(256) rms_norm_kernel(const float *__restrict__ in, uint32_t n,
                                                        const float *__restrict__ weight, float eps,
@@ -515,9 +677,19 @@ static hipError_t launch_router_staged(hipStream_t s, const uint16_t *router, ui
 hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
-                               uint32_t *non_finite, uint32_t *host_ids, float *host_probs) {
+                               uint32_t *non_finite, uint32_t *host_ids, float *host_probs, uint32_t *tickets) {
     const bool staged = experts <= 256 && hidden % 8 == 0 && (uint64_t)experts * hidden * 2 < (1ull << 30) && ((uintptr_t)router & 15u) == 0 &&
                         ((uintptr_t)x & 15u) == 0;
+    // Decode batches: the expert-parallel fold, then the selection.
+    if (staged && experts >= 2 * RF_EXPERTS && (uint64_t)experts * hidden * 2 < 0x80000000ull) {
+        hipLaunchKernelGGL(router_fold_kernel, dim3((experts + RF_EXPERTS - 1) / RF_EXPERTS, batch), dim3(64), 0, s,
+                           router, hidden, experts, k, x, logits, tickets, ids, probabilities, non_finite, host_ids,
+                           host_probs);
+        if (!tickets)
+            hipLaunchKernelGGL(top_k_host_kernel, dim3(batch), dim3(256), 0, s, logits, experts, k, ids,
+                               probabilities, non_finite, host_ids, host_probs);
+        return hipGetLastError();
+    }
     if (staged && experts <= 128)
         return launch_router_staged<128>(s, router, hidden, experts, k, batch, x, logits, ids, probabilities,
                                          non_finite, host_ids, host_probs);

@@ -61,6 +61,7 @@ struct dmhip_ctx {
     dm::Scratch in, out, enc, aux;          // host-slice staging
     dm::Scratch partials;                    // per-wave argmax candidates
     dm::ArgmaxState *argmax_state = nullptr;  // device
+    uint32_t *router_tickets = nullptr;       // device, kRouterTickets counters, zero between launches
     uint32_t *argmax_ticket = nullptr;        // device, zero between launches: ticket, then (at +8) the best key
     uint32_t *argmax_index = nullptr;         // device
     uint32_t *flags = nullptr;                // device: [0] non-finite

@@ -230,7 +230,9 @@ int dmhip_context_new(int device, dmhip_ctx **out) {
         hipMalloc((void **)&ctx->argmax_index, 64) != hipSuccess ||
         hipMalloc((void **)&ctx->flags, 64) != hipSuccess ||
         hipMalloc((void **)&ctx->argmax_ticket, 64) != hipSuccess ||
-        hipMemsetAsync(ctx->argmax_ticket, 0, 64, ctx->stream) != hipSuccess) {
+        hipMemsetAsync(ctx->argmax_ticket, 0, 64, ctx->stream) != hipSuccess ||
+        hipMalloc((void **)&ctx->router_tickets, kRouterTickets * 4) != hipSuccess ||
+        hipMemsetAsync(ctx->router_tickets, 0, kRouterTickets * 4, ctx->stream) != hipSuccess) {
         dmhip_context_free(ctx);
         return fail(DMHIP_ERR_COMMAND, "could not create the HIP streams of device %d", device);
     }
@@ -251,6 +253,7 @@ void dmhip_context_free(dmhip_ctx *ctx) {
     ctx->partials.release();
     if (ctx->argmax_state) (void)hipFree(ctx->argmax_state);
     if (ctx->argmax_ticket) (void)hipFree(ctx->argmax_ticket);
+    if (ctx->router_tickets) (void)hipFree(ctx->router_tickets);
     if (ctx->argmax_index) (void)hipFree(ctx->argmax_index);
     if (ctx->flags) (void)hipFree(ctx->flags);
     for (hipEvent_t e : ctx->timing_events) (void)hipEventDestroy(e);
@@ -766,7 +769,7 @@ int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_
     DM_CHECK(set_device(ctx));
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                (uint32_t)k, (uint32_t)batch, x, logits, ids, probabilities,
-                               ctx->flags));
+                               ctx->flags, nullptr, nullptr, batch <= kRouterTickets ? ctx->router_tickets : nullptr));
     return DMHIP_OK;
 }
 

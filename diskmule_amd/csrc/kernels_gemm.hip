@@ -23,10 +23,12 @@
 // bytes 64h + 4s .. 64h + 4s + 3, and A is stored in that order.
 // Other weight types take the decode-GEMV path in chunks of 16 tokens.
 //
-// Tiling: a workgroup (8 waves, two per SIMD) owns a 64 x 128 tile of C;
-// wave w computes the 64 x 64 half w / 4 over every fourth Q4_K block
-// (w % 4, w % 4 + 4, ...), so every W element is dequantized by exactly one
-// wave and no operand is shared through LDS.  A comes from global memory
+// Tiling: a workgroup of 4 waves (one per SIMD) owns a 128 x 64 tile of C
+// (8 waves, two per SIMD, and a 64 x 128 tile for prefills of at most 64
+// tokens); wave w computes the 128 x 64 tile (64 x 64 half w / 4) over every
+// fourth Q4_K block (w % 4, w % 4 + 4, ...), so every W element is
+// dequantized by exactly one wave and feeds 4 (2) MFMA row tiles, and no
+// operand is shared through LDS.  A comes from global memory
 // already in MFMA fragment order (one 1 KiB load per 32 rows and step); a
 // wave stages its W block (64 rows x 144 bytes, contiguous 16-byte loads) in
 // its own LDS area and dequantizes from there, with the next block's W in
@@ -37,23 +39,36 @@
 #include "dm_qmv.h"
 #include "runtime.h"
 
+#include <stdlib.h>
+
 namespace dm {
 
 namespace {
 
-constexpr uint32_t kBM = 64, kBN = 128;
-constexpr uint32_t kKSplit = 4, kNHalves = 2, kWaves = kKSplit * kNHalves;  // two waves per SIMD
-constexpr uint32_t kWN = kBN / kNHalves;  // columns of a wave's tile
+// Workgroup tilings (BM rows of C x BN columns; wave tile BM x WN):
+//  * BM = 64:  BN = 128, 8 waves (4-way K split x 2 column halves), two waves
+//    per SIMD, wave tile 64 x 64 (2 x 2 MFMA tiles of 32 x 32);
+//  * BM = 128: BN = 64, 4 waves (4-way K split), one wave per SIMD, wave
+//    tile 128 x 64 (4 x 2 MFMA tiles): each dequantized weight feeds four
+//    MFMA row tiles instead of two.
+template <uint32_t BM> struct Tiling {
+    static constexpr uint32_t kBM = BM, kBN = BM == 64 ? 128 : 64;
+    static constexpr uint32_t kKSplit = 4, kNHalves = BM == 64 ? 2 : 1, kWaves = kKSplit * kNHalves;
+    static constexpr uint32_t kWN = kBN / kNHalves;  // columns of a wave's tile
+    static constexpr uint32_t kRM = BM / 32;          // MFMA row tiles of a wave
+    static constexpr uint32_t kStageBytes = kWN * 144;              // one Q4_K block of a wave's W rows
+    static constexpr uint32_t kStageLoads = kStageBytes / 16 / 64;  // 16-byte loads per lane
+    static constexpr uint32_t kRedLd = kWN + 4;                     // floats per row of a partial tile in LDS
+    static constexpr uint32_t kLdsBytes = kWaves * kBM * kRedLd * 4;  // partial tiles of the final sum
+    static_assert(kWaves * kStageBytes <= kLdsBytes, "the W staging areas fit in the reduction area");
+    static_assert(kStageBytes % 1024 == 0, "whole staging loads");
+    static_assert(kLdsBytes <= 160 * 1024, "one workgroup's LDS");
+};
+constexpr uint32_t kPadRows = 128;  // workspace rows are padded to a multiple of every tiling's BM
 // MFMA steps between the load of an A fragment and its use.  Loads complete
 // in order, so this is also the time every W load has to arrive.
 constexpr uint32_t kADist = 4;
 static_assert(16 % kADist == 0, "the A ring repeats every block");
-constexpr uint32_t kStageBytes = kWN * 144;              // one Q4_K block of a wave's W rows
-constexpr uint32_t kStageLoads = kStageBytes / 16 / 64;  // 16-byte loads per lane
-constexpr uint32_t kRedLd = kWN + 4;                     // floats per row of a partial tile in LDS
-constexpr uint32_t kLdsBytes = kWaves * kBM * kRedLd * 4;  // partial tiles of the final sum
-static_assert(kWaves * kStageBytes <= kLdsBytes, "the W staging areas fit in the reduction area");
-static_assert(kStageBytes % 1024 == 0, "whole staging loads");
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 16-byte aligned
 
@@ -212,20 +227,26 @@ __global__ void __launch_bounds__(512) gemm_prep_kernel(const uint16_t *__restri
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K GEMM main kernel.  Grid: one workgroup (8 waves, two per SIMD) per
-// 64 x 128 tile of C.  Wave w owns the 64 x 64 half w / 4 of the tile over
-// blocks w % 4, w % 4 + 4, ...  A lone wave issues VALU work at half the
-// SIMD's rate, and the dequantization is VALU work: the second wave of each
-// SIMD supplies the other half while the MFMAs run.  Per block and wave: 16
-// MFMA steps of 4 MFMAs (2 row x 2 column 32 x 32 tiles), the A fragments of
+// Q4_K GEMM main kernel.  Grid: one workgroup per BM x BN tile of C (see
+// Tiling).  Wave w owns the BM x WN part w / 4 of the tile over blocks
+// w % 4, w % 4 + 4, ...  With BM = 64 two waves share each SIMD: a lone wave
+// issues VALU work at half the SIMD's rate, and the dequantization is VALU
+// work, so the second wave supplies the other half while the MFMAs run; with
+// BM = 128 each dequantized weight serves twice the MFMAs instead.  Per block
+// and wave: 16 MFMA steps of RM x 2 MFMAs (32 x 32 tiles), the A fragments of
 // step s + kADist in flight during step s, the W block read from the wave's
 // LDS area (the next block's W arrives in registers meanwhile).
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__restrict__ a16,
+template <uint32_t BM>
+__global__ void __launch_bounds__(64 * Tiling<BM>::kWaves)
+    __attribute__((amdgpu_waves_per_eu(BM == 64 ? 2 : 1, BM == 64 ? 2 : 1))) gemm_q4k_kernel(const half8 *__restrict__ a16,
                                                                const float *__restrict__ rowscale,
                                                                const uint8_t *__restrict__ w, uint32_t m_rows,
                                                                uint32_t n_rows, uint32_t k, uint32_t w_bytes,
                                                                uint32_t m_tiles, float *__restrict__ c) {
+    using T = Tiling<BM>;
+    constexpr uint32_t kBN = T::kBN, kKSplit = T::kKSplit, kWaves = T::kWaves, kWN = T::kWN, kRM = T::kRM;
+    constexpr uint32_t kStageBytes = T::kStageBytes, kStageLoads = T::kStageLoads, kRedLd = T::kRedLd;
     extern __shared__ v4u gsm[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar offsets
@@ -247,7 +268,7 @@ __global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__re
         mt = id % m_tiles;
         nt = id / m_tiles;
     }
-    const uint32_t m0 = mt * kBM, n0 = nt * kBN, wn0 = n0 + nh * kWN;
+    const uint32_t m0 = mt * BM, n0 = nt * kBN, wn0 = n0 + nh * kWN;
     const uint32_t blocks = k / 256, row_bytes = blocks * 144;
     const uint32_t mine = kpart < blocks ? (blocks - kpart + kKSplit - 1) / kKSplit : 0;
 
@@ -256,7 +277,7 @@ __global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__re
     // n_rows start at kNowhere (>= 2^31 > every W offset): they read zeros.
     constexpr uint32_t kNowhere = 0x80000000u;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, w_bytes);
-    const __amdgpu_buffer_rsrc_t ars = make_rsrc(a16 + (size_t)2 * mt * blocks * 1024, 2 * blocks * 1024 * 16);
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(a16 + (size_t)kRM * mt * blocks * 1024, kRM * blocks * 1024 * 16);
     v4u *stage = gsm + wave * (kStageBytes / 16);
 
     // W staging: chunk j * 64 + lane of the block's kWN rows x 9 chunks,
@@ -286,9 +307,9 @@ __global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__re
     const v4u *hdr_slot = stage + ln * 9;
     const v4u *q_slot = stage + ln * 9 + 1 + 4 * h;
 
-    floatx16 acc[2][2];
+    floatx16 acc[kRM][2];
 #pragma unroll
-    for (int r = 0; r < 2; r++)
+    for (uint32_t r = 0; r < kRM; r++)
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -300,12 +321,11 @@ __global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__re
         put_w();
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         fetch_w(mine > 1 ? b + kKSplit : b);
-        half8 afr[2][kADist];
+        half8 afr[kRM][kADist];
 #pragma unroll
-        for (uint32_t s = 0; s < kADist; s++) {
-            afr[0][s] = a_frag(0, b, s);
-            afr[1][s] = a_frag(1, b, s);
-        }
+        for (uint32_t s = 0; s < kADist; s++)
+#pragma unroll
+            for (uint32_t r = 0; r < kRM; r++) afr[r][s] = a_frag(r, b, s);
         for (uint32_t i = 0; i < mine; i++, b += kKSplit) {
             const uint32_t bn = i + 1 < mine ? b + kKSplit : b;  // next block (clamped)
             const uint32_t bnn = i + 2 < mine ? b + 2 * kKSplit : bn;
@@ -332,7 +352,7 @@ __global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__re
                 for (int x = 0; x < 4; x++) ss[t][x] = sub_scale(d, dmin, (scs >> (8 * x)) & 0xffu, (mns >> (8 * x)) & 0xffu);
             }
             // Weights of step 0; then each step issues the A loads of step
-            // s + kADist, its 4 MFMAs, and the weights of step s + 1.  The
+            // s + kADist, its 2 RM MFMAs, and the weights of step s + 1.  The
             // scheduling barriers keep every step's loads where they are
             // written, so each A fragment (and every older load) has kADist
             // steps to arrive.
@@ -353,7 +373,9 @@ __global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__re
                 // before this step's MFMAs consume the current ones, so they
                 // live in other registers.
                 const uint32_t pb = s + kADist < 16 ? b : bn, ps = (s + kADist) % 16;
-                const half8 an0 = a_frag(0, pb, ps), an1 = a_frag(1, pb, ps);
+                half8 an[kRM];
+#pragma unroll
+                for (uint32_t r = 0; r < kRM; r++) an[r] = a_frag(r, pb, ps);
                 half8 bn_[2];
                 if (s + 1 < 16) {
                     const uint32_t s1 = s + 1;
@@ -364,14 +386,12 @@ __global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__re
 #pragma unroll
                     for (int t = 0; t < 2; t++) bn_[t] = dequant8(q[t][s1 % 4], ss[t][2 * (s1 / 8)], ss[t][2 * (s1 / 8) + 1]);
                 }
-                const half8 a0 = afr[0][s % kADist], a1 = afr[1][s % kADist];
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    acc[0][t] = mfma32(a0, bv[t], acc[0][t]);
-                    acc[1][t] = mfma32(a1, bv[t], acc[1][t]);
-                }
-                afr[0][s % kADist] = an0;
-                afr[1][s % kADist] = an1;
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (uint32_t r = 0; r < kRM; r++) acc[r][t] = mfma32(afr[r][s % kADist], bv[t], acc[r][t]);
+#pragma unroll
+                for (uint32_t r = 0; r < kRM; r++) afr[r][s % kADist] = an[r];
                 if (s + 1 < 16) {
 #pragma unroll
                     for (int t = 0; t < 2; t++) bv[t] = bn_[t];
@@ -396,28 +416,31 @@ __global__ void __launch_bounds__(64 * kWaves) gemm_q4k_kernel(const half8 *__re
     __syncthreads();
     float *red = (float *)gsm;
 #pragma unroll
-    for (int r = 0; r < 2; r++)
+    for (uint32_t r = 0; r < kRM; r++)
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int j = 0; j < 16; j++) {
                 const uint32_t row = 32 * r + 8 * (j / 4) + 4 * h + (j % 4), col = 32 * t + ln;
-                red[(wave * kBM + row) * kRedLd + col] = acc[r][t][j];
+                red[(wave * BM + row) * kRedLd + col] = acc[r][t][j];
             }
     __syncthreads();
-    const uint32_t row = tid >> 3, col0 = 16 * (tid & 7u);  // 64 rows x 8 chunks of 16 columns
-    const uint32_t half = col0 / kWN, hcol = col0 % kWN;
-    const uint32_t m = m0 + row;
-    if (m < m_rows) {
+    // BM rows x BN / 16 chunks of 16 columns, over the workgroup's threads
+    constexpr uint32_t kChunks = BM * (kBN / 16);
+    for (uint32_t q = tid; q < kChunks; q += 64 * kWaves) {
+        const uint32_t row = q / (kBN / 16), col0 = 16 * (q % (kBN / 16));
+        const uint32_t half = col0 / kWN, hcol = col0 % kWN;
+        const uint32_t m = m0 + row;
+        if (m >= m_rows) continue;
         const float scale = rowscale[m];
-        const float *src = red + ((half * kKSplit) * kBM + row) * kRedLd + hcol;
+        const float *src = red + ((half * kKSplit) * BM + row) * kRedLd + hcol;
         float *dst = c + (size_t)m * n_rows + n0 + col0;
         const bool whole = n0 + col0 + 16 <= n_rows && (n_rows & 3u) == 0 && ((uintptr_t)c & 15u) == 0;
 #pragma unroll
         for (uint32_t v = 0; v < 4; v++) {
             floatx4 sum = *(const floatx4 *)(src + 4 * v);
 #pragma unroll
-            for (uint32_t kp = 1; kp < kKSplit; kp++) sum += *(const floatx4 *)(src + kp * kBM * kRedLd + 4 * v);
+            for (uint32_t kp = 1; kp < kKSplit; kp++) sum += *(const floatx4 *)(src + kp * BM * kRedLd + 4 * v);
             sum *= scale;
             if (whole) {
                 *(floatx4 *)(dst + 4 * v) = sum;
@@ -438,7 +461,25 @@ __global__ void bf16_to_f32_kernel(const uint16_t *__restrict__ a, size_t count,
 
 namespace {
 
-size_t padded_rows(size_t m) { return (m + kBM - 1) / kBM * kBM; }
+size_t padded_rows(size_t m) { return (m + kPadRows - 1) / kPadRows * kPadRows; }
+
+int env_int(const char *name) {
+    const char *v = getenv(name);
+    return v ? atoi(v) : 0;
+}
+
+template <uint32_t BM>
+hipError_t launch_gemm(dmhip_ctx *ctx, const half8 *a16, const float *rowscale, const void *weights, size_t m,
+                       size_t n, size_t k, uint64_t w_bytes, float *c) {
+    using T = Tiling<BM>;
+    const uint32_t n_tiles = (uint32_t)((n + T::kBN - 1) / T::kBN), m_tiles = (uint32_t)((m + BM - 1) / BM);
+    static LdsLimit limit;
+    hipError_t e = limit.ensure((const void *)gemm_q4k_kernel<BM>, T::kLdsBytes);
+    if (e != hipSuccess) return e;
+    return launch_kernel(ctx, gemm_q4k_kernel<BM>, dim3(n_tiles * m_tiles), dim3(64 * T::kWaves), T::kLdsBytes, a16,
+                         rowscale, (const uint8_t *)weights, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)w_bytes,
+                         m_tiles, c);
+}
 
 // Workspace of the Q4_K path: a16 | rowscale.
 size_t q4k_workspace(size_t m, size_t k) {
@@ -488,13 +529,15 @@ int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t type, size_t m, size_t n, size_t 
                            dim3((uint32_t)(mp / 8), (uint32_t)((k / 256 + kPackBlocks - 1) / kPackBlocks)), dim3(512),
                            0, ctx->stream, a_bf16, (uint32_t)m, (uint32_t)k, a16, rowscale);
         DM_HIP(hipGetLastError());
-        const uint32_t n_tiles = (uint32_t)((n + kBN - 1) / kBN), m_tiles = (uint32_t)(mp / kBM);
-        static LdsLimit limit;  // 136 KiB of dynamic LDS
-        DM_HIP(limit.ensure((const void *)gemm_q4k_kernel, kLdsBytes));
-        {
-            DM_HIP(launch_kernel(ctx, gemm_q4k_kernel, dim3(n_tiles * m_tiles), dim3(64 * kWaves), kLdsBytes,
-                                 (const half8 *)a16, (const float *)rowscale, (const uint8_t *)weights, (uint32_t)m,
-                                 (uint32_t)n, (uint32_t)k, (uint32_t)w_bytes, m_tiles, c));
+        // Tiling: 128 x 64 workgroup tiles (four MFMA row tiles per dequantized
+        // weight; 9-11% faster than 64 x 128 at C5), 64 x 128 for prefills of
+        // at most 64 tokens; DMHIP_GEMM_BM (64, 128) overrides.
+        static const int forced_bm = env_int("DMHIP_GEMM_BM");
+        const uint32_t bm = (forced_bm == 64 || forced_bm == 128) ? (uint32_t)forced_bm : (m > 64 ? 128u : 64u);
+        if (bm == 128) {
+            DM_HIP(launch_gemm<128>(ctx, a16, rowscale, weights, m, n, k, w_bytes, c));
+        } else {
+            DM_HIP(launch_gemm<64>(ctx, a16, rowscale, weights, m, n, k, w_bytes, c));
         }
         DM_HIP(hipGetLastError());
         return DMHIP_OK;

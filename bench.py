@@ -361,10 +361,15 @@ def cpu_baseline(w, x, seconds):
         if time.perf_counter() - t0 >= seconds:
             break
     dt = time.perf_counter() - t0
+    # one more step on a single thread (the scalar rate per core)
+    t1 = time.perf_counter()
+    capi.argmax(capi.matvec(Q6_K, rows, cols, w, x, threads=1))
+    dt1 = time.perf_counter() - t1
     return {"value": step_bytes * reps / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"full C2 step (Q6_K 151936x4096 matvec + argmax) repeated {reps}x in {dt:.1f}s "
                       f"on {threads} host threads; oracle/dm_oracle.c restating src/cpu.rs (the Rust "
                       f"reference cannot be built here)",
+            "value_1_thread": step_bytes / dt1 / 1e9,
             "argmax": int(idx)}
 
 

@@ -39,8 +39,9 @@ class OracleError(RuntimeError):
 
 
 def build() -> str:
-    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
-    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off); always
+    rebuilds, so a changed compiler or flag cannot leave a stale library."""
+    subprocess.run(["make", "-s", "-B", "-C", _HERE], check=True)
     return _LIB_PATH
 
 

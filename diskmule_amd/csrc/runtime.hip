@@ -220,7 +220,11 @@ int dmhip_context_new(int device, dmhip_ctx **out) {
         delete ctx;
         return fail(DMHIP_ERR_NO_DEVICE, "HIP device %d did not answer", device);
     }
-    snprintf(ctx->name, sizeof ctx->name, "%s (%s)", prop.name, prop.gcnArchName);
+    // some runtimes report an empty marketing name: then the arch alone
+    if (prop.name[0])
+        snprintf(ctx->name, sizeof ctx->name, "%s (%s)", prop.name, prop.gcnArchName);
+    else
+        snprintf(ctx->name, sizeof ctx->name, "%s", prop.gcnArchName);
     ctx->compute_units = prop.multiProcessorCount;
     // Default-priority streams only.
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||

@@ -282,6 +282,40 @@ def test_q8_0_gemv_matches_oracle(ctx, rows, cols, batch):
         assert_close(got[b], want[b], f"Q8_0 {rows}x{cols} token {b}")
 
 
+@pytest.mark.parametrize("kind", [Q6_K, Q4_K])
+def test_fused_argmax_ties_resolve_to_the_lowest_row(ctx, kind):
+    """Rows repeat with period 97, so the maximum appears in about 500 rows
+    spread over many workgroups: the device-wide key maximum must return the
+    first of them (src/cpu.rs:275-293 keeps the first maximum)."""
+    rows, cols, period = 48000, 4096, 97
+    base = synth.quantized_matrix(kind, period, cols, synth.weight_seed(97, kind))
+    rb = base.size // period
+    w = np.concatenate([base.reshape(period, rb)] * (rows // period + 1))[:rows].reshape(-1)
+    x = synth.normal(synth.activation_seed(97), cols)
+    wb, xb, yb, ib = dev(ctx, w), dev(ctx, x), dev_out(ctx, rows * 4), dev_out(ctx, 4)
+    ctx.matvec_argmax_device(kind, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr, ib.device_ptr)
+    got = yb.read(0, rows * 4, np.float32)
+    idx = ctx.argmax_result()
+    want_row = capi.argmax(capi.matvec(kind, period, cols, base, x))
+    assert idx == want_row == capi.argmax(got)
+    assert np.count_nonzero(got == got[idx]) >= rows // period
+
+
+@pytest.mark.parametrize("kind", [Q6_K, Q8_0])
+def test_prefill_gemm_other_types_take_the_tokenwise_path(ctx, kind):
+    """Types without the MFMA GEMM run the decode GEMV in chunks of 16 tokens."""
+    m, n, k = 20, 96, 512
+    a = synth.to_bf16_bits(synth.normal(synth.activation_seed(8, kind), m * k))
+    w = synth.quantized_matrix(kind, n, k, synth.weight_seed(8, kind))
+    want = capi.gemm_tokenwise(kind, m, n, k, a, w)
+    ab, wb, cb = dev(ctx, a), dev(ctx, w), dev_out(ctx, m * n * 4)
+    ws = dev_out(ctx, ctx.gemm_workspace_bytes(m, k))
+    ctx.gemm_device(kind, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr)
+    got = cb.read(0, m * n * 4, np.float32).reshape(m, n)
+    for r in range(m):
+        assert_close(got[r], want[r], f"type {kind} token {r}")
+
+
 def test_q8_0_argmax_is_exact(ctx):
     rows, cols = 50000, 4096
     w = synth.quantized_matrix(Q8_0, rows, cols, synth.weight_seed(88))

@@ -763,7 +763,7 @@ int env_int(const char *name) {
 }
 
 // Blocks per fetch (G) and split of each tile's block groups over S waves:
-// enough waves to keep every SIMD busy, at least two groups per wave, and
+// enough waves to keep every SIMD busy, at least one group per wave, and
 // the workgroup's LDS (dynamic plus split-K scratch) within the 160 KiB of
 // a gfx950 workgroup.  DMHIP_QMV8_SPLIT (1..16, a power of two) and
 // DMHIP_QMV8_G (1, 2, 4) override the rules for tuning.  s == 0: no plan.
@@ -782,7 +782,7 @@ Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint
     if (forced_s == 1 || forced_s == 2 || forced_s == 4 || forced_s == 8 || forced_s == 16) {
         s = (uint32_t)forced_s;
     } else {
-        while (s < kMaxWaves8 && (size_t)tiles * s < 4096 && groups >= 4 * s) s *= 2;
+        while (s < kMaxWaves8 && (size_t)tiles * s < 4096 && groups >= 2 * s) s *= 2;
     }
     for (; s >= 1; s /= 2) {
         const uint32_t waves = s > 8 ? s : 8;

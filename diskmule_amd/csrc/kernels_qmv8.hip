@@ -873,13 +873,18 @@ Plan8 plan8_grouped(uint32_t type, uint32_t rows, uint32_t columns, uint32_t bat
     static const int forced_g = env_int("DMHIP_QMV8_GROUPED_G");
     Plan8 p;
     const uint32_t tiles = (rows + 15) / 16, blocks = columns / 256;
-    uint32_t g = (forced_g == 1 || forced_g == 2) ? (uint32_t)forced_g : (blocks >= 8 ? 2u : 1u);
+    // Small launches (C4's routed experts: 384 and 1024 job tiles) measured
+    // 4-5% faster with single-block groups over 4 waves per tile.
+    const bool small = (size_t)tiles * jobs < 1536 && blocks >= 2;
+    uint32_t g = (forced_g == 1 || forced_g == 2) ? (uint32_t)forced_g : (blocks >= 8 && !small ? 2u : 1u);
     if (blocks < 2) g = 1;
     for (; g >= 1; g /= 2) {
         const uint32_t groups = (blocks + g - 1) / g;
         uint32_t s = 1;
         if (forced_s == 1 || forced_s == 2 || forced_s == 4 || forced_s == 8) {
             s = (uint32_t)forced_s;
+        } else if (small) {
+            s = 4;
         } else {
             while (s < 8 && (size_t)tiles * jobs * s < 4096 && groups >= 2 * s) s *= 2;
         }

@@ -404,7 +404,7 @@ def main() -> int:
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
-              "multi-GPU path; see DESIGN.md for how the path would shard)", file=sys.stderr)
+              "multi-GPU path; the kernels work on one GPU's share of the rows)", file=sys.stderr)
         return 2
 
     from diskmule_amd import HipContext, synth

@@ -5,8 +5,8 @@
  * This header is the drop-in boundary.  It replaces the public surface of the
  * reference's Metal backend (src/metal.rs, re-exported at :2571-2572) and of
  * its expert residency (src/expert.rs) for the operators on the quantized
- * path.  A Rust `hip` module binds these symbols 1:1 (the binding is shown in
- * INTEGRATION.md) so the graph code keeps calling `matvec_mapped`,
+ * path.  A Rust `hip` module binds these symbols 1:1 (an `extern "C"` block
+ * over this header) so the graph code keeps calling `matvec_mapped`,
  * `matvec_owned`, `argmax`, `top_k_softmax`, `rms_norm`, `silu_mul` and
  * `ExpertCache::with_expert` by name.
  *

@@ -265,6 +265,27 @@ def test_output_head_q6_k_with_argmax(ctx):
     assert idx == want_idx
 
 
+@pytest.mark.parametrize("kind,rows,cols,batch", [(Q4_K, 70000, 4096, 1), (Q6_K, 66001, 2048, 2),
+                                                 (Q6_K, 65600, 768, 1), (Q4_K, 66000, 12288, 1)])
+def test_tall_matvec_line_aligned_staging(ctx, kind, rows, cols, batch):
+    """Tall matrices take the persistent plan, whose waves fetch whole
+    128-byte lines one block at a time and keep each fetch's last line for
+    the next block of the row: Q6_K rows start anywhere in a line, row counts
+    that end mid-tile, three-block rows, two tokens."""
+    print(f"tall type={kind} {rows}x{cols} batch={batch}", flush=True)
+    w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(60, rows))
+    x = synth.normal(synth.activation_seed(60, rows), batch * cols).reshape(batch, cols)
+    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, batch * rows * 4)
+    ctx.matvec_device(kind, rows, cols, wb.device_ptr, batch, xb.device_ptr, yb.device_ptr)
+    got = yb.read(0, batch * rows * 4, np.float32).reshape(batch, rows)
+    for b in range(batch):
+        assert_close(got[b], capi.matvec(kind, rows, cols, w, x[b]), f"token {b}")
+    if batch == 1:
+        ib = dev_out(ctx, 4)
+        ctx.matvec_argmax_device(kind, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr, ib.device_ptr)
+        assert ctx.argmax_result() == capi.argmax(yb.read(0, rows * 4, np.float32))
+
+
 @pytest.mark.parametrize("rows,cols,batch", [(1000, 2048, 1), (4096, 4096, 2), (300, 12288, 1), (40000, 4096, 1),
                                              (513, 4128, 1), (700, 2048, 5), (513, 4128, 3)])
 def test_q8_0_gemv_matches_oracle(ctx, rows, cols, batch):

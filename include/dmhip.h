@@ -185,7 +185,9 @@ int dmhip_matvec_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t 
 
 /* Batch-1 matvec plus greedy argmax over the rows (src/cpu.rs:275-293).
    *index_device receives the row index as uint32; a non-finite row makes the
-   next dmhip_argmax_result() report NonFinite. */
+   next dmhip_argmax_result() report NonFinite.  The reduction uses counters
+   owned by the context and reset by each launch, so calls on one context are
+   ordered on its stream (as every call of a context is). */
 int dmhip_matvec_argmax_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows,
                                size_t columns, const void *weights, const float *x,
                                float *y, uint32_t *index_device);

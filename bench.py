@@ -174,7 +174,55 @@ def bench_c1(ctx, synth, steps, warmup):
                         "gbps": per / (ms * 1e-3) / 1e9, "frac_of_peak": per / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     log(f"C1: cold kernel {out['cold']['kernel_ms'] * 1e3:.2f} us ({out['cold']['kernel_gbps']:.0f} GB/s); "
         f"sustained {ms * 1e3:.2f} us per matrix ({out['sustained']['gbps']:.0f} GB/s)")
+    out["floor"] = c1_floor(ctx, wbs, xb, yb, rows, cols, w.size, step_bytes, steps)
     return out
+
+
+def c1_floor(ctx, wbs, xb, yb, rows, cols, wbytes, step_bytes, steps):
+    """What bounds a single C1 launch: back-to-back durations of an empty
+    kernel (256 x 256, the GEMV's grid), of a kernel that only reads the same
+    9.4 MB (cold: rotating copies; warm: one copy), and of the VALU form of
+    the GEMV; plus the GEMV's phase stamps (s_memrealtime, 100 MHz) over a
+    few cold launches."""
+    n = max(steps, 2 * len(wbs))
+
+    def per_launch(body):
+        for i in range(3):
+            body(i)
+        ctx.synchronize()
+        time.sleep(0.05)
+        with Timed(ctx, kernels=False) as t:
+            for i in range(n):
+                body(i)
+        return t.wall_ms / n * 1e3
+
+    res = {"empty_kernel_us": per_launch(lambda i: ctx.probe_empty(256, 256)),
+           "read_only_cold_us": per_launch(lambda i: ctx.probe_read(wbs[i % len(wbs)].device_ptr, wbytes)),
+           "read_only_warm_us": per_launch(lambda i: ctx.probe_read(wbs[0].device_ptr, wbytes)),
+           "valu_gemv_cold_us": per_launch(lambda i: ctx.matvec_valu_device(Q4_K, rows, cols, wbs[i % len(wbs)].device_ptr,
+                                                                        xb.device_ptr, yb.device_ptr)),
+           "valu_gemv_warm_us": per_launch(lambda i: ctx.matvec_valu_device(Q4_K, rows, cols, wbs[0].device_ptr,
+                                                                        xb.device_ptr, yb.device_ptr))}
+    res["read_only_cold_gbps"] = step_bytes / (res["read_only_cold_us"] * 1e-6) / 1e9
+    spans, spread, rec, first, tail = [], [], [], [], []
+    for i in range(8):
+        ctx.synchronize()
+        time.sleep(0.002)
+        st = ctx.matvec_phase_trace(Q4_K, rows, cols, wbs[(3 + i) % len(wbs)].device_ptr, xb.device_ptr, yb.device_ptr)
+        t0 = st[:, 0].min()
+        spans.append((st[:, 3].max() - t0) * 0.01)
+        spread.append((st[:, 0].max() - t0) * 0.01)
+        rec.append(float(np.mean(st[:, 1] - st[:, 0])) * 0.01)
+        first.append(float(np.mean(st[:, 2] - st[:, 0])) * 0.01)
+        tail.append(float(np.mean(st[:, 3] - st[:, 2])) * 0.01)
+    med = lambda v: float(np.median(v))
+    res["phases_us"] = {"workgroups": int(st.shape[0]), "span": med(spans), "entry_spread": med(spread),
+                        "entry_to_records_built": med(rec), "entry_to_first_weights": med(first),
+                        "first_weights_to_end": med(tail),
+                        "note": "medians over 8 cold launches of per-workgroup means; the 100 MHz counter"}
+    log(f"C1 floor: empty {res['empty_kernel_us']:.2f} us, read-only cold {res['read_only_cold_us']:.2f} / warm "
+        f"{res['read_only_warm_us']:.2f} us, VALU GEMV cold {res['valu_gemv_cold_us']:.2f} us; phases {res['phases_us']}")
+    return res
 
 
 def bench_q8(ctx, synth, steps, warmup):
@@ -221,12 +269,12 @@ def bench_c3(ctx, synth, steps, warmup):
     for batch in (1, 4, 8):
         h = synth.normal(synth.activation_seed(3, batch), batch * hidden)
         hb, yb = upload(ctx, h), ctx.new_owned_buffer(batch * hidden * 4)
-        ws = ctx.new_owned_buffer(ctx.ffn_workspace_bytes(batch, ffn))
+        ws = ctx.new_owned_buffer(ctx.ffn_workspace_bytes(batch, hidden, ffn))
 
         def call(i, sets):
             gb, ub, db = sets[i % len(sets)]
             ctx.ffn_device(batch, hidden, ffn, Q4_K, gb.device_ptr, Q4_K, ub.device_ptr, Q6_K, db.device_ptr,
-                           1e-6, hb.device_ptr, yb.device_ptr, ws.device_ptr)
+                           1e-6, hb.device_ptr, yb.device_ptr, ws.device_ptr, len(ws))
 
         step_bytes = weight_bytes + 2 * batch * hidden * 4
         res = {}
@@ -327,7 +375,8 @@ def bench_c5(ctx, synth, steps, warmup):
     for n in (4096, 12288):
         w = synth.quantized_matrix(Q4_K, n, k, synth.weight_seed(5, n))
         wb, cb = upload(ctx, w), ctx.new_owned_buffer(m * n * 4)
-        call = lambda: ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr)
+        call = lambda: ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr,
+                                       len(ws))
         for _ in range(warmup):
             call()
         wall, kern, _ = timed_loop(ctx, lambda i: call(), steps)

@@ -55,20 +55,34 @@ using namespace dm;
 
 extern "C" {
 
-size_t dmhip_ffn_workspace_bytes(size_t batch, size_t ffn) {
-    // gate, up and activation rows, plus room for a normalized copy of h
-    // (hidden <= 4 * ffn is assumed by the callers on this path).
-    return (7 * batch * ffn + 256) * sizeof(float);
+size_t dmhip_ffn_workspace_bytes(size_t batch, size_t hidden, size_t ffn) {
+    // The unfused path's normalized copy of h, gate, up and activation rows
+    // (the fused path uses only the activation rows), each region rounded to
+    // 256 bytes.  0 when the size does not fit a size_t.
+    size_t floats[4] = {batch * hidden, batch * ffn, batch * ffn, batch * ffn};
+    if (batch && (hidden > SIZE_MAX / 4 / batch || ffn > SIZE_MAX / 4 / batch)) return 0;
+    size_t total = 0;
+    for (size_t f : floats) {
+        const size_t bytes = (f * sizeof(float) + 255) & ~(size_t)255;
+        if (bytes > SIZE_MAX - total) return 0;
+        total += bytes;
+    }
+    return total;
 }
 
 int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn, uint32_t gate_type,
                      const void *gate, uint32_t up_type, const void *up, uint32_t down_type,
-                     const void *down, float epsilon, const float *h, float *y, void *workspace) {
+                     const void *down, float epsilon, const float *h, float *y, void *workspace,
+                     size_t workspace_len) {
     if (!ctx || !gate || !up || !down || !h || !y || !workspace)
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "ffn arguments must not be null");
     if (batch < 1 || batch > 16)
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "batch %zu is outside 1..=16", batch);
     if (hidden == 0 || ffn == 0) return fail(DMHIP_ERR_EMPTY_INPUT, "FFN requires a non-empty input");
+    const size_t need = dmhip_ffn_workspace_bytes(batch, hidden, ffn);
+    if (need == 0 || workspace_len < need)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "FFN workspace holds %zu bytes; the shape needs %zu",
+                    workspace_len, need);
     if (!isfinite(epsilon) || epsilon <= 0.0f)
         return fail(DMHIP_ERR_INVALID_POSITIVE_PARAMETER, "RMSNorm epsilon requires a finite positive parameter");
     uint64_t rb;
@@ -85,14 +99,19 @@ int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn, ui
     if (hidden > 0xffffffffull || ffn > 0xffffffffull)
         return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "HIP vector length exceeds the 32-bit kernel limit");
     DM_CHECK_STATUS(set_device(ctx));
-    float *ws = (float *)workspace;
-    float *normalized = ws;                       // [batch][hidden]
-    float *g = normalized + batch * hidden;       // [batch][ffn]
-    float *u = g + batch * ffn;                   // [batch][ffn]
-    float *a = u + batch * ffn;                   // [batch][ffn]
-    // Fused: RMSNorm folded into the gate/up kernel's activation scale and
-    // silu(gate) * up in its epilogue, then the down projection.
-    if (gate_type == up_type && qmv_supported(gate_type, ffn, hidden, gate, batch) &&
+    // [batch][ffn] activation rows first (all the fused path uses), then the
+    // unfused path's [batch][hidden] normalized rows, gate and up rows.
+    auto region = [](size_t floats) { return (floats * sizeof(float) + 255) & ~(size_t)255; };
+    char *ws = (char *)workspace;
+    float *a = (float *)ws;
+    float *normalized = (float *)(ws + region(batch * ffn));
+    float *g = (float *)((char *)normalized + region(batch * hidden));
+    float *u = (float *)((char *)g + region(batch * ffn));
+    // Fused (Q4_K or Q6_K pairs, the types of the gate/up kernels): RMSNorm
+    // folded into the gate/up kernel's activation scale and silu(gate) * up
+    // in its epilogue, then the down projection.
+    if (gate_type == up_type && (gate_type == 12 || gate_type == 14) &&  // Q4_K, Q6_K
+        qmv_supported(gate_type, ffn, hidden, gate, batch) &&
         qmv_supported(up_type, ffn, hidden, up, batch)) {
         if (qmv8_gate_up_supported(gate_type, ffn, hidden, batch))
             DM_HIP(launch_qmv8_gate_up(ctx, gate_type, (uint32_t)ffn, (uint32_t)hidden, gate, up,

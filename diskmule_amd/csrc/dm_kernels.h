@@ -41,6 +41,10 @@ struct ArgmaxState {
 };
 
 hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t n);
+// Launch-floor probes: an empty kernel; a read of n bytes (16-byte aligned
+// src; bytes past the last whole 16 are not read).
+hipError_t launch_probe_empty(hipStream_t s, uint32_t workgroups, uint32_t threads);
+hipError_t launch_probe_read(hipStream_t s, const void *src, size_t n, uint32_t *sink);
 hipError_t launch_dequantize(hipStream_t s, uint32_t type, const uint8_t *enc, uint32_t be,
                              uint32_t bb, size_t elements, float *out);
 hipError_t launch_gemv_exact(hipStream_t s, uint32_t type, uint32_t be, uint32_t bb, uint32_t rows,
@@ -56,7 +60,14 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
                                uint32_t *non_finite, uint32_t *host_ids = nullptr,
-                               float *host_probs = nullptr, uint32_t *tickets = nullptr);
+                               float *host_probs = nullptr, uint32_t *tickets = nullptr,
+                               uint32_t *host_bad = nullptr);
+// With host_ids, the selection and one word per token (nonzero when that
+// token's logits held a non-finite value; with the one-workgroup-per-token
+// fallback kernel word 0 stands for all tokens) are written to host memory.
+// p[0..n) = value, stream-ordered (a kernel, so that callers may capture it
+// in a graph).
+hipError_t launch_fill_u32(hipStream_t s, uint32_t *p, uint32_t n, uint32_t value);
 // Per-token counters of the fused router selection (zero between launches).
 constexpr uint32_t kRouterTickets = 4096;
 hipError_t launch_rms_norm(hipStream_t s, const float *in, uint32_t batch, uint32_t n,

@@ -92,6 +92,7 @@ struct dmhip_expert_cache {
 
 namespace {
 constexpr size_t kSelectionPairs = 16 * dm::kMaxTopK;  // batch <= 16
+constexpr size_t kSelectionBytes = kSelectionPairs * 8 + 16 * 4;  // ids, probabilities, per-token flags
 constexpr size_t kReleaseEvents = 64;
 }
 
@@ -226,7 +227,7 @@ int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len
             dmhip_expert_cache_free(c);
             return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not create the slot release events");
         }
-    if (hipHostMalloc((void **)&c->host_selection, kSelectionPairs * 8, hipHostMallocDefault) != hipSuccess) {
+    if (hipHostMalloc((void **)&c->host_selection, kSelectionBytes, hipHostMallocDefault) != hipSuccess) {
         c->host_selection = nullptr;
         dmhip_expert_cache_free(c);
         return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate the pinned router selection buffer");
@@ -347,10 +348,20 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     // 1. Router logits (exact fold) and top-k softmax on the GPU.
     uint32_t *sel_ids = (uint32_t *)c->host_selection;
     float *sel_probs = (float *)(c->host_selection + kSelectionPairs * 4);
+    uint32_t *sel_bad = (uint32_t *)(c->host_selection + kSelectionPairs * 8);
+    // The previous call has finished (it ends with a synchronisation): the
+    // flags can be cleared from here; the device flag the fallback router
+    // sets is cleared on the stream.
+    memset(sel_bad, 0, 16 * 4);
+    DM_HIP(launch_fill_u32(ctx->stream, ctx->flags, 1, 0));
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs, ctx->flags, sel_ids,
-                               sel_probs, batch <= kRouterTickets ? ctx->router_tickets : nullptr));
+                               sel_probs, batch <= kRouterTickets ? ctx->router_tickets : nullptr, sel_bad));
     DM_HIP(hipStreamSynchronize(ctx->stream));
+    // top_k_softmax rejects non-finite logits (src/cpu.rs:240-245); nothing
+    // has been acquired yet.
+    for (size_t t = 0; t < batch; t++)
+        if (sel_bad[t]) return fail(DMHIP_ERR_NON_FINITE, "top-k softmax received a non-finite value");
     memcpy(ids, sel_ids, pairs * 4);
     memcpy(probabilities, sel_probs, pairs * 4);
 

@@ -39,7 +39,6 @@
 #include "dm_qmv.h"
 #include "runtime.h"
 
-#include <stdlib.h>
 
 namespace dm {
 
@@ -463,11 +462,6 @@ namespace {
 
 size_t padded_rows(size_t m) { return (m + kPadRows - 1) / kPadRows * kPadRows; }
 
-int env_int(const char *name) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : 0;
-}
-
 template <uint32_t BM>
 hipError_t launch_gemm(dmhip_ctx *ctx, const half8 *a16, const float *rowscale, const void *weights, size_t m,
                        size_t n, size_t k, uint64_t w_bytes, float *c) {
@@ -502,9 +496,13 @@ size_t dmhip_gemm_workspace_bytes(size_t m, size_t k) {
 }
 
 int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t type, size_t m, size_t n, size_t k,
-                      const uint16_t *a_bf16, const void *weights, float *c, void *workspace) {
+                      const uint16_t *a_bf16, const void *weights, float *c, void *workspace,
+                      size_t workspace_len) {
     if (!ctx || !a_bf16 || !weights || !c || !workspace)
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "gemm arguments must not be null");
+    if (workspace_len < dmhip_gemm_workspace_bytes(m, k))
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "gemm workspace holds %zu bytes; the shape needs %zu",
+                    workspace_len, dmhip_gemm_workspace_bytes(m, k));
     if (!(type == 0 || type == 1 || type == 6 || type == 8 || type == 12 || type == 14))
         return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "HIP GEMM does not support %s", type_name(type));
     uint64_t rb;
@@ -531,9 +529,8 @@ int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t type, size_t m, size_t n, size_t 
         DM_HIP(hipGetLastError());
         // Tiling: 128 x 64 workgroup tiles (four MFMA row tiles per dequantized
         // weight; 9-11% faster than 64 x 128 at C5), 64 x 128 for prefills of
-        // at most 64 tokens; DMHIP_GEMM_BM (64, 128) overrides.
-        static const int forced_bm = env_int("DMHIP_GEMM_BM");
-        const uint32_t bm = (forced_bm == 64 || forced_bm == 128) ? (uint32_t)forced_bm : (m > 64 ? 128u : 64u);
+        // at most 64 tokens.
+        const uint32_t bm = m > 64 ? 128u : 64u;
         if (bm == 128) {
             DM_HIP(launch_gemm<128>(ctx, a16, rowscale, weights, m, n, k, w_bytes, c));
         } else {

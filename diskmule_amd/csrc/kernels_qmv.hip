@@ -34,7 +34,6 @@
 #include "dm_device.h"
 #include "dm_qmv.h"
 
-#include <stdlib.h>
 
 namespace dm {
 
@@ -736,14 +735,7 @@ struct Plan {
     int nt, r, s, mb, g;
 };
 
-int env_int(const char *name) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : 0;
-}
-
 Plan choose_plan(uint32_t type, uint32_t rows, uint32_t blocks, uint32_t batch, int mode) {
-    static const int forced_g = env_int("DMHIP_QMV_G");
-    static const int forced_s = env_int("DMHIP_QMV_SPLIT");
     Plan p;
     p.nt = batch > 8 ? 2 : 1;
     const uint32_t tiles = (rows + 15) / 16;
@@ -755,20 +747,15 @@ Plan choose_plan(uint32_t type, uint32_t rows, uint32_t blocks, uint32_t batch, 
     p.r = (batch > 2 && mode != 2 && tiles >= 2048) ? 2 : 1;
     const uint32_t rr = mode == 2 ? 2 * p.r : p.r;
     // Blocks per staged group: 2 (runs of 2 blocks stream faster), or 1 when
-    // the row has a single block or LDS is short; DMHIP_QMV_G (1, 2) overrides.
-    p.g = (forced_g == 1 || forced_g == 2) ? forced_g : (blocks >= 2 ? 2 : 1);
+    // the row has a single block or LDS is short.
+    p.g = blocks >= 2 ? 2 : 1;
     // Split each tile's block groups over S waves of a workgroup until the
     // launch has about 4096 waves, with at least two groups per wave (S = 8
-    // only for prepared activations of up to 8 tokens, else S <= 4);
-    // DMHIP_QMV_SPLIT (1, 2, 4, 8) overrides.
+    // only for prepared activations of up to 8 tokens, else S <= 4).
     const uint32_t waves = (tiles + p.r - 1) / p.r;
     const uint32_t s_max = (p.mb == 0 && p.nt == 1) ? 8 : 4;
     uint32_t s = 1;
-    if (forced_s == 1 || forced_s == 2 || forced_s == 4 || (forced_s == 8 && s_max == 8)) {
-        s = (uint32_t)forced_s;
-    } else {
-        while (s < s_max && (size_t)waves * s < 4096 && (blocks + p.g - 1) / p.g >= 4 * s) s *= 2;
-    }
+    while (s < s_max && (size_t)waves * s < 4096 && (blocks + p.g - 1) / p.g >= 4 * s) s *= 2;
     // Dynamic (activations, staging) plus static (split-K partials) LDS
     // within the 160 KiB of a workgroup: first one block per group, then a
     // narrower split.

@@ -34,7 +34,6 @@
 #include "dm_device.h"
 #include "dm_qmv.h"
 
-#include <stdlib.h>
 
 namespace dm {
 
@@ -86,16 +85,73 @@ namespace {
 // Activation records of TOK tokens (token t at x + t * x_stride) written by
 // the workgroup into LDS at `rec` (record of block b, token t at
 // (b * TOK + t) * REC).  Wave k handles
-// blocks k, k + WAVES, ...: lane l loads the four values of step t = l >> 4,
+// blocks k, k + WAVES, ...: lane l takes the four values of step t = l >> 4,
 // lane group g = (l >> 2) & 3, columns 4q .. 4q+3 (q = l & 3) of the block,
 // and the block gets its own power-of-two scale 2^e (max|x| 2^-e < 2^22 over
 // the block; a wave-wide maximum, no barrier).  The scale is stored after the
 // record; it is NaN when the block holds a non-finite value, which makes
 // every output of that token NaN.  With NORM each wave also leaves its part
 // of sum(x^2) per token in red_ss[tok * WAVES + wave].
-template <uint32_t TYPE, int TOK, uint32_t WAVES, bool NORM>
+//
+// The values of a wave's first XP blocks are loaded by preload_x8 before the
+// kernel requests its weights: a wave's loads complete in the order they were
+// issued, so activations requested after the weights could only be used
+// once the weights had arrived.
+template <int TOK, int XP> struct XPre8 {
+    floatx4 v[TOK][XP];
+};
+
+template <uint32_t TYPE, int TOK, uint32_t WAVES, int XP>
+__device__ __forceinline__ void preload_x8(const float *__restrict__ x, int x_stride, uint32_t columns,
+                                           XPre8<TOK, XP> &pre) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t blocks = columns / 256;
+    const uint32_t t = lane >> 4, g = (lane >> 2) & 3u, q = lane & 3u;
+#pragma unroll
+    for (int tok = 0; tok < TOK; tok++)
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            // No branch around the loads: a branch that may skip a load makes
+            // every later wait on the wave's loads wait for all of them.
+            const uint32_t b = wave + (uint32_t)i * WAVES;
+            const uint32_t bc = b < blocks ? b : 0u;
+            // Written as the instruction: the compiler sinks a plain load to
+            // its first use, behind the weight loads.  wait_x8 waits for it.
+            const float *xb = x + (ptrdiff_t)tok * x_stride + (size_t)bc * 256 + column8<TYPE>(t, g, 4 * q);
+            asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(pre.v[tok][i]) : "v"(xb) : "memory");
+        }
+}
+
+// Waits until at most `later` vector-memory loads issued after the preload
+// are outstanding (loads complete in order, so the preload has landed).  The
+// values are operands of the wait, so no use of them can move above it, and
+// the memory clobbers of the loads and the wait keep every other memory
+// operation out of the span between them: exactly the `later` weight loads
+// of the first fetch lie in it.
+template <uint32_t later, int TOK, int XP>
+__device__ __forceinline__ void wait_x8(XPre8<TOK, XP> &pre) {
+    static_assert(later < 64, "vmcnt is 6 bits");
+    static_assert(TOK * XP == 1 || TOK * XP == 2 || TOK * XP == 4, "1, 2 or 4 preloaded blocks");
+    floatx4 a = pre.v[0][0];
+    floatx4 b = TOK * XP > 1 ? pre.v[(TOK * XP > 1 && XP == 1) ? 1 : 0][XP > 1 ? 1 : 0] : a;
+    floatx4 c = TOK * XP > 2 ? pre.v[0][XP > 2 ? 2 : 0] : a;
+    floatx4 d = TOK * XP > 3 ? pre.v[0][XP > 3 ? 3 : 0] : a;
+    if constexpr (TOK * XP == 1) {
+        asm volatile("s_waitcnt vmcnt(%1)" : "+v"(a) : "n"(later) : "memory");
+    } else if constexpr (TOK * XP == 2) {
+        asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(later) : "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(later) : "memory");
+    }
+    pre.v[0][0] = a;
+    if constexpr (TOK * XP > 1) pre.v[XP == 1 ? 1 : 0][XP == 1 ? 0 : 1] = b;
+    if constexpr (TOK * XP > 2) pre.v[0][2 < XP ? 2 : 0] = c;
+    if constexpr (TOK * XP > 3) pre.v[0][3 < XP ? 3 : 0] = d;
+}
+
+template <uint32_t TYPE, int TOK, uint32_t WAVES, bool NORM, int XP>
 __device__ __forceinline__ void build_records8(const float *__restrict__ x, int x_stride, uint32_t columns,
-                                               uint8_t *rec, float *red_ss) {
+                                               uint8_t *rec, float *red_ss, const XPre8<TOK, XP> &pre) {
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t blocks = columns / 256;
@@ -103,17 +159,18 @@ __device__ __forceinline__ void build_records8(const float *__restrict__ x, int 
 #pragma unroll
     for (int tok = 0; tok < TOK; tok++) {
         float ss = 0.0f;
-        for (uint32_t b = wave; b < blocks; b += WAVES) {
-            const float *xb = x + (ptrdiff_t)tok * x_stride + (size_t)b * 256 + column8<TYPE>(t, g, 4 * q);
+        // `store` false: computed for a block past the end (a clamped
+        // preload), nothing written.
+        auto record = [&](uint32_t b, const floatx4 vin, bool store) {
             float v[4];
             float mx = 0.0f;
             uint32_t bad = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                v[j] = xb[j];
+                v[j] = vin[j];
                 bad |= !__builtin_isfinite(v[j]);
                 mx = fmaxf(mx, fabsf(v[j]));
-                if (NORM) ss = __builtin_fmaf(v[j], v[j], ss);
+                if (NORM && store) ss = __builtin_fmaf(v[j], v[j], ss);
             }
             mx = wave_max(mx);
             bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
@@ -145,7 +202,8 @@ __device__ __forceinline__ void build_records8(const float *__restrict__ x, int 
             }
             uint8_t *r = rec + ((size_t)b * TOK + tok) * REC;
 #pragma unroll
-            for (int k = 0; k < 3; k++) *(uint32_t *)(r + t * kStep8 + (g * 3 + k) * 16 + 4 * q) = term[k];
+            for (int k = 0; k < 3; k++)
+                if (store) *(uint32_t *)(r + t * kStep8 + (g * 3 + k) * 16 + 4 * q) = term[k];
             if constexpr (TYPE == kQ8_0) {
                 // signed codes, no offset: nothing besides the A fragments
             } else if (TYPE == kQ6_K) {
@@ -155,15 +213,27 @@ __device__ __forceinline__ void build_records8(const float *__restrict__ x, int 
                     sum[k] += __shfl_xor(sum[k], 1, 64);
                     sum[k] += __shfl_xor(sum[k], 2, 64);
                 }
-                if (q == 0) *(i32x4 *)(r + 4 * kStep8 + (t * 4 + g) * 16) = i32x4{-32 * sum[0], -32 * sum[1], -32 * sum[2], 0};
+                if (store && q == 0) *(i32x4 *)(r + 4 * kStep8 + (t * 4 + g) * 16) = i32x4{-32 * sum[0], -32 * sum[1], -32 * sum[2], 0};
             } else {
                 // sub-block 2g + (t >> 1) = lanes (t, g, q) and (t ^ 1, g, q)
                 sx += __shfl_xor(sx, 1, 64);
                 sx += __shfl_xor(sx, 2, 64);
                 sx += __shfl_xor(sx, 16, 64);
-                if (q == 0 && (t & 1u) == 0) *(float *)(r + 4 * kStep8 + (2 * g + (t >> 1)) * 4) = (float)sx;
+                if (store && q == 0 && (t & 1u) == 0) *(float *)(r + 4 * kStep8 + (2 * g + (t >> 1)) * 4) = (float)sx;
             }
-            if (lane == 0) *(float *)(r + REC - 16) = bad ? __builtin_nanf("") : ldexpf(1.0f, e);
+            if (store && lane == 0) *(float *)(r + REC - 16) = bad ? __builtin_nanf("") : ldexpf(1.0f, e);
+        };
+        // The preloaded blocks are computed whether or not they exist, so no
+        // branch separates their loads from this use (the compiler would
+        // otherwise move the loads into the branch, behind the weights).
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const uint32_t b = wave + (uint32_t)i * WAVES;
+            record(b < blocks ? b : 0u, pre.v[tok][i], b < blocks);
+        }
+        for (uint32_t b = wave + XP * WAVES; b < blocks; b += WAVES) {
+            const float *xb = x + (ptrdiff_t)tok * x_stride + (size_t)b * 256 + column8<TYPE>(t, g, 4 * q);
+            record(b, floatx4{xb[0], xb[1], xb[2], xb[3]}, true);
         }
         if (NORM) {
             ss = wave_sum(ss);
@@ -389,7 +459,7 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ6_K> &raw, const i32x4 *
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// Main kernel.  WAVES = max(8, S) waves per workgroup.
+// Main kernel.  W waves per workgroup (a multiple of S).
 //  * S == 1 (tall matrices): persistent.  Workgroup b owns an even share
 //    [t0, t1) of the 16-row tiles; each wave takes the next tile from an LDS
 //    counter when it starts the last block group of its current one, so the
@@ -408,15 +478,18 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ6_K> &raw, const i32x4 *
 // workgroup's LDS allows on a C2-sized row; a tighter budget makes the
 // compiler wait for each prefetch right after issuing it.
 // ---------------------------------------------------------------------------
-template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W>
 __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
                                           uint32_t rows, uint32_t columns, uint32_t row_bytes,
                                           uint32_t total_bytes, const float *__restrict__ x, int x_stride,
                                           int normalize, float epsilon, int glm, float *__restrict__ y,
                                           int y_stride, ArgmaxPartial *__restrict__ partials,
-                                          const ArgmaxFinish finish) {
-    constexpr uint32_t WAVES = S > 8 ? S : 8;
+                                          const ArgmaxFinish finish, uint64_t *__restrict__ trace) {
+    constexpr uint32_t WAVES = W;
+    static_assert(W % S == 0, "a workgroup holds whole tiles");
     constexpr int NM = MODE == 2 ? 2 : 1;  // weight matrices streamed
+    // activation blocks of each wave loaded ahead of the weights
+    constexpr int XP = TOK == 1 ? (MODE == 2 ? 2 : 4) : 1;
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
     constexpr uint32_t BB = kBlock8<TYPE>;
     using ST = Stage8<TYPE, G>;
@@ -428,6 +501,11 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     __shared__ unsigned long long wg_key[WAVES];
     __shared__ uint32_t wg_bad[WAVES];
 
+    // Phase stamps of the workgroup (measurement only): entry, activation
+    // records built, first weight group landed, last output written.
+    const bool stamp = trace != nullptr && threadIdx.x == 0;
+    uint64_t t_entry = 0, t_records = 0, t_weights = 0;
+    if (stamp) t_entry = __builtin_amdgcn_s_memrealtime();
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t kpart = wave % S;
@@ -459,43 +537,47 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     // Staging chunk j*64 + lane: row r, chunk c of the tile.
     uint32_t src_row[NL], src_chunk[NL];
     uint32_t next_row_base = nowhere;
-    auto setup = [&](uint32_t tl) {
+    auto setup = [&](uint32_t tl, bool live) {
 #pragma unroll
         for (uint32_t j = 0; j < NL; j++) {
             const uint32_t item = j * 64 + lane, r = item / CH, c = item % CH;
             const uint32_t rr = tl * 16 + r;
-            src_row[j] = (item < ITEMS && rr < rows) ? rr * row_bytes : nowhere;
+            src_row[j] = (live && item < ITEMS && rr < rows) ? rr * row_bytes : nowhere;
             src_chunk[j] = 16 * c;
         }
         const uint32_t rw = tl * 16 + n;
-        next_row_base = rw < rows ? rw * row_bytes : nowhere;
+        next_row_base = (live && rw < rows) ? rw * row_bytes : nowhere;
     };
     v4u st[NL], st2[MODE == 2 ? NL : 1];
-    auto fetch = [&](uint32_t grp) {
+    auto fetch = [&](uint32_t grp, bool live) {
 #pragma unroll
         for (uint32_t j = 0; j < NL; j++) {
             const uint32_t off =
-                src_row[j] == nowhere ? nowhere : ((src_row[j] + grp * G * BB) & ~3u) + src_chunk[j];
+                (!live || src_row[j] == nowhere) ? nowhere : ((src_row[j] + grp * G * BB) & ~3u) + src_chunk[j];
             st[j] = __builtin_bit_cast(v4u, rsrc_load16(rsrc, off));
             if constexpr (MODE == 2) st2[j] = __builtin_bit_cast(v4u, rsrc_load16(rsrc2, off));
         }
     };
 
-    // The first weights are requested before the records are built.
+    // The wave's first activation values, then its first weights, are
+    // requested before the records are built.
+    XPre8<TOK, XP> xpre;
+    preload_x8<TYPE, TOK, WAVES, XP>(x, x_stride, columns, xpre);
+    // Issued without a branch (an idle wave's loads all read past the end).
     bool active = tile < t_end;
-    if (active) {
-        setup(tile);
-        if (kpart < groups) fetch(kpart);
-    }
+    setup(active ? tile : 0u, active);
+    fetch(kpart, active && kpart < groups);
+    wait_x8<NL * NM>(xpre);
     uint32_t row_base = next_row_base;
 
     const bool norm = MODE == 2 && normalize;
     if (norm)
-        build_records8<TYPE, TOK, WAVES, true>(x, x_stride, columns, (uint8_t *)lds8, red_ss);
+        build_records8<TYPE, TOK, WAVES, true, XP>(x, x_stride, columns, (uint8_t *)lds8, red_ss, xpre);
     else
-        build_records8<TYPE, TOK, WAVES, false>(x, x_stride, columns, (uint8_t *)lds8, red_ss);
+        build_records8<TYPE, TOK, WAVES, false, XP>(x, x_stride, columns, (uint8_t *)lds8, red_ss, xpre);
     for (uint32_t i = threadIdx.x; i < kZero8 / 16; i += 64 * WAVES) lds8[rec_bytes / 16 + i] = i32x4{0, 0, 0, 0};
     __syncthreads();
+    if (stamp) t_records = __builtin_amdgcn_s_memrealtime();
     // Output scale per token: 1, or the RMSNorm factor (unit weight)
     // inv = (ss/n + eps).sqrt().recip() (src/cpu.rs:98-142) folded in.
     float tscale[TOK];
@@ -529,6 +611,7 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
                 if constexpr (MODE == 2) stage2[j * 64 + lane] = st2[j];
             }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (stamp && t_weights == 0) t_weights = __builtin_amdgcn_s_memrealtime();
     };
     // acc[m][tok]: matrix m (gate, up) of token tok
     auto compute_group = [&](uint32_t grp, uint32_t rb, float (&acc)[NM][TOK]) {
@@ -592,14 +675,14 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
             for (uint32_t grp = 0; grp < groups; grp++) {
                 put_stage();
                 if (grp + 1 < groups) {
-                    fetch(grp + 1);
+                    fetch(grp + 1, true);
                 } else {
                     uint32_t claimed = 0;
                     if (lane == 0) claimed = atomicAdd(&next_tile, 1u);
                     next = __builtin_amdgcn_readfirstlane(claimed);
                     if (next < t_end) {
-                        setup(next);
-                        fetch(0);
+                        setup(next, true);
+                        fetch(0, true);
                     }
                 }
                 compute_group(grp, rb, acc);
@@ -625,7 +708,7 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
         if (active) {
             for (uint32_t grp = kpart; grp < groups; grp += S) {
                 put_stage();
-                if (grp + S < groups) fetch(grp + S);
+                if (grp + S < groups) fetch(grp + S, true);
                 compute_group(grp, row_base, acc);
             }
         }
@@ -651,6 +734,13 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
         }
     }
 
+    if (stamp) {
+        uint64_t *t = trace + 4 * (size_t)blockIdx.x;
+        t[0] = t_entry;
+        t[1] = t_records;
+        t[2] = t_weights;
+        t[3] = __builtin_amdgcn_s_memrealtime();
+    }
     if constexpr (MODE == 1) {
         best = wave_max_u64(best);
         bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
@@ -696,14 +786,14 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     }
 }
 
-template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
-__global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W>
+__global__ void __launch_bounds__(64 * W)
     __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2))) qmv8_kernel(
     const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows, uint32_t columns,
     uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x, int normalize, float epsilon,
-    float *__restrict__ y, ArgmaxPartial *__restrict__ partials, ArgmaxFinish finish) {
-    qmv8_body<TYPE, S, MODE, TOK, G>(w, w2, rows, columns, row_bytes, total_bytes, x, (int)columns, normalize,
-                                     epsilon, 0, y, (int)rows, partials, finish);
+    float *__restrict__ y, ArgmaxPartial *__restrict__ partials, ArgmaxFinish finish, uint64_t *trace) {
+    qmv8_body<TYPE, S, MODE, TOK, G, W>(w, w2, rows, columns, row_bytes, total_bytes, x, (int)columns, normalize,
+                                        epsilon, 0, y, (int)rows, partials, finish, trace);
 }
 
 // Grouped launch over the routed-expert jobs of a MoE layer: job
@@ -727,9 +817,9 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8)) __attribute__((amdgpu_wa
                         float *__restrict__ y, int glm) {
     const Job8 j = jobs.job[blockIdx.y];
     const uint8_t *w = (const uint8_t *)j.w;
-    qmv8_body<TYPE, S, MODE, TOK, G>(w, w + w2_offset, rows, columns, row_bytes, total_bytes, x + j.x_off,
+    qmv8_body<TYPE, S, MODE, TOK, G, (S > 8 ? S : 8)>(w, w + w2_offset, rows, columns, row_bytes, total_bytes, x + j.x_off,
                                      j.x_stride, 0, 0.0f, glm, y + j.y_off, j.y_stride, nullptr,
-                                     ArgmaxFinish{nullptr, nullptr, nullptr, nullptr});
+                                     ArgmaxFinish{nullptr, nullptr, nullptr, nullptr}, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -757,42 +847,52 @@ struct Plan8 {
     uint32_t s = 0, g = 1;
 };
 
-int env_int(const char *name) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : 0;
+// Waves per workgroup of a plan with split S: eight up to S = 8 (several
+// tiles per workgroup below that), S above.
+constexpr uint32_t waves8(uint32_t s) { return s <= 8 ? 8u : s; }
+
+bool fits8(uint32_t type, uint32_t blocks, uint32_t batch, uint32_t mats, uint32_t s, uint32_t g) {
+    const uint32_t waves = waves8(s);
+    // static: split-K scratch, token maxima, argmax candidates, counters
+    const size_t stat = (s > 1 ? (size_t)waves * 64 * batch * mats * sizeof(float) : 4) + 768;
+    return lds8_bytes(type, blocks, batch, waves, g, mats) + stat <= kMaxLds8;
 }
 
 // Blocks per fetch (G) and split of each tile's block groups over S waves:
-// enough waves to keep every SIMD busy, at least one group per wave, and
-// the workgroup's LDS (dynamic plus split-K scratch) within the 160 KiB of
-// a gfx950 workgroup.  DMHIP_QMV8_SPLIT (1..16, a power of two) and
-// DMHIP_QMV8_G (1, 2, 4) override the rules for tuning.  s == 0: no plan.
-Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t mats) {
-    static const int forced_s = env_int("DMHIP_QMV8_SPLIT");
-    static const int forced_g = env_int("DMHIP_QMV8_G");
+// enough waves to keep every SIMD busy, at least one group per wave, and the
+// workgroup's LDS (dynamic plus split-K scratch) within the 160 KiB of a
+// gfx950 workgroup.  Two blocks per fetch on tall matrices halve the cache
+// lines requested twice (a block's last line is the next block's first);
+// short ones need the parallelism of single-block groups more.  Measured on
+// MI355X (kernel trace medians): a 4096 x 4096 Q4_K matrix runs 5.7 us with
+// 16 waves of one block per tile against 6.2 us with one 4-wave workgroup of
+// four-block fetches per tile, and 4096 x 2048 runs 4.2 us with 8 waves
+// against 5.2 us with four of two-block fetches.
+// force_s / force_g (both nonzero) pin the plan when it fits (measurement).
+// s == 0: no plan.
+Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t mats, uint32_t force_s = 0,
+            uint32_t force_g = 0) {
     Plan8 p;
     const uint32_t tiles = (rows + 15) / 16, blocks = columns / 256;
-    // Two blocks per fetch halve the cache lines requested twice (a block's
-    // last line is the next block's first) on tall matrices; short ones
-    // need the parallelism of single-block groups more.
-    p.g = (forced_g == 1 || forced_g == 2 || forced_g == 4) ? (uint32_t)forced_g : (tiles >= 2048 ? 2u : 1u);
+    if (force_s || force_g) {
+        const bool ok_s = force_s == 1 || force_s == 2 || force_s == 4 || force_s == 8 || force_s == 16;
+        const bool ok_g = force_g == 1 || force_g == 2 || force_g == 4;
+        if (ok_s && ok_g && force_g <= blocks && fits8(type, blocks, batch, mats, force_s, force_g)) {
+            p.s = force_s;
+            p.g = force_g;
+        }
+        return p;
+    }
+    p.g = tiles >= 2048 ? 2u : 1u;
     while (p.g > 1 && blocks < 2 * p.g) p.g /= 2;
     const uint32_t groups = (blocks + p.g - 1) / p.g;
     uint32_t s = 1;
-    if (forced_s == 1 || forced_s == 2 || forced_s == 4 || forced_s == 8 || forced_s == 16) {
-        s = (uint32_t)forced_s;
-    } else {
-        while (s < kMaxWaves8 && (size_t)tiles * s < 4096 && groups >= 2 * s) s *= 2;
-    }
-    for (; s >= 1; s /= 2) {
-        const uint32_t waves = s > 8 ? s : 8;
-        // static: split-K scratch, token maxima, argmax candidates, counters
-        const size_t stat = (s > 1 ? (size_t)waves * 64 * batch * mats * sizeof(float) : 4) + 768;
-        if (lds8_bytes(type, blocks, batch, waves, p.g, mats) + stat <= kMaxLds8) {
+    while (s < kMaxWaves8 && (size_t)tiles * s < 4096 && groups >= 2 * s) s *= 2;
+    for (; s >= 1; s /= 2)
+        if (fits8(type, blocks, batch, mats, s, p.g)) {
             p.s = s;
             return p;
         }
-    }
     p.s = 0;
     return p;
 }
@@ -808,11 +908,12 @@ struct Args8 {
     ArgmaxPartial *partials;
     uint32_t *count;
     ArgmaxFinish finish;
+    uint64_t *trace;
 };
 
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
 hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
-    constexpr uint32_t WAVES = S > 8 ? S : 8;
+    constexpr uint32_t WAVES = waves8(S);
     const uint32_t rows = a.rows, columns = a.columns;
     const uint32_t tiles = (rows + 15) / 16;
     const uint32_t blocks = columns / 256;
@@ -833,7 +934,7 @@ hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
         grid = (tiles + per - 1) / per;
     }
     if (a.count) *a.count = grid;
-    auto kernel = qmv8_kernel<TYPE, S, MODE, TOK, G>;
+    auto kernel = qmv8_kernel<TYPE, S, MODE, TOK, G, WAVES>;
     if (lds > 64 * 1024) {
         static LdsLimit limit;
         hipError_t e = limit.ensure((const void *)kernel, lds);
@@ -841,7 +942,7 @@ hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
     }
     return launch_kernel(ctx, kernel, dim3(grid), dim3(64 * WAVES), lds, (const uint8_t *)a.w,
                          (const uint8_t *)a.w2, rows, columns, row_bytes, row_bytes * rows, a.x, a.normalize,
-                         a.epsilon, a.y, a.partials, a.finish);
+                         a.epsilon, a.y, a.partials, a.finish, a.trace);
 }
 
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
@@ -864,26 +965,22 @@ hipError_t run8_g(dmhip_ctx *ctx, const Plan8 &p, const Args8 &a) {
 
 // Grouped jobs: blocks per fetch (G = 2 for rows of 8 or more blocks, whose
 // runs of 2 blocks stream about 60% faster than single blocks; G = 1
-// otherwise; DMHIP_QMV8_GROUPED_G forces 1 or 2), and a split of each tile's
+// otherwise), and a split of each tile's
 // block groups that gives the whole launch about 4096 wave-tiles with at
 // least one group per wave.
 Plan8 plan8_grouped(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t mats,
                     uint32_t jobs) {
-    static const int forced_s = env_int("DMHIP_QMV8_GROUPED_SPLIT");
-    static const int forced_g = env_int("DMHIP_QMV8_GROUPED_G");
     Plan8 p;
     const uint32_t tiles = (rows + 15) / 16, blocks = columns / 256;
     // Small launches (C4's routed experts: 384 and 1024 job tiles) measured
     // 4-5% faster with single-block groups over 4 waves per tile.
     const bool small = (size_t)tiles * jobs < 1536 && blocks >= 2;
-    uint32_t g = (forced_g == 1 || forced_g == 2) ? (uint32_t)forced_g : (blocks >= 8 && !small ? 2u : 1u);
+    uint32_t g = blocks >= 8 && !small ? 2u : 1u;
     if (blocks < 2) g = 1;
     for (; g >= 1; g /= 2) {
         const uint32_t groups = (blocks + g - 1) / g;
         uint32_t s = 1;
-        if (forced_s == 1 || forced_s == 2 || forced_s == 4 || forced_s == 8) {
-            s = (uint32_t)forced_s;
-        } else if (small) {
+        if (small) {
             s = 4;
         } else {
             while (s < 8 && (size_t)tiles * jobs * s < 4096 && groups >= 2 * s) s *= 2;
@@ -941,8 +1038,9 @@ hipError_t run8_grouped_s(dmhip_ctx *ctx, const Plan8 &p, uint32_t rows, uint32_
 }
 
 template <uint32_t TYPE>
-hipError_t launch8(dmhip_ctx *ctx, uint32_t batch, int mode, const Args8 &a) {
-    const Plan8 p = plan8(TYPE, a.rows, a.columns, batch, mode == 2 ? 2u : 1u);
+hipError_t launch8(dmhip_ctx *ctx, uint32_t batch, int mode, const Args8 &a, uint32_t force_s = 0,
+                   uint32_t force_g = 0) {
+    const Plan8 p = plan8(TYPE, a.rows, a.columns, batch, mode == 2 ? 2u : 1u, force_s, force_g);
     if (p.s == 0) return hipErrorInvalidValue;
     if (mode == 1) return run8_g<TYPE, 1, 1>(ctx, p, a);
     if (mode == 2) {
@@ -971,19 +1069,19 @@ bool qmv8_gate_up_supported(uint32_t type, size_t rows, size_t columns, size_t b
 
 hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
                        uint32_t batch, const float *x, float *y, ArgmaxPartial *partials, uint32_t *count,
-                       ArgmaxFinish finish) {
-    const Args8 a{rows, columns, w, w, x, 0, 0.0f, y, partials, count, finish};
+                       ArgmaxFinish finish, uint64_t *trace, uint32_t force_s, uint32_t force_g) {
+    const Args8 a{rows, columns, w, w, x, 0, 0.0f, y, partials, count, finish, trace};
     const int mode = partials ? 1 : 0;
-    if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, mode, a);
-    if (type == kQ8_0) return launch8<kQ8_0>(ctx, batch, mode, a);
-    return launch8<kQ6_K>(ctx, batch, mode, a);
+    if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, mode, a, force_s, force_g);
+    if (type == kQ8_0) return launch8<kQ8_0>(ctx, batch, mode, a, force_s, force_g);
+    return launch8<kQ6_K>(ctx, batch, mode, a, force_s, force_g);
 }
 
 hipError_t launch_qmv8_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns,
                                const void *gate, const void *up, uint32_t batch, const float *x, float *act,
                                int normalize, float epsilon) {
     const Args8 a{rows, columns, gate, up, x, normalize, epsilon, act, nullptr, nullptr,
-                  ArgmaxFinish{nullptr, nullptr, nullptr, nullptr}};
+                  ArgmaxFinish{nullptr, nullptr, nullptr, nullptr}, nullptr};
     if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, 2, a);
     return launch8<kQ6_K>(ctx, batch, 2, a);
 }

@@ -135,8 +135,10 @@ __global__ void argmax_finish_kernel(const ArgmaxState *state, uint32_t *index) 
 
 // ---- top-k softmax (src/cpu.rs:232-260) -------------------------------
 // One workgroup per row of `count` logits.  Selection i is the largest key
-// strictly below selection i-1 (keys are unique: value, then index).
-__device__ void block_top_k(const float *logits, uint32_t count, uint32_t k, uint32_t *ids,
+// strictly below selection i-1 (keys are unique: value, then index).  A
+// non-finite logit sets *non_finite; the return value (the same in every
+// thread) says whether the row held one.
+__device__ bool block_top_k(const float *logits, uint32_t count, uint32_t k, uint32_t *ids,
                             float *probabilities, uint32_t *non_finite) {
     __shared__ uint64_t partial[16];
     __shared__ uint64_t chosen[kMaxTopK];
@@ -146,6 +148,7 @@ __device__ void block_top_k(const float *logits, uint32_t count, uint32_t k, uin
     for (uint32_t i = tid; i < count; i += nthreads)
         if (!__builtin_isfinite(logits[i])) bad = 1;
     if (bad) atomicOr(non_finite, 1u);
+    const bool row_bad = __syncthreads_or((int)bad) != 0;
     uint64_t previous = ~0ull;
     for (uint32_t s = 0; s < k; s++) {
         uint64_t best = 0;
@@ -181,6 +184,7 @@ __device__ void block_top_k(const float *logits, uint32_t count, uint32_t k, uin
         }
         for (uint32_t s = 0; s < k; s++) probabilities[s] = values[s] / sum;
     }
+    return row_bad;
 }
 
 __global__ void __launch_bounds__(256) top_k_kernel(const float *__restrict__ logits,
@@ -241,7 +245,7 @@ template <uint32_t CC>
 __global__ void __launch_bounds__(256) router_staged_kernel(
     const uint16_t *__restrict__ router, uint32_t hidden, uint32_t experts, uint32_t k,
     const float *__restrict__ x, float *__restrict__ logits, uint32_t *ids, float *probabilities,
-    uint32_t *non_finite, uint32_t *host_ids, float *host_probs) {
+    uint32_t *non_finite, uint32_t *host_ids, float *host_probs, uint32_t *host_bad) {
     constexpr uint32_t ROW = CC * 2 + 16;  // LDS bytes per expert row
     constexpr uint32_t PR = CC * 2 / 16;   // 16-byte pieces of a row per chunk
     constexpr uint32_t XP = CC * 4 / 16;   // 16-byte pieces of x per chunk
@@ -345,12 +349,13 @@ __global__ void __launch_bounds__(256) router_staged_kernel(
     __syncthreads();
     uint32_t *ti = ids + (size_t)token * k;
     float *tp = probabilities + (size_t)token * k;
-    block_top_k(s_logits, E, k, ti, tp, non_finite);
+    const bool bad = block_top_k(s_logits, E, k, ti, tp, non_finite);
     if (host_ids && tid == 0) {
         for (uint32_t s = 0; s < k; s++) {
             host_ids[(size_t)token * k + s] = ti[s];
             host_probs[(size_t)token * k + s] = tp[s];
         }
+        host_bad[token] = bad;
     }
 }
 
@@ -376,7 +381,7 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
                                                          uint32_t experts, uint32_t k, const float *__restrict__ x,
                                                          float *logits, uint32_t *tickets, uint32_t *ids,
                                                          float *probabilities, uint32_t *non_finite,
-                                                         uint32_t *host_ids, float *host_probs) {
+                                                         uint32_t *host_ids, float *host_probs, uint32_t *host_bad) {
     __shared__ v4a rf_lds[2 * RF_BUF / 4];
     const uint32_t lane = threadIdx.x, e0 = blockIdx.x * RF_EXPERTS, token = blockIdx.y;
     const uint32_t chunks = (hidden + RF_CHUNK - 1) / RF_CHUNK;
@@ -481,13 +486,14 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
     __syncthreads();
     uint32_t *ti = ids + (size_t)token * k;
     float *tp = probabilities + (size_t)token * k;
-    block_top_k(s_row, experts, k, ti, tp, non_finite);
+    const bool bad = block_top_k(s_row, experts, k, ti, tp, non_finite);
     if (lane == 0) {
         if (host_ids) {
             for (uint32_t s = 0; s < k; s++) {
                 host_ids[(size_t)token * k + s] = ti[s];
                 host_probs[(size_t)token * k + s] = tp[s];
             }
+            host_bad[token] = bad;
         }
         __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -499,7 +505,7 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
 __global__ void __launch_bounds__(256) top_k_host_kernel(const float *__restrict__ logits, uint32_t count,
                                                          uint32_t k, uint32_t *ids, float *probabilities,
                                                          uint32_t *non_finite, uint32_t *host_ids,
-                                                         float *host_probs) {
+                                                         float *host_probs, uint32_t *host_bad) {
     __shared__ float s_row[256];
     const uint32_t row = blockIdx.x;
     uint32_t *ti = ids + (size_t)row * k;
@@ -507,12 +513,13 @@ __global__ void __launch_bounds__(256) top_k_host_kernel(const float *__restrict
     // the row once into LDS (count <= 256), where the k selection rounds read it
     if (threadIdx.x < count) s_row[threadIdx.x] = logits[(size_t)row * count + threadIdx.x];
     __syncthreads();
-    block_top_k(s_row, count, k, ti, tp, non_finite);
+    const bool bad = block_top_k(s_row, count, k, ti, tp, non_finite);
     if (host_ids && threadIdx.x == 0) {
         for (uint32_t s = 0; s < k; s++) {
             host_ids[(size_t)row * k + s] = ti[s];
             host_probs[(size_t)row * k + s] = tp[s];
         }
+        host_bad[row] = bad;
     }
 }
 
@@ -600,7 +607,46 @@ __global__ void __launch_bounds__(256) copy_bytes_kernel(uint8_t *__restrict__ d
     }
 }
 
+// ---- launch-floor probes (measurement) ----------------------------------
+// An empty kernel, and a kernel that only reads: each 256-thread workgroup
+// streams 16 KB with four 16-byte loads per lane issued before any use, and
+// writes only if the checksum equals `magic` (never, in practice), so the
+// loads cannot be dropped.  Their durations bound what a GEMV of the same
+// bytes can reach.
+__global__ void probe_empty_kernel() {}
+
+__global__ void __launch_bounds__(256) probe_read_kernel(const u32x4 *__restrict__ src, size_t n16,
+                                                         uint32_t magic, uint32_t *sink) {
+    const size_t base = (size_t)blockIdx.x * 1024 + threadIdx.x;
+    u32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const size_t i = base + 256 * j;
+        v[j] = i < n16 ? src[i] : u32x4{0, 0, 0, 0};
+    }
+    uint32_t h = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) h += v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) h ^= __shfl_xor(h, m, 64);
+    if (h == magic) sink[0] = h;
+}
+
 // ---- host-side launchers -------------------------------------------------
+
+hipError_t launch_probe_empty(hipStream_t s, uint32_t workgroups, uint32_t threads) {
+    hipLaunchKernelGGL(probe_empty_kernel, dim3(workgroups), dim3(threads), 0, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_probe_read(hipStream_t s, const void *src, size_t n, uint32_t *sink) {
+    const size_t n16 = n / 16;
+    const size_t groups = (n16 + 1023) / 1024;
+    if (groups == 0) return hipSuccess;
+    hipLaunchKernelGGL(probe_read_kernel, dim3((uint32_t)groups), dim3(256), 0, s, (const u32x4 *)src, n16,
+                       0x9e3779b9u, sink);
+    return hipGetLastError();
+}
 
 hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t n) {
     size_t blocks = (n / 16 + 255) / 256;
@@ -662,7 +708,8 @@ template <uint32_t CC>
 static hipError_t launch_router_staged(hipStream_t s, const uint16_t *router, uint32_t hidden,
                                        uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                        float *logits, uint32_t *ids, float *probabilities,
-                                       uint32_t *non_finite, uint32_t *host_ids, float *host_probs) {
+                                       uint32_t *non_finite, uint32_t *host_ids, float *host_probs,
+                                       uint32_t *host_bad) {
     const size_t lds = 2 * (((size_t)experts * (CC * 2 + 16) + CC * 4 + 15) & ~(size_t)15);
     // the largest slot ring, once per device
     static LdsLimit limit;
@@ -670,32 +717,34 @@ static hipError_t launch_router_staged(hipStream_t s, const uint16_t *router, ui
     hipError_t e = limit.ensure((const void *)router_staged_kernel<CC>, most);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(router_staged_kernel<CC>, dim3(batch), dim3(256), lds, s, router, hidden, experts, k, x,
-                       logits, ids, probabilities, non_finite, host_ids, host_probs);
+                       logits, ids, probabilities, non_finite, host_ids, host_probs, host_bad);
     return hipGetLastError();
 }
 
 hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
-                               uint32_t *non_finite, uint32_t *host_ids, float *host_probs, uint32_t *tickets) {
+                               uint32_t *non_finite, uint32_t *host_ids, float *host_probs, uint32_t *tickets,
+                               uint32_t *host_bad) {
+    if (host_ids && (!host_probs || !host_bad)) return hipErrorInvalidValue;
     const bool staged = experts <= 256 && hidden % 8 == 0 && (uint64_t)experts * hidden * 2 < (1ull << 30) && ((uintptr_t)router & 15u) == 0 &&
                         ((uintptr_t)x & 15u) == 0;
     // Decode batches: the expert-parallel fold, then the selection.
     if (staged && experts >= 2 * RF_EXPERTS && (uint64_t)experts * hidden * 2 < 0x80000000ull) {
         hipLaunchKernelGGL(router_fold_kernel, dim3((experts + RF_EXPERTS - 1) / RF_EXPERTS, batch), dim3(64), 0, s,
                            router, hidden, experts, k, x, logits, tickets, ids, probabilities, non_finite, host_ids,
-                           host_probs);
+                           host_probs, host_bad);
         if (!tickets)
             hipLaunchKernelGGL(top_k_host_kernel, dim3(batch), dim3(256), 0, s, logits, experts, k, ids,
-                               probabilities, non_finite, host_ids, host_probs);
+                               probabilities, non_finite, host_ids, host_probs, host_bad);
         return hipGetLastError();
     }
     if (staged && experts <= 128)
         return launch_router_staged<128>(s, router, hidden, experts, k, batch, x, logits, ids, probabilities,
-                                         non_finite, host_ids, host_probs);
+                                         non_finite, host_ids, host_probs, host_bad);
     if (staged)
         return launch_router_staged<64>(s, router, hidden, experts, k, batch, x, logits, ids, probabilities,
-                                        non_finite, host_ids, host_probs);
+                                        non_finite, host_ids, host_probs, host_bad);
     hipLaunchKernelGGL(router_top_k_kernel, dim3(batch), dim3(256), experts * sizeof(float), s,
                        router, hidden, experts,
                        k, x, logits, ids, probabilities, non_finite);
@@ -703,7 +752,20 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
     if (e != hipSuccess || !host_ids) return e;
     e = hipMemcpyAsync(host_ids, ids, (size_t)batch * k * 4, hipMemcpyDeviceToHost, s);
     if (e != hipSuccess) return e;
-    return hipMemcpyAsync(host_probs, probabilities, (size_t)batch * k * 4, hipMemcpyDeviceToHost, s);
+    e = hipMemcpyAsync(host_probs, probabilities, (size_t)batch * k * 4, hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) return e;
+    // this kernel only sets the shared flag: it stands for every token
+    return hipMemcpyAsync(host_bad, non_finite, 4, hipMemcpyDeviceToHost, s);
+}
+
+__global__ void fill_u32_kernel(uint32_t *p, uint32_t n, uint32_t value) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = value;
+}
+
+hipError_t launch_fill_u32(hipStream_t s, uint32_t *p, uint32_t n, uint32_t value) {
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((n + 255) / 256 < 64 ? (n + 255) / 256 : 64), dim3(256), 0, s, p, n,
+                       value);
+    return hipGetLastError();
 }
 
 hipError_t launch_rms_norm(hipStream_t s, const float *in, uint32_t batch, uint32_t n,

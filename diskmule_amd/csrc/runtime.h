@@ -66,6 +66,7 @@ struct dmhip_ctx {
     uint32_t *argmax_index = nullptr;         // device
     uint32_t *flags = nullptr;                // device: [0] non-finite
     bool argmax_pending = false;
+    bool router_pending = false;  // a dmhip_router_top_k_device awaits dmhip_router_result
     uint32_t *argmax_user_index = nullptr;
     // Measurement: start/stop event pairs around the dominant kernels, and
     // a pool of idle events (created without a system-scope fence) reused

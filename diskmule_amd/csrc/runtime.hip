@@ -771,9 +771,24 @@ int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_
     DM_CHECK(count_u32(hidden));
     if (batch == 0) return DMHIP_OK;
     DM_CHECK(set_device(ctx));
+    DM_HIP(launch_fill_u32(ctx->stream, ctx->flags, 1, 0));
+    ctx->router_pending = true;
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                (uint32_t)k, (uint32_t)batch, x, logits, ids, probabilities,
                                ctx->flags, nullptr, nullptr, batch <= kRouterTickets ? ctx->router_tickets : nullptr));
+    return DMHIP_OK;
+}
+
+int dmhip_router_result(dmhip_ctx *ctx) {
+    DM_REQUIRE(ctx);
+    if (!ctx->router_pending)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "no router_top_k is pending on this context");
+    DM_CHECK(set_device(ctx));
+    uint32_t flag = 0;
+    DM_HIP(hipMemcpyAsync(&flag, ctx->flags, 4, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    ctx->router_pending = false;
+    if (flag) return fail(DMHIP_ERR_NON_FINITE, "top-k softmax received a non-finite value");
     return DMHIP_OK;
 }
 
@@ -813,6 +828,65 @@ int dmhip_copy_device(dmhip_ctx *ctx, void *dst, const void *src, size_t n) {
     DM_REQUIRE(src);
     DM_CHECK(set_device(ctx));
     DM_HIP(launch_copy_bytes(ctx->stream, dst, src, n));
+    return DMHIP_OK;
+}
+
+int dmhip_probe_empty(dmhip_ctx *ctx, uint32_t workgroups, uint32_t threads) {
+    DM_REQUIRE(ctx);
+    if (workgroups == 0 || threads == 0 || threads > 1024 || threads % 64)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "probe grid %u x %u is not a launchable shape", workgroups,
+                    threads);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_probe_empty(ctx->stream, workgroups, threads));
+    return DMHIP_OK;
+}
+
+int dmhip_probe_read(dmhip_ctx *ctx, const void *src, size_t n) {
+    DM_REQUIRE(ctx);
+    if (n == 0) return DMHIP_OK;
+    DM_REQUIRE(src);
+    if (((uintptr_t)src & 15u) || (n & 15u))
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "probe_read needs a 16-byte aligned source and length");
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_probe_read(ctx->stream, src, n, ctx->flags + 1));
+    return DMHIP_OK;
+}
+
+int dmhip_matvec_phase_trace(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, const void *weights,
+                             const float *x, float *y, uint64_t *stamps, size_t capacity, size_t *workgroups) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(weights);
+    DM_REQUIRE(x);
+    DM_REQUIRE(y);
+    DM_REQUIRE(stamps);
+    DM_REQUIRE(workgroups);
+    DM_CHECK(validate_device_matvec(type, rows, columns, 1));
+    if (!qmv_supported(type, rows, columns, weights, 1) || !qmv8_supported(type, rows, columns, 1))
+        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "the int8 decode GEMV does not take %s %zu x %zu",
+                    type_name(type), rows, columns);
+    if (capacity / 4 < (rows + 15) / 16)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "phase trace needs %zu stamps, got room for %zu",
+                    4 * ((rows + 15) / 16), capacity);
+    DM_CHECK(set_device(ctx));
+    uint32_t count = 0;
+    DM_HIP(launch_qmv8(ctx, type, (uint32_t)rows, (uint32_t)columns, weights, 1, x, y, nullptr, &count,
+                       ArgmaxFinish{nullptr, nullptr, nullptr, nullptr}, stamps));
+    *workgroups = count;
+    return DMHIP_OK;
+}
+
+int dmhip_matvec_valu_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, const void *weights,
+                             const float *x, float *y) {
+    DM_REQUIRE(ctx);
+    DM_REQUIRE(weights);
+    DM_REQUIRE(x);
+    DM_REQUIRE(y);
+    DM_CHECK(validate_device_matvec(type, rows, columns, 1));
+    if (!qmv_valu_supported(type, rows, columns, weights, x, 1))
+        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "the VALU decode GEMV does not take %s %zu x %zu",
+                    type_name(type), rows, columns);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_qmv_valu(ctx, type, (uint32_t)rows, (uint32_t)columns, weights, x, y));
     return DMHIP_OK;
 }
 

@@ -39,9 +39,10 @@ EXPORTED_SYMBOLS = [
     "dmhip_matvec_mapped", "dmhip_matvec_owned", "dmhip_dequantize", "dmhip_matvec_device",
     "dmhip_matvec_batch_device", "dmhip_matvec_argmax_device", "dmhip_argmax_result", "dmhip_rms_norm_device",
     "dmhip_silu_mul_device", "dmhip_ffn_workspace_bytes", "dmhip_ffn_device",
-    "dmhip_router_top_k_device", "dmhip_gemm_workspace_bytes", "dmhip_gemm_device",
+    "dmhip_router_top_k_device", "dmhip_router_result", "dmhip_gemm_workspace_bytes", "dmhip_gemm_device",
     "dmhip_event_record", "dmhip_event_elapsed_ms", "dmhip_event_free",
     "dmhip_kernel_timing_enable", "dmhip_kernel_timing_read", "dmhip_copy_device",
+    "dmhip_probe_empty", "dmhip_probe_read", "dmhip_matvec_phase_trace", "dmhip_matvec_valu_device",
     "dmhip_expert_cache_new", "dmhip_expert_cache_free", "dmhip_expert_cache_stats_get",
     "dmhip_expert_cache_slots_per_layer", "dmhip_expert_acquire", "dmhip_expert_release",
     "dmhip_moe_layer",
@@ -123,12 +124,13 @@ def load_library() -> ctypes.CDLL:
         "dmhip_argmax_result": ([_vp, _szp], ctypes.c_int),
         "dmhip_rms_norm_device": ([_vp, _sz, _sz, _vp, _vp, ctypes.c_float, _vp], ctypes.c_int),
         "dmhip_silu_mul_device": ([_vp, _sz, _vp, _vp, _vp], ctypes.c_int),
-        "dmhip_ffn_workspace_bytes": ([_sz, _sz], _sz),
+        "dmhip_ffn_workspace_bytes": ([_sz, _sz, _sz], _sz),
         "dmhip_ffn_device": ([_vp, _sz, _sz, _sz, _u32, _vp, _u32, _vp, _u32, _vp, ctypes.c_float,
-                              _vp, _vp, _vp], ctypes.c_int),
+                              _vp, _vp, _vp, _sz], ctypes.c_int),
         "dmhip_router_top_k_device": ([_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_router_result": ([_vp], ctypes.c_int),
         "dmhip_gemm_workspace_bytes": ([_sz, _sz], _sz),
-        "dmhip_gemm_device": ([_vp, _u32, _sz, _sz, _sz, _vp, _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_gemm_device": ([_vp, _u32, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _sz], ctypes.c_int),
         "dmhip_event_record": ([_vp, ctypes.POINTER(_vp)], ctypes.c_int),
         "dmhip_event_elapsed_ms": ([_vp, _vp, ctypes.POINTER(ctypes.c_float)], ctypes.c_int),
         "dmhip_event_free": ([_vp], None),
@@ -136,6 +138,10 @@ def load_library() -> ctypes.CDLL:
         "dmhip_kernel_timing_read": ([_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint64)],
                                      ctypes.c_int),
         "dmhip_copy_device": ([_vp, _vp, _vp, _sz], ctypes.c_int),
+        "dmhip_probe_empty": ([_vp, _u32, _u32], ctypes.c_int),
+        "dmhip_probe_read": ([_vp, _vp, _sz], ctypes.c_int),
+        "dmhip_matvec_phase_trace": ([_vp, _u32, _sz, _sz, _vp, _vp, _vp, _vp, _sz, _szp], ctypes.c_int),
+        "dmhip_matvec_valu_device": ([_vp, _u32, _sz, _sz, _vp, _vp, _vp], ctypes.c_int),
         "dmhip_expert_cache_new": ([_vp, _vp, _sz, ctypes.POINTER(_Layout), _sz, _sz, ctypes.POINTER(_vp)],
                                    ctypes.c_int),
         "dmhip_expert_cache_free": ([_vp], None),
@@ -369,24 +375,28 @@ class HipContext:
     def silu_mul_device(self, count, g_ptr, u_ptr, out_ptr) -> None:
         _check(load_library().dmhip_silu_mul_device(self._h, count, g_ptr, u_ptr, out_ptr))
 
-    def ffn_workspace_bytes(self, batch, ffn) -> int:
-        return int(load_library().dmhip_ffn_workspace_bytes(batch, ffn))
+    def ffn_workspace_bytes(self, batch, hidden, ffn) -> int:
+        return int(load_library().dmhip_ffn_workspace_bytes(batch, hidden, ffn))
 
     def ffn_device(self, batch, hidden, ffn, gate_type, gate_ptr, up_type, up_ptr, down_type,
-                   down_ptr, eps, h_ptr, y_ptr, ws_ptr) -> None:
+                   down_ptr, eps, h_ptr, y_ptr, ws_ptr, ws_len) -> None:
         _check(load_library().dmhip_ffn_device(self._h, batch, hidden, ffn, gate_type, gate_ptr, up_type,
-                                               up_ptr, down_type, down_ptr, eps, h_ptr, y_ptr, ws_ptr))
+                                               up_ptr, down_type, down_ptr, eps, h_ptr, y_ptr, ws_ptr, ws_len))
 
     def router_top_k_device(self, batch, hidden, experts, k, router_ptr, x_ptr, logits_ptr, ids_ptr,
                             probs_ptr) -> None:
         _check(load_library().dmhip_router_top_k_device(self._h, batch, hidden, experts, k, router_ptr,
                                                         x_ptr, logits_ptr, ids_ptr, probs_ptr))
 
+    def router_result(self) -> None:
+        """Raises NonFinite when the last router_top_k_device saw a non-finite logit."""
+        _check(load_library().dmhip_router_result(self._h))
+
     def gemm_workspace_bytes(self, m, k) -> int:
         return int(load_library().dmhip_gemm_workspace_bytes(m, k))
 
-    def gemm_device(self, kind, m, n, k, a_ptr, w_ptr, c_ptr, ws_ptr) -> None:
-        _check(load_library().dmhip_gemm_device(self._h, kind, m, n, k, a_ptr, w_ptr, c_ptr, ws_ptr))
+    def gemm_device(self, kind, m, n, k, a_ptr, w_ptr, c_ptr, ws_ptr, ws_len) -> None:
+        _check(load_library().dmhip_gemm_device(self._h, kind, m, n, k, a_ptr, w_ptr, c_ptr, ws_ptr, ws_len))
 
     def event_record(self) -> int:
         ev = _vp()
@@ -410,6 +420,28 @@ class HipContext:
 
     def copy_device(self, dst_ptr: int, src_ptr: int, nbytes: int) -> None:
         _check(load_library().dmhip_copy_device(self._h, dst_ptr, src_ptr, nbytes))
+
+    # -- measurement hooks ----------------------------------------------------
+    def probe_empty(self, workgroups: int, threads: int) -> None:
+        _check(load_library().dmhip_probe_empty(self._h, workgroups, threads))
+
+    def probe_read(self, src_ptr: int, nbytes: int) -> None:
+        _check(load_library().dmhip_probe_read(self._h, src_ptr, nbytes))
+
+    def matvec_phase_trace(self, kind, rows, columns, w_ptr, x_ptr, y_ptr) -> np.ndarray:
+        """One int8 GEMV launch with per-workgroup s_memrealtime stamps (100 MHz):
+        returns int64 [workgroups, 4] = entry, records built, first weights, end."""
+        cap = 4 * ((rows + 15) // 16)
+        buf = self.new_owned_buffer(8 * cap)
+        wg = ctypes.c_size_t()
+        _check(load_library().dmhip_matvec_phase_trace(self._h, kind, rows, columns, w_ptr, x_ptr, y_ptr,
+                                                       buf.device_ptr, cap, ctypes.byref(wg)))
+        stamps = buf.read(0, 8 * 4 * wg.value, np.uint64).reshape(wg.value, 4).astype(np.int64)
+        buf.free()
+        return stamps
+
+    def matvec_valu_device(self, kind, rows, columns, w_ptr, x_ptr, y_ptr) -> None:
+        _check(load_library().dmhip_matvec_valu_device(self._h, kind, rows, columns, w_ptr, x_ptr, y_ptr))
 
     @staticmethod
     def event_free(ev: int) -> None:

@@ -215,12 +215,14 @@ int dmhip_silu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const
 
 /* Dense gated FFN at decode for `batch` tokens (src/qwen35/cpu.rs:415-427):
    y = down(silu(gate(n)) * up(n)) with n = rms_norm(h, eps), unit weight.
-   `workspace` holds at least dmhip_ffn_workspace_bytes(batch, ffn) bytes. */
-size_t dmhip_ffn_workspace_bytes(size_t batch, size_t ffn);
+   `workspace` is device memory of workspace_len bytes, at least
+   dmhip_ffn_workspace_bytes(batch, hidden, ffn); a shorter one is rejected
+   (InvalidArgument) before any work. */
+size_t dmhip_ffn_workspace_bytes(size_t batch, size_t hidden, size_t ffn);
 int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn,
                      uint32_t gate_type, const void *gate, uint32_t up_type, const void *up,
                      uint32_t down_type, const void *down, float epsilon, const float *h,
-                     float *y, void *workspace);
+                     float *y, void *workspace, size_t workspace_len);
 
 /* Router for `batch` tokens: logits = bf16 router rows . x (exact sequential
    fold, src/cpu.rs:391-394), then top_k_softmax per token
@@ -228,12 +230,20 @@ int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn,
 int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t experts,
                               size_t k, const uint16_t *router_bf16, const float *x,
                               float *logits, uint32_t *ids, float *probabilities);
+/* Waits for the last dmhip_router_top_k_device and returns NonFinite when
+   any token's logits held a non-finite value (top_k_softmax rejects them,
+   src/cpu.rs:240-245); the ids and probabilities of such a call are not
+   meaningful. */
+int dmhip_router_result(dmhip_ctx *ctx);
 
 /* Prefill GEMM: C[m][n] = sum_k A[m][k] * W[n][k], A bf16 [m][k] row-major,
-   W `n` encoded rows of `k` columns, C f32 [m][n]. */
+   W `n` encoded rows of `k` columns, C f32 [m][n].  `workspace` is device
+   memory of workspace_len bytes, at least dmhip_gemm_workspace_bytes(m, k);
+   a shorter one is rejected (InvalidArgument) before any work. */
 size_t dmhip_gemm_workspace_bytes(size_t m, size_t k);
 int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t m, size_t n, size_t k,
-                      const uint16_t *a_bf16, const void *weights, float *c, void *workspace);
+                      const uint16_t *a_bf16, const void *weights, float *c, void *workspace,
+                      size_t workspace_len);
 
 /* Events on the compute stream, for timing. */
 int dmhip_event_record(dmhip_ctx *ctx, void **event);
@@ -251,6 +261,34 @@ int dmhip_kernel_timing_read(dmhip_ctx *ctx, double *total_ms, uint64_t *launche
 /* Stream-ordered device-to-device copy by a plain streaming kernel (also the
    calibration kernel for HBM byte counters). */
 int dmhip_copy_device(dmhip_ctx *ctx, void *dst, const void *src, size_t n);
+
+/* Launch-floor probes (measurement hooks, no counterpart in the reference):
+   an empty kernel of `workgroups` x `threads` (threads a multiple of 64,
+   at most 1024), and a kernel that reads the n bytes at `src` (a 16-byte
+   aligned device address; n a multiple of 16) with 16-byte loads, four per
+   lane, and keeps nothing.  Their durations bound what a GEMV over the same
+   bytes can reach. */
+int dmhip_probe_empty(dmhip_ctx *ctx, uint32_t workgroups, uint32_t threads);
+int dmhip_probe_read(dmhip_ctx *ctx, const void *src, size_t n);
+
+/* The batch-1 int8 decode GEMV that dmhip_matvec_device runs for Q4_K, Q6_K
+   and Q8_0 rows, with phase stamps (measurement hook): thread 0 of workgroup
+   i writes four values of the 100 MHz s_memrealtime counter to
+   stamps[4i .. 4i+3]: entry, activation records built, first weight group
+   landed, end.  `capacity` counts uint64 elements and must be at least
+   4 * ceil(rows / 16); *workgroups receives the number of workgroups. */
+int dmhip_matvec_phase_trace(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
+                             const void *weights, const float *x, float *y, uint64_t *stamps,
+                             size_t capacity, size_t *workgroups);
+
+/* The VALU form of the batch-1 Q4_K decode GEMV (measurement hook): per
+   weight a v_cvt_f32_ubyte of the masked nibble and an fma, activations held
+   in registers, cross-lane butterflies for the row sums; rows of 1, 2, 4, 8
+   or 16 super-blocks, 16-byte aligned weights and x.  Measured slower than
+   the int8-MFMA kernel at every shape tried, so dmhip_matvec_device does not
+   choose it. */
+int dmhip_matvec_valu_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
+                             const void *weights, const float *x, float *y);
 
 /* ---------------------------------------------------------------------- */
 /* Routed-expert residency (src/expert.rs)                                 */
@@ -311,6 +349,7 @@ int dmhip_expert_release(dmhip_expert_cache *cache, size_t layer, size_t slot);
    order.  Expert gate_up rows are [gate; up] (2*width rows of `hidden`
    columns), down rows are `hidden` rows of `width` columns.  x and y are
    device [batch][hidden]; ids/probabilities receive host [batch][k].
+   Non-finite router logits return NonFinite before any expert is acquired.
    The call returns after the layer finished. */
 int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *cache, size_t layer, size_t batch,
                     size_t hidden, size_t width, size_t experts, size_t k,

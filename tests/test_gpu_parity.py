@@ -166,6 +166,33 @@ def test_decode_gemv_matches_oracle(ctx, kind, rows, cols, cfg):
     print(f"  rel_err={e:.2e} cosine={c:.9f}", flush=True)
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (1000, 2048), (37, 256), (65, 1024), (12288, 4096)])
+def test_valu_gemv_matches_oracle(ctx, rows, cols):
+    """The VALU form of the batch-1 Q4_K GEMV (a measurement hook): row counts
+    that end mid-pass, 1..16 blocks per row."""
+    w = synth.quantized_matrix(Q4_K, rows, cols, synth.weight_seed(120, rows))
+    x = synth.normal(synth.activation_seed(120, cols), cols)
+    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, rows * 4)
+    ctx.matvec_valu_device(Q4_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr)
+    assert_close(yb.read(0, rows * 4, np.float32), capi.matvec(Q4_K, rows, cols, w, x), f"VALU {rows}x{cols}")
+    with pytest.raises(HipError) as e:
+        ctx.matvec_valu_device(Q6_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr)
+    assert e.value.variant == "UnsupportedTensorType"
+
+
+def test_phase_trace_hook_runs_the_gemv(ctx):
+    """The phase-stamped launch computes the same GEMV, and every workgroup's
+    stamps are in phase order."""
+    rows, cols = 4096, 4096
+    w = synth.quantized_matrix(Q4_K, rows, cols, synth.weight_seed(1))
+    x = synth.normal(synth.activation_seed(1), cols)
+    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, rows * 4)
+    st = ctx.matvec_phase_trace(Q4_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr)
+    assert st.shape[0] >= 1 and st.shape[1] == 4
+    assert (np.diff(st, axis=1) >= 0).all()
+    assert_close(yb.read(0, rows * 4, np.float32), capi.matvec(Q4_K, rows, cols, w, x), "traced C1")
+
+
 @pytest.mark.parametrize("batch", [2, 4, 8, 9, 16])
 def test_batched_gemv_matches_oracle(ctx, batch):
     rows, cols = 1000, 2048
@@ -331,7 +358,7 @@ def test_prefill_gemm_other_types_take_the_tokenwise_path(ctx, kind):
     want = capi.gemm_tokenwise(kind, m, n, k, a, w)
     ab, wb, cb = dev(ctx, a), dev(ctx, w), dev_out(ctx, m * n * 4)
     ws = dev_out(ctx, ctx.gemm_workspace_bytes(m, k))
-    ctx.gemm_device(kind, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr)
+    ctx.gemm_device(kind, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr, len(ws))
     got = cb.read(0, m * n * 4, np.float32).reshape(m, n)
     for r in range(m):
         assert_close(got[r], want[r], f"type {kind} token {r}")
@@ -430,13 +457,45 @@ def test_dense_ffn_matches_oracle(ctx, batch):
     want = capi.dense_ffn(batch, hidden, ffn, Q4_K, g, Q4_K, u, Q6_K, d, h)
     gb, ub, db, hb = dev(ctx, g), dev(ctx, u), dev(ctx, d), dev(ctx, h)
     yb = dev_out(ctx, batch * hidden * 4)
-    ws = dev_out(ctx, ctx.ffn_workspace_bytes(batch, ffn))
+    ws = dev_out(ctx, ctx.ffn_workspace_bytes(batch, hidden, ffn))
     ctx.ffn_device(batch, hidden, ffn, Q4_K, gb.device_ptr, Q4_K, ub.device_ptr, Q6_K, db.device_ptr,
-                   1e-6, hb.device_ptr, yb.device_ptr, ws.device_ptr)
+                   1e-6, hb.device_ptr, yb.device_ptr, ws.device_ptr, len(ws))
     got = yb.read(0, batch * hidden * 4, np.float32).reshape(batch, hidden)
     for b in range(batch):
         e, c = assert_close(got[b], want[b], f"C3 token {b}")
     print(f"  rel_err={e:.2e} cosine={c:.9f}", flush=True)
+
+
+@pytest.mark.parametrize("gu_type,dn_type,batch", [(Q4_K, Q6_K, 2), (Q8_0, Q8_0, 2), (Q8_0, Q6_K, 1),
+                                                    (Q4_K, Q4_K, 5)])
+def test_ffn_wide_hidden_stays_inside_its_workspace(ctx, gu_type, dn_type, batch):
+    """hidden = 8 * ffn: the workspace is allocated at exactly the advertised
+    size with a guard region after it, which must come back unchanged; the
+    fused (Q4_K pairs) and unfused (Q8_0 pairs) paths both match the oracle,
+    and a workspace one byte short is rejected."""
+    hidden, ffn = 2048, 256
+    g = synth.quantized_matrix(gu_type, ffn, hidden, synth.weight_seed(33, 0))
+    u = synth.quantized_matrix(gu_type, ffn, hidden, synth.weight_seed(33, 1))
+    d = synth.quantized_matrix(dn_type, hidden, ffn, synth.weight_seed(33, 2))
+    h = synth.normal(synth.activation_seed(33, batch), batch * hidden).reshape(batch, hidden)
+    want = capi.dense_ffn(batch, hidden, ffn, gu_type, g, gu_type, u, dn_type, d, h)
+    gb, ub, db, hb = dev(ctx, g), dev(ctx, u), dev(ctx, d), dev(ctx, h)
+    yb = dev_out(ctx, batch * hidden * 4)
+    need = ctx.ffn_workspace_bytes(batch, hidden, ffn)
+    assert need >= batch * (hidden + 3 * ffn) * 4
+    guard = 4096
+    ws = dev_out(ctx, need + guard)
+    ws.write(need, np.full(guard, 0xA5, np.uint8))
+    ctx.ffn_device(batch, hidden, ffn, gu_type, gb.device_ptr, gu_type, ub.device_ptr, dn_type, db.device_ptr,
+                   1e-6, hb.device_ptr, yb.device_ptr, ws.device_ptr, need)
+    got = yb.read(0, batch * hidden * 4, np.float32).reshape(batch, hidden)
+    for b in range(batch):
+        assert_close(got[b], want[b], f"token {b}")
+    assert (ws.read(need, guard) == 0xA5).all(), "FFN wrote past its workspace"
+    with pytest.raises(HipError) as e:
+        ctx.ffn_device(batch, hidden, ffn, gu_type, gb.device_ptr, gu_type, ub.device_ptr, dn_type,
+                       db.device_ptr, 1e-6, hb.device_ptr, yb.device_ptr, ws.device_ptr, need - 1)
+    assert e.value.variant == "InvalidArgument"
 
 
 # ---- config 4: routed experts ------------------------------------------------
@@ -477,6 +536,65 @@ def test_router_top_k_is_bit_exact(ctx, batch, hidden, experts, k):
         top = capi.top_k_softmax(want, k)
         assert ids[t].tolist() == [e for e, _ in top]
         assert np.allclose(probs[t], [p for _, p in top], rtol=1e-6)
+
+
+def test_router_rejects_non_finite_logits(ctx):
+    """top_k_softmax rejects non-finite logits (src/cpu.rs:240-245): an Inf in
+    a token makes dmhip_router_result report NonFinite, and the next clean
+    call reports nothing (the flag is cleared per call)."""
+    batch, hidden, experts, k = 3, 2048, 128, 8
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(6, 1), experts * hidden) * np.float32(0.02))
+    x = synth.normal(synth.activation_seed(6, 1), batch * hidden).reshape(batch, hidden)
+    rb = dev(ctx, router)
+    lb, ib, pb = dev_out(ctx, batch * experts * 4), dev_out(ctx, batch * k * 4), dev_out(ctx, batch * k * 4)
+    bad = x.copy()
+    bad[1, 77] = np.inf
+    xb = dev(ctx, bad)
+    ctx.router_top_k_device(batch, hidden, experts, k, rb.device_ptr, xb.device_ptr, lb.device_ptr, ib.device_ptr,
+                            pb.device_ptr)
+    with pytest.raises(HipError) as e:
+        ctx.router_result()
+    assert e.value.variant == "NonFinite"
+    xb = dev(ctx, x)
+    ctx.router_top_k_device(batch, hidden, experts, k, rb.device_ptr, xb.device_ptr, lb.device_ptr, ib.device_ptr,
+                            pb.device_ptr)
+    ctx.router_result()
+    ids = ib.read(0, batch * k * 4, np.uint32).reshape(batch, k)
+    for t in range(batch):
+        want = capi.top_k_softmax(capi.matvec_bf16(experts, hidden, router, x[t]), k)
+        assert ids[t].tolist() == [i for i, _ in want]
+
+
+@pytest.mark.parametrize("experts,hidden", [(128, 2048), (12, 1024), (300, 512)])
+def test_moe_layer_rejects_non_finite_router_input(ctx, experts, hidden):
+    """A non-finite token makes the layer return NonFinite before any expert
+    is acquired (no cache counters move), for the expert-parallel router,
+    the one-workgroup router (< 16 experts) and the fallback (> 256); a clean
+    call afterwards succeeds."""
+    width, k, batch = 256, 4, 2
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(44, experts), experts * hidden) * np.float32(0.02))
+    gu_bytes, dn_bytes = 2 * width * synth.row_bytes(Q4_K, hidden), hidden * synth.row_bytes(Q6_K, width)
+    gu = synth.quantized_matrix(Q4_K, experts * 2 * width, hidden, synth.weight_seed(44, 1))
+    dn = synth.quantized_matrix(Q6_K, experts * hidden, width, synth.weight_seed(44, 2))
+    src = np.concatenate([gu, dn])
+    cache = ExpertCache(ctx, src, [ExpertLayerLayout(experts, 0, gu_bytes, gu.size, dn_bytes)], 4)
+    x = synth.normal(synth.activation_seed(44, experts), batch * hidden).reshape(batch, hidden)
+    bad = x.copy()
+    bad[batch - 1, 3] = np.nan
+    rb, yb = dev(ctx, router), dev_out(ctx, batch * hidden * 4)
+    with pytest.raises(HipError) as e:
+        ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                      dev(ctx, bad).device_ptr, yb.device_ptr)
+    assert e.value.variant == "NonFinite"
+    assert cache.stats()["misses"] == 0 and cache.stats()["hits"] == 0
+    ids, _ = ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                           dev(ctx, x).device_ptr, yb.device_ptr)
+    sel, _, want = capi.moe_layer(batch, hidden, width, experts, k, router, Q4_K, gu, Q6_K, dn, x)
+    assert np.array_equal(ids, sel)
+    got = yb.read(0, batch * hidden * 4, np.float32).reshape(batch, hidden)
+    for t in range(batch):
+        assert_close(got[t], want[t], f"token {t}")
+    cache.free()
 
 
 def test_expert_cache_known_answer(ctx, golden):
@@ -555,7 +673,7 @@ def test_prefill_gemm_matches_oracle(ctx, n):
     want = capi.gemm_tokenwise(Q4_K, mm, n, k, a[: mm * k], w)
     ab, wb, cb = dev(ctx, a), dev(ctx, w), dev_out(ctx, m * n * 4)
     ws = dev_out(ctx, ctx.gemm_workspace_bytes(m, k))
-    ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr)
+    ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr, len(ws))
     got = cb.read(0, m * n * 4, np.float32).reshape(m, n)[:mm]
     worst = 0.0
     for r in range(mm):
@@ -575,7 +693,7 @@ def test_prefill_gemm_ragged_shapes(ctx, m, n, k):
     want = capi.gemm_tokenwise(Q4_K, m, n, k, a, w)
     ab, wb, cb = dev(ctx, a), dev(ctx, w), dev_out(ctx, m * n * 4)
     ws = dev_out(ctx, ctx.gemm_workspace_bytes(m, k))
-    ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr)
+    ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr, len(ws))
     got = cb.read(0, m * n * 4, np.float32).reshape(m, n)
     for r in range(m):
         assert_close(got[r], want[r], f"C5 ragged token {r}")

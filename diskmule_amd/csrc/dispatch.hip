@@ -78,23 +78,21 @@ int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn, ui
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "ffn arguments must not be null");
     if (batch < 1 || batch > 16)
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "batch %zu is outside 1..=16", batch);
-    if (hidden == 0 || ffn == 0) return fail(DMHIP_ERR_EMPTY_INPUT, "FFN requires a non-empty input");
+    if (hidden == 0 || ffn == 0) return fail_empty("FFN");
     const size_t need = dmhip_ffn_workspace_bytes(batch, hidden, ffn);
     if (need == 0 || workspace_len < need)
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "FFN workspace holds %zu bytes; the shape needs %zu",
                     workspace_len, need);
     if (!isfinite(epsilon) || epsilon <= 0.0f)
-        return fail(DMHIP_ERR_INVALID_POSITIVE_PARAMETER, "RMSNorm epsilon requires a finite positive parameter");
+        return fail_positive("RMSNorm epsilon");
     uint64_t rb;
     const uint32_t types[3] = {gate_type, up_type, down_type};
     const size_t cols[3] = {hidden, hidden, ffn};
     for (int i = 0; i < 3; i++) {
         uint32_t t = types[i];
         if (!(t == 0 || t == 1 || t == 6 || t == 8 || t == 12 || t == 14))
-            return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "HIP FFN does not support %s", type_name(t));
-        if (!row_byte_len(t, cols[i], &rb))
-            return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT, "%s row of %zu values is not whole blocks",
-                        type_name(t), cols[i]);
+            return fail_unsupported(t, "HIP FFN");
+        if (!row_byte_len(t, cols[i], &rb)) return fail_element_count(t, cols[i]);
     }
     if (hidden > 0xffffffffull || ffn > 0xffffffffull)
         return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "HIP vector length exceeds the 32-bit kernel limit");

@@ -4,17 +4,29 @@
 // the reference's (clock per layer, hit updates last_used, a miss evicts the
 // unpinned slot with the smallest (is_some, last_used, index)), and the
 // positional reads become asynchronous host->HBM copies on the context's
-// two upload streams (alternating by expert).  Ordering is by events, never
-// by host waits:
+// two upload streams (alternating by expert).  The expert bytes come from
+// host memory the caller provides (ideally pinned), or from a file: then a
+// miss reads gate_up and down with two parallel positional reads into one
+// entry of a small pinned staging ring (src/expert.rs:203-215, :241-256), and
+// the ring bounds the host memory the cache uses.
+//
+// Ordering is by events, never by device-wide waits:
 //   * an upload into a slot first waits for the `released` event recorded
-//     after the last compute work that read the slot;
+//     after the last compute work that read the slot, and for the `ready`
+//     event of the slot's previous upload (which may be on the other upload
+//     stream);
 //   * compute work that uses a freshly loaded slot waits for its `ready`
-//     event (the end of its upload).
+//     event (the end of its upload);
+//   * a staging entry is refilled only after the host has waited for the
+//     copy out of it (`done`).
 #include "runtime.h"
 
+#include <errno.h>
 #include <string.h>
+#include <unistd.h>
 
 #include <chrono>
+#include <thread>
 #include <vector>
 
 #include "dm_qmv.h"
@@ -53,10 +65,18 @@ struct Slot {
     bool has = false;
     size_t expert = 0;
     uint64_t last_used = 0;
-    bool pinned = false;
-    void *gate_up = nullptr;
+    // Holders through dmhip_expert_acquire; a slot with pins is never a
+    // victim.  (The MoE layer's own acquires do not pin: it never evicts a
+    // slot its open phase uses.)
+    uint32_t pins = 0;
+    dmhip_buf *gate_up_buf = nullptr;  // cache-owned, len = gate_up_bytes
+    dmhip_buf *down_buf = nullptr;     // cache-owned, len = down_bytes
+    void *gate_up = nullptr;           // their device addresses
     void *down = nullptr;
-    hipEvent_t ready = nullptr;     // end of the last upload into the slot
+    hipEvent_t upload_start = nullptr;  // start of the last upload (memory source: timed)
+    hipEvent_t ready = nullptr;         // end of the last upload into the slot
+    bool uploaded = false;              // ready has been recorded
+    bool timing_pending = false;        // upload_start..ready not yet added to io_wait
     // End of the last compute that read it: an event of the cache's ring,
     // shared by the slots released together.  Once the ring wraps the event
     // may be recorded again later on the same stream, which only makes a
@@ -71,19 +91,31 @@ struct Layer {
     uint64_t clock = 0;
 };
 
+// One pinned host buffer of the file source's staging ring.
+struct Staging {
+    uint8_t *host = nullptr;
+    hipEvent_t done = nullptr;  // end of the copies out of it
+    bool busy = false;          // done has been recorded
+};
+
 }  // namespace dm
 
 struct dmhip_expert_cache {
     dmhip_ctx *ctx = nullptr;
     int device = 0;
+    // Memory source (fd < 0) or file source.
     const uint8_t *source = nullptr;
     size_t source_len = 0;
+    int fd = -1;
+    std::vector<dm::Staging> staging;
+    size_t next_staging = 0;
     std::vector<dm::Layer> layers;
     dmhip_expert_cache_stats stats = {};
     // MoE workspace (device): grows on demand.
     dm::Scratch work;
     // Pinned host copy of the router's selection (ids, then probabilities;
-    // kSelectionPairs pairs), written by the router kernel itself.
+    // kSelectionPairs pairs, then one non-finite flag per token), written by
+    // the router kernel itself.
     uint8_t *host_selection = nullptr;
     // Release events, used round-robin: one record per released group.
     std::vector<hipEvent_t> release_events;
@@ -94,20 +126,105 @@ namespace {
 constexpr size_t kSelectionPairs = 16 * dm::kMaxTopK;  // batch <= 16
 constexpr size_t kSelectionBytes = kSelectionPairs * 8 + 16 * 4;  // ids, probabilities, per-token flags
 constexpr size_t kReleaseEvents = 64;
+constexpr size_t kStagingEntries = 4;  // file source: experts in flight from storage
 }
 
 using namespace dm;
 
 namespace {
 
+// read_exact_at (src/expert.rs:241-256): the whole range or an error; an
+// interrupted read is retried, a zero-byte read is an unexpected end of
+// file (error 0).
+int read_exact_at(int fd, uint64_t offset, uint8_t *dst, size_t n) {
+    while (n > 0) {
+        const ssize_t got = pread(fd, dst, n, (off_t)offset);
+        if (got == 0) return 0;
+        if (got < 0) {
+            if (errno == EINTR) continue;
+            return errno ? errno : EIO;
+        }
+        dst += got;
+        n -= (size_t)got;
+        offset += (uint64_t)got;
+    }
+    return -1;  // complete
+}
+
+// Adds the device-measured duration of finished uploads into io_wait (the
+// memory source: the host never waits for its asynchronous copies, so the
+// time the bytes took to arrive is what io_wait reports).  `wait` waits for
+// uploads still in flight.
+void account_uploads(dmhip_expert_cache *c, bool wait) {
+    for (Layer &layer : c->layers)
+        for (Slot &s : layer.slots) {
+            if (!s.timing_pending) continue;
+            if (!wait && hipEventQuery(s.ready) != hipSuccess) continue;
+            float ms = 0.0f;
+            if (hipEventSynchronize(s.ready) == hipSuccess &&
+                hipEventElapsedTime(&ms, s.upload_start, s.ready) == hipSuccess)
+                c->stats.io_wait_ns += (uint64_t)((double)ms * 1e6);
+            s.timing_pending = false;
+        }
+}
+
+// Copies expert `expert` of the layer into slot s on an upload stream that
+// first waits for the slot's last readers and its previous upload.
+int upload_expert(dmhip_expert_cache *c, const dmhip_expert_layer_layout &L, size_t expert, Slot &s) {
+    const size_t gu_bytes = L.gate_up_bytes, dn_bytes = L.down_bytes;
+    const uint64_t gu_off = L.gate_up_offset + (uint64_t)expert * gu_bytes;
+    const uint64_t dn_off = L.down_offset + (uint64_t)expert * dn_bytes;
+    const auto started = std::chrono::steady_clock::now();
+    const uint8_t *gu_src, *dn_src;
+    Staging *entry = nullptr;
+    if (c->fd >= 0) {
+        entry = &c->staging[c->next_staging++ % c->staging.size()];
+        if (entry->busy) DM_HIP(hipEventSynchronize(entry->done));
+        entry->busy = false;
+        // the two reads in parallel, as rayon::join does (src/expert.rs:209-212)
+        int gu_err = -1, dn_err = -1;
+        std::thread reader([&] { gu_err = read_exact_at(c->fd, gu_off, entry->host, gu_bytes); });
+        dn_err = read_exact_at(c->fd, dn_off, entry->host + gu_bytes, dn_bytes);
+        reader.join();
+        if (gu_err >= 0) return fail_io(gu_err);
+        if (dn_err >= 0) return fail_io(dn_err);
+        gu_src = entry->host;
+        dn_src = entry->host + gu_bytes;
+    } else {
+        gu_src = c->source + gu_off;
+        dn_src = c->source + dn_off;
+    }
+    // experts alternate between the two upload streams
+    hipStream_t up = (c->ctx->upload_next++ & 1u) ? c->ctx->upload2 : c->ctx->upload;
+    if (s.released_recorded) DM_HIP(hipStreamWaitEvent(up, s.released, 0));
+    if (s.uploaded) DM_HIP(hipStreamWaitEvent(up, s.ready, 0));
+    if (c->fd < 0) {
+        if (s.timing_pending) account_uploads(c, true);
+        DM_HIP(hipEventRecord(s.upload_start, up));
+    }
+    DM_HIP(hipMemcpyAsync(s.gate_up, gu_src, gu_bytes, hipMemcpyHostToDevice, up));
+    DM_HIP(hipMemcpyAsync(s.down, dn_src, dn_bytes, hipMemcpyHostToDevice, up));
+    DM_HIP(hipEventRecord(s.ready, up));
+    s.uploaded = true;
+    s.timing_pending = c->fd < 0;
+    if (entry) {
+        DM_HIP(hipEventRecord(entry->done, up));
+        entry->busy = true;
+        c->stats.io_wait_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                                   std::chrono::steady_clock::now() - started).count();
+    }
+    DM_HIP(hipStreamWaitEvent(c->ctx->stream, s.ready, 0));
+    return DMHIP_OK;
+}
+
+// ExpertCache::acquire (src/expert.rs:166-229): the slot holding `expert`,
+// or the victim it is loaded into.  Counters as in the reference: a miss
+// counts before its reads, so a failed read leaves misses (and evictions)
+// counted but no reads; the slot then keeps its previous expert.
 int acquire(dmhip_expert_cache *c, size_t layer_index, size_t expert, size_t *slot_out) {
-    if (layer_index >= c->layers.size())
-        return fail(DMHIP_ERR_INVALID_LAYER, "expert cache layer %zu is outside its %zu layers",
-                    layer_index, c->layers.size());
+    if (layer_index >= c->layers.size()) return fail_layer(layer_index, c->layers.size());
     Layer &layer = c->layers[layer_index];
-    if (expert >= layer.layout.expert_count)
-        return fail(DMHIP_ERR_INVALID_EXPERT, "expert %zu is outside layer %zu's %zu experts", expert,
-                    layer_index, layer.layout.expert_count);
+    if (expert >= layer.layout.expert_count) return fail_expert(layer_index, expert, layer.layout.expert_count);
     layer.clock += 1;
     for (size_t i = 0; i < layer.slots.size(); i++) {
         Slot &s = layer.slots[i];
@@ -122,31 +239,17 @@ int acquire(dmhip_expert_cache *c, size_t layer_index, size_t expert, size_t *sl
     size_t victim = SIZE_MAX;
     for (size_t i = 0; i < layer.slots.size(); i++) {
         const Slot &s = layer.slots[i];
-        if (s.pinned) continue;
+        if (s.pins) continue;
         if (victim == SIZE_MAX) { victim = i; continue; }
         const Slot &v = layer.slots[victim];
         if (s.has < v.has || (s.has == v.has && s.last_used < v.last_used)) victim = i;
     }
-    if (victim == SIZE_MAX)
-        return fail(DMHIP_ERR_ALL_SLOTS_PINNED, "all expert slots in layer %zu are pinned by in-flight work",
-                    layer_index);
+    if (victim == SIZE_MAX) return fail_pinned(layer_index);
     Slot &s = layer.slots[victim];
     if (s.has) c->stats.evictions += 1;
-    const auto started = std::chrono::steady_clock::now();
-    const size_t gu_bytes = layer.layout.gate_up_bytes, dn_bytes = layer.layout.down_bytes;
-    const uint8_t *gu_src = c->source + layer.layout.gate_up_offset + expert * gu_bytes;
-    const uint8_t *dn_src = c->source + layer.layout.down_offset + expert * dn_bytes;
-    // experts alternate between the two upload streams
-    hipStream_t up = (c->ctx->upload_next++ & 1u) ? c->ctx->upload2 : c->ctx->upload;
-    if (s.released_recorded) DM_HIP(hipStreamWaitEvent(up, s.released, 0));
-    DM_HIP(hipMemcpyAsync(s.gate_up, gu_src, gu_bytes, hipMemcpyHostToDevice, up));
-    DM_HIP(hipMemcpyAsync(s.down, dn_src, dn_bytes, hipMemcpyHostToDevice, up));
-    DM_HIP(hipEventRecord(s.ready, up));
-    DM_HIP(hipStreamWaitEvent(c->ctx->stream, s.ready, 0));
-    c->stats.io_wait_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
-                               std::chrono::steady_clock::now() - started).count();
+    DM_CHECK_STATUS(upload_expert(c, layer.layout, expert, s));
     c->stats.reads += 2;
-    c->stats.bytes_read += gu_bytes + dn_bytes;
+    c->stats.bytes_read += layer.layout.gate_up_bytes + layer.layout.down_bytes;
     s.has = true;
     s.expert = expert;
     s.last_used = layer.clock;
@@ -154,21 +257,118 @@ int acquire(dmhip_expert_cache *c, size_t layer_index, size_t expert, size_t *sl
     return DMHIP_OK;
 }
 
-// Unpins `count` slots of a layer after the compute work enqueued so far,
-// with one event record for all of them.
-int release_slots(dmhip_expert_cache *c, size_t layer, const size_t *slots, size_t count) {
+// Records one event after the compute work enqueued so far and makes it the
+// `released` event of `count` slots of a layer (their last readers).
+int record_release(dmhip_expert_cache *c, size_t layer, const size_t *slots, size_t count) {
     hipEvent_t ev = c->release_events[c->next_release++ % kReleaseEvents];
     DM_HIP(hipEventRecord(ev, c->ctx->stream));
     for (size_t i = 0; i < count; i++) {
         Slot &s = c->layers[layer].slots[slots[i]];
         s.released = ev;
         s.released_recorded = true;
-        s.pinned = false;
     }
     return DMHIP_OK;
 }
 
-int release(dmhip_expert_cache *c, size_t layer, size_t slot) { return release_slots(c, layer, &slot, 1); }
+dmhip_buf *new_slot_buffer(dmhip_ctx *ctx, size_t bytes) {
+    dmhip_buf *b = new dmhip_buf();
+    b->ctx = ctx;
+    b->device = ctx->device;
+    b->len = bytes;
+    b->cache_owned = true;
+    // 256 spare bytes: vector loads of a row's end may read a few bytes past it
+    if (hipMalloc(&b->dev, bytes + 256) != hipSuccess || hipMemset(b->dev, 0, bytes + 256) != hipSuccess) {
+        if (b->dev) (void)hipFree(b->dev);
+        delete b;
+        return nullptr;
+    }
+    return b;
+}
+
+void free_slot_buffer(dmhip_buf *b) {
+    if (!b) return;
+    if (b->dev) (void)hipFree(b->dev);
+    delete b;
+}
+
+void destroy(dmhip_expert_cache *c) {
+    (void)hipSetDevice(c->device);
+    // Wait for the cache's own work: uploads into the slots, the copies out
+    // of the staging ring and the compute released last from each slot.
+    for (Layer &layer : c->layers)
+        for (Slot &s : layer.slots) {
+            if (s.uploaded) (void)hipEventSynchronize(s.ready);
+            if (s.released_recorded) (void)hipEventSynchronize(s.released);
+        }
+    for (Staging &e : c->staging)
+        if (e.busy) (void)hipEventSynchronize(e.done);
+    for (Layer &layer : c->layers)
+        for (Slot &s : layer.slots) {
+            free_slot_buffer(s.gate_up_buf);
+            free_slot_buffer(s.down_buf);
+            if (s.ready) (void)hipEventDestroy(s.ready);
+            if (s.upload_start) (void)hipEventDestroy(s.upload_start);
+        }
+    for (hipEvent_t ev : c->release_events)
+        if (ev) (void)hipEventDestroy(ev);
+    for (Staging &e : c->staging) {
+        if (e.host) (void)hipHostFree(e.host);
+        if (e.done) (void)hipEventDestroy(e.done);
+    }
+    // the work area's readers were released above; the context (and its
+    // stream) may already be gone
+    c->work.stream = nullptr;
+    c->work.release();
+    if (c->host_selection) (void)hipHostFree(c->host_selection);
+    delete c;
+}
+
+// The shared part of both constructors: slots, events, selection buffer.
+int build_cache(dmhip_ctx *ctx, const dmhip_expert_layer_layout *layouts, size_t layer_count,
+                size_t slots_per_layer, dmhip_expert_cache *c) {
+    c->ctx = ctx;
+    c->device = ctx->device;
+    c->work.stream = ctx->stream;
+    c->layers.resize(layer_count);
+    uint64_t resident = 0;
+    for (size_t l = 0; l < layer_count; l++) {
+        Layer &layer = c->layers[l];
+        layer.layout = layouts[l];
+        layer.slots.resize(slots_per_layer);
+        for (Slot &s : layer.slots) {
+            s.gate_up_buf = new_slot_buffer(ctx, layer.layout.gate_up_bytes);
+            s.down_buf = new_slot_buffer(ctx, layer.layout.down_bytes);
+            if (!s.gate_up_buf || !s.down_buf)
+                return fail_alloc(!s.gate_up_buf ? layer.layout.gate_up_bytes : layer.layout.down_bytes);
+            s.gate_up = s.gate_up_buf->dev;
+            s.down = s.down_buf->dev;
+            if (hipEventCreate(&s.ready) != hipSuccess || hipEventCreate(&s.upload_start) != hipSuccess)
+                return fail(DMHIP_ERR_COMMAND, "could not create the expert slot events");
+            resident += layer.layout.gate_up_bytes + layer.layout.down_bytes;
+        }
+    }
+    c->stats.resident_bytes = resident;
+    c->release_events.assign(kReleaseEvents, nullptr);
+    for (hipEvent_t &ev : c->release_events)
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+            ev = nullptr;
+            return fail(DMHIP_ERR_COMMAND, "could not create the slot release events");
+        }
+    if (hipHostMalloc((void **)&c->host_selection, kSelectionBytes, hipHostMallocDefault) != hipSuccess) {
+        c->host_selection = nullptr;
+        return fail_alloc(kSelectionBytes);
+    }
+    return DMHIP_OK;
+}
+
+int check_layouts(const dmhip_expert_layer_layout *layouts, size_t layer_count, size_t slots_per_layer) {
+    if (slots_per_layer == 0)
+        return fail(DMHIP_ERR_NO_SLOTS, "expert cache requires at least one slot per layer");
+    if (layer_count && !layouts) return fail(DMHIP_ERR_INVALID_ARGUMENT, "layouts must not be null");
+    for (size_t l = 0; l < layer_count; l++)
+        if (layouts[l].gate_up_bytes == 0 || layouts[l].down_bytes == 0) return fail_alloc(0);
+    return DMHIP_OK;
+}
 
 }  // namespace
 
@@ -179,14 +379,10 @@ int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len
                            size_t slots_per_layer, dmhip_expert_cache **out) {
     if (!ctx || !out) return fail(DMHIP_ERR_INVALID_ARGUMENT, "context and out must not be null");
     *out = nullptr;
-    if (slots_per_layer == 0)
-        return fail(DMHIP_ERR_NO_SLOTS, "expert cache requires at least one slot per layer");
-    if (layer_count && (!layouts || !source))
-        return fail(DMHIP_ERR_INVALID_ARGUMENT, "layouts and source must not be null");
+    DM_CHECK_STATUS(check_layouts(layouts, layer_count, slots_per_layer));
+    if (layer_count && !source) return fail(DMHIP_ERR_INVALID_ARGUMENT, "source must not be null");
     for (size_t l = 0; l < layer_count; l++) {
         const dmhip_expert_layer_layout &L = layouts[l];
-        if (L.gate_up_bytes == 0 || L.down_bytes == 0)
-            return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a 0-byte device buffer");
         unsigned __int128 gu_end = (unsigned __int128)L.gate_up_offset +
                                    (unsigned __int128)L.expert_count * L.gate_up_bytes;
         unsigned __int128 dn_end = (unsigned __int128)L.down_offset +
@@ -197,65 +393,73 @@ int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len
     }
     DM_CHECK_STATUS(set_device(ctx));
     dmhip_expert_cache *c = new dmhip_expert_cache();
-    c->ctx = ctx;
-    c->device = ctx->device;
     c->source = (const uint8_t *)source;
     c->source_len = source_len;
-    c->layers.resize(layer_count);
-    uint64_t resident = 0;
+    const int st = build_cache(ctx, layouts, layer_count, slots_per_layer, c);
+    if (st != DMHIP_OK) {
+        destroy(c);
+        return st;
+    }
+    *out = c;
+    return DMHIP_OK;
+}
+
+int dmhip_expert_cache_new_file(dmhip_ctx *ctx, int fd, const dmhip_expert_layer_layout *layouts,
+                                size_t layer_count, size_t slots_per_layer, dmhip_expert_cache **out) {
+    if (!ctx || !out) return fail(DMHIP_ERR_INVALID_ARGUMENT, "context and out must not be null");
+    *out = nullptr;
+    if (fd < 0) return fail(DMHIP_ERR_INVALID_ARGUMENT, "file descriptor %d is not open", fd);
+    DM_CHECK_STATUS(check_layouts(layouts, layer_count, slots_per_layer));
     for (size_t l = 0; l < layer_count; l++) {
-        Layer &layer = c->layers[l];
-        layer.layout = layouts[l];
-        layer.slots.resize(slots_per_layer);
-        for (Slot &s : layer.slots) {
-            if (hipMalloc(&s.gate_up, layer.layout.gate_up_bytes + 256) != hipSuccess ||
-                hipMalloc(&s.down, layer.layout.down_bytes + 256) != hipSuccess ||
-                hipMemset(s.gate_up, 0, layer.layout.gate_up_bytes + 256) != hipSuccess ||
-                hipMemset(s.down, 0, layer.layout.down_bytes + 256) != hipSuccess ||
-                hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess) {
-                dmhip_expert_cache_free(c);
-                return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate expert slot buffers");
+        const dmhip_expert_layer_layout &L = layouts[l];
+        // expert_offset's overflow checks (src/expert.rs:231-239), up front
+        const unsigned __int128 gu_end = (unsigned __int128)L.gate_up_offset +
+                                         (unsigned __int128)L.expert_count * L.gate_up_bytes;
+        const unsigned __int128 dn_end = (unsigned __int128)L.down_offset +
+                                         (unsigned __int128)L.expert_count * L.down_bytes;
+        if (gu_end > (unsigned __int128)UINT64_MAX || dn_end > (unsigned __int128)UINT64_MAX)
+            return fail(DMHIP_ERR_INVALID_LAYOUT, "layer %zu expert file offsets overflow", l);
+    }
+    DM_CHECK_STATUS(set_device(ctx));
+    dmhip_expert_cache *c = new dmhip_expert_cache();
+    c->fd = fd;
+    int st = build_cache(ctx, layouts, layer_count, slots_per_layer, c);
+    size_t entry_bytes = 0;
+    for (size_t l = 0; l < layer_count; l++) {
+        const size_t b = layouts[l].gate_up_bytes + layouts[l].down_bytes;
+        entry_bytes = b > entry_bytes ? b : entry_bytes;
+    }
+    if (st == DMHIP_OK && layer_count) {
+        c->staging.resize(kStagingEntries);
+        for (Staging &e : c->staging) {
+            if (hipHostMalloc((void **)&e.host, entry_bytes, hipHostMallocDefault) != hipSuccess) {
+                e.host = nullptr;
+                st = fail_alloc(entry_bytes);
+                break;
             }
-            resident += layer.layout.gate_up_bytes + layer.layout.down_bytes;
+            if (hipEventCreateWithFlags(&e.done, hipEventDisableTiming) != hipSuccess) {
+                e.done = nullptr;
+                st = fail(DMHIP_ERR_COMMAND, "could not create the staging events");
+                break;
+            }
         }
     }
-    c->stats.resident_bytes = resident;
-    c->release_events.assign(kReleaseEvents, nullptr);
-    for (hipEvent_t &ev : c->release_events)
-        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
-            ev = nullptr;
-            dmhip_expert_cache_free(c);
-            return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not create the slot release events");
-        }
-    if (hipHostMalloc((void **)&c->host_selection, kSelectionBytes, hipHostMallocDefault) != hipSuccess) {
-        c->host_selection = nullptr;
-        dmhip_expert_cache_free(c);
-        return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate the pinned router selection buffer");
+    if (st != DMHIP_OK) {
+        destroy(c);
+        return st;
     }
     *out = c;
     return DMHIP_OK;
 }
 
 void dmhip_expert_cache_free(dmhip_expert_cache *c) {
-    if (!c) return;
-    // The context may already be gone: wait on the device, not its streams.
-    (void)hipSetDevice(c->device);
-    (void)hipDeviceSynchronize();
-    for (Layer &layer : c->layers)
-        for (Slot &s : layer.slots) {
-            if (s.gate_up) (void)hipFree(s.gate_up);
-            if (s.down) (void)hipFree(s.down);
-            if (s.ready) (void)hipEventDestroy(s.ready);
-        }
-    for (hipEvent_t ev : c->release_events)
-        if (ev) (void)hipEventDestroy(ev);
-    c->work.release();
-    if (c->host_selection) (void)hipHostFree(c->host_selection);
-    delete c;
+    if (c) destroy(c);
 }
 
-int dmhip_expert_cache_stats_get(const dmhip_expert_cache *c, dmhip_expert_cache_stats *stats) {
+int dmhip_expert_cache_stats_get(dmhip_expert_cache *c, dmhip_expert_cache_stats *stats) {
     if (!c || !stats) return fail(DMHIP_ERR_INVALID_ARGUMENT, "cache and stats must not be null");
+    DM_CHECK_STATUS(set_device(c->ctx));
+    account_uploads(c, true);
     *stats = c->stats;
     return DMHIP_OK;
 }
@@ -265,8 +469,8 @@ size_t dmhip_expert_cache_slots_per_layer(const dmhip_expert_cache *c) {
 }
 
 int dmhip_expert_acquire(dmhip_expert_cache *c, size_t layer, size_t expert,
-                         const volatile int *cancelled, size_t *slot, const void **gate_up,
-                         const void **down) {
+                         const volatile int *cancelled, size_t *slot, const dmhip_buf **gate_up,
+                         const dmhip_buf **down) {
     if (!c || !slot || !gate_up || !down)
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "cache and outputs must not be null");
     if (cancelled && *cancelled) return fail(DMHIP_ERR_CANCELLED, "expert loading was cancelled");
@@ -275,19 +479,24 @@ int dmhip_expert_acquire(dmhip_expert_cache *c, size_t layer, size_t expert,
     DM_CHECK_STATUS(acquire(c, layer, expert, &s));
     if (cancelled && *cancelled) return fail(DMHIP_ERR_CANCELLED, "expert loading was cancelled");
     Slot &slot_ref = c->layers[layer].slots[s];
-    slot_ref.pinned = true;
+    slot_ref.pins += 1;
     *slot = s;
-    *gate_up = slot_ref.gate_up;
-    *down = slot_ref.down;
+    *gate_up = slot_ref.gate_up_buf;
+    *down = slot_ref.down_buf;
     return DMHIP_OK;
 }
 
 int dmhip_expert_release(dmhip_expert_cache *c, size_t layer, size_t slot) {
     if (!c) return fail(DMHIP_ERR_INVALID_ARGUMENT, "cache must not be null");
-    if (layer >= c->layers.size() || slot >= c->layers[layer].slots.size())
-        return fail(DMHIP_ERR_INVALID_LAYER, "slot %zu of layer %zu does not exist", slot, layer);
+    if (layer >= c->layers.size()) return fail_layer(layer, c->layers.size());
+    if (slot >= c->layers[layer].slots.size())
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "slot %zu of layer %zu does not exist", slot, layer);
+    Slot &s = c->layers[layer].slots[slot];
+    if (s.pins == 0) return fail(DMHIP_ERR_INVALID_ARGUMENT, "slot %zu of layer %zu is not acquired", slot, layer);
     DM_CHECK_STATUS(set_device(c->ctx));
-    return release(c, layer, slot);
+    DM_CHECK_STATUS(record_release(c, layer, &slot, 1));
+    s.pins -= 1;
+    return DMHIP_OK;
 }
 
 int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t batch,
@@ -299,18 +508,18 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     if (c->ctx != ctx) return fail(DMHIP_ERR_INVALID_ARGUMENT, "the cache belongs to another context");
     if (batch < 1 || batch > 16) return fail(DMHIP_ERR_INVALID_ARGUMENT, "batch %zu is outside 1..=16", batch);
     if (k == 0 || k > experts)
-        return fail(DMHIP_ERR_INVALID_TOP_K, "top-k count %zu is outside 1..=%zu", k, experts);
+        return fail_top_k(k, experts);
     if (k > kMaxTopK || experts > 16384)
         return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "router with %zu experts, top-%zu exceeds the kernel limits",
                     experts, k);
-    if (hidden == 0 || width == 0) return fail(DMHIP_ERR_EMPTY_INPUT, "MoE layer requires a non-empty input");
+    if (hidden == 0 || width == 0) return fail_empty("MoE layer");
     if (layer >= c->layers.size())
-        return fail(DMHIP_ERR_INVALID_LAYER, "expert cache layer %zu is outside its %zu layers", layer,
-                    c->layers.size());
+        return fail_layer(layer, c->layers.size());
     const dmhip_expert_layer_layout &L = c->layers[layer].layout;
     uint64_t gu_row, dn_row;
     if (!row_byte_len(gate_up_type, hidden, &gu_row) || !row_byte_len(down_type, width, &dn_row))
-        return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT, "expert rows are not whole blocks");
+        return fail_element_count(row_byte_len(gate_up_type, hidden, &gu_row) ? down_type : gate_up_type,
+                                  row_byte_len(gate_up_type, hidden, &gu_row) ? width : hidden);
     if (L.gate_up_bytes != 2 * width * gu_row || L.down_bytes != hidden * dn_row)
         return fail(DMHIP_ERR_INVALID_LAYOUT,
                     "layer %zu slots hold %zu + %zu bytes; the expert shape needs %llu + %llu", layer,
@@ -361,7 +570,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     // top_k_softmax rejects non-finite logits (src/cpu.rs:240-245); nothing
     // has been acquired yet.
     for (size_t t = 0; t < batch; t++)
-        if (sel_bad[t]) return fail(DMHIP_ERR_NON_FINITE, "top-k softmax received a non-finite value");
+        if (sel_bad[t]) return fail_non_finite("top-k softmax");
     memcpy(ids, sel_ids, pairs * 4);
     memcpy(probabilities, sel_probs, pairs * 4);
 
@@ -424,7 +633,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
                                        gu_jobs.data(), gu_jobs.size(), x, d_act));
             DM_HIP(launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(),
                                        dn_jobs.size(), d_act, d_eo));
-            return release_slots(c, layer, group_slot.data(), group_slot.size());
+            return record_release(c, layer, group_slot.data(), group_slot.size());
         }
         phase_tokens.emplace_back(order.size());
         std::vector<uint32_t> &tokens = phase_tokens.back();
@@ -448,7 +657,14 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
             DM_CHECK_STATUS(enqueue_matvec(ctx, down_type, hidden, width, s.down, cnt,
                                            d_act + (p0 + q0) * width, d_eo + (p0 + q0) * hidden));
         }
-        return release_slots(c, layer, group_slot.data(), group_slot.size());
+        return record_release(c, layer, group_slot.data(), group_slot.size());
+    };
+    // A failure after slots of the open phase were acquired still records
+    // their release after whatever was enqueued, so that a later upload into
+    // one of them waits for that work.
+    auto fail_phase = [&](size_t p0, size_t p1, int status) -> int {
+        if (p1 > p0) (void)record_release(c, layer, slot_of.data() + p0, p1 - p0);
+        return status;
     };
     for (size_t p = 0; p < pairs; p++) {
         // Would this acquire evict a slot the open phase still needs?  Check
@@ -462,7 +678,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
             size_t victim = SIZE_MAX;
             for (size_t i = 0; i < Ly.slots.size(); i++) {
                 const Slot &s = Ly.slots[i];
-                if (s.pinned) continue;
+                if (s.pins) continue;
                 if (victim == SIZE_MAX) { victim = i; continue; }
                 const Slot &v = Ly.slots[victim];
                 if (s.has < v.has || (s.has == v.has && s.last_used < v.last_used)) victim = i;
@@ -471,13 +687,18 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
             for (size_t q = begin; q < p; q++)
                 if (slot_of[q] == victim) used = true;
             if (used) {
-                DM_CHECK_STATUS(run_phase(begin, p));
+                const int st = run_phase(begin, p);
+                if (st != DMHIP_OK) return fail_phase(begin, p, st);
                 begin = p;
             }
         }
-        DM_CHECK_STATUS(acquire(c, layer, e, &slot_of[p]));
+        const int st = acquire(c, layer, e, &slot_of[p]);
+        if (st != DMHIP_OK) return fail_phase(begin, p, st);
     }
-    DM_CHECK_STATUS(run_phase(begin, pairs));
+    {
+        const int st = run_phase(begin, pairs);
+        if (st != DMHIP_OK) return fail_phase(begin, pairs, st);
+    }
 
     // 3. Ordered combine and copy out.
     if (!grouped) DM_HIP(hipMemcpyAsync(d_pos, pos.data(), pairs * 4, hipMemcpyHostToDevice, ctx->stream));

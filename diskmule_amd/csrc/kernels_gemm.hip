@@ -504,13 +504,11 @@ int dmhip_gemm_device(dmhip_ctx *ctx, uint32_t type, size_t m, size_t n, size_t 
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "gemm workspace holds %zu bytes; the shape needs %zu",
                     workspace_len, dmhip_gemm_workspace_bytes(m, k));
     if (!(type == 0 || type == 1 || type == 6 || type == 8 || type == 12 || type == 14))
-        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "HIP GEMM does not support %s", type_name(type));
+        return fail_unsupported(type, "HIP GEMM");
     uint64_t rb;
-    if (!row_byte_len(type, k, &rb))
-        return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT, "%s row of %zu values is not whole blocks",
-                    type_name(type), k);
+    if (!row_byte_len(type, k, &rb)) return fail_element_count(type, k);
     if (m == 0 || n == 0) return DMHIP_OK;
-    if (k == 0) return fail(DMHIP_ERR_EMPTY_INPUT, "gemm requires a non-empty input");
+    if (k == 0) return fail_empty("gemm");
     if (m > 0xffffffffull || n > 0xffffffffull || k > 0xffffffffull)
         return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "HIP vector length exceeds the 32-bit kernel limit");
     DM_CHECK_STATUS(set_device(ctx));

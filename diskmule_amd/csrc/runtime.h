@@ -14,8 +14,29 @@
 
 namespace dm {
 
-// Records `code` with a formatted message as the calling thread's last error.
+// Records `code` with a formatted message as the calling thread's last error
+// (its payload reset to the bare status).
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// The calling thread's last failure payload.
+dmhip_error_detail &last_detail();
+// Failures that carry a payload: the reference's message text and fields.
+// `operation` / `argument` must be static strings.
+int fail_alloc(size_t bytes);
+int fail_empty(const char *operation);
+int fail_vector_length(const char *operation, const char *argument, size_t expected, size_t actual);
+int fail_positive(const char *operation);
+int fail_non_finite(const char *operation);
+int fail_unsupported(uint32_t type, const char *what);  // "<what> does not support <type>"
+int fail_element_count(uint32_t type, uint64_t elements);
+int fail_byte_length(uint32_t type, uint64_t expected, uint64_t actual);
+int fail_input_length(size_t expected, size_t actual);
+int fail_output_length(size_t expected, size_t actual);
+int fail_top_k(size_t k, size_t length);
+int fail_mapped_range(size_t offset, size_t end, size_t length);
+int fail_layer(size_t layer, size_t count);
+int fail_expert(size_t layer, size_t expert, size_t count);
+int fail_pinned(size_t layer);
+int fail_io(int os_error);  // 0: unexpected end of file
 // Maps a HIP runtime error onto DMHIP_ERR_COMMAND (MetalError::Command).
 int hip_fail(hipError_t e, const char *what);
 
@@ -31,10 +52,13 @@ int hip_fail(hipError_t e, const char *what);
         if (dm_s_ != DMHIP_OK) return dm_s_; \
     } while (0)
 
-// Device allocation that grows on demand (scratch for the host-slice API).
+// Device allocation that grows on demand (scratch for the host-slice API),
+// used by work on `stream`: replacing or freeing it first waits for that
+// stream (no stream: the caller has already waited for its users).
 struct Scratch {
     void *ptr = nullptr;
     size_t bytes = 0;
+    hipStream_t stream = nullptr;
     int ensure(size_t need);
     void release();
 };
@@ -94,6 +118,9 @@ struct dmhip_buf {
     int device = 0;
     void *dev = nullptr;
     size_t len = 0;
+    // Owned by an expert cache (a slot's gate_up or down bytes):
+    // dmhip_buffer_free leaves it alone; the cache frees it.
+    bool cache_owned = false;
 };
 
 namespace dm {

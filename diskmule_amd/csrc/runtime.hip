@@ -15,6 +15,7 @@
 namespace dm {
 
 static thread_local std::string g_last_error;
+static thread_local dmhip_error_detail g_last_detail;
 
 int fail(int code, const char *fmt, ...) {
     char buffer[512];
@@ -23,7 +24,131 @@ int fail(int code, const char *fmt, ...) {
     vsnprintf(buffer, sizeof buffer, fmt, args);
     va_end(args);
     g_last_error = buffer;
+    g_last_detail = dmhip_error_detail{};
+    g_last_detail.status = code;
     return code;
+}
+
+dmhip_error_detail &last_detail() { return g_last_detail; }
+
+int fail_alloc(size_t bytes) {
+    fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a %zu-byte device buffer", bytes);
+    g_last_detail.bytes = bytes;
+    return DMHIP_ERR_BUFFER_ALLOCATION;
+}
+
+int fail_empty(const char *operation) {
+    fail(DMHIP_ERR_EMPTY_INPUT, "%s requires a non-empty input", operation);
+    g_last_detail.operation = operation;
+    return DMHIP_ERR_EMPTY_INPUT;
+}
+
+int fail_vector_length(const char *operation, const char *argument, size_t expected, size_t actual) {
+    fail(DMHIP_ERR_INVALID_VECTOR_LENGTH, "%s %s has length %zu; expected %zu", operation, argument, actual,
+         expected);
+    g_last_detail.operation = operation;
+    g_last_detail.argument = argument;
+    g_last_detail.expected = expected;
+    g_last_detail.actual = actual;
+    return DMHIP_ERR_INVALID_VECTOR_LENGTH;
+}
+
+int fail_positive(const char *operation) {
+    fail(DMHIP_ERR_INVALID_POSITIVE_PARAMETER, "%s requires a finite positive parameter", operation);
+    g_last_detail.operation = operation;
+    return DMHIP_ERR_INVALID_POSITIVE_PARAMETER;
+}
+
+int fail_non_finite(const char *operation) {
+    fail(DMHIP_ERR_NON_FINITE, "%s received a non-finite value", operation);
+    g_last_detail.operation = operation;
+    return DMHIP_ERR_NON_FINITE;
+}
+
+int fail_unsupported(uint32_t type, const char *what) {
+    fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "%s does not support %s", what, type_name(type));
+    g_last_detail.kind = type_name(type);
+    return DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE;
+}
+
+int fail_element_count(uint32_t type, uint64_t elements) {
+    uint32_t be = 0, bb = 0;
+    type_layout(type, &be, &bb);
+    fail(DMHIP_ERR_INVALID_ELEMENT_COUNT, "%s output length %llu is not divisible by its %u-element block",
+         type_name(type), (unsigned long long)elements, be);
+    g_last_detail.kind = type_name(type);
+    g_last_detail.elements = elements;
+    g_last_detail.block_elements = be;
+    return DMHIP_ERR_INVALID_ELEMENT_COUNT;
+}
+
+int fail_byte_length(uint32_t type, uint64_t expected, uint64_t actual) {
+    fail(DMHIP_ERR_INVALID_BYTE_LENGTH, "%s requires %llu encoded bytes, got %llu", type_name(type),
+         (unsigned long long)expected, (unsigned long long)actual);
+    g_last_detail.kind = type_name(type);
+    g_last_detail.expected = expected;
+    g_last_detail.actual = actual;
+    return DMHIP_ERR_INVALID_BYTE_LENGTH;
+}
+
+int fail_input_length(size_t expected, size_t actual) {
+    fail(DMHIP_ERR_INVALID_INPUT_LENGTH, "matvec input has %zu columns; expected %zu", actual, expected);
+    g_last_detail.expected = expected;
+    g_last_detail.actual = actual;
+    return DMHIP_ERR_INVALID_INPUT_LENGTH;
+}
+
+int fail_output_length(size_t expected, size_t actual) {
+    fail(DMHIP_ERR_INVALID_OUTPUT_LENGTH, "matvec output has %zu rows; expected %zu", actual, expected);
+    g_last_detail.expected = expected;
+    g_last_detail.actual = actual;
+    return DMHIP_ERR_INVALID_OUTPUT_LENGTH;
+}
+
+int fail_top_k(size_t k, size_t length) {
+    fail(DMHIP_ERR_INVALID_TOP_K, "top-k count %zu is outside 1..=%zu", k, length);
+    g_last_detail.k = k;
+    g_last_detail.length = length;
+    return DMHIP_ERR_INVALID_TOP_K;
+}
+
+int fail_mapped_range(size_t offset, size_t end, size_t length) {
+    fail(DMHIP_ERR_MAPPED_RANGE, "mapped buffer range %zu..%zu exceeds its %zu-byte file mapping", offset, end,
+         length);
+    g_last_detail.offset = offset;
+    g_last_detail.end = end;
+    g_last_detail.length = length;
+    return DMHIP_ERR_MAPPED_RANGE;
+}
+
+int fail_layer(size_t layer, size_t count) {
+    fail(DMHIP_ERR_INVALID_LAYER, "expert cache layer %zu is outside its %zu layers", layer, count);
+    g_last_detail.layer = layer;
+    g_last_detail.count = count;
+    return DMHIP_ERR_INVALID_LAYER;
+}
+
+int fail_expert(size_t layer, size_t expert, size_t count) {
+    fail(DMHIP_ERR_INVALID_EXPERT, "expert %zu is outside layer %zu's %zu experts", expert, layer, count);
+    g_last_detail.layer = layer;
+    g_last_detail.expert = expert;
+    g_last_detail.count = count;
+    return DMHIP_ERR_INVALID_EXPERT;
+}
+
+int fail_pinned(size_t layer) {
+    fail(DMHIP_ERR_ALL_SLOTS_PINNED, "all expert slots in layer %zu are pinned by in-flight work", layer);
+    g_last_detail.layer = layer;
+    return DMHIP_ERR_ALL_SLOTS_PINNED;
+}
+
+int fail_io(int os_error) {
+    if (os_error)
+        fail(DMHIP_ERR_IO, "%s", strerror(os_error));
+    else
+        fail(DMHIP_ERR_IO, "failed to fill whole buffer");
+    g_last_detail.os_error = os_error;
+    return DMHIP_ERR_IO;
 }
 
 int hip_fail(hipError_t e, const char *what) {
@@ -37,15 +162,15 @@ int Scratch::ensure(size_t need) {
     hipError_t e = hipMalloc(&ptr, grow + 256);
     if (e != hipSuccess) {
         ptr = nullptr;
-        return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a %zu-byte device buffer", need);
+        return fail_alloc(need);
     }
     bytes = grow;
     return DMHIP_OK;
 }
 
 void Scratch::release() {
-    // Work already enqueued may still read the old allocation.
-    if (ptr) (void)hipDeviceSynchronize();
+    // Work already enqueued on the stream may still read the old allocation.
+    if (ptr && stream) (void)hipStreamSynchronize(stream);
     if (ptr) (void)hipFree(ptr);
     ptr = nullptr;
     bytes = 0;
@@ -130,29 +255,15 @@ static bool matvec_kind_supported(uint32_t type) {
 // MetalContext::prepare_matvec (src/metal.rs:1513-1560), same order of checks.
 static int prepare_matvec(uint32_t type, size_t rows, size_t columns, size_t encoded_length,
                           size_t input_len, size_t output_len, size_t *row_bytes_out) {
-    if (input_len != columns)
-        return fail(DMHIP_ERR_INVALID_INPUT_LENGTH, "matvec input has %zu columns; expected %zu",
-                    input_len, columns);
-    if (output_len != rows)
-        return fail(DMHIP_ERR_INVALID_OUTPUT_LENGTH, "matvec output has %zu rows; expected %zu",
-                    output_len, rows);
-    if (!matvec_kind_supported(type))
-        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE,
-                    "HIP matrix-vector multiplication does not support %s", type_name(type));
+    if (input_len != columns) return fail_input_length(columns, input_len);
+    if (output_len != rows) return fail_output_length(rows, output_len);
+    if (!matvec_kind_supported(type)) return fail_unsupported(type, "HIP matrix-vector multiplication");
     uint64_t row_bytes;
-    if (!row_byte_len(type, columns, &row_bytes)) {
-        uint32_t be, bb;
-        type_layout(type, &be, &bb);
-        return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT,
-                    "%s output length %zu is not divisible by its %u-element block",
-                    type_name(type), columns, be);
-    }
+    if (!row_byte_len(type, columns, &row_bytes)) return fail_element_count(type, columns);
     if (rows != 0 && row_bytes > SIZE_MAX / rows)
         return fail(DMHIP_ERR_OVERFLOW, "matrix dimensions or encoded byte length overflowed");
     size_t matrix_bytes = rows * (size_t)row_bytes;
-    if (encoded_length != matrix_bytes)
-        return fail(DMHIP_ERR_INVALID_BYTE_LENGTH, "%s requires %zu encoded bytes, got %zu",
-                    type_name(type), matrix_bytes, encoded_length);
+    if (encoded_length != matrix_bytes) return fail_byte_length(type, matrix_bytes, encoded_length);
     *row_bytes_out = (size_t)row_bytes;
     return DMHIP_OK;
 }
@@ -163,22 +274,18 @@ static int count_u32(size_t n) {
 }
 
 static int require_nonempty(const char *operation, size_t n) {
-    if (n == 0) return fail(DMHIP_ERR_EMPTY_INPUT, "%s requires a non-empty input", operation);
+    if (n == 0) return fail_empty(operation);
     return DMHIP_OK;
 }
 
 static int validate_vector_length(const char *operation, const char *argument, size_t expected,
                                   size_t actual) {
-    if (actual != expected)
-        return fail(DMHIP_ERR_INVALID_VECTOR_LENGTH, "%s %s has length %zu; expected %zu",
-                    operation, argument, actual, expected);
+    if (actual != expected) return fail_vector_length(operation, argument, expected, actual);
     return DMHIP_OK;
 }
 
 static int require_positive(const char *operation, float v) {
-    if (!isfinite(v) || v <= 0.0f)
-        return fail(DMHIP_ERR_INVALID_POSITIVE_PARAMETER, "%s requires a finite positive parameter",
-                    operation);
+    if (!isfinite(v) || v <= 0.0f) return fail_positive(operation);
     return DMHIP_OK;
 }
 
@@ -206,6 +313,12 @@ using namespace dm;
 extern "C" {
 
 const char *dmhip_last_error(void) { return dm::g_last_error.c_str(); }
+
+int dmhip_last_error_detail(dmhip_error_detail *out) {
+    if (!out) return DMHIP_ERR_INVALID_ARGUMENT;
+    *out = dm::g_last_detail;
+    return DMHIP_OK;
+}
 
 int dmhip_context_new(int device, dmhip_ctx **out) {
     DM_REQUIRE(out);
@@ -240,6 +353,7 @@ int dmhip_context_new(int device, dmhip_ctx **out) {
         dmhip_context_free(ctx);
         return fail(DMHIP_ERR_COMMAND, "could not create the HIP streams of device %d", device);
     }
+    for (Scratch *sc : {&ctx->in, &ctx->out, &ctx->enc, &ctx->aux, &ctx->partials}) sc->stream = ctx->stream;
     *out = ctx;
     return DMHIP_OK;
 }
@@ -298,8 +412,7 @@ static int new_buffer(dmhip_ctx *ctx, size_t length, dmhip_buf **out) {
     // its end (they are discarded); the spare keeps them inside the allocation.
     if (hipMalloc(&b->dev, length + 256) != hipSuccess) {
         delete b;
-        return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a %zu-byte device buffer",
-                    length);
+        return fail_alloc(length);
     }
     *out = b;
     return DMHIP_OK;
@@ -309,7 +422,7 @@ int dmhip_map_read_only(dmhip_ctx *ctx, const void *host, size_t length, dmhip_b
     DM_REQUIRE(ctx);
     DM_REQUIRE(out);
     *out = nullptr;
-    if (length == 0) return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a 0-byte device buffer");
+    if (length == 0) return fail_alloc(0);
     DM_REQUIRE(host);
     DM_CHECK(set_device(ctx));
     dmhip_buf *b;
@@ -329,7 +442,7 @@ int dmhip_new_owned_buffer(dmhip_ctx *ctx, size_t length, dmhip_buf **out) {
     DM_REQUIRE(ctx);
     DM_REQUIRE(out);
     *out = nullptr;
-    if (length == 0) return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate a 0-byte device buffer");
+    if (length == 0) return fail_alloc(0);
     DM_CHECK(set_device(ctx));
     dmhip_buf *b;
     DM_CHECK(new_buffer(ctx, length, &b));
@@ -344,7 +457,7 @@ int dmhip_new_owned_buffer(dmhip_ctx *ctx, size_t length, dmhip_buf **out) {
 }
 
 void dmhip_buffer_free(dmhip_buf *b) {
-    if (!b) return;
+    if (!b || b->cache_owned) return;
     // The context may already be gone; only the device id is needed.  hipFree
     // waits for work still using the allocation.
     (void)hipSetDevice(b->device);
@@ -359,9 +472,7 @@ static int check_range(const dmhip_buf *b, size_t offset, size_t n) {
     size_t end;
     if (__builtin_add_overflow(offset, n, &end))
         return fail(DMHIP_ERR_OVERFLOW, "matrix dimensions or encoded byte length overflowed");
-    if (end > b->len)
-        return fail(DMHIP_ERR_MAPPED_RANGE, "mapped buffer range %zu..%zu exceeds its %zu-byte file mapping",
-                    offset, end, b->len);
+    if (end > b->len) return fail_mapped_range(offset, end, b->len);
     return DMHIP_OK;
 }
 
@@ -414,10 +525,10 @@ int dmhip_copy_to_device(dmhip_ctx *ctx, void *device_dst, const void *src, size
 int dmhip_host_alloc_pinned(size_t bytes, void **out) {
     DM_REQUIRE(out);
     *out = nullptr;
-    if (bytes == 0) return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate 0 pinned bytes");
+    if (bytes == 0) return fail_alloc(0);
     if (hipHostMalloc(out, bytes, hipHostMallocDefault) != hipSuccess) {
         *out = nullptr;
-        return fail(DMHIP_ERR_BUFFER_ALLOCATION, "could not allocate %zu pinned host bytes", bytes);
+        return fail_alloc(bytes);
     }
     return DMHIP_OK;
 }
@@ -438,7 +549,7 @@ int dmhip_rms_norm(dmhip_ctx *ctx, const float *input, size_t input_len, const f
     DM_REQUIRE(input);
     DM_REQUIRE(output);
     if (!all_finite(input, input_len))
-        return fail(DMHIP_ERR_NON_FINITE, "RMSNorm received a non-finite value");
+        return fail_non_finite("RMSNorm");
     DM_CHECK(count_u32(input_len));
     DM_CHECK(set_device(ctx));
     size_t bytes = input_len * sizeof(float);
@@ -483,7 +594,7 @@ int dmhip_argmax(dmhip_ctx *ctx, const float *input, size_t input_len, size_t *i
     DM_CHECK(require_nonempty("argmax", input_len));
     DM_REQUIRE(input);
     if (!all_finite(input, input_len))
-        return fail(DMHIP_ERR_NON_FINITE, "argmax received a non-finite value");
+        return fail_non_finite("argmax");
     DM_CHECK(count_u32(input_len));
     DM_CHECK(set_device(ctx));
     size_t bytes = input_len * sizeof(float);
@@ -502,12 +613,12 @@ int dmhip_top_k_softmax(dmhip_ctx *ctx, const float *logits, size_t logits_len, 
                         size_t *indices, float *probabilities) {
     DM_REQUIRE(ctx);
     if (k == 0 || k > logits_len)
-        return fail(DMHIP_ERR_INVALID_TOP_K, "top-k count %zu is outside 1..=%zu", k, logits_len);
+        return fail_top_k(k, logits_len);
     DM_REQUIRE(logits);
     DM_REQUIRE(indices);
     DM_REQUIRE(probabilities);
     if (!all_finite(logits, logits_len))
-        return fail(DMHIP_ERR_NON_FINITE, "top-k softmax received a non-finite value");
+        return fail_non_finite("top-k softmax");
     DM_CHECK(count_u32(logits_len));
     if (k > kMaxTopK)
         return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "top-k count %zu exceeds the kernel limit %u", k, kMaxTopK);
@@ -597,18 +708,12 @@ int dmhip_dequantize(dmhip_ctx *ctx, uint32_t type, const dmhip_buf *encoded, si
     DM_REQUIRE(encoded);
     // cpu::dequantize validation (src/cpu.rs:313-341).
     if (!(type == 0 || type == 1 || type == 6 || type == 8 || type == 12 || type == 14))
-        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "HIP dequantization does not support %s",
-                    type_name(type));
+        return fail_unsupported(type, "HIP dequantization");
     uint64_t expected;
     uint32_t be, bb;
     type_layout(type, &be, &bb);
-    if (!row_byte_len(type, elements, &expected))
-        return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT,
-                    "%s output length %zu is not divisible by its %u-element block",
-                    type_name(type), elements, be);
-    if (length != expected)
-        return fail(DMHIP_ERR_INVALID_BYTE_LENGTH, "%s requires %llu encoded bytes, got %zu",
-                    type_name(type), (unsigned long long)expected, length);
+    if (!row_byte_len(type, elements, &expected)) return fail_element_count(type, elements);
+    if (length != expected) return fail_byte_length(type, expected, length);
     DM_CHECK(check_range(encoded, offset, length));
     if (elements == 0) return DMHIP_OK;
     DM_REQUIRE(output);
@@ -626,16 +731,9 @@ int dmhip_dequantize(dmhip_ctx *ctx, uint32_t type, const dmhip_buf *encoded, si
 
 static int validate_device_matvec(uint32_t type, size_t rows, size_t columns, size_t batch) {
     if (!(type == 0 || type == 1 || type == 6 || type == 8 || type == 12 || type == 14))
-        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE,
-                    "HIP matrix-vector multiplication does not support %s", type_name(type));
+        return fail_unsupported(type, "HIP matrix-vector multiplication");
     uint64_t rb;
-    if (!row_byte_len(type, columns, &rb)) {
-        uint32_t be, bb;
-        type_layout(type, &be, &bb);
-        return fail(DMHIP_ERR_INVALID_ELEMENT_COUNT,
-                    "%s output length %zu is not divisible by its %u-element block",
-                    type_name(type), columns, be);
-    }
+    if (!row_byte_len(type, columns, &rb)) return fail_element_count(type, columns);
     if (batch < 1 || batch > 16)
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "batch %zu is outside 1..=16", batch);
     DM_CHECK(count_u32(rows));
@@ -721,7 +819,7 @@ int dmhip_argmax_result(dmhip_ctx *ctx, size_t *index) {
     DM_HIP(hipMemcpyAsync(&result, ctx->argmax_user_index, 4, hipMemcpyDeviceToHost, ctx->stream));
     DM_HIP(hipStreamSynchronize(ctx->stream));
     ctx->argmax_pending = false;
-    if (state.non_finite) return fail(DMHIP_ERR_NON_FINITE, "argmax received a non-finite value");
+    if (state.non_finite) return fail_non_finite("argmax");
     *index = result;
     return DMHIP_OK;
 }
@@ -758,7 +856,7 @@ int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_
                               float *logits, uint32_t *ids, float *probabilities) {
     DM_REQUIRE(ctx);
     if (k == 0 || k > experts)
-        return fail(DMHIP_ERR_INVALID_TOP_K, "top-k count %zu is outside 1..=%zu", k, experts);
+        return fail_top_k(k, experts);
     if (k > kMaxTopK || experts > 16384)
         return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "router with %zu experts, top-%zu exceeds the kernel limits",
                     experts, k);
@@ -788,7 +886,7 @@ int dmhip_router_result(dmhip_ctx *ctx) {
     DM_HIP(hipMemcpyAsync(&flag, ctx->flags, 4, hipMemcpyDeviceToHost, ctx->stream));
     DM_HIP(hipStreamSynchronize(ctx->stream));
     ctx->router_pending = false;
-    if (flag) return fail(DMHIP_ERR_NON_FINITE, "top-k softmax received a non-finite value");
+    if (flag) return fail_non_finite("top-k softmax");
     return DMHIP_OK;
 }
 
@@ -862,8 +960,7 @@ int dmhip_matvec_phase_trace(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t 
     DM_REQUIRE(workgroups);
     DM_CHECK(validate_device_matvec(type, rows, columns, 1));
     if (!qmv_supported(type, rows, columns, weights, 1) || !qmv8_supported(type, rows, columns, 1))
-        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "the int8 decode GEMV does not take %s %zu x %zu",
-                    type_name(type), rows, columns);
+        return fail_unsupported(type, "the int8 decode GEMV at this shape");
     if (capacity / 4 < (rows + 15) / 16)
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "phase trace needs %zu stamps, got room for %zu",
                     4 * ((rows + 15) / 16), capacity);
@@ -883,8 +980,7 @@ int dmhip_matvec_valu_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t 
     DM_REQUIRE(y);
     DM_CHECK(validate_device_matvec(type, rows, columns, 1));
     if (!qmv_valu_supported(type, rows, columns, weights, x, 1))
-        return fail(DMHIP_ERR_UNSUPPORTED_TENSOR_TYPE, "the VALU decode GEMV does not take %s %zu x %zu",
-                    type_name(type), rows, columns);
+        return fail_unsupported(type, "the VALU decode GEMV at this shape");
     DM_CHECK(set_device(ctx));
     DM_HIP(launch_qmv_valu(ctx, type, (uint32_t)rows, (uint32_t)columns, weights, x, y));
     return DMHIP_OK;

@@ -26,12 +26,12 @@ VARIANTS = {
     9: "UnsupportedTensorType", 10: "InvalidElementCount", 11: "InvalidByteLength",
     12: "Overflow", 13: "InvalidInputLength", 14: "InvalidOutputLength", 15: "InvalidTopK",
     16: "MappedRange", 17: "Command", 18: "NoSlots", 19: "InvalidLayer", 20: "InvalidExpert",
-    21: "AllSlotsPinned", 22: "Cancelled", 23: "InvalidLayout", 24: "InvalidArgument",
+    21: "AllSlotsPinned", 22: "Cancelled", 23: "InvalidLayout", 24: "InvalidArgument", 25: "Io",
 }
 
 # Every function include/dmhip.h declares (checked against the header by tests).
 EXPORTED_SYMBOLS = [
-    "dmhip_last_error", "dmhip_context_new", "dmhip_context_free", "dmhip_device_name",
+    "dmhip_last_error", "dmhip_last_error_detail", "dmhip_context_new", "dmhip_context_free", "dmhip_device_name",
     "dmhip_synchronize", "dmhip_stream", "dmhip_map_read_only", "dmhip_new_owned_buffer",
     "dmhip_buffer_free", "dmhip_buffer_len", "dmhip_buffer_device_ptr", "dmhip_buffer_write",
     "dmhip_buffer_read", "dmhip_copy_to_host", "dmhip_copy_to_device", "dmhip_host_alloc_pinned", "dmhip_host_free_pinned", "dmhip_rms_norm",
@@ -43,7 +43,8 @@ EXPORTED_SYMBOLS = [
     "dmhip_event_record", "dmhip_event_elapsed_ms", "dmhip_event_free",
     "dmhip_kernel_timing_enable", "dmhip_kernel_timing_read", "dmhip_copy_device",
     "dmhip_probe_empty", "dmhip_probe_read", "dmhip_matvec_phase_trace", "dmhip_matvec_valu_device",
-    "dmhip_expert_cache_new", "dmhip_expert_cache_free", "dmhip_expert_cache_stats_get",
+    "dmhip_expert_cache_new", "dmhip_expert_cache_new_file", "dmhip_expert_cache_free",
+    "dmhip_expert_cache_stats_get",
     "dmhip_expert_cache_slots_per_layer", "dmhip_expert_acquire", "dmhip_expert_release",
     "dmhip_moe_layer",
 ]
@@ -52,9 +53,13 @@ F32, F16, Q5_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 6, 8, 12, 14, 30
 
 
 class HipError(RuntimeError):
-    def __init__(self, code: int, message: str):
+    """A failed call: `variant` names the MetalError / ExpertCacheError variant
+    and `detail` holds that variant's fields (dmhip_last_error_detail)."""
+
+    def __init__(self, code: int, message: str, detail: dict | None = None):
         self.code = code
         self.variant = VARIANTS.get(code, f"Unknown({code})")
+        self.detail = detail or {}
         super().__init__(f"{self.variant}: {message}")
 
 
@@ -77,6 +82,30 @@ class _Layout(ctypes.Structure):
                 ("gate_up_bytes", _sz), ("down_offset", ctypes.c_uint64), ("down_bytes", _sz)]
 
 
+class _Detail(ctypes.Structure):
+    _fields_ = [("status", ctypes.c_int32), ("os_error", ctypes.c_int32), ("operation", ctypes.c_char_p),
+                ("argument", ctypes.c_char_p), ("kind", ctypes.c_char_p)] + \
+               [(n, ctypes.c_uint64) for n in ("expected", "actual", "offset", "end", "length", "left", "right",
+                                               "output", "elements", "block_elements", "k", "bytes", "layer",
+                                               "expert", "count")]
+
+    # the fields each variant carries (include/dmhip.h)
+    FIELDS = {
+        2: ("bytes",), 3: ("left", "right", "output"), 5: ("operation",),
+        6: ("operation", "argument", "expected", "actual"), 7: ("operation",), 8: ("operation",), 9: ("kind",),
+        10: ("kind", "elements", "block_elements"), 11: ("kind", "expected", "actual"), 13: ("expected", "actual"),
+        14: ("expected", "actual"), 15: ("k", "length"), 16: ("offset", "end", "length"), 19: ("layer", "count"),
+        20: ("layer", "expert", "count"), 21: ("layer",), 25: ("os_error",),
+    }
+
+    def as_dict(self) -> dict:
+        out = {}
+        for name in self.FIELDS.get(self.status, ()):
+            v = getattr(self, name)
+            out[name] = v.decode() if isinstance(v, bytes) else v
+        return out
+
+
 class _Stats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in
                 ("hits", "misses", "evictions", "reads", "bytes_read", "io_wait_ns", "resident_bytes")]
@@ -93,6 +122,7 @@ def load_library() -> ctypes.CDLL:
     lib = ctypes.CDLL(_LIB)
     sig = {
         "dmhip_last_error": ([], ctypes.c_char_p),
+        "dmhip_last_error_detail": ([ctypes.POINTER(_Detail)], ctypes.c_int),
         "dmhip_context_new": ([ctypes.c_int, ctypes.POINTER(_vp)], ctypes.c_int),
         "dmhip_context_free": ([_vp], None),
         "dmhip_device_name": ([_vp, ctypes.c_char_p, _sz], ctypes.c_int),
@@ -144,6 +174,8 @@ def load_library() -> ctypes.CDLL:
         "dmhip_matvec_valu_device": ([_vp, _u32, _sz, _sz, _vp, _vp, _vp], ctypes.c_int),
         "dmhip_expert_cache_new": ([_vp, _vp, _sz, ctypes.POINTER(_Layout), _sz, _sz, ctypes.POINTER(_vp)],
                                    ctypes.c_int),
+        "dmhip_expert_cache_new_file": ([_vp, ctypes.c_int, ctypes.POINTER(_Layout), _sz, _sz,
+                                         ctypes.POINTER(_vp)], ctypes.c_int),
         "dmhip_expert_cache_free": ([_vp], None),
         "dmhip_expert_cache_stats_get": ([_vp, ctypes.POINTER(_Stats)], ctypes.c_int),
         "dmhip_expert_cache_slots_per_layer": ([_vp], _sz),
@@ -163,8 +195,11 @@ def load_library() -> ctypes.CDLL:
 
 def _check(code: int) -> None:
     if code != 0:
-        msg = load_library().dmhip_last_error()
-        raise HipError(code, msg.decode() if msg else "")
+        lib = load_library()
+        msg = lib.dmhip_last_error()
+        d = _Detail()
+        lib.dmhip_last_error_detail(ctypes.byref(d))
+        raise HipError(code, msg.decode() if msg else "", d.as_dict() if d.status == code else {})
 
 
 def _f32(a) -> np.ndarray:
@@ -228,6 +263,20 @@ class OwnedBuffer(_Buffer):
 class MappedBuffer(_Buffer):
     """MetalMappedBuffer (src/metal.rs:207-211, :280-288): a GGUF mapping
     uploaded to HBM once, offsets unchanged."""
+
+
+class SlotBuffer(OwnedBuffer):
+    """An expert slot's gate_up or down bytes, owned by the cache: the
+    &MetalOwnedBuffer the reference's with_expert closure receives
+    (src/expert.rs:138-164).  Valid while the slot is acquired; never freed
+    here."""
+
+    def __init__(self, ctx: "HipContext", handle: int):
+        self._ctx = ctx
+        self._h = _vp(handle)
+
+    def free(self) -> None:
+        self._h = _vp(None)
 
 
 class HipContext:
@@ -498,25 +547,38 @@ class ExpertLayerLayout:
 
 class ExpertCache:
     """ExpertCache (src/expert.rs:64-229): per-layer LRU of HBM slots filled
-    from host memory by asynchronous uploads."""
+    by asynchronous uploads, from host memory (`source` an array or a
+    PinnedHostBuffer) or from a file (`file`: an object with fileno(), or a
+    descriptor), as the reference's Arc<File>."""
 
-    def __init__(self, ctx: HipContext, source, layouts: Sequence[ExpertLayerLayout], slots_per_layer: int):
+    def __init__(self, ctx: HipContext, source, layouts: Sequence[ExpertLayerLayout], slots_per_layer: int,
+                 file=None):
         self._ctx = ctx
-        if isinstance(source, PinnedHostBuffer):
-            self._source = source
-            addr, n = source.address, source.nbytes
-        else:
-            arr = np.ascontiguousarray(source, dtype=np.uint8)
-            self._source = arr
-            addr, n = arr.ctypes.data, arr.size
         lay = (_Layout * max(len(layouts), 1))()
         for i, l in enumerate(layouts):
             lay[i] = _Layout(l.expert_count, l.gate_up_offset, l.gate_up_bytes, l.down_offset, l.down_bytes)
         h = _vp()
-        _check(load_library().dmhip_expert_cache_new(ctx.handle, addr, n, lay, len(layouts), slots_per_layer,
-                                                     ctypes.byref(h)))
+        if file is not None:
+            self._source = file  # keeps the descriptor's owner alive
+            fd = file if isinstance(file, int) else file.fileno()
+            _check(load_library().dmhip_expert_cache_new_file(ctx.handle, fd, lay, len(layouts), slots_per_layer,
+                                                              ctypes.byref(h)))
+        else:
+            if isinstance(source, PinnedHostBuffer):
+                self._source = source
+                addr, n = source.address, source.nbytes
+            else:
+                arr = np.ascontiguousarray(source, dtype=np.uint8)
+                self._source = arr
+                addr, n = arr.ctypes.data, arr.size
+            _check(load_library().dmhip_expert_cache_new(ctx.handle, addr, n, lay, len(layouts), slots_per_layer,
+                                                         ctypes.byref(h)))
         self._h = h
         ctx._children.add(self)
+
+    @classmethod
+    def from_file(cls, ctx: HipContext, file, layouts: Sequence[ExpertLayerLayout], slots_per_layer: int):
+        return cls(ctx, None, layouts, slots_per_layer, file=file)
 
     @property
     def handle(self):
@@ -530,22 +592,33 @@ class ExpertCache:
         _check(load_library().dmhip_expert_cache_stats_get(self._h, ctypes.byref(s)))
         return {n: getattr(s, n) for n, _ in _Stats._fields_}
 
-    def with_expert(self, layer: int, expert: int, cancelled: Callable[[], bool], use_expert):
-        """src/expert.rs:138-164: cancellation checked before and after the
-        acquire; the slot stays pinned while `use_expert(gate_up_ptr,
-        down_ptr, slot)` enqueues its work."""
-        flag = ctypes.c_int(1 if cancelled() else 0)
+    def acquire(self, layer: int, expert: int, cancelled: bool = False):
+        """dmhip_expert_acquire: (slot, gate_up SlotBuffer, down SlotBuffer),
+        the slot pinned until release()."""
+        flag = ctypes.c_int(1 if cancelled else 0)
         slot = ctypes.c_size_t()
         gu = _vp()
         dn = _vp()
         _check(load_library().dmhip_expert_acquire(self._h, layer, expert, ctypes.byref(flag),
                                                    ctypes.byref(slot), ctypes.byref(gu), ctypes.byref(dn)))
+        return slot.value, SlotBuffer(self._ctx, gu.value), SlotBuffer(self._ctx, dn.value)
+
+    def release(self, layer: int, slot: int) -> None:
+        _check(load_library().dmhip_expert_release(self._h, layer, slot))
+
+    def with_expert(self, layer: int, expert: int, cancelled: Callable[[], bool], use_expert):
+        """src/expert.rs:138-164: cancellation checked before and after the
+        acquire; the slot stays pinned while `use_expert(gate_up, down)`
+        (the slot's SlotBuffers) enqueues its work."""
+        if cancelled():
+            raise HipError(22, "expert loading was cancelled")
+        slot, gu, dn = self.acquire(layer, expert, False)
         try:
             if cancelled():
                 raise HipError(22, "expert loading was cancelled")
-            return use_expert(gu.value, dn.value, slot.value)
+            return use_expert(gu, dn)
         finally:
-            _check(load_library().dmhip_expert_release(self._h, layer, slot.value))
+            self.release(layer, slot)
 
     def free(self):
         if getattr(self, "_h", None):

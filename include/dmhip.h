@@ -63,8 +63,47 @@ typedef enum dmhip_status {
     DMHIP_ERR_ALL_SLOTS_PINNED = 21,     /* ExpertCacheError::AllSlotsPinned */
     DMHIP_ERR_CANCELLED = 22,            /* ExpertCacheError::Cancelled */
     DMHIP_ERR_INVALID_LAYOUT = 23,       /* ExpertCacheError::InvalidLayout */
-    DMHIP_ERR_INVALID_ARGUMENT = 24      /* a null handle or pointer */
+    DMHIP_ERR_INVALID_ARGUMENT = 24,     /* a null handle or pointer, or a C-API misuse */
+    DMHIP_ERR_IO = 25                    /* ExpertCacheError::Io (a failed or short pread) */
 } dmhip_status;
+
+/* The payload of the calling thread's last failure: the fields of the
+   MetalError / ExpertCacheError variant its status mirrors (src/metal.rs:3-126,
+   src/expert.rs:13-42), so a binding can rebuild the variant exactly.  Fields
+   a variant does not use are zero / NULL.  The strings are static (they live
+   as long as the library).
+     BufferAllocation            bytes
+     VectorLength                left, right, output
+     EmptyInput                  operation
+     InvalidVectorLength         operation, argument, expected, actual
+     InvalidPositiveParameter    operation
+     NonFinite                   operation
+     UnsupportedTensorType       kind
+     InvalidElementCount         kind, elements, block_elements
+     InvalidByteLength           kind, expected, actual
+     InvalidInputLength          expected, actual
+     InvalidOutputLength         expected, actual
+     InvalidTopK                 k, length
+     MappedRange                 offset, end, length
+     InvalidLayer                layer, count
+     InvalidExpert               layer, expert, count
+     AllSlotsPinned              layer
+     Io                          os_error (an errno value; 0: unexpected end of file)
+     Command, InvalidLayout      the message (dmhip_last_error) */
+typedef struct dmhip_error_detail {
+    int32_t status;
+    int32_t os_error;
+    const char *operation;
+    const char *argument;
+    const char *kind;
+    uint64_t expected, actual;
+    uint64_t offset, end, length;
+    uint64_t left, right, output;
+    uint64_t elements, block_elements;
+    uint64_t k;
+    uint64_t bytes;
+    uint64_t layer, expert, count;
+} dmhip_error_detail;
 
 /* ggml tensor type ids accepted by the matvec entry points. */
 enum {
@@ -86,6 +125,8 @@ typedef struct dmhip_expert_cache dmhip_expert_cache;
 
 /* Last failure message on the calling thread ("" if none). */
 const char *dmhip_last_error(void);
+/* Payload of the calling thread's last failure (status DMHIP_OK if none). */
+int dmhip_last_error_detail(dmhip_error_detail *out);
 
 /* MetalContext::new (src/metal.rs:291-346): selects HIP device `device`,
    creates its compute stream and its upload stream (default priority). */
@@ -303,8 +344,11 @@ typedef struct dmhip_expert_layer_layout {
     size_t down_bytes;
 } dmhip_expert_layer_layout;
 
-/* ExpertCacheStats (src/expert.rs:53-62). io_wait is nanoseconds the host
-   waited for uploads to finish. */
+/* ExpertCacheStats (src/expert.rs:53-62).  io_wait_ns is the time spent
+   bringing missed experts in: for a file-backed cache the host's wall time in
+   the positional reads (and in waiting for a staging buffer), as
+   src/expert.rs:220 measures it; for a memory-backed cache, whose uploads the
+   host never waits for, the summed device-measured duration of the uploads. */
 typedef struct dmhip_expert_cache_stats {
     uint64_t hits;
     uint64_t misses;
@@ -315,30 +359,51 @@ typedef struct dmhip_expert_cache_stats {
     uint64_t resident_bytes;
 } dmhip_expert_cache_stats;
 
-/* ExpertCache::new (src/expert.rs:88-128).  The source is host memory holding
-   the expert tensors at the layout offsets (the reference reads them from the
-   GGUF file with pread; here the caller provides the bytes, ideally in pinned
-   memory from dmhip_host_alloc_pinned so uploads are asynchronous DMA).  Each
-   layer gets `slots_per_layer` HBM slots of gate_up_bytes + down_bytes. */
+/* ExpertCache::new (src/expert.rs:88-128) over host memory: `source` holds the
+   expert tensors at the layout offsets (ideally pinned memory from
+   dmhip_host_alloc_pinned, so that uploads are asynchronous DMA) and must
+   stay valid while the cache lives.  Each layer gets `slots_per_layer` HBM
+   slots of gate_up_bytes + down_bytes. */
 int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len,
                            const dmhip_expert_layer_layout *layouts, size_t layer_count,
                            size_t slots_per_layer, dmhip_expert_cache **out);
+
+/* ExpertCache::new (src/expert.rs:88-128) over a file, the reference's
+   Arc<File>: a miss reads the expert's gate_up and down ranges (absolute
+   file offsets, src/expert.rs:203-215) with two parallel positional reads
+   into one of four pinned staging buffers and copies it into the slot
+   asynchronously, so host memory stays bounded by the ring.  The descriptor
+   must stay open while the cache lives.  A short file is found when an
+   expert is first read: that acquire fails with Io (os_error 0, unexpected
+   end of file), as read_exact_at does (src/expert.rs:241-256). */
+int dmhip_expert_cache_new_file(dmhip_ctx *ctx, int fd, const dmhip_expert_layer_layout *layouts,
+                                size_t layer_count, size_t slots_per_layer, dmhip_expert_cache **out);
+
+/* Frees the slots after waiting for the cache's own uploads and for the
+   work released from its slots. */
 void dmhip_expert_cache_free(dmhip_expert_cache *cache);
-int dmhip_expert_cache_stats_get(const dmhip_expert_cache *cache,
-                                 dmhip_expert_cache_stats *stats);
+/* ExpertCache::stats (src/expert.rs:130-132); waits for uploads in flight so
+   that their duration is part of io_wait_ns. */
+int dmhip_expert_cache_stats_get(dmhip_expert_cache *cache, dmhip_expert_cache_stats *stats);
 size_t dmhip_expert_cache_slots_per_layer(const dmhip_expert_cache *cache);
 
 /* ExpertCache::with_expert, split into acquire/release for a C caller
-   (src/expert.rs:138-164).  acquire: checks `cancelled` (may be NULL) before
-   and after, finds or loads the expert into a slot (LRU of
-   src/expert.rs:166-229; a miss enqueues the upload on the upload stream and
-   makes the compute stream wait for it), pins the slot and returns the device
-   addresses of its gate_up and down bytes.  Work that reads the slot must be
-   enqueued on the compute stream before release.  release: unpins the slot;
-   a later upload into it waits for that work. */
+   (src/expert.rs:138-164).  acquire checks `cancelled` (may be NULL) before
+   and after, finds or loads the expert into a slot (the LRU of
+   src/expert.rs:166-229; a miss enqueues the upload and makes the compute
+   stream wait for it), pins the slot and returns its gate_up and down bytes
+   as buffers owned by the cache -- the &MetalOwnedBuffer pair the reference
+   hands its closure, usable with dmhip_matvec_owned and dmhip_buffer_read
+   (dmhip_buffer_free ignores them).  Work that reads the slot must be
+   enqueued on the context's compute stream (every entry point of the
+   context does) before the matching release.  Pins count: each acquire
+   needs its own release, and a pinned slot is never evicted (all slots of
+   the layer pinned: AllSlotsPinned).  release records the end of the work
+   enqueued so far as the slot's last use (a later upload into it waits for
+   it) and drops one pin; releasing an unpinned slot is InvalidArgument. */
 int dmhip_expert_acquire(dmhip_expert_cache *cache, size_t layer, size_t expert,
-                         const volatile int *cancelled, size_t *slot, const void **gate_up,
-                         const void **down);
+                         const volatile int *cancelled, size_t *slot, const dmhip_buf **gate_up,
+                         const dmhip_buf **down);
 int dmhip_expert_release(dmhip_expert_cache *cache, size_t layer, size_t slot);
 
 /* One routed-expert layer at decode for `batch` tokens (1..16), the

@@ -605,9 +605,10 @@ def test_expert_cache_known_answer(ctx, golden):
     cache = ExpertCache(ctx, src, [ExpertLayerLayout(**lay)], c["slots_per_layer"])
     assert cache.slots_per_layer() == 1
     for layer, expert, gate, down in c["accesses"]:
-        def use(gu_ptr, dn_ptr, slot):
-            assert ctx.copy_to_host(gu_ptr, 4).tolist() == gate
-            assert ctx.copy_to_host(dn_ptr, 4).tolist() == down
+        def use(gate_up, down_buf):
+            # the closure of src/expert.rs:290-298: gate.as_bytes(), down.as_bytes()
+            assert gate_up.as_bytes().tolist() == gate
+            assert down_buf.as_bytes().tolist() == down
         cache.with_expert(layer, expert, lambda: False, use)
     st = cache.stats()
     for key, value in c["expected_stats"].items():
@@ -624,6 +625,202 @@ def test_expert_cache_known_answer(ctx, golden):
     with pytest.raises(HipError) as e:
         ExpertCache(ctx, src, [ExpertLayerLayout(**lay)], 0)
     assert e.value.variant == "NoSlots"
+
+
+def _expert_source(experts=16, hidden=2048, width=768, seed=4):
+    gu_bytes = 2 * width * synth.row_bytes(Q4_K, hidden)
+    dn_bytes = hidden * synth.row_bytes(Q6_K, width)
+    gu = synth.quantized_matrix(Q4_K, experts * 2 * width, hidden, synth.weight_seed(seed, 0))
+    dn = synth.quantized_matrix(Q6_K, experts * hidden, width, synth.weight_seed(seed, 1))
+    # a 64-byte file header in front, so offsets are absolute file offsets
+    blob = np.concatenate([np.full(64, 0x5A, np.uint8), gu, dn])
+    layout = ExpertLayerLayout(experts, 64, gu_bytes, 64 + gu.size, dn_bytes)
+    return blob, layout, gu, dn, gu_bytes, dn_bytes
+
+
+def test_acquired_slots_feed_matvec_owned(ctx):
+    """The drop-in path of src/gemma4/metal.rs:972-1031: with_expert hands the
+    slot's gate_up and down buffers to a closure that runs matvec_owned on
+    them (offset 0, the expert's byte length); the results match the oracle's
+    matvec of that expert, and a range past the slot is MappedRange
+    (src/metal.rs:1161-1168)."""
+    hidden, width = 2048, 768
+    blob, layout, gu, dn, gu_bytes, dn_bytes = _expert_source(hidden=hidden, width=width)
+    cache = ExpertCache(ctx, blob, [layout], 2)
+    x = synth.normal(synth.activation_seed(4, 77), hidden)
+    for expert in (3, 11, 3):
+        gu_e = gu[expert * gu_bytes:(expert + 1) * gu_bytes]
+        dn_e = dn[expert * dn_bytes:(expert + 1) * dn_bytes]
+        want_gu = capi.matvec(Q4_K, 2 * width, hidden, gu_e, x)
+        act = synth.normal(synth.activation_seed(4, expert), width)
+        want_dn = capi.matvec(Q6_K, hidden, width, dn_e, act)
+
+        def closure(gate_up, down):
+            assert len(gate_up) == gu_bytes and len(down) == dn_bytes
+            out = np.zeros(2 * width, np.float32)
+            ctx.matvec_owned(Q4_K, 2 * width, hidden, gate_up, 0, gu_bytes, x, out)
+            out2 = np.zeros(hidden, np.float32)
+            ctx.matvec_owned(Q6_K, hidden, width, down, 0, dn_bytes, act, out2)
+            with pytest.raises(HipError) as e:
+                ctx.matvec_owned(Q6_K, hidden // 2, width, down, dn_bytes // 2 + 630, dn_bytes // 2, act,
+                                 np.zeros(hidden // 2, np.float32))
+            assert e.value.variant == "MappedRange"
+            assert e.value.detail == {"offset": dn_bytes // 2 + 630, "end": dn_bytes + 630, "length": dn_bytes}
+            return out, out2
+
+        got_gu, got_dn = cache.with_expert(0, expert, lambda: False, closure)
+        assert_close(got_gu, want_gu, f"expert {expert} gate_up")
+        assert_close(got_dn, want_dn, f"expert {expert} down")
+    st = cache.stats()
+    assert (st["hits"], st["misses"], st["evictions"]) == (1, 2, 0)
+    cache.free()
+
+
+def test_slot_reuse_waits_for_the_previous_expert_s_readers(ctx):
+    """One slot.  Many GEMVs that read expert A's slot are enqueued (device
+    entry points, nothing waits), then A is released and B acquired into the
+    same slot: B's upload must wait for A's readers, so every A output still
+    equals the oracle's, and B's bytes are B's."""
+    hidden, width = 2048, 768
+    blob, layout, gu, dn, gu_bytes, dn_bytes = _expert_source(hidden=hidden, width=width)
+    cache = ExpertCache(ctx, blob, [layout], 1)
+    x = synth.normal(synth.activation_seed(4, 88), hidden)
+    xb = dev(ctx, x)
+    reps = 64
+    out = dev_out(ctx, reps * 2 * width * 4)
+    slot, g, d = cache.acquire(0, 5)
+    for r in range(reps):
+        ctx.matvec_device(Q4_K, 2 * width, hidden, g.device_ptr, 1, xb.device_ptr, out.device_ptr + r * 2 * width * 4)
+    cache.release(0, slot)
+    slot2, g2, d2 = cache.acquire(0, 9)
+    assert slot2 == slot and g2.device_ptr == g.device_ptr
+    want_a = capi.matvec(Q4_K, 2 * width, hidden, gu[5 * gu_bytes:6 * gu_bytes], x)
+    got = out.read(0, reps * 2 * width * 4, np.float32).reshape(reps, 2 * width)
+    for r in range(reps):
+        assert np.array_equal(got[r], got[0]), f"launch {r} read other bytes"
+    assert_close(got[0], want_a, "expert A through its released slot")
+    assert np.array_equal(g2.as_bytes(), gu[9 * gu_bytes:10 * gu_bytes])
+    assert np.array_equal(d2.as_bytes(), dn[9 * dn_bytes:10 * dn_bytes])
+    cache.release(0, slot2)
+    cache.free()
+
+
+def test_pinned_slots_are_never_evicted(ctx):
+    """AllSlotsPinned when every slot of the layer is held; pins count (two
+    acquires of one expert need two releases); releasing an unpinned slot is
+    rejected."""
+    blob, layout, gu, dn, gu_bytes, dn_bytes = _expert_source(experts=4, hidden=256, width=256)
+    cache = ExpertCache(ctx, blob, [layout], 1)
+    slot, g, _ = cache.acquire(0, 1)
+    slot_again, _, _ = cache.acquire(0, 1)  # a hit on the pinned slot
+    assert slot_again == slot
+    with pytest.raises(HipError) as e:
+        cache.acquire(0, 2)
+    assert e.value.variant == "AllSlotsPinned" and e.value.detail == {"layer": 0}
+    cache.release(0, slot)
+    with pytest.raises(HipError) as e:
+        cache.acquire(0, 2)  # still pinned once
+    assert e.value.variant == "AllSlotsPinned"
+    cache.release(0, slot)
+    s2, g2, _ = cache.acquire(0, 2)
+    assert np.array_equal(g2.as_bytes(), gu[2 * gu_bytes:3 * gu_bytes])
+    cache.release(0, s2)
+    with pytest.raises(HipError) as e:
+        cache.release(0, s2)
+    assert e.value.variant == "InvalidArgument"
+    with pytest.raises(HipError) as e:
+        cache.acquire(0, 4)
+    assert e.value.variant == "InvalidExpert" and e.value.detail == {"layer": 0, "expert": 4, "count": 4}
+    st = cache.stats()
+    # src/expert.rs:166-229 counts: a miss (1), a hit, a refused miss, a refused
+    # miss, a miss evicting 1; the refused misses count as misses with no read
+    assert (st["hits"], st["misses"], st["evictions"], st["reads"]) == (1, 4, 1, 4)
+    cache.free()
+
+
+def test_file_backed_cache_matches_the_memory_backed_one(ctx, tmp_path):
+    """ExpertCache over a file (the reference's Arc<File>, positional reads
+    into pinned staging): C4 through moe_layer gives the same ids, outputs and
+    LRU counters as the memory-backed cache; io_wait is the host's read time
+    (positive); an expert past the end of the file fails with Io (unexpected
+    end of file) and counts a miss but no read."""
+    hidden, width, experts, k, batch = 2048, 768, 16, 4, 4
+    blob, layout, gu, dn, gu_bytes, dn_bytes = _expert_source(experts=experts, hidden=hidden, width=width)
+    path = tmp_path / "experts.bin"
+    blob.tofile(path)
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(4, 5), experts * hidden) * np.float32(0.02))
+    rb = dev(ctx, router)
+    mem = ExpertCache(ctx, blob, [layout], 3)
+    with open(path, "rb") as f:
+        fil = ExpertCache.from_file(ctx, f, [layout], 3)
+        ys = []
+        for cache in (mem, fil):
+            yb = dev_out(ctx, batch * hidden * 4)
+            outs = []
+            for step in range(3):
+                x = synth.normal(synth.activation_seed(4, 300 + step), batch * hidden)
+                ids, probs = ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                                           dev(ctx, x).device_ptr, yb.device_ptr)
+                outs.append((ids, probs, yb.read(0, batch * hidden * 4, np.float32)))
+            ys.append(outs)
+        for (i1, p1, y1), (i2, p2, y2) in zip(*ys):
+            assert np.array_equal(i1, i2) and np.array_equal(p1, p2)
+            assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+        sm, sf = mem.stats(), fil.stats()
+        for key in ("hits", "misses", "evictions", "reads", "bytes_read", "resident_bytes"):
+            assert sm[key] == sf[key], key
+        assert sf["io_wait_ns"] > 0 and sm["io_wait_ns"] > 0
+        x = synth.normal(synth.activation_seed(4, 300), batch * hidden).reshape(batch, hidden)
+        _, _, want = capi.moe_layer(batch, hidden, width, experts, k, router, Q4_K, gu, Q6_K, dn, x)
+        for t in range(batch):
+            assert_close(ys[1][0][2].reshape(batch, hidden)[t], want[t], f"file-backed token {t}")
+        fil.free()
+    # a layout that claims one more expert than the file holds
+    short = ExpertLayerLayout(experts + 1, layout.gate_up_offset, gu_bytes, layout.down_offset, dn_bytes)
+    with open(path, "rb") as f:
+        cache = ExpertCache.from_file(ctx, f, [short], 2)
+        with pytest.raises(HipError) as e:
+            cache.acquire(0, experts)
+        assert e.value.variant == "Io" and e.value.detail == {"os_error": 0}
+        st = cache.stats()
+        assert (st["misses"], st["reads"], st["bytes_read"]) == (1, 0, 0)
+        slot, g, d = cache.acquire(0, 0)
+        assert np.array_equal(g.as_bytes(), gu[:gu_bytes]) and np.array_equal(d.as_bytes(), dn[:dn_bytes])
+        cache.release(0, slot)
+        cache.free()
+    mem.free()
+
+
+def test_error_payloads_carry_the_variant_fields(ctx):
+    """dmhip_last_error_detail: each validation variant carries the fields of
+    its MetalError counterpart (src/metal.rs:3-126)."""
+    x = np.zeros(256, np.float32)
+    enc = np.zeros(144, np.uint8)
+    out = np.zeros(1, np.float32)
+    cases = [
+        (lambda: ctx.matvec(Q4_K, 1, 256, enc, x[:10], out), "InvalidInputLength", {"expected": 256, "actual": 10}),
+        (lambda: ctx.matvec(Q4_K, 1, 256, enc, x, np.zeros(2, np.float32)), "InvalidOutputLength",
+         {"expected": 1, "actual": 2}),
+        (lambda: ctx.matvec(13, 1, 256, np.zeros(176, np.uint8), x, out), "UnsupportedTensorType",
+         {"kind": "Q5_K"}),
+        (lambda: ctx.matvec(Q4_K, 1, 100, enc, x[:100], out), "InvalidElementCount",
+         {"kind": "Q4_K", "elements": 100, "block_elements": 256}),
+        (lambda: ctx.matvec(Q4_K, 1, 256, enc[:100], x, out), "InvalidByteLength",
+         {"kind": "Q4_K", "expected": 144, "actual": 100}),
+        (lambda: ctx.argmax([]), "EmptyInput", {"operation": "argmax"}),
+        (lambda: ctx.argmax([1.0, np.inf]), "NonFinite", {"operation": "argmax"}),
+        (lambda: ctx.top_k_softmax([1.0, 2.0], 3), "InvalidTopK", {"k": 3, "length": 2}),
+        (lambda: ctx.rms_norm([1.0, 2.0], [1.0], 1e-6, np.zeros(2, np.float32)), "InvalidVectorLength",
+         {"operation": "RMSNorm", "argument": "weight", "expected": 2, "actual": 1}),
+        (lambda: ctx.rms_norm([1.0, 2.0], None, 0.0, np.zeros(2, np.float32)), "InvalidPositiveParameter",
+         {"operation": "RMSNorm epsilon"}),
+        (lambda: ctx.new_owned_buffer(0), "BufferAllocation", {"bytes": 0}),
+    ]
+    for fn, variant, detail in cases:
+        with pytest.raises(HipError) as e:
+            fn()
+        assert e.value.variant == variant, (variant, e.value)
+        assert e.value.detail == detail, (variant, e.value.detail)
 
 
 @pytest.mark.parametrize("batch", [1, 4, 16])

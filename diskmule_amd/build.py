@@ -2,11 +2,15 @@
 
 Every HIP source is compiled for gfx950 only, with FMA contraction off (all
 fused multiply-adds in the kernels are explicit) and without packed-FP32
-instruction selection.
+instruction selection.  The build fails if any kernel uses scratch (private
+memory): register spills cost bandwidth, and the first launch of such a
+kernel makes the runtime allocate scratch backing, which the
+allocation-free entry point promises never happens.
 """
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
 
@@ -18,7 +22,8 @@ SOURCES = ["runtime.hip", "dispatch.hip", "kernels_simple.hip", "kernels_qmv.hip
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-         "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
+         "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+         "-Rpass-analysis=kernel-resource-usage"]
 # Extra hipcc flags per source file (none at present).
 SOURCE_FLAGS: dict = {}
 
@@ -46,16 +51,35 @@ def build(verbose: bool = False, jobs: int = 6) -> str:
     return LIB
 
 
+def scratch_users(text: str) -> list:
+    """Kernels whose resource-usage remarks report scratch bytes per lane."""
+    users, name = [], None
+    for line in text.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            users.append(f"{name} ({m.group(1)} bytes/lane)")
+    return users
+
+
 def _drain(procs, verbose):
     failed = None
     for cmd, p in procs:
         out, _ = p.communicate()
         text = out.decode(errors="replace")
-        # hipcc's host pass does not know the packed-fp32 feature: harmless.
-        lines = [l for l in text.splitlines() if "packed-fp32-ops" not in l]
+        # hipcc's host pass does not know the packed-fp32 feature: harmless;
+        # the resource-usage remarks are read, not shown.
+        lines = [l for l in text.splitlines()
+                 if "packed-fp32-ops" not in l and "remark:" not in l and not re.match(r"^\s*(\d+\s*)?\|", l)]
         if verbose or p.returncode:
             sys.stderr.write("\n".join(lines) + ("\n" if lines else ""))
         if p.returncode and failed is None:
+            failed = cmd
+        spills = scratch_users(text)
+        if spills and failed is None:
+            sys.stderr.write("kernels using scratch:\n  " + "\n  ".join(spills) + "\n")
             failed = cmd
     procs.clear()
     if failed:

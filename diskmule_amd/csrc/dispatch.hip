@@ -3,9 +3,40 @@
 
 #include <math.h>
 
+#include <atomic>
+
 #include "dm_qmv.h"
 
 namespace dm {
+
+// Device memory of the allocation-free FFN entry point: a fixed array in the
+// code object, so each GPU that loads the library holds its own copy until
+// the process ends.  In host code `scratch` names a host-side stand-in, not
+// a device address: the address of a device's copy comes from
+// hipGetSymbolAddress (noalloc_resolve), once per device, and only that
+// address is handed to kernels.
+constexpr size_t kNoAllocScratchBytes = 8u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static std::atomic<void *> g_scratch_address[64];
+
+int noalloc_resolve(int device) {
+    if (device < 0 || device >= 64) return fail(DMHIP_ERR_NO_DEVICE, "device %d is outside 0..63", device);
+    // Every code object of the library is loaded onto the device here, at
+    // set-up: the runtime loads one (and allocates its device memory) when
+    // one of its kernels is first resolved, which must not happen inside an
+    // allocation-free call.
+    for (const void *anchor : {module_anchor_simple(), module_anchor_qmv(), module_anchor_qmv8(),
+                               module_anchor_qmv_valu(), module_anchor_gemm(), module_anchor_expert()}) {
+        hipFuncAttributes attr;
+        DM_HIP(hipFuncGetAttributes(&attr, anchor));
+    }
+    if (g_scratch_address[device].load(std::memory_order_acquire)) return DMHIP_OK;
+    void *ptr = nullptr;
+    DM_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) return fail(DMHIP_ERR_COMMAND, "no device address for the allocation-free scratch on device %d", device);
+    g_scratch_address[device].store(ptr, std::memory_order_release);
+    return DMHIP_OK;
+}
 
 int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, const void *w,
                    size_t batch, const float *x, float *y) {
@@ -68,6 +99,48 @@ size_t dmhip_ffn_workspace_bytes(size_t batch, size_t hidden, size_t ffn) {
         total += bytes;
     }
     return total;
+}
+
+size_t dmhip_ffn_noalloc_scratch_bytes(void) { return dm::kNoAllocScratchBytes; }
+
+int dmhip_ffn_device_noalloc(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn, uint32_t gate_type,
+                             const void *gate, uint32_t up_type, const void *up, uint32_t down_type,
+                             const void *down, float epsilon, const float *h, float *y) {
+    if (!ctx) return fail(DMHIP_ERR_INVALID_ARGUMENT, "ctx must not be null");
+    if (batch < 1 || batch > 16)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT, "batch %zu is outside 1..=16", batch);
+    const size_t ws = dmhip_ffn_workspace_bytes(batch, hidden, ffn);
+    // batches above 2 prepare activation fragments of h (gate/up) and of the
+    // activation rows (down); the larger of the two regions is lent
+    size_t lend = 0;
+    if (batch > 2) {
+        const uint32_t types[2] = {gate_type, down_type};
+        const size_t cols[2] = {hidden, ffn};
+        for (int i = 0; i < 2; i++) {
+            const size_t b = qmv_prepare_bytes(types[i], cols[i], batch);
+            lend = b > lend ? b : lend;
+        }
+    }
+    if (ws == 0 || ws > kNoAllocScratchBytes || lend > kNoAllocScratchBytes - ws)
+        return fail(DMHIP_ERR_INVALID_ARGUMENT,
+                    "FFN of batch %zu, hidden %zu, ffn %zu needs %zu scratch bytes; the allocation-free entry "
+                    "point holds %zu",
+                    batch, hidden, ffn, ws + lend, kNoAllocScratchBytes);
+    const int device = ctx->device;
+    void *base = (device >= 0 && device < 64) ? g_scratch_address[device].load(std::memory_order_acquire) : nullptr;
+    if (!base) return fail(DMHIP_ERR_COMMAND, "the allocation-free scratch of device %d is not resolved", device);
+    // the fp16 path's fragments go to the lent region for this call only
+    struct Lend {
+        dmhip_ctx *c;
+        ~Lend() {
+            c->aux_lent = nullptr;
+            c->aux_lent_bytes = 0;
+        }
+    } guard{ctx};
+    ctx->aux_lent = batch > 2 ? (char *)base + ws : nullptr;
+    ctx->aux_lent_bytes = batch > 2 ? lend : 0;
+    return dmhip_ffn_device(ctx, batch, hidden, ffn, gate_type, gate, up_type, up, down_type, down, epsilon, h, y,
+                           base, ws);
 }
 
 int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn, uint32_t gate_type,

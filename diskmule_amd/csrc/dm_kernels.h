@@ -40,6 +40,15 @@ struct ArgmaxState {
     uint32_t done;  // waves that have folded their key in (fused argmax)
 };
 
+// One kernel of each source file (each file is its own code object, which
+// the runtime loads onto a device when one of its kernels is first used).
+const void *module_anchor_simple();
+const void *module_anchor_qmv();
+const void *module_anchor_qmv8();
+const void *module_anchor_qmv_valu();
+const void *module_anchor_gemm();
+const void *module_anchor_expert();
+
 hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t n);
 // Launch-floor probes: an empty kernel; a read of n bytes (16-byte aligned
 // src; bytes past the last whole 16 are not read).

@@ -78,6 +78,10 @@ hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uin
 // whole 256-value super-blocks at a 16-byte aligned base, batch 1-2.
 bool qmv_supported(uint32_t type, size_t rows, size_t columns, const void *w, size_t batch);
 
+// Bytes of the activation fragments the fp16 kernel prepares for `batch`
+// tokens (batches above 2) of rows of `columns` values.
+size_t qmv_prepare_bytes(uint32_t type, size_t columns, size_t batch);
+
 // y[b][r] = W[r] . x[b]; when `argmax` is non-null (batch 1) the kernels
 // also reset `argmax`, fold a greedy argmax over the rows into it and write
 // the winning row to *index_out.

@@ -114,28 +114,31 @@ template <uint32_t TYPE>
 __device__ __forceinline__ void build_fragment(const float *xt, uint32_t blk, uint32_t t, uint32_t kg,
                                                float down, half8 &hi, half8 &lo) {
     const float *xb = xt + (size_t)blk * 256;
+    // the halves are gathered in scalars and the vectors built once (element
+    // inserts across the branch put the vectors in private memory)
+    _Float16 h[8], l[8];
     if (TYPE == kQ4_K && t == 8) {
-        hi = half8{0, 0, 0, 0, 0, 0, 0, 0};
-        lo = half8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const float *sb = xb + 32 * (2 * kg + j);
             float s = 0.0f;
             for (int i = 0; i < 32; i++) s += sb[i] * down;
             s = s * 0.015625f;  // 2^-6 keeps |sum| inside fp16
-            const _Float16 h = (_Float16)s;
-            hi[j] = h;
-            lo[j] = (_Float16)(s - (float)h);
+            h[j] = (_Float16)s;
+            l[j] = (_Float16)(s - (float)h[j]);
         }
+#pragma unroll
+        for (int j = 2; j < 8; j++) h[j] = l[j] = (_Float16)0.0f;
     } else {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const float v = xb[fragment_column<TYPE>(kg, t, j)] * down;
-            const _Float16 h = (_Float16)v;
-            hi[j] = h;
-            lo[j] = (_Float16)(v - (float)h);
+            h[j] = (_Float16)v;
+            l[j] = (_Float16)(v - (float)h[j]);
         }
     }
+    hi = half8{h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+    lo = half8{l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
 }
 
 }  // namespace
@@ -835,22 +838,35 @@ template <uint32_t TYPE, int MODE>
 hipError_t dispatch(dmhip_ctx *ctx, const Plan &p, const Args &a, uint32_t *w) {
     if (p.mb == 2) return run_s<TYPE, 1, 1, MODE, 2>(ctx, p, a, w);
     if (p.mb == 4) return run_s<TYPE, 1, 1, MODE, 4>(ctx, p, a, w);
-    if (p.nt == 1)
-        return p.r == 1 ? run_s<TYPE, 1, 1, MODE, 0>(ctx, p, a, w) : run_s<TYPE, 1, 2, MODE, 0>(ctx, p, a, w);
-    return p.r == 1 ? run_s<TYPE, 2, 1, MODE, 0>(ctx, p, a, w) : run_s<TYPE, 2, 2, MODE, 0>(ctx, p, a, w);
+    if constexpr (MODE == 2) {
+        // the gate/up pair already streams two matrices: one tile per wave
+        return p.nt == 1 ? run_s<TYPE, 1, 1, MODE, 0>(ctx, p, a, w) : run_s<TYPE, 2, 1, MODE, 0>(ctx, p, a, w);
+    } else {
+        if (p.nt == 1)
+            return p.r == 1 ? run_s<TYPE, 1, 1, MODE, 0>(ctx, p, a, w) : run_s<TYPE, 1, 2, MODE, 0>(ctx, p, a, w);
+        return p.r == 1 ? run_s<TYPE, 2, 1, MODE, 0>(ctx, p, a, w) : run_s<TYPE, 2, 2, MODE, 0>(ctx, p, a, w);
+    }
 }
 
-// Activation fragments for batches above 2 go to the context's aux scratch:
+// Activation fragments for batches above 2 go to the context's aux scratch
+// (or, during an allocation-free call, to the scratch it lent the context):
 // [xp | yscale], written by the preparation kernel.
 hipError_t prepare(dmhip_ctx *ctx, uint32_t type, uint32_t columns, uint32_t batch, const float *x,
                    int normalize, float eps, _Float16 **xp_out, float **ysc_out) {
     const uint32_t spb = type == kQ4_K ? 9 : 8;
     const size_t frags = (size_t)(columns / 256) * spb * 4;
     const size_t xp_bytes = frags * 2 * batch * 8 * sizeof(_Float16);
-    if (ctx->aux.ensure(((xp_bytes + 255) & ~(size_t)255) + 64 * sizeof(float)) != DMHIP_OK)
-        return hipErrorOutOfMemory;
-    _Float16 *xp = (_Float16 *)ctx->aux.ptr;
-    float *ysc = (float *)((char *)ctx->aux.ptr + ((xp_bytes + 255) & ~(size_t)255));
+    const size_t need = ((xp_bytes + 255) & ~(size_t)255) + 64 * sizeof(float);
+    void *base;
+    if (ctx->aux_lent) {
+        if (need > ctx->aux_lent_bytes) return hipErrorOutOfMemory;
+        base = ctx->aux_lent;
+    } else {
+        if (ctx->aux.ensure(need) != DMHIP_OK) return hipErrorOutOfMemory;
+        base = ctx->aux.ptr;
+    }
+    _Float16 *xp = (_Float16 *)base;
+    float *ysc = (float *)((char *)base + ((xp_bytes + 255) & ~(size_t)255));
     uint32_t gx = (uint32_t)((frags + 255) / 256);
     if (gx > 64) gx = 64;
     const dim3 grid(gx, batch);
@@ -873,6 +889,16 @@ hipError_t prepare(dmhip_ctx *ctx, uint32_t type, uint32_t columns, uint32_t bat
     *ysc_out = ysc;
     return hipGetLastError();
 }
+
+}  // namespace
+
+size_t qmv_prepare_bytes(uint32_t type, size_t columns, size_t batch) {
+    const size_t spb = type == kQ4_K ? 9 : 8;
+    const size_t xp_bytes = (columns / 256) * spb * 4 * 2 * batch * 8 * sizeof(_Float16);
+    return ((xp_bytes + 255) & ~(size_t)255) + 64 * sizeof(float);
+}
+
+namespace {
 
 Args make_args(uint32_t type, uint32_t rows, uint32_t columns, const void *w, const void *w2,
                uint32_t batch, const float *x, int normalize, float epsilon, float *y) {
@@ -940,5 +966,8 @@ hipError_t launch_qmv_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint
     if (e != hipSuccess) return e;
     return type == kQ4_K ? dispatch<kQ4_K, 2>(ctx, p, a, nullptr) : dispatch<kQ6_K, 2>(ctx, p, a, nullptr);
 }
+
+// A kernel of this file: resolving it loads the file's code object.
+const void *module_anchor_qmv() { return (const void *)argmax_partials_kernel; }
 
 }  // namespace dm

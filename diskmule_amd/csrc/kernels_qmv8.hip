@@ -786,9 +786,17 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     }
 }
 
+// Register budget: four waves per SIMD (128 VGPRs), or two (256) for
+// four-block fetches and for the gate/up kernels that need more (Q6_K pairs,
+// two-token two-block fetches); with less they spill to scratch.
+template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
+constexpr int waves_per_eu8() {
+    return (G > 2 || (MODE == 2 && (TYPE == kQ6_K || (TOK == 2 && G == 2)))) ? 2 : 4;
+}
+
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W>
 __global__ void __launch_bounds__(64 * W)
-    __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2))) qmv8_kernel(
+    __attribute__((amdgpu_waves_per_eu(waves_per_eu8<TYPE, MODE, TOK, G>()))) qmv8_kernel(
     const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows, uint32_t columns,
     uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x, int normalize, float epsilon,
     float *__restrict__ y, ArgmaxPartial *__restrict__ partials, ArgmaxFinish finish, uint64_t *trace) {
@@ -811,8 +819,8 @@ struct JobTable8 {
 };
 
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
-__global__ void __launch_bounds__(64 * (S > 8 ? S : 8)) __attribute__((amdgpu_waves_per_eu(4)))
-    qmv8_grouped_kernel(JobTable8 jobs, uint32_t rows, uint32_t columns, uint32_t row_bytes,
+__global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
+    __attribute__((amdgpu_waves_per_eu(waves_per_eu8<TYPE, MODE, TOK, G>()))) qmv8_grouped_kernel(JobTable8 jobs, uint32_t rows, uint32_t columns, uint32_t row_bytes,
                         uint32_t total_bytes, uint64_t w2_offset, const float *__restrict__ x,
                         float *__restrict__ y, int glm) {
     const Job8 j = jobs.job[blockIdx.y];
@@ -877,7 +885,8 @@ Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint
     if (force_s || force_g) {
         const bool ok_s = force_s == 1 || force_s == 2 || force_s == 4 || force_s == 8 || force_s == 16;
         const bool ok_g = force_g == 1 || force_g == 2 || force_g == 4;
-        if (ok_s && ok_g && force_g <= blocks && fits8(type, blocks, batch, mats, force_s, force_g)) {
+        const bool pair_ok = (mats == 1 || (force_s <= 8 && force_g <= 2)) && (force_s <= 8 || force_g <= 2);
+        if (ok_s && ok_g && pair_ok && force_g <= blocks && fits8(type, blocks, batch, mats, force_s, force_g)) {
             p.s = force_s;
             p.g = force_g;
         }
@@ -886,8 +895,9 @@ Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint
     p.g = tiles >= 2048 ? 2u : 1u;
     while (p.g > 1 && blocks < 2 * p.g) p.g /= 2;
     const uint32_t groups = (blocks + p.g - 1) / p.g;
+    const uint32_t s_max = mats == 2 ? 8u : kMaxWaves8;  // gate/up: see run8_s
     uint32_t s = 1;
-    while (s < kMaxWaves8 && (size_t)tiles * s < 4096 && groups >= 2 * s) s *= 2;
+    while (s < s_max && (size_t)tiles * s < 4096 && groups >= 2 * s) s *= 2;
     for (; s >= 1; s /= 2)
         if (fits8(type, blocks, batch, mats, s, p.g)) {
             p.s = s;
@@ -952,13 +962,19 @@ hipError_t run8_s(dmhip_ctx *ctx, uint32_t s, const Args8 &a) {
     case 2: return run8<TYPE, 2, MODE, TOK, G>(ctx, a);
     case 4: return run8<TYPE, 4, MODE, TOK, G>(ctx, a);
     case 8: return run8<TYPE, 8, MODE, TOK, G>(ctx, a);
-    default: return run8<TYPE, 16, MODE, TOK, G>(ctx, a);
+    default:
+        // gate/up plans and four-block fetches stop at 8 waves (plan8): their
+        // registers do not fit the 16-wave workgroup's budget
+        if constexpr (MODE == 2 || G == 4) return hipErrorInvalidValue;
+        else return run8<TYPE, 16, MODE, TOK, G>(ctx, a);
     }
 }
 
 template <uint32_t TYPE, int MODE, int TOK>
 hipError_t run8_g(dmhip_ctx *ctx, const Plan8 &p, const Args8 &a) {
-    if (p.g == 4) return run8_s<TYPE, MODE, TOK, 4>(ctx, p.s, a);
+    if constexpr (MODE != 2) {
+        if (p.g == 4) return run8_s<TYPE, MODE, TOK, 4>(ctx, p.s, a);
+    }
     if (p.g == 2) return run8_s<TYPE, MODE, TOK, 2>(ctx, p.s, a);
     return run8_s<TYPE, MODE, TOK, 1>(ctx, p.s, a);
 }
@@ -1130,5 +1146,8 @@ hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uin
     }
     return hipSuccess;
 }
+
+// A kernel of this file: resolving it loads the file's code object.
+const void *module_anchor_qmv8() { return (const void *)qmv8_kernel<kQ4_K, 16, 0, 1, 1, 16>; }
 
 }  // namespace dm

@@ -211,4 +211,7 @@ hipError_t launch_qmv_valu(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_
     }
 }
 
+// A kernel of this file: resolving it loads the file's code object.
+const void *module_anchor_qmv_valu() { return (const void *)qmv_valu_q4k_kernel<16>; }
+
 }  // namespace dm

@@ -84,6 +84,10 @@ struct dmhip_ctx {
     int compute_units = 0;
     dm::Scratch in, out, enc, aux;          // host-slice staging
     dm::Scratch partials;                    // per-wave argmax candidates
+    // Device memory an allocation-free call lends the fp16 path in place of
+    // `aux` for its duration (null otherwise).
+    void *aux_lent = nullptr;
+    size_t aux_lent_bytes = 0;
     dm::ArgmaxState *argmax_state = nullptr;  // device
     uint32_t *router_tickets = nullptr;       // device, kRouterTickets counters, zero between launches
     uint32_t *argmax_ticket = nullptr;        // device, zero between launches: ticket, then (at +8) the best key
@@ -131,6 +135,9 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
 int enqueue_matvec_argmax(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
                           const void *w, const float *x, float *y, uint32_t *index_device);
 int set_device(dmhip_ctx *ctx);
+// Resolves (once per device, with that device current) the device address of
+// the allocation-free FFN's scratch array.
+int noalloc_resolve(int device);
 
 // While ctx->kernel_timing is set, records an event on the compute stream
 // when constructed (before a launch) and another when destroyed (after it).

@@ -347,13 +347,24 @@ int dmhip_context_new(int device, dmhip_ctx **out) {
         hipMalloc((void **)&ctx->argmax_index, 64) != hipSuccess ||
         hipMalloc((void **)&ctx->flags, 64) != hipSuccess ||
         hipMalloc((void **)&ctx->argmax_ticket, 64) != hipSuccess ||
-        hipMemsetAsync(ctx->argmax_ticket, 0, 64, ctx->stream) != hipSuccess ||
         hipMalloc((void **)&ctx->router_tickets, kRouterTickets * 4) != hipSuccess ||
-        hipMemsetAsync(ctx->router_tickets, 0, kRouterTickets * 4, ctx->stream) != hipSuccess) {
+        // Counters start at zero.  Cleared by the library's own fill kernel:
+        // the first launch from the library's code object materialises its
+        // data (the allocation-free entry point's scratch array) on this
+        // device here, at set-up, rather than inside a later call.
+        launch_fill_u32(ctx->stream, ctx->argmax_ticket, 16, 0) != hipSuccess ||
+        launch_fill_u32(ctx->stream, ctx->router_tickets, kRouterTickets, 0) != hipSuccess ||
+        launch_fill_u32(ctx->stream, ctx->flags, 16, 0) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
         dmhip_context_free(ctx);
         return fail(DMHIP_ERR_COMMAND, "could not create the HIP streams of device %d", device);
     }
     for (Scratch *sc : {&ctx->in, &ctx->out, &ctx->enc, &ctx->aux, &ctx->partials}) sc->stream = ctx->stream;
+    const int resolved = noalloc_resolve(device);
+    if (resolved != DMHIP_OK) {
+        dmhip_context_free(ctx);
+        return resolved;
+    }
     *out = ctx;
     return DMHIP_OK;
 }

@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = [
     "dmhip_matvec_mapped", "dmhip_matvec_owned", "dmhip_dequantize", "dmhip_matvec_device",
     "dmhip_matvec_batch_device", "dmhip_matvec_argmax_device", "dmhip_argmax_result", "dmhip_rms_norm_device",
     "dmhip_silu_mul_device", "dmhip_ffn_workspace_bytes", "dmhip_ffn_device",
+    "dmhip_ffn_noalloc_scratch_bytes", "dmhip_ffn_device_noalloc",
     "dmhip_router_top_k_device", "dmhip_router_result", "dmhip_gemm_workspace_bytes", "dmhip_gemm_device",
     "dmhip_event_record", "dmhip_event_elapsed_ms", "dmhip_event_free",
     "dmhip_kernel_timing_enable", "dmhip_kernel_timing_read", "dmhip_copy_device",
@@ -157,6 +158,9 @@ def load_library() -> ctypes.CDLL:
         "dmhip_ffn_workspace_bytes": ([_sz, _sz, _sz], _sz),
         "dmhip_ffn_device": ([_vp, _sz, _sz, _sz, _u32, _vp, _u32, _vp, _u32, _vp, ctypes.c_float,
                               _vp, _vp, _vp, _sz], ctypes.c_int),
+        "dmhip_ffn_noalloc_scratch_bytes": ([], _sz),
+        "dmhip_ffn_device_noalloc": ([_vp, _sz, _sz, _sz, _u32, _vp, _u32, _vp, _u32, _vp, ctypes.c_float,
+                                      _vp, _vp], ctypes.c_int),
         "dmhip_router_top_k_device": ([_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
         "dmhip_router_result": ([_vp], ctypes.c_int),
         "dmhip_gemm_workspace_bytes": ([_sz, _sz], _sz),
@@ -431,6 +435,16 @@ class HipContext:
                    down_ptr, eps, h_ptr, y_ptr, ws_ptr, ws_len) -> None:
         _check(load_library().dmhip_ffn_device(self._h, batch, hidden, ffn, gate_type, gate_ptr, up_type,
                                                up_ptr, down_type, down_ptr, eps, h_ptr, y_ptr, ws_ptr, ws_len))
+
+    @staticmethod
+    def ffn_noalloc_scratch_bytes() -> int:
+        return int(load_library().dmhip_ffn_noalloc_scratch_bytes())
+
+    def ffn_device_noalloc(self, batch, hidden, ffn, gate_type, gate_ptr, up_type, up_ptr, down_type, down_ptr,
+                           eps, h_ptr, y_ptr) -> None:
+        """ffn_device without a workspace (the library's fixed per-device scratch)."""
+        _check(load_library().dmhip_ffn_device_noalloc(self._h, batch, hidden, ffn, gate_type, gate_ptr, up_type,
+                                                       up_ptr, down_type, down_ptr, eps, h_ptr, y_ptr))
 
     def router_top_k_device(self, batch, hidden, experts, k, router_ptr, x_ptr, logits_ptr, ids_ptr,
                             probs_ptr) -> None:

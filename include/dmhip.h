@@ -265,6 +265,24 @@ int dmhip_ffn_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn,
                      uint32_t down_type, const void *down, float epsilon, const float *h,
                      float *y, void *workspace, size_t workspace_len);
 
+/* dmhip_ffn_device without a workspace argument, for callers that cannot
+   allocate device memory (code under HIP graph capture, tight serving loops,
+   harnesses that forbid allocation); no counterpart in the reference.  The
+   scratch comes from a fixed array in the library's code object of
+   dmhip_ffn_noalloc_scratch_bytes() bytes (8 MiB) per device, resolved when
+   a context is created on that device; a shape whose workspace (and, for
+   batches above 2, activation fragments) exceed it is rejected
+   (InvalidArgument) before any work.  Nothing is allocated: no hipMalloc,
+   no growth of the context's scratch.  Every call on one device shares that
+   device's array, so calls that overlap on one device (two contexts, or two
+   streams, in flight at once) race; calls ordered on one context's stream
+   do not. */
+size_t dmhip_ffn_noalloc_scratch_bytes(void);
+int dmhip_ffn_device_noalloc(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t ffn,
+                             uint32_t gate_type, const void *gate, uint32_t up_type, const void *up,
+                             uint32_t down_type, const void *down, float epsilon, const float *h,
+                             float *y);
+
 /* Router for `batch` tokens: logits = bf16 router rows . x (exact sequential
    fold, src/cpu.rs:391-394), then top_k_softmax per token
    (src/cpu.rs:232-260).  ids [batch][k] uint32, probabilities [batch][k]. */

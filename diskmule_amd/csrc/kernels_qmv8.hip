@@ -488,8 +488,11 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     constexpr uint32_t WAVES = W;
     static_assert(W % S == 0, "a workgroup holds whole tiles");
     constexpr int NM = MODE == 2 ? 2 : 1;  // weight matrices streamed
-    // activation blocks of each wave loaded ahead of the weights
-    constexpr int XP = TOK == 1 ? (MODE == 2 ? 2 : 4) : 1;
+    // Activation blocks of each wave loaded ahead of the weights: what a
+    // wave's share of a 4096-column row is (16 blocks over W waves), so that
+    // no record is computed for a block past the end; wider rows load the
+    // rest after the weights.
+    constexpr int XP = TOK == 2 ? 1 : (W >= 16 ? 1 : 2);
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
     constexpr uint32_t BB = kBlock8<TYPE>;
     using ST = Stage8<TYPE, G>;

@@ -38,7 +38,7 @@ sys.path.insert(0, ROOT)
 METRIC = "Q4_K/Q6_K GEMV achieved HBM GB/s (% peak); prefill GEMM TFLOP/s; decode tok/s"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-Q4_K, Q6_K = 12, 14
+Q4_K, Q6_K, Q8_0 = 12, 14, 8
 
 
 def log(*a):
@@ -367,26 +367,33 @@ def bench_c4(ctx, synth, steps, warmup):
 
 
 def bench_c5(ctx, synth, steps, warmup):
+    """C5: 512-token prefill GEMM at K = 4096, N = 4096 and 12288, for Q4_K
+    (the headline) and the other two quantized types of the path.  `ms` is
+    the whole call (A preparation + GEMM); `kernel_ms_per_step` the GEMM
+    kernel alone (events on its dispatch)."""
     m, k = 512, 4096
     a = synth.to_bf16_bits(synth.normal(synth.activation_seed(5), m * k))
     ab = upload(ctx, a)
     ws = ctx.new_owned_buffer(ctx.gemm_workspace_bytes(m, k))
     out = {}
-    for n in (4096, 12288):
-        w = synth.quantized_matrix(Q4_K, n, k, synth.weight_seed(5, n))
-        wb, cb = upload(ctx, w), ctx.new_owned_buffer(m * n * 4)
-        call = lambda: ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr,
-                                       len(ws))
-        for _ in range(warmup):
-            call()
-        wall, kern, _ = timed_loop(ctx, lambda i: call(), steps)
-        ms = wall / steps
-        flops = 2.0 * m * n * k
-        out[f"N{n}"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
-                        "frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
-                        "kernel_ms_per_step": kern / steps,
-                        "kernel_tflops": flops / (kern / steps * 1e-3) / 1e12 if kern else None}
-        log(f"C5 N={n}: {ms * 1e3:.1f} us, {out[f'N{n}']['tflops']:.1f} TFLOP/s")
+    for kind, tag in ((Q4_K, ""), (Q6_K, "_q6_k"), (Q8_0, "_q8_0")):
+        for n in (4096, 12288):
+            w = synth.quantized_matrix(kind, n, k, synth.weight_seed(5, n))
+            wb, cb = upload(ctx, w), ctx.new_owned_buffer(m * n * 4)
+            call = lambda: ctx.gemm_device(kind, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr,
+                                           len(ws))
+            for _ in range(warmup):
+                call()
+            wall, kern, _ = timed_loop(ctx, lambda i: call(), steps)
+            ms = wall / steps
+            flops = 2.0 * m * n * k
+            out[f"N{n}{tag}"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+                                 "frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                                 "kernel_ms_per_step": kern / steps,
+                                 "kernel_tflops": flops / (kern / steps * 1e-3) / 1e12 if kern else None}
+            log(f"C5{tag} N={n}: {ms * 1e3:.1f} us, {out[f'N{n}{tag}']['tflops']:.1f} TFLOP/s")
+            wb.free()
+            cb.free()
     out["mfma_util_counters"] = load_mfma_util()
     return out
 

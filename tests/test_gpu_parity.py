@@ -349,10 +349,10 @@ def test_fused_argmax_ties_resolve_to_the_lowest_row(ctx, kind):
     assert np.count_nonzero(got == got[idx]) >= rows // period
 
 
-@pytest.mark.parametrize("kind", [Q6_K, Q8_0])
-def test_prefill_gemm_other_types_take_the_tokenwise_path(ctx, kind):
-    """Types without the MFMA GEMM run the decode GEMV in chunks of 16 tokens."""
-    m, n, k = 20, 96, 512
+@pytest.mark.parametrize("kind", [Q4_K, Q6_K, Q8_0])
+def test_prefill_gemm_short_prefills_take_the_tokenwise_path(ctx, kind):
+    """Up to 16 tokens run the decode GEMV (one pass over W per 16 tokens)."""
+    m, n, k = 16, 96, 512
     a = synth.to_bf16_bits(synth.normal(synth.activation_seed(8, kind), m * k))
     w = synth.quantized_matrix(kind, n, k, synth.weight_seed(8, kind))
     want = capi.gemm_tokenwise(kind, m, n, k, a, w)
@@ -859,41 +859,49 @@ def test_moe_layer_matches_oracle(ctx, batch):
 
 # ---- config 5: prefill GEMM ----------------------------------------------------
 
-@pytest.mark.parametrize("n", [4096, 12288])
-def test_prefill_gemm_matches_oracle(ctx, n):
-    m, k = 512, 4096
-    print(f"C5 n={n}", flush=True)
-    a = synth.to_bf16_bits(synth.normal(synth.activation_seed(5), m * k))
-    w = synth.quantized_matrix(Q4_K, n, k, synth.weight_seed(5, n))
-    rows = slice(0, 512) if n == 4096 else slice(0, 96)
-    mm = rows.stop - rows.start
-    want = capi.gemm_tokenwise(Q4_K, mm, n, k, a[: mm * k], w)
+def _gemm_check(ctx, kind, m, n, k, seed, what):
+    """dmhip_gemm_device against the oracle's one-matvec-per-token GEMM
+    (src/gemma4/metal.rs:514-536 over src/cpu.rs:345-399), every token."""
+    print(f"{what}: type {kind} m={m} n={n} k={k}", flush=True)
+    a = synth.to_bf16_bits(synth.normal(synth.activation_seed(seed, kind), m * k))
+    w = synth.quantized_matrix(kind, n, k, synth.weight_seed(seed, n * 31 + kind))
+    want = capi.gemm_tokenwise(kind, m, n, k, a, w)
     ab, wb, cb = dev(ctx, a), dev(ctx, w), dev_out(ctx, m * n * 4)
     ws = dev_out(ctx, ctx.gemm_workspace_bytes(m, k))
-    ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr, len(ws))
-    got = cb.read(0, m * n * 4, np.float32).reshape(m, n)[:mm]
+    ctx.gemm_device(kind, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr, len(ws))
+    got = cb.read(0, m * n * 4, np.float32).reshape(m, n)
     worst = 0.0
-    for r in range(mm):
-        e, _ = assert_close(got[r], want[r], f"C5 token {r}")
+    for r in range(m):
+        e, _ = assert_close(got[r], want[r], f"{what} type {kind} token {r}")
         worst = max(worst, e)
     print(f"  worst rel_err={worst:.2e}", flush=True)
+    return worst
 
 
-@pytest.mark.parametrize("m,n,k", [(100, 200, 2048), (9, 136, 4608), (65, 264, 12288), (8, 128, 256)])
-def test_prefill_gemm_ragged_shapes(ctx, m, n, k):
-    """M not a multiple of the 64-row tile (padding rows), N not a multiple of
-    the 128-column tile, and K other than 4096 (the preparation's general
-    path: the row maximum in a loop, several workgroups per row group)."""
-    print(f"C5 ragged m={m} n={n} k={k}", flush=True)
-    a = synth.to_bf16_bits(synth.normal(synth.activation_seed(7), m * k))
-    w = synth.quantized_matrix(Q4_K, n, k, synth.weight_seed(7, n))
-    want = capi.gemm_tokenwise(Q4_K, m, n, k, a, w)
-    ab, wb, cb = dev(ctx, a), dev(ctx, w), dev_out(ctx, m * n * 4)
-    ws = dev_out(ctx, ctx.gemm_workspace_bytes(m, k))
-    ctx.gemm_device(Q4_K, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr, len(ws))
-    got = cb.read(0, m * n * 4, np.float32).reshape(m, n)
-    for r in range(m):
-        assert_close(got[r], want[r], f"C5 ragged token {r}")
+@pytest.mark.parametrize("n", [4096, 12288])
+def test_prefill_gemm_matches_oracle(ctx, n):
+    """C5: Q4_K, 512 tokens, K = 4096; every token of both N (all 4 M tiles,
+    every N tile and XCD position)."""
+    _gemm_check(ctx, Q4_K, 512, n, 4096, 5, "C5")
+
+
+@pytest.mark.parametrize("kind", [Q6_K, Q8_0])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (4096, 12288)])
+def test_prefill_gemm_q6_k_and_q8_0_on_mfma(ctx, kind, n, k):
+    """The MFMA GEMM for the other two quantized types of the north star, at
+    M = 512 and K = 4096 / 12288 (src/cpu.rs:576-583, :618-645)."""
+    _gemm_check(ctx, kind, 512, n, k, 6, "prefill")
+
+
+@pytest.mark.parametrize("kind", [Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("m,n,k", [(17, 64, 256), (100, 200, 2048), (65, 264, 2816), (300, 136, 4608)])
+def test_prefill_gemm_ragged_shapes(ctx, kind, m, n, k):
+    """M not a multiple of the 128-row tile (padding rows; 17 = the smallest
+    MFMA prefill), N not a multiple of the 64-column tile, a single K block
+    (three waves without blocks), and K quarters of unequal length; K = 2816
+    (11 blocks) gives Q6_K rows whose 210-byte blocks start 2 bytes off a
+    dword boundary on every other row."""
+    _gemm_check(ctx, kind, m, n, k, 7, "ragged")
 
 
 def test_objects_outliving_their_context_exit_cleanly():

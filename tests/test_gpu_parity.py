@@ -259,6 +259,106 @@ def test_matvec_batch_validation(ctx):
         ctx.matvec_batch_device(Q4_K, 8, 100, [wb.device_ptr], xb.device_ptr, 0, yb.device_ptr, 8)
 
 
+def _outlier_activations(seed, count, spikes=1e4):
+    """N(0,1) values with, in every 256-value block, one element `spikes`
+    times larger than its neighbours (random place and sign), and every
+    seventh block scaled down by 1e-4 (small blocks beside large ones)."""
+    x = synth.normal(synth.activation_seed(seed), count).astype(np.float64)
+    rng = np.random.default_rng(seed)
+    blocks = count // 256
+    place = rng.integers(0, 256, blocks)
+    sign = rng.choice([-1.0, 1.0], blocks)
+    for b in range(blocks):
+        if b % 7 == 3:
+            x[256 * b:256 * b + 256] *= 1e-4
+        else:
+            x[256 * b + place[b]] = sign[b] * spikes * (1.0 + abs(x[256 * b + place[b]]))
+    return x.astype(np.float32)
+
+
+def _int8_record_bound(kind, rows, cols, w, x):
+    """The int8 path's worst-case error per output row: each 256-value block
+    of x is rounded to integers of 22 bits relative to the block's largest
+    element, so |x~ - x| <= 2^-22 max_block|x|, and row r's error is at most
+    sum over blocks of 2^-22 max_block|x| sum_block |W[r]| (fp32 rounding of
+    the per-block sums adds a few ulp of the result on top)."""
+    dense = capi.dequantize(kind, w, rows * cols).reshape(rows, cols).astype(np.float64)
+    ax = np.abs(x.astype(np.float64))
+    xb = ax.reshape(-1, 256).max(axis=1) * 2.0 ** -22
+    wb = np.abs(dense).reshape(rows, -1, 256).sum(axis=2)
+    # plus the fp32 summation noise of the reference's sequential fold
+    # (random-walk size, 8 sqrt(cols) ulp of sum |W x|)
+    noise = 8.0 * np.sqrt(cols) * np.finfo(np.float32).eps * (np.abs(dense) @ ax)
+    return wb @ xb + noise
+
+
+@pytest.mark.parametrize("kind,rows,cols,batch", [(Q4_K, 4096, 4096, 1), (Q6_K, 4096, 4096, 2),
+                                                 (Q8_0, 4096, 4096, 1), (Q4_K, 1000, 2048, 4),
+                                                 (Q6_K, 1000, 2048, 8)])
+def test_in_block_outliers_stay_within_the_bound(ctx, kind, rows, cols, batch):
+    """One element 10^4 times its neighbours inside each 256-value block, and
+    blocks 10^4 smaller than the rest: batches of 1-2 tokens take the int8
+    records (22 bits per block, checked against the bound derived above, and
+    the tolerance), batches above 2 the fp16 path (per-token scale)."""
+    print(f"outliers type={kind} {rows}x{cols} batch={batch}", flush=True)
+    w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(130, kind))
+    x = np.stack([_outlier_activations(131 + b, cols) for b in range(batch)])
+    want = np.stack([capi.matvec(kind, rows, cols, w, x[b]) for b in range(batch)])
+    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, batch * rows * 4)
+    ctx.matvec_device(kind, rows, cols, wb.device_ptr, batch, xb.device_ptr, yb.device_ptr)
+    got = yb.read(0, batch * rows * 4, np.float32).reshape(batch, rows)
+    for b in range(batch):
+        e, _ = assert_close(got[b], want[b], f"outliers type {kind} token {b}")
+        if batch <= 2:
+            bound = _int8_record_bound(kind, rows, cols, w, x[b])
+            err = np.abs(got[b].astype(np.float64) - want[b])
+            assert (err <= bound).all(), f"token {b}: worst excess {np.max(err - bound):.3g}"
+        print(f"  token {b}: rel_err={e:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("kind", [Q6_K, Q4_K])
+def test_argmax_with_in_block_outliers(ctx, kind):
+    """The fused argmax on outlier activations: the index equals the CPU's
+    whenever the CPU's top-2 gap exceeds twice the int8 path's error bound
+    (and always equals the argmax of the GPU's own logits)."""
+    rows, cols = 30000, 4096
+    w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(132, kind))
+    x = _outlier_activations(133, cols)
+    want = capi.matvec(kind, rows, cols, w, x)
+    wb, xb, yb, ib = dev(ctx, w), dev(ctx, x), dev_out(ctx, rows * 4), dev_out(ctx, 4)
+    ctx.matvec_argmax_device(kind, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr, ib.device_ptr)
+    idx = ctx.argmax_result()
+    got = yb.read(0, rows * 4, np.float32)
+    assert_close(got, want, "outlier logits")
+    assert idx == capi.argmax(got)
+    bound = _int8_record_bound(kind, rows, cols, w, x).max()
+    gap = top2_gap(want)
+    print(f"  argmax gpu={idx} cpu={capi.argmax(want)} gap={gap:.4g} bound={bound:.3g}", flush=True)
+    if gap > 2 * bound:
+        assert idx == capi.argmax(want)
+
+
+@pytest.mark.parametrize("kind", [Q4_K, Q6_K, Q8_0])
+def test_prefill_gemm_with_in_block_outliers(ctx, kind):
+    """The GEMM's A preparation scales each K quarter of a row by one power of
+    two: outliers 10^4 times their neighbours and blocks 10^4 smaller than the
+    rest (bf16 values down to 2^-17 of the quarter's maximum convert to fp16
+    exactly)."""
+    m, n, k = 160, 192, 4096
+    a = synth.to_bf16_bits(np.concatenate([_outlier_activations(140 + r, k) for r in range(m)]))
+    w = synth.quantized_matrix(kind, n, k, synth.weight_seed(141, kind))
+    want = capi.gemm_tokenwise(kind, m, n, k, a, w)
+    ab, wb, cb = dev(ctx, a), dev(ctx, w), dev_out(ctx, m * n * 4)
+    ws = dev_out(ctx, ctx.gemm_workspace_bytes(m, k))
+    ctx.gemm_device(kind, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr, len(ws))
+    got = cb.read(0, m * n * 4, np.float32).reshape(m, n)
+    worst = 0.0
+    for r in range(m):
+        e, _ = assert_close(got[r], want[r], f"outlier GEMM type {kind} token {r}")
+        worst = max(worst, e)
+    print(f"  type {kind}: worst rel_err={worst:.2e}", flush=True)
+
+
 def test_q6_k_large_scales_take_the_exact_split_path(ctx):
     rows, cols = 64, 1024
     w = synth.quantized_matrix(Q6_K, rows, cols, synth.weight_seed(55)).reshape(-1, 210).copy()

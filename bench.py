@@ -8,13 +8,15 @@ activation resident in HBM before the timed region.  ``value`` is the
 algorithmic bytes of a step divided by the wall time per step on the
 compute stream (HIP events, all launches of the step included).
 
-``roofline`` describes the dominant kernel (the Q6_K MFMA matvec): its
-average duration comes from HIP events the library records around each of
-its launches inside the timed region; ``traffic`` is the HBM bytes per
-launch from rocprofv3 FETCH_SIZE/WRITE_SIZE runs (profiles/), when present.
+``roofline`` describes the dominant kernel, the one the timed step runs
+(the int8 Q6_K GEMV with the argmax folded into its epilogue, one launch per
+step): its average launch duration is the region time per step of the
+back-to-back timed loop; ``traffic`` is the HBM bytes per launch from
+rocprofv3 FETCH_SIZE/WRITE_SIZE runs (profiles/), when present.
 
-``cpu_baseline`` times the CPU port of src/cpu.rs (oracle/dm_oracle.c,
-16 threads) on the same C2 workload, on this machine's host cores.
+``cpu_baseline`` times the CPU port of src/cpu.rs (oracle/dm_oracle.c) on
+the same C2 workload, on this machine's host cores, with the thread count
+rayon's default pool would take (std::thread::available_parallelism).
 
 ``details`` holds the other BASELINE configurations (C1, C3, C4, C5), each
 measured the same way, and a Q8_0 GEMV entry (the third k-quant of the north
@@ -111,10 +113,11 @@ def bench_c2(ctx, synth, steps, warmup):
         for _ in range(steps):
             ctx.matvec_argmax_device(Q6_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr, ib.device_ptr)
     ms = t.wall_ms / steps
-    # The GEMV kernel on its own: the same matrix through matvec_device (the
-    # int8 kernel without the argmax epilogue), launched back to back with
-    # events around the region only, so region / launches is the kernel's
-    # average launch duration (a kernel trace of this run shows the same).
+    # A step is one launch (the int8 GEMV with the argmax folded into its
+    # epilogue), back to back: the region time per step is that kernel's
+    # average launch duration plus the dispatch gap, so the roofline figure
+    # is the timed step's kernel.  The kernel without the argmax epilogue
+    # (matvec_device) is timed the same way for comparison.
     ctx.matvec_device(Q6_K, rows, cols, wb.device_ptr, 1, xb.device_ptr, yb.device_ptr)
     ctx.synchronize()
     time.sleep(0.2)
@@ -126,7 +129,7 @@ def bench_c2(ctx, synth, steps, warmup):
     return {
         "rows": rows, "columns": cols, "weight_bytes": int(w.size), "step_bytes": int(step_bytes),
         "ms_per_step": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9,
-        "kernel_ms": kms, "kernel_gbps": step_bytes / (kms * 1e-3) / 1e9, "argmax": int(idx),
+        "gemv_no_argmax_ms": kms, "gemv_no_argmax_gbps": step_bytes / (kms * 1e-3) / 1e9, "argmax": int(idx),
     }, (w, x)
 
 
@@ -412,10 +415,40 @@ def bench_copy(ctx, synth, steps, warmup):
     return {"bytes_read": n, "bytes_written": n, "ms": ms, "gbps": 2 * n / (ms * 1e-3) / 1e9}
 
 
+def host_parallelism():
+    """The thread count Rust's std::thread::available_parallelism() reports
+    (rayon's default pool size): the CPUs in this process's affinity mask,
+    capped by a cgroup v2 CPU quota when one is set."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            n = max(1, min(n, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(w, x, seconds):
-    """The CPU port of src/cpu.rs:345-399 + :275-293 on the C2 workload."""
+    """The CPU port of src/cpu.rs:345-399 + :275-293 on the C2 workload, on
+    the thread count the reference's rayon pool would use."""
     from oracle import capi
-    threads = min(16, os.cpu_count() or 1)
+    threads = host_parallelism()
     rows, cols = 151936, 4096
     step_bytes = w.size + cols * 4 + rows * 4
     reps, t0 = 0, time.perf_counter()
@@ -432,8 +465,9 @@ def cpu_baseline(w, x, seconds):
     dt1 = time.perf_counter() - t1
     return {"value": step_bytes * reps / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"full C2 step (Q6_K 151936x4096 matvec + argmax) repeated {reps}x in {dt:.1f}s "
-                      f"on {threads} host threads; oracle/dm_oracle.c restating src/cpu.rs (the Rust "
-                      f"reference cannot be built here)",
+                      f"on {threads} host threads; oracle/dm_oracle.c (gcc -O3 -ffp-contract=off) restating "
+                      f"src/cpu.rs (the Rust reference cannot be built here)",
+            "nproc": os.cpu_count(), "cpu_model": cpu_model(),
             "value_1_thread": step_bytes / dt1 / 1e9,
             "argmax": int(idx)}
 
@@ -508,8 +542,8 @@ def main() -> int:
                    "weight_type": "Q6_K", "rows": 151936, "columns": 4096, "batch": 1,
                    "arithmetic": "int8 MFMA on the raw 6-bit codes and 3-term int8 activations (22 bits "
                                  "per 256-value block): exact int32 group dots, fp32 block accumulation"},
-        "roofline": {"bound": "hbm", "achieved": round(c2["kernel_gbps"], 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(c2["kernel_gbps"] / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(c2["gbps"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(c2["gbps"] / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic()},
         "cpu_baseline": cpu,
         "details": details,

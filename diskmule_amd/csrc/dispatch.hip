@@ -26,7 +26,8 @@ int noalloc_resolve(int device) {
     // one of its kernels is first resolved, which must not happen inside an
     // allocation-free call.
     for (const void *anchor : {module_anchor_simple(), module_anchor_qmv(), module_anchor_qmv8(),
-                               module_anchor_qmv_valu(), module_anchor_gemm(), module_anchor_expert()}) {
+                               module_anchor_qmv_valu(), module_anchor_gemm(), module_anchor_expert(),
+                               module_anchor_dense()}) {
         hipFuncAttributes attr;
         DM_HIP(hipFuncGetAttributes(&attr, anchor));
     }
@@ -61,6 +62,11 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
         return DMHIP_OK;
     }
     KernelTimer timer(ctx);
+    if (dense_supported(type, rows, columns, w, x, batch)) {
+        DM_HIP(launch_dense_gemv(ctx->stream, ctx->compute_units, type, w, (uint32_t)rows, (uint32_t)columns,
+                                 (size_t)row_bytes, (uint32_t)batch, x, y));
+        return DMHIP_OK;
+    }
     DM_HIP(launch_gemv_exact(ctx->stream, type, be, bb, (uint32_t)rows, (uint32_t)columns,
                              (size_t)row_bytes, (const uint8_t *)w, (uint32_t)batch, x, y));
     return DMHIP_OK;

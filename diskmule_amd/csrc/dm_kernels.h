@@ -47,6 +47,12 @@ const void *module_anchor_qmv();
 const void *module_anchor_qmv8();
 const void *module_anchor_qmv_valu();
 const void *module_anchor_gemm();
+const void *module_anchor_dense();
+// GEMV over F32 / F16 rows (kernels_dense.hip): whole 16-byte chunks,
+// 16-byte aligned operands, up to 64 KiB of activations per group of 4 tokens.
+bool dense_supported(uint32_t type, size_t rows, size_t columns, const void *w, const float *x, size_t batch);
+hipError_t launch_dense_gemv(hipStream_t s, int cus, uint32_t type, const void *w, uint32_t rows, uint32_t columns,
+                             size_t row_bytes, uint32_t batch, const float *x, float *y);
 const void *module_anchor_expert();
 
 hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t n);
@@ -82,6 +88,7 @@ constexpr uint32_t kRouterTickets = 4096;
 hipError_t launch_rms_norm(hipStream_t s, const float *in, uint32_t batch, uint32_t n,
                            const float *weight, float eps, float *out);
 hipError_t launch_silu_mul(hipStream_t s, const float *gate, const float *up, size_t n, float *out);
+hipError_t launch_softcap(hipStream_t s, const float *in, size_t n, float cap, float *out);
 hipError_t launch_moe_combine(hipStream_t s, const float *expert_out, const float *p, uint32_t batch,
                               uint32_t k, uint32_t hidden, float *y);
 hipError_t launch_silu_mul_glm_pairs(hipStream_t s, const float *gate_up, uint32_t pairs,

@@ -782,6 +782,23 @@ hipError_t launch_silu_mul(hipStream_t s, const float *gate, const float *up, si
     return hipGetLastError();
 }
 
+// Logit softcap, src/cpu.rs:263-273: cap * tanh(value / cap), fp32 (the
+// division, tanh and product each round once).
+__global__ void softcap_kernel(const float *__restrict__ in, size_t n, float cap, float *__restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const float q = in[i] / cap;
+        out[i] = cap * tanhf(q);
+    }
+}
+
+hipError_t launch_softcap(hipStream_t s, const float *in, size_t n, float cap, float *out) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(softcap_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, in, n, cap, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_moe_combine(hipStream_t s, const float *expert_out, const float *p, uint32_t batch,
                               uint32_t k, uint32_t hidden, float *y) {
     size_t total = (size_t)batch * hidden;

@@ -599,6 +599,26 @@ int dmhip_silu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const flo
     return DMHIP_OK;
 }
 
+int dmhip_softcap(dmhip_ctx *ctx, const float *input, size_t input_len, float cap, float *output,
+                  size_t output_len) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(require_nonempty("logit softcap", input_len));
+    DM_CHECK(validate_vector_length("logit softcap", "output", input_len, output_len));
+    DM_CHECK(require_positive("logit softcap", cap));
+    DM_REQUIRE(input);
+    DM_REQUIRE(output);
+    DM_CHECK(count_u32(input_len));
+    DM_CHECK(set_device(ctx));
+    size_t bytes = input_len * sizeof(float);
+    DM_CHECK(ctx->in.ensure(bytes));
+    DM_CHECK(ctx->out.ensure(bytes));
+    DM_HIP(hipMemcpyAsync(ctx->in.ptr, input, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(launch_softcap(ctx->stream, (const float *)ctx->in.ptr, input_len, cap, (float *)ctx->out.ptr));
+    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
 int dmhip_argmax(dmhip_ctx *ctx, const float *input, size_t input_len, size_t *index) {
     DM_REQUIRE(ctx);
     DM_REQUIRE(index);
@@ -859,6 +879,17 @@ int dmhip_silu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const
     DM_REQUIRE(output);
     DM_CHECK(set_device(ctx));
     DM_HIP(launch_silu_mul(ctx->stream, gate, up, count, output));
+    return DMHIP_OK;
+}
+
+int dmhip_softcap_device(dmhip_ctx *ctx, size_t count, const float *input, float cap, float *output) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(require_nonempty("logit softcap", count));
+    DM_CHECK(require_positive("logit softcap", cap));
+    DM_REQUIRE(input);
+    DM_REQUIRE(output);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_softcap(ctx->stream, input, count, cap, output));
     return DMHIP_OK;
 }
 

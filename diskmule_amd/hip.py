@@ -35,10 +35,10 @@ EXPORTED_SYMBOLS = [
     "dmhip_synchronize", "dmhip_stream", "dmhip_map_read_only", "dmhip_new_owned_buffer",
     "dmhip_buffer_free", "dmhip_buffer_len", "dmhip_buffer_device_ptr", "dmhip_buffer_write",
     "dmhip_buffer_read", "dmhip_copy_to_host", "dmhip_copy_to_device", "dmhip_host_alloc_pinned", "dmhip_host_free_pinned", "dmhip_rms_norm",
-    "dmhip_silu_mul", "dmhip_argmax", "dmhip_top_k_softmax", "dmhip_matvec",
+    "dmhip_silu_mul", "dmhip_softcap", "dmhip_argmax", "dmhip_top_k_softmax", "dmhip_matvec",
     "dmhip_matvec_mapped", "dmhip_matvec_owned", "dmhip_dequantize", "dmhip_matvec_device",
     "dmhip_matvec_batch_device", "dmhip_matvec_argmax_device", "dmhip_argmax_result", "dmhip_rms_norm_device",
-    "dmhip_silu_mul_device", "dmhip_ffn_workspace_bytes", "dmhip_ffn_device",
+    "dmhip_silu_mul_device", "dmhip_softcap_device", "dmhip_ffn_workspace_bytes", "dmhip_ffn_device",
     "dmhip_ffn_noalloc_scratch_bytes", "dmhip_ffn_device_noalloc",
     "dmhip_router_top_k_device", "dmhip_router_result", "dmhip_gemm_workspace_bytes", "dmhip_gemm_device",
     "dmhip_event_record", "dmhip_event_elapsed_ms", "dmhip_event_free",
@@ -142,6 +142,7 @@ def load_library() -> ctypes.CDLL:
         "dmhip_host_free_pinned": ([_vp], None),
         "dmhip_rms_norm": ([_vp, _f32p, _sz, _f32p, _sz, ctypes.c_float, _f32p, _sz], ctypes.c_int),
         "dmhip_silu_mul": ([_vp, _f32p, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_softcap": ([_vp, _f32p, _sz, ctypes.c_float, _f32p, _sz], ctypes.c_int),
         "dmhip_argmax": ([_vp, _f32p, _sz, _szp], ctypes.c_int),
         "dmhip_top_k_softmax": ([_vp, _f32p, _sz, _sz, _szp, _f32p], ctypes.c_int),
         "dmhip_matvec": ([_vp, _u32, _sz, _sz, _u8p, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
@@ -155,6 +156,7 @@ def load_library() -> ctypes.CDLL:
         "dmhip_argmax_result": ([_vp, _szp], ctypes.c_int),
         "dmhip_rms_norm_device": ([_vp, _sz, _sz, _vp, _vp, ctypes.c_float, _vp], ctypes.c_int),
         "dmhip_silu_mul_device": ([_vp, _sz, _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_softcap_device": ([_vp, _sz, _vp, ctypes.c_float, _vp], ctypes.c_int),
         "dmhip_ffn_workspace_bytes": ([_sz, _sz, _sz], _sz),
         "dmhip_ffn_device": ([_vp, _sz, _sz, _sz, _u32, _vp, _u32, _vp, _u32, _vp, ctypes.c_float,
                               _vp, _vp, _vp, _sz], ctypes.c_int),
@@ -364,6 +366,11 @@ class HipContext:
         g, u = _f32(gate), _f32(up)
         _check(load_library().dmhip_silu_mul(self._h, _fp(g), g.size, _fp(u), u.size, _fp(output), output.size))
 
+    def softcap(self, input, cap: float, output: np.ndarray) -> None:
+        """MetalContext::softcap (src/metal.rs:600-622)."""
+        x = _f32(input)
+        _check(load_library().dmhip_softcap(self._h, _fp(x), x.size, cap, _fp(output), output.size))
+
     def argmax(self, input) -> int:
         x = _f32(input)
         idx = ctypes.c_size_t()
@@ -427,6 +434,9 @@ class HipContext:
 
     def silu_mul_device(self, count, g_ptr, u_ptr, out_ptr) -> None:
         _check(load_library().dmhip_silu_mul_device(self._h, count, g_ptr, u_ptr, out_ptr))
+
+    def softcap_device(self, count, in_ptr, cap, out_ptr) -> None:
+        _check(load_library().dmhip_softcap_device(self._h, count, in_ptr, cap, out_ptr))
 
     def ffn_workspace_bytes(self, batch, hidden, ffn) -> int:
         return int(load_library().dmhip_ffn_workspace_bytes(batch, hidden, ffn))

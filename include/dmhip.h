@@ -185,6 +185,12 @@ int dmhip_rms_norm(dmhip_ctx *ctx, const float *input, size_t input_len, const f
 int dmhip_silu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const float *up,
                    size_t up_len, float *output, size_t output_len);
 
+/* MetalContext::softcap (src/metal.rs:600-622): output = cap * tanh(input /
+   cap), src/cpu.rs:263-273.  Checks in the reference's order: EmptyInput,
+   VectorLength (output), InvalidPositiveParameter (cap not finite and > 0). */
+int dmhip_softcap(dmhip_ctx *ctx, const float *input, size_t input_len, float cap, float *output,
+                  size_t output_len);
+
 /* MetalContext::argmax (src/metal.rs:624-644): first maximum, lowest index on
    ties, non-finite input rejected. */
 int dmhip_argmax(dmhip_ctx *ctx, const float *input, size_t input_len, size_t *index);
@@ -253,6 +259,10 @@ int dmhip_rms_norm_device(dmhip_ctx *ctx, size_t batch, size_t count, const floa
 /* out = silu(gate) * up, count values (src/qwen35/cpu.rs:422-424). */
 int dmhip_silu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const float *up,
                           float *output);
+
+/* Logit softcap over `count` device values (src/cpu.rs:263-273), as
+   dmhip_softcap; input and output may be the same buffer. */
+int dmhip_softcap_device(dmhip_ctx *ctx, size_t count, const float *input, float cap, float *output);
 
 /* Dense gated FFN at decode for `batch` tokens (src/qwen35/cpu.rs:415-427):
    y = down(silu(gate(n)) * up(n)) with n = rms_norm(h, eps), unit weight.

@@ -80,6 +80,8 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_top_k_softmax.argtypes = [_f32p, _sz, _sz, _szp, _f32p]
     l.orc_rms_norm.argtypes = [_f32p, _sz, _f32p, _sz, ctypes.c_float, _f32p, _sz]
     l.orc_silu.argtypes = [ctypes.c_float]
+    l.orc_softcap_in_place.argtypes = [_f32p, _sz, ctypes.c_float]
+    l.orc_softcap_in_place.restype = ctypes.c_int
     l.orc_silu.restype = ctypes.c_float
     l.orc_silu_mul_glm.argtypes = [_f32p, _f32p, _sz, _f32p]
     l.orc_silu_mul_glm.restype = None
@@ -228,6 +230,17 @@ def rms_norm_status(x, weight, epsilon: float, out_len: int) -> int:
 
 def silu(value: float) -> np.float32:
     return np.float32(lib().orc_silu(value))
+
+
+def softcap(values, cap: float) -> np.ndarray:
+    out = np.array(values, dtype=np.float32, copy=True).ravel()
+    _check(lib().orc_softcap_in_place(_p(out, _f32p), out.size, cap), "softcap")
+    return out
+
+
+def softcap_status(values, cap: float) -> int:
+    out = np.array(values, dtype=np.float32, copy=True).ravel()
+    return lib().orc_softcap_in_place(_p(out, _f32p), out.size, cap)
 
 
 def silu_mul_glm(gate, up) -> np.ndarray:

@@ -448,6 +448,18 @@ float orc_silu(float value)
     return value * sigmoid;
 }
 
+/* src/cpu.rs:263-273  logit softcap: the division, tanh and product each
+   round once in f32 (Rust's f32::tanh is the C library's tanhf). */
+int orc_softcap_in_place(float *values, size_t count, float cap)
+{
+    if (!isfinite(cap) || cap <= 0.0f) return ORC_INVALID_POSITIVE_PARAMETER;
+    for (size_t i = 0; i < count; i++) {
+        float q = values[i] / cap;
+        values[i] = cap * tanhf(q);
+    }
+    return ORC_OK;
+}
+
 /* src/glm52/expert.rs:260-267  (gate / (1 + exp(-gate))) * up */
 void orc_silu_mul_glm(const float *gate, const float *up, size_t count, float *output)
 {

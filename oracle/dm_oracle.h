@@ -87,6 +87,9 @@ int orc_top_k_softmax(const float *logits, size_t count, size_t k, size_t *indic
 int orc_rms_norm(const float *input, size_t count, const float *weight, size_t weight_len,
                  float epsilon, float *output, size_t output_len);
 float orc_silu(float value);
+/* src/cpu.rs:263-273: values[i] = cap * tanh(values[i] / cap) in place;
+   InvalidPositiveParameter unless cap is finite and > 0. */
+int orc_softcap_in_place(float *values, size_t count, float cap);
 void orc_silu_mul_glm(const float *gate, const float *up, size_t count, float *output);
 
 int orc_dense_ffn(size_t batch, size_t hidden, size_t ffn, uint32_t gate_type,

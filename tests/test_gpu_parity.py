@@ -87,6 +87,21 @@ def test_encoded_matvec_kernels_match_the_cpu_reference(ctx, kind):
     assert_metal_tolerance(got, want, f"type {kind}")
 
 
+@pytest.mark.parametrize("kind", [F32, F16])
+@pytest.mark.parametrize("rows,cols,batch", [(4096, 4096, 1), (12288, 4096, 2), (1000, 2560, 3), (37, 520, 5),
+                                             (70001, 256, 1), (9, 8192, 4)])
+def test_dense_gemv_matches_oracle(ctx, kind, rows, cols, batch):
+    """F32 / F16 rows on the wide-load GEMV: columns that are not a multiple
+    of a 64-lane pass, odd row counts, 1-5 tokens (groups of up to 4)."""
+    w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(160, kind))
+    x = synth.normal(synth.activation_seed(160, cols), batch * cols).reshape(batch, cols)
+    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, batch * rows * 4)
+    ctx.matvec_device(kind, rows, cols, wb.device_ptr, batch, xb.device_ptr, yb.device_ptr)
+    got = yb.read(0, batch * rows * 4, np.float32).reshape(batch, rows)
+    for b in range(batch):
+        assert_close(got[b], capi.matvec(kind, rows, cols, w, x[b]), f"type {kind} {rows}x{cols} token {b}")
+
+
 def test_mapped_matvec_reads_a_nonzero_file_offset(ctx, golden):
     c = golden[0]["matvec_row_major"]
     enc = np.array(c["encoded"], dtype=np.uint8)
@@ -411,6 +426,35 @@ def test_tall_matvec_line_aligned_staging(ctx, kind, rows, cols, batch):
         ib = dev_out(ctx, 4)
         ctx.matvec_argmax_device(kind, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr, ib.device_ptr)
         assert ctx.argmax_result() == capi.argmax(yb.read(0, rows * 4, np.float32))
+
+
+def test_softcap_matches_the_reference_fixture(ctx):
+    """MetalContext::softcap (src/metal.rs:600-622) on the reference's own
+    fixture (src/metal.rs:2166-2168, 2231-2235: 513 values, cap 30, absolute
+    tolerance 2e-6), a wide range of magnitudes, the device form in place,
+    and the reference's check order."""
+    fixture = np.array([((i % 31) - 15) * 0.071 for i in range(513)], dtype=np.float32)
+    out = np.zeros(513, dtype=np.float32)
+    ctx.softcap(fixture, 30.0, out)
+    assert np.abs(out - capi.softcap(fixture, 30.0)).max() <= 2.0e-6
+    wide = np.concatenate([synth.normal(synth.activation_seed(150), 4000) * np.float32(20.0),
+                           np.float32([0.0, -0.0, 1e-30, 1e4, -1e4, 3.4e38, -3.4e38])])
+    for cap in (30.0, 1.5):
+        out = np.zeros(wide.size, dtype=np.float32)
+        ctx.softcap(wide, cap, out)
+        want = capi.softcap(wide, cap).astype(np.float64)
+        ulp = np.spacing(np.maximum(np.abs(want), 1e-38).astype(np.float32)).astype(np.float64)
+        assert (np.abs(out - want) <= 4 * ulp).all(), cap
+    buf = dev(ctx, wide)
+    ctx.softcap_device(wide.size, buf.device_ptr, 30.0, buf.device_ptr)
+    np.testing.assert_allclose(buf.read(0, wide.size * 4, np.float32), capi.softcap(wide, 30.0), rtol=0, atol=1e-4)
+    for args, variant in (((np.zeros(0, np.float32), -1.0, np.zeros(0, np.float32)), "EmptyInput"),
+                          ((fixture, -1.0, np.zeros(3, np.float32)), "InvalidVectorLength"),
+                          ((fixture, 0.0, np.zeros(513, np.float32)), "InvalidPositiveParameter"),
+                          ((fixture, float("nan"), np.zeros(513, np.float32)), "InvalidPositiveParameter")):
+        with pytest.raises(HipError) as e:
+            ctx.softcap(*args)
+        assert e.value.variant == variant
 
 
 @pytest.mark.parametrize("rows,cols,batch", [(1000, 2048, 1), (4096, 4096, 2), (300, 12288, 1), (40000, 4096, 1),

@@ -284,3 +284,26 @@ def test_lru_matches_python_model_on_random_traces():
     assert (st["hits"], st["misses"], st["evictions"]) == (hits, misses, evictions)
     assert st["reads"] == 2 * misses and st["bytes_read"] == 16 * misses
     assert st["resident_bytes"] == 2 * slots * 16
+
+
+def test_softcap_matches_float64_and_its_invariants():
+    """src/cpu.rs:263-273 on the reference's fixture input (src/metal.rs:
+    2166-2168, 2231-2235: ((i % 31) - 15) * 0.071, cap 30) and a wide range:
+    within 2 ulp of cap * tanh(x / cap) in float64, odd, bounded by the cap,
+    identity-like near zero; caps that are not finite and positive are
+    rejected (InvalidPositiveParameter)."""
+    fixture = np.array([((i % 31) - 15) * 0.071 for i in range(513)], dtype=np.float32)
+    wide = np.concatenate([fixture, np.float32([0.0, -0.0, 1e-30, -1e-30, 29.9, -29.9, 30.0, 1e4, -1e4, 3.4e38,
+                                                -3.4e38])])
+    for cap in (30.0, 1.5, 50.0):
+        got = capi.softcap(wide, cap)
+        want = cap * np.tanh(wide.astype(np.float64) / cap)
+        ulp = np.spacing(np.maximum(np.abs(want), 1e-38).astype(np.float32)).astype(np.float64)
+        assert (np.abs(got - want) <= 2 * ulp).all(), cap
+        assert (np.abs(got) <= cap).all()
+        np.testing.assert_array_equal(capi.softcap(-wide, cap), -got)
+    small = capi.softcap(np.float32([1e-6, -2e-7]), 30.0)
+    np.testing.assert_allclose(small, [1e-6, -2e-7], rtol=1e-6)
+    for cap in (0.0, -1.0, float("inf"), float("nan")):
+        assert capi.softcap_status(fixture, cap) == 11
+

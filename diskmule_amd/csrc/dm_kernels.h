@@ -48,8 +48,9 @@ const void *module_anchor_qmv8();
 const void *module_anchor_qmv_valu();
 const void *module_anchor_gemm();
 const void *module_anchor_dense();
-// GEMV over F32 / F16 rows (kernels_dense.hip): whole 16-byte chunks,
-// 16-byte aligned operands, up to 64 KiB of activations per group of 4 tokens.
+// GEMV over F32 / F16 rows (whole 16-byte chunks, 16-byte aligned) and Q5_0
+// rows (whole 64-value pairs of blocks, dword aligned), up to 64 KiB of
+// activations per group of 4 tokens (kernels_dense.hip).
 bool dense_supported(uint32_t type, size_t rows, size_t columns, const void *w, const float *x, size_t batch);
 hipError_t launch_dense_gemv(hipStream_t s, int cus, uint32_t type, const void *w, uint32_t rows, uint32_t columns,
                              size_t row_bytes, uint32_t batch, const float *x, float *y);

@@ -101,6 +101,17 @@ def q8_0_blocks(seed: int, blocks: int, chunk: int = 1 << 20) -> np.ndarray:
     return out.reshape(-1)
 
 
+def q5_0_blocks(seed: int, blocks: int, chunk: int = 1 << 20) -> np.ndarray:
+    """Q5_0 blocks (d, 32 high bits, 16 nibble bytes) with random codes."""
+    out = np.empty((blocks, 22), dtype=np.uint8)
+    for b0 in range(0, blocks, chunk):
+        nb = min(chunk, blocks - b0)
+        d = splitmix64(seed, 4 * b0, 4 * nb).reshape(nb, 4)
+        out[b0:b0 + nb, 0:2] = _f16_bits(1e-3 + 9e-3 * unit(d[:, 0]))[:, None].view(np.uint8)
+        out[b0:b0 + nb, 2:22] = np.ascontiguousarray(d[:, 1:4]).view(np.uint8)[:, :20]
+    return out.reshape(-1)
+
+
 def quantized_matrix(ggml_type: int, rows: int, columns: int, seed: int) -> np.ndarray:
     """Row-major encoded matrix: ``rows`` rows of ``columns`` values."""
     elems, _ = BLOCK[ggml_type]
@@ -111,6 +122,8 @@ def quantized_matrix(ggml_type: int, rows: int, columns: int, seed: int) -> np.n
         return q6_k_blocks(seed, blocks)
     if ggml_type == Q8_0:
         return q8_0_blocks(seed, blocks)
+    if ggml_type == Q5_0:
+        return q5_0_blocks(seed, blocks)
     if ggml_type == F32:
         return normal(seed, rows * columns).view(np.uint8)
     if ggml_type == F16:

@@ -87,12 +87,14 @@ def test_encoded_matvec_kernels_match_the_cpu_reference(ctx, kind):
     assert_metal_tolerance(got, want, f"type {kind}")
 
 
-@pytest.mark.parametrize("kind", [F32, F16])
-@pytest.mark.parametrize("rows,cols,batch", [(4096, 4096, 1), (12288, 4096, 2), (1000, 2560, 3), (37, 520, 5),
-                                             (70001, 256, 1), (9, 8192, 4)])
+@pytest.mark.parametrize("kind", [F32, F16, Q5_0])
+@pytest.mark.parametrize("rows,cols,batch", [(4096, 4096, 1), (12288, 4096, 2), (1000, 2560, 3), (37, 544, 5),
+                                             (70001, 256, 1), (9, 8192, 4), (300, 64, 2)])
 def test_dense_gemv_matches_oracle(ctx, kind, rows, cols, batch):
-    """F32 / F16 rows on the wide-load GEMV: columns that are not a multiple
-    of a 64-lane pass, odd row counts, 1-5 tokens (groups of up to 4)."""
+    """F32 / F16 / Q5_0 rows on the wide-load GEMV: columns that are not a
+    multiple of a 64-lane pass, odd row counts, 1-5 tokens (groups of up to
+    4); Q5_0 blocks 2 bytes off a dword boundary in every other block (544
+    columns, not whole block pairs, take the exact kernel)."""
     w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(160, kind))
     x = synth.normal(synth.activation_seed(160, cols), batch * cols).reshape(batch, cols)
     wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, batch * rows * 4)

@@ -109,6 +109,7 @@ typedef struct dmhip_error_detail {
 enum {
     DMHIP_TYPE_F32 = 0,
     DMHIP_TYPE_F16 = 1,
+    DMHIP_TYPE_Q5_0 = 6,
     DMHIP_TYPE_Q8_0 = 8,
     DMHIP_TYPE_Q4_K = 12,
     DMHIP_TYPE_Q6_K = 14,

@@ -106,3 +106,72 @@ def test_bf16_rounding_is_nearest_even():
     assert got.tolist()[:2] == [1.0, 1.0]
     assert got[2] == np.float32(1.015625)
     assert got[3] == -2.5
+
+
+# ---- the Rust binding (rust/hip.rs) is a transcription of the header --------
+
+def _rust_source():
+    return open(os.path.join(ROOT, "rust", "hip.rs")).read()
+
+
+def _c_struct_fields(name):
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "dmhip.h")).read(), flags=re.S)
+    body = re.search(r"typedef struct %s \{(.*?)\}" % name, text, flags=re.S).group(1)
+    fields = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        names = decl.split()[-1] if "," not in decl else decl
+        for part in re.split(r"\s*,\s*", names):
+            fields.append(re.sub(r"^.*[\s*]", "", part.strip()))
+    return fields
+
+
+def _rust_struct_fields(name):
+    body = re.search(r"pub struct %s \{(.*?)\}" % name, _rust_source(), flags=re.S).group(1)
+    return re.findall(r"pub (\w+):", body)
+
+
+def test_rust_ffi_declares_every_header_function():
+    block = _rust_source().split("unsafe extern \"C\" {", 1)[1].split("\n    }\n", 1)[0]
+    declared = sorted(set(re.findall(r"pub fn (dmhip_\w+)\(", block)))
+    # the two measurement hooks for one kernel variant each are C-only
+    c_only = {"dmhip_matvec_phase_trace", "dmhip_matvec_valu_device"}
+    assert declared == sorted(set(header_functions()) - c_only)
+
+
+def test_rust_status_constants_match_the_header():
+    text = open(os.path.join(ROOT, "include", "dmhip.h")).read()
+    c = dict((n, int(v)) for n, v in re.findall(r"(DMHIP_(?:OK|ERR_\w+)) = (\d+)", text))
+    rust = dict((n, int(v)) for n, v in re.findall(r"pub const (DMHIP_(?:OK|ERR_\w+)): c_int = (\d+);",
+                                                   _rust_source()))
+    assert rust == c and len(c) == 26
+
+
+def test_rust_structs_have_the_header_field_order():
+    for name in ("dmhip_error_detail", "dmhip_expert_layer_layout", "dmhip_expert_cache_stats"):
+        assert _rust_struct_fields(name) == _c_struct_fields(name), name
+
+
+def test_rust_type_ids_match_the_header():
+    text = open(os.path.join(ROOT, "include", "dmhip.h")).read()
+    c = dict((n, int(v)) for n, v in re.findall(r"(DMHIP_TYPE_\w+) = (\d+)", text))
+    rust = dict((n, int(v)) for n, v in re.findall(r"pub const (DMHIP_TYPE_\w+): u32 = (\d+);", _rust_source()))
+    assert rust == c
+
+
+def test_gguf_writer_places_tensors_where_the_reference_parser_would():
+    from tests import gguf_file
+    import tempfile
+    data = [("a", [256, 3], 12, bytes(range(144)) * 3), ("b", [7], 0, bytes(28)),
+            ("c", [32, 2, 2], 8, bytes(34 * 4))]
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "t.gguf")
+        gguf_file.write(path, data, alignment=64)
+        blob = open(path, "rb").read()
+    infos = gguf_file.read_tensors(blob)
+    assert [t.name for t in infos] == ["a", "b", "c"]
+    for t, (_, dims, kind, raw) in zip(infos, data):
+        assert t.absolute_offset % 64 == 0 and t.dimensions == dims and t.kind == kind
+        assert blob[t.absolute_offset:t.absolute_offset + t.byte_len] == raw

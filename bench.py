@@ -19,10 +19,11 @@ the same C2 workload, on this machine's host cores, with the thread count
 rayon's default pool would take (std::thread::available_parallelism).
 
 ``details`` holds the other BASELINE configurations (C1, C3, C4, C5), each
-measured the same way, and a Q8_0 GEMV entry (the third k-quant of the north
-star, which no configuration uses).
+measured the same way, a Q8_0 GEMV entry (the third k-quant of the north
+star, which no configuration uses) and F16 / F32 / Q5_0 GEMV entries (the
+other row types of a Gemma-class GGUF).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|dense|copy]
 """
 from __future__ import annotations
 
@@ -249,6 +250,43 @@ def bench_q8(ctx, synth, steps, warmup):
         out[f"{rows}x{cols}"] = {"ms": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9,
                                  "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         log(f"Q8_0 {rows}x{cols}: {ms * 1e3:.1f} us per launch ({out[f'{rows}x{cols}']['gbps']:.0f} GB/s)")
+    return out
+
+
+def bench_dense(ctx, synth, steps, warmup):
+    """The other GGUF row types a Gemma-class model holds (F16, F32, Q5_0;
+    no BASELINE config): batch-1 GEMV at 12288 x 4096 and 4096 x 4096 (F32
+    only the latter) over rotating copies (more than the 256 MB MALL),
+    back-to-back launches."""
+    out = {}
+    for kind, tag, shapes in ((1, "F16", ((12288, 4096), (4096, 4096))), (0, "F32", ((4096, 4096),)),
+                              (6, "Q5_0", ((12288, 4096), (4096, 4096)))):
+        for rows, cols in shapes:
+            w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(9, kind))
+            x = synth.normal(synth.activation_seed(9), cols)
+            copies = max(2, -(-300_000_000 // w.size))
+            wbs = [upload(ctx, w)]
+            for _ in range(copies - 1):
+                b = ctx.new_owned_buffer(w.size)
+                ctx.copy_device(b.device_ptr, wbs[0].device_ptr, w.size)
+                wbs.append(b)
+            xb, yb = upload(ctx, x), ctx.new_owned_buffer(rows * 4)
+            n = max(steps, 2 * copies)
+            for i in range(warmup):
+                ctx.matvec_device(kind, rows, cols, wbs[i % copies].device_ptr, 1, xb.device_ptr, yb.device_ptr)
+            ctx.synchronize()
+            time.sleep(0.2)
+            with Timed(ctx, kernels=False) as t:
+                for i in range(n):
+                    ctx.matvec_device(kind, rows, cols, wbs[i % copies].device_ptr, 1, xb.device_ptr, yb.device_ptr)
+            ms = t.wall_ms / n
+            step_bytes = w.size + 4 * cols + 4 * rows
+            key = f"{tag}_{rows}x{cols}"
+            out[key] = {"ms": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9,
+                        "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+            log(f"{key}: {ms * 1e3:.1f} us per launch ({out[key]['gbps']:.0f} GB/s)")
+            for b in wbs:
+                b.free()
     return out
 
 
@@ -524,14 +562,15 @@ def main() -> int:
     log("device:", ctx.device_name())
     if args.only:
         fn = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-              "q8": bench_q8, "copy": bench_copy}[args.only]
+              "q8": bench_q8, "dense": bench_dense, "copy": bench_copy}[args.only]
         res = fn(ctx, synth, args.steps, args.warmup)
         print(json.dumps(res[0] if isinstance(res, tuple) else res))
         return 0
 
     c2, (w2, x2) = bench_c2(ctx, synth, args.steps, args.warmup)
     details = {"C2": c2}
-    for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5), ("Q8_0", bench_q8)):
+    for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5), ("Q8_0", bench_q8),
+                     ("dense", bench_dense)):
         details[name] = fn(ctx, synth, max(3, args.steps // 2), args.warmup)
     log("CPU baseline")
     cpu = cpu_baseline(w2, x2, args.cpu_seconds)

@@ -735,7 +735,6 @@ int run_gemm(dmhip_ctx *ctx, size_t m, size_t n, size_t k, const uint16_t *a_bf1
                        a_bf16, (uint32_t)m, (uint32_t)k, (uint32_t)mp, a16, rowscale);
     DM_HIP(hipGetLastError());
     return launch_gemm<F, kRowTiles>(ctx, mp, m, n, k, a16, rowscale, weights, w_bytes, c);
-    return DMHIP_OK;
 }
 
 }  // namespace

@@ -50,12 +50,14 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
                           nullptr, nullptr));
         return DMHIP_OK;
     }
-    if (type == 8 && batch > 2 && qmv_supported(type, rows, columns, w, 2)) {
-        // Q8_0 (8) has only the int8 kernel (1-2 tokens): one launch per pair
-        // of tokens, each streaming the matrix at HBM rate, beats the exact
-        // per-element kernel by an order of magnitude.
-        for (size_t t = 0; t < batch; t += 2) {
-            const uint32_t n = batch - t < 2 ? (uint32_t)(batch - t) : 2u;
+    if (type == 8 && batch > 1 && qmv_supported(type, rows, columns, w, 1)) {
+        // Q8_0 (8) has only the int8 kernel (1-4 tokens, fewer on long rows):
+        // one launch per group of tokens, each streaming the matrix at HBM
+        // rate, beats the exact per-element kernel by an order of magnitude.
+        size_t per = 4;
+        while (per > 1 && !qmv_supported(type, rows, columns, w, per)) per /= 2;
+        for (size_t t = 0; t < batch; t += per) {
+            const uint32_t n = batch - t < per ? (uint32_t)(batch - t) : (uint32_t)per;
             DM_HIP(launch_qmv(ctx, type, (uint32_t)rows, (uint32_t)columns, w, n, x + t * columns, y + t * rows,
                               nullptr, nullptr));
         }

@@ -25,8 +25,9 @@ struct ArgmaxFinish {
     unsigned long long *best;
 };
 
-// True when the int8-MFMA matvec (decode batches of 1-2 tokens, Q4_K/Q6_K/
-// Q8_0) takes this shape; the caller has already checked qmv_supported.
+// True when the int8-MFMA matvec (decode batches of 1-4 tokens, Q4_K/Q6_K/
+// Q8_0, whose activation records fit the workgroup's LDS) takes this shape;
+// the caller has already checked qmv_supported.
 bool qmv8_supported(uint32_t type, size_t rows, size_t columns, size_t batch);
 
 // y[b][r] = W[r] . x[b] with the int8-MFMA kernels.  With `trace` (a

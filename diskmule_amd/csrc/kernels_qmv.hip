@@ -713,9 +713,10 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_partials_kernel(
 
 bool qmv_supported(uint32_t type, size_t rows, size_t columns, const void *w, size_t batch) {
     if (type == kQ8_0) {
-        // Q8_0 has the int8 kernel only: batch 1-2, whole 8-block super-blocks
-        // (272 bytes, 16-byte aligned rows), 32-bit offsets with slack.
-        if (columns == 0 || columns % 256 || batch < 1 || batch > 2 || rows == 0) return false;
+        // Q8_0 has the int8 kernel only: batch 1-4 (records permitting),
+        // whole 8-block super-blocks (272 bytes, 16-byte aligned rows),
+        // 32-bit offsets with slack.
+        if (columns == 0 || columns % 256 || batch < 1 || batch > 4 || rows == 0) return false;
         const uint64_t row_bytes = (uint64_t)(columns / 256) * 272;
         if (row_bytes * (rows + 2) + 1024 >= 0xffffffffull || ((uintptr_t)w & 15u)) return false;
         return qmv8_supported(type, rows, columns, batch);

@@ -1,5 +1,5 @@
 // kernels_qmv8.hip -- int8-MFMA quantized matvec for gfx950: decode batches
-// of one or two tokens over Q4_K / Q6_K / Q8_0 rows.
+// of one to four tokens over Q4_K / Q6_K / Q8_0 rows.
 //
 // y[b][r] = sum_c W[r][c] * x[b][c] (src/cpu.rs:345-399 semantics; the group
 // dots are exact integers, the blocks accumulate in fp32).
@@ -44,6 +44,10 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kStep8 = 192;  // A bytes of one MFMA step: 4 groups x 3 terms x 16
 constexpr uint32_t kZero8 = 1024;  // zeroed LDS bytes read by lanes whose A row is idle
 constexpr uint32_t kMaxWaves8 = 16;
+// Tokens per launch: lane group g writes token g.  A batch's records must
+// fit the workgroup's LDS with the staging areas (plan8), which bounds the
+// row length: 4 tokens of Q4_K rows up to about 8192 columns.
+constexpr uint32_t kMaxTokens8 = 4;
 
 // Bytes of one block's record for one token: A fragments of the four steps
 // (768), then Q6_K seeds (4 steps x 4 groups x 4 int32) or Q4_K sub-block
@@ -131,22 +135,22 @@ __device__ __forceinline__ void preload_x8(const float *__restrict__ x, int x_st
 template <uint32_t later, int TOK, int XP>
 __device__ __forceinline__ void wait_x8(XPre8<TOK, XP> &pre) {
     static_assert(later < 64, "vmcnt is 6 bits");
-    static_assert(TOK * XP == 1 || TOK * XP == 2 || TOK * XP == 4, "1, 2 or 4 preloaded blocks");
-    floatx4 a = pre.v[0][0];
-    floatx4 b = TOK * XP > 1 ? pre.v[(TOK * XP > 1 && XP == 1) ? 1 : 0][XP > 1 ? 1 : 0] : a;
-    floatx4 c = TOK * XP > 2 ? pre.v[0][XP > 2 ? 2 : 0] : a;
-    floatx4 d = TOK * XP > 3 ? pre.v[0][XP > 3 ? 3 : 0] : a;
-    if constexpr (TOK * XP == 1) {
+    constexpr int N = TOK * XP;
+    static_assert(N >= 1 && N <= 4, "1 to 4 preloaded blocks");
+    // preloaded block i is pre.v[i / XP][i % XP]
+    floatx4 &a = pre.v[0][0];
+    floatx4 &b = pre.v[(N > 1 ? 1 : 0) / XP][(N > 1 ? 1 : 0) % XP];
+    floatx4 &c = pre.v[(N > 2 ? 2 : 0) / XP][(N > 2 ? 2 : 0) % XP];
+    floatx4 &d = pre.v[(N > 3 ? 3 : 0) / XP][(N > 3 ? 3 : 0) % XP];
+    if constexpr (N == 1) {
         asm volatile("s_waitcnt vmcnt(%1)" : "+v"(a) : "n"(later) : "memory");
-    } else if constexpr (TOK * XP == 2) {
+    } else if constexpr (N == 2) {
         asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(later) : "memory");
+    } else if constexpr (N == 3) {
+        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(a), "+v"(b), "+v"(c) : "n"(later) : "memory");
     } else {
         asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(later) : "memory");
     }
-    pre.v[0][0] = a;
-    if constexpr (TOK * XP > 1) pre.v[XP == 1 ? 1 : 0][XP == 1 ? 0 : 1] = b;
-    if constexpr (TOK * XP > 2) pre.v[0][2 < XP ? 2 : 0] = c;
-    if constexpr (TOK * XP > 3) pre.v[0][3 < XP ? 3 : 0] = d;
 }
 
 template <uint32_t TYPE, int TOK, uint32_t WAVES, bool NORM, int XP>
@@ -492,7 +496,7 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     // wave's share of a 4096-column row is (16 blocks over W waves), so that
     // no record is computed for a block past the end; wider rows load the
     // rest after the weights.
-    constexpr int XP = TOK == 2 ? 1 : (W >= 16 ? 1 : 2);
+    constexpr int XP = TOK >= 2 ? 1 : (W >= 16 ? 1 : 2);
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
     constexpr uint32_t BB = kBlock8<TYPE>;
     using ST = Stage8<TYPE, G>;
@@ -638,10 +642,24 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     auto finish_row = [&](float (&acc)[NM][TOK], uint32_t rb, uint32_t tl) {
         const uint32_t row = tl * 16 + n;
         if (g < (uint32_t)TOK && rb != nowhere) {
-            const float ts = TOK == 1 || g == 0 ? tscale[0] : tscale[TOK - 1];
-            float v = (TOK == 1 || g == 0 ? acc[0][0] : acc[0][TOK - 1]) * ts;
+            // after the cross-group sums every lane group holds every token:
+            // lane group g writes token g.  The candidates pass through an
+            // empty asm as plain values, so the selection cannot become an
+            // index into the arrays (which would put them in scratch).
+            float ts = tscale[0], gate = acc[0][0], up = acc[NM - 1][0];
+#pragma unroll
+            for (int tok = 1; tok < TOK; tok++) {
+                float t_ts = tscale[tok], t_gate = acc[0][tok], t_up = acc[NM - 1][tok];
+                asm volatile("" : "+v"(t_ts), "+v"(t_gate), "+v"(t_up));
+                if (g == (uint32_t)tok) {
+                    ts = t_ts;
+                    gate = t_gate;
+                    up = t_up;
+                }
+            }
+            float v = gate * ts;
             if constexpr (MODE == 2) {
-                const float u = (TOK == 1 || g == 0 ? acc[NM - 1][0] : acc[NM - 1][TOK - 1]) * ts;
+                const float u = up * ts;
                 if (glm) {
                     // routed-expert activation (src/glm52/expert.rs:260-267)
                     v = (v / (1.0f + expf(-v))) * u;
@@ -794,7 +812,7 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
 // two-token two-block fetches); with less they spill to scratch.
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
 constexpr int waves_per_eu8() {
-    return (G > 2 || (MODE == 2 && (TYPE == kQ6_K || (TOK == 2 && G == 2)))) ? 2 : 4;
+    return (G > 2 || TOK > 2 || (MODE == 2 && (TYPE == kQ6_K || (TOK == 2 && G == 2)))) ? 2 : 4;
 }
 
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W>
@@ -934,8 +952,9 @@ hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
     const size_t lds = lds8_bytes(TYPE, blocks, TOK, WAVES, G, MODE == 2 ? 2u : 1u);
     uint32_t grid;
     if (S == 1) {
-        // persistent: as many workgroups as fit on the device at once
-        const uint32_t by_regs = 4 * (G <= 2 ? 4 : 2) / WAVES;
+        // persistent: as many workgroups as fit on the device at once (the
+        // register budget allows waves_per_eu8 waves per SIMD)
+        const uint32_t by_regs = 4 * waves_per_eu8<TYPE, MODE, TOK, G>() / WAVES;
         uint32_t by_lds = (uint32_t)(kMaxLds8 / (lds + 4096));
         uint32_t per_cu = by_regs < by_lds ? by_regs : by_lds;
         if (per_cu == 0) per_cu = 1;
@@ -975,8 +994,10 @@ hipError_t run8_s(dmhip_ctx *ctx, uint32_t s, const Args8 &a) {
 
 template <uint32_t TYPE, int MODE, int TOK>
 hipError_t run8_g(dmhip_ctx *ctx, const Plan8 &p, const Args8 &a) {
-    if constexpr (MODE != 2) {
+    if constexpr (MODE != 2 && TOK <= 2) {
         if (p.g == 4) return run8_s<TYPE, MODE, TOK, 4>(ctx, p.s, a);
+    } else {
+        if (p.g == 4) return hipErrorInvalidValue;  // not instantiated: plan8 picks G <= 2
     }
     if (p.g == 2) return run8_s<TYPE, MODE, TOK, 2>(ctx, p.s, a);
     return run8_s<TYPE, MODE, TOK, 1>(ctx, p.s, a);
@@ -1066,22 +1087,40 @@ hipError_t launch8(dmhip_ctx *ctx, uint32_t batch, int mode, const Args8 &a, uin
         if constexpr (TYPE == kQ8_0) {
             return hipErrorInvalidValue;  // gate/up pairs are Q4_K or Q6_K
         } else {
+            // 1-2 tokens (qmv8_gate_up_supported)
+            if (batch > 2) return hipErrorInvalidValue;
             return batch == 1 ? run8_g<TYPE, 2, 1>(ctx, p, a) : run8_g<TYPE, 2, 2>(ctx, p, a);
         }
     }
-    return batch == 1 ? run8_g<TYPE, 0, 1>(ctx, p, a) : run8_g<TYPE, 0, 2>(ctx, p, a);
+    switch (batch) {
+    case 1: return run8_g<TYPE, 0, 1>(ctx, p, a);
+    case 2: return run8_g<TYPE, 0, 2>(ctx, p, a);
+    case 3: return run8_g<TYPE, 0, 3>(ctx, p, a);
+    default: return run8_g<TYPE, 0, 4>(ctx, p, a);
+    }
 }
 
 }  // namespace
 
 bool qmv8_supported(uint32_t type, size_t rows, size_t columns, size_t batch) {
     if (type != kQ4_K && type != kQ6_K && type != kQ8_0) return false;
-    if (batch < 1 || batch > 2 || columns % 256 || columns == 0) return false;
+    if (batch < 1 || batch > kMaxTokens8 || columns % 256 || columns == 0) return false;
+    // 3-4 tokens of Q4_K / Q6_K: the int8 kernel against the fp16 one and its
+    // preparation launch, measured per launch on MI355X: 4096 x 4096 Q4_K
+    // 7.4 / 8.5 us against 11.0 us, Q6_K 9.4 / 10.8 against 12.3 us, but
+    // 12288 x 4096 Q4_K 17.4 / 21.1 against 17.7 / 17.8 us (the records of
+    // every token make each block's work longer than its bytes take to
+    // arrive).  Q8_0 has only this kernel.
+    if (batch > 2 && type != kQ8_0 && (uint64_t)rows * columns > (20ull << 20)) return false;
     return plan8(type, (uint32_t)rows, (uint32_t)columns, (uint32_t)batch, 1).s != 0;
 }
 
 bool qmv8_gate_up_supported(uint32_t type, size_t rows, size_t columns, size_t batch) {
     if (type != kQ4_K && type != kQ6_K) return false;
+    // Gate/up pairs of 3-4 tokens measured slower here than on the fp16
+    // kernels with their preparation launch (C3, Q4_K 12288 x 4096, 4
+    // tokens: 37.5 us against 19.4 + 4.6 us): the records of both matrices'
+    // token blocks leave one 8-wave workgroup per CU.
     if (batch < 1 || batch > 2 || columns % 256 || columns == 0) return false;
     return plan8(type, (uint32_t)rows, (uint32_t)columns, (uint32_t)batch, 2).s != 0;
 }

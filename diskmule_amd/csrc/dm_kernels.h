@@ -70,12 +70,20 @@ hipError_t launch_argmax(hipStream_t s, const float *v, size_t n, ArgmaxState *s
                          uint32_t *index);
 hipError_t launch_argmax_init(hipStream_t s, ArgmaxState *state);
 hipError_t launch_argmax_finish(hipStream_t s, const ArgmaxState *state, uint32_t *index);
+// Where a selection kernel records a row with a non-finite logit: it stores
+// `mark` into *word.  A caller that checks the word after each call gives
+// each call a new nonzero mark, so the word needs no reset between calls (a
+// stale word equals the current mark only after 2^32 calls).
+struct BadFlag {
+    uint32_t *word;
+    uint32_t mark;
+};
 hipError_t launch_top_k(hipStream_t s, const float *logits, uint32_t rows, uint32_t count,
-                        uint32_t k, uint32_t *ids, float *probabilities, uint32_t *non_finite);
+                        uint32_t k, uint32_t *ids, float *probabilities, BadFlag non_finite);
 hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
-                               uint32_t *non_finite, uint32_t *host_ids = nullptr,
+                               BadFlag non_finite, uint32_t *host_ids = nullptr,
                                float *host_probs = nullptr, uint32_t *tickets = nullptr,
                                uint32_t *host_bad = nullptr);
 // With host_ids, the selection and one word per token (nonzero when that

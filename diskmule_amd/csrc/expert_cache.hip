@@ -562,13 +562,13 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     float *sel_probs = (float *)(c->host_selection + kSelectionPairs * 4);
     uint32_t *sel_bad = (uint32_t *)(c->host_selection + kSelectionPairs * 8);
     // The previous call has finished (it ends with a synchronisation): the
-    // flags can be cleared from here; the device flag the fallback router
-    // sets is cleared on the stream.
+    // per-token words can be cleared from here.
     memset(sel_bad, 0, 16 * 4);
-    DM_HIP(launch_fill_u32(ctx->stream, ctx->flags, 1, 0));
+    ctx->router_mark = ctx->router_mark + 1 ? ctx->router_mark + 1 : 1;
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
-                               (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs, ctx->flags, sel_ids,
-                               sel_probs, batch <= kRouterTickets ? ctx->router_tickets : nullptr, sel_bad));
+                               (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs,
+                               BadFlag{ctx->flags, ctx->router_mark}, sel_ids, sel_probs,
+                               batch <= kRouterTickets ? ctx->router_tickets : nullptr, sel_bad));
     DM_HIP(hipStreamSynchronize(ctx->stream));
     // top_k_softmax rejects non-finite logits (src/cpu.rs:240-245); nothing
     // has been acquired yet.

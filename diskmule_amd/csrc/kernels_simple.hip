@@ -136,10 +136,10 @@ __global__ void argmax_finish_kernel(const ArgmaxState *state, uint32_t *index) 
 // ---- top-k softmax (src/cpu.rs:232-260) -------------------------------
 // One workgroup per row of `count` logits.  Selection i is the largest key
 // strictly below selection i-1 (keys are unique: value, then index).  A
-// non-finite logit sets *non_finite; the return value (the same in every
-// thread) says whether the row held one.
+// non-finite logit stores non_finite.mark into *non_finite.word; the return
+// value (the same in every thread) says whether the row held one.
 __device__ bool block_top_k(const float *logits, uint32_t count, uint32_t k, uint32_t *ids,
-                            float *probabilities, uint32_t *non_finite) {
+                            float *probabilities, BadFlag non_finite) {
     __shared__ uint64_t partial[16];
     __shared__ uint64_t chosen[kMaxTopK];
     __shared__ float values[kMaxTopK];
@@ -147,7 +147,7 @@ __device__ bool block_top_k(const float *logits, uint32_t count, uint32_t k, uin
     uint32_t bad = 0;
     for (uint32_t i = tid; i < count; i += nthreads)
         if (!__builtin_isfinite(logits[i])) bad = 1;
-    if (bad) atomicOr(non_finite, 1u);
+    if (bad) *non_finite.word = non_finite.mark;  // every writer stores the same value
     const bool row_bad = __syncthreads_or((int)bad) != 0;
     uint64_t previous = ~0ull;
     for (uint32_t s = 0; s < k; s++) {
@@ -189,7 +189,7 @@ __device__ bool block_top_k(const float *logits, uint32_t count, uint32_t k, uin
 
 __global__ void __launch_bounds__(256) top_k_kernel(const float *__restrict__ logits,
                                                     uint32_t count, uint32_t k, uint32_t *ids,
-                                                    float *probabilities, uint32_t *non_finite) {
+                                                    float *probabilities, BadFlag non_finite) {
     uint32_t row = blockIdx.x;
     block_top_k(logits + (size_t)row * count, count, k, ids + (size_t)row * k,
                 probabilities + (size_t)row * k, non_finite);
@@ -201,7 +201,7 @@ __global__ void __launch_bounds__(256) top_k_kernel(const float *__restrict__ lo
 __global__ void __launch_bounds__(256) router_top_k_kernel(
     const uint16_t *__restrict__ router, uint32_t hidden, uint32_t experts, uint32_t k,
     const float *__restrict__ x, float *__restrict__ logits, uint32_t *ids,
-    float *probabilities, uint32_t *non_finite) {
+    float *probabilities, BadFlag non_finite) {
     uint32_t token = blockIdx.x;
     extern __shared__ float s_logits[];
     const float *xt = x + (size_t)token * hidden;
@@ -245,7 +245,7 @@ template <uint32_t CC>
 __global__ void __launch_bounds__(256) router_staged_kernel(
     const uint16_t *__restrict__ router, uint32_t hidden, uint32_t experts, uint32_t k,
     const float *__restrict__ x, float *__restrict__ logits, uint32_t *ids, float *probabilities,
-    uint32_t *non_finite, uint32_t *host_ids, float *host_probs, uint32_t *host_bad) {
+    BadFlag non_finite, uint32_t *host_ids, float *host_probs, uint32_t *host_bad) {
     constexpr uint32_t ROW = CC * 2 + 16;  // LDS bytes per expert row
     constexpr uint32_t PR = CC * 2 / 16;   // 16-byte pieces of a row per chunk
     constexpr uint32_t XP = CC * 4 / 16;   // 16-byte pieces of x per chunk
@@ -380,7 +380,7 @@ static_assert((RF_WPIECES + RF_XPIECES) % 64 == 0, "whole loads per lane");
 __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restrict__ router, uint32_t hidden,
                                                          uint32_t experts, uint32_t k, const float *__restrict__ x,
                                                          float *logits, uint32_t *tickets, uint32_t *ids,
-                                                         float *probabilities, uint32_t *non_finite,
+                                                         float *probabilities, BadFlag non_finite,
                                                          uint32_t *host_ids, float *host_probs, uint32_t *host_bad) {
     __shared__ v4a rf_lds[2 * RF_BUF / 4];
     const uint32_t lane = threadIdx.x, e0 = blockIdx.x * RF_EXPERTS, token = blockIdx.y;
@@ -504,7 +504,7 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
 // host_ids is set.
 __global__ void __launch_bounds__(256) top_k_host_kernel(const float *__restrict__ logits, uint32_t count,
                                                          uint32_t k, uint32_t *ids, float *probabilities,
-                                                         uint32_t *non_finite, uint32_t *host_ids,
+                                                         BadFlag non_finite, uint32_t *host_ids,
                                                          float *host_probs, uint32_t *host_bad) {
     __shared__ float s_row[256];
     const uint32_t row = blockIdx.x;
@@ -698,7 +698,7 @@ hipError_t launch_argmax_finish(hipStream_t s, const ArgmaxState *state, uint32_
 }
 
 hipError_t launch_top_k(hipStream_t s, const float *logits, uint32_t rows, uint32_t count,
-                        uint32_t k, uint32_t *ids, float *probabilities, uint32_t *non_finite) {
+                        uint32_t k, uint32_t *ids, float *probabilities, BadFlag non_finite) {
     hipLaunchKernelGGL(top_k_kernel, dim3(rows), dim3(256), 0, s, logits, count, k, ids,
                        probabilities, non_finite);
     return hipGetLastError();
@@ -708,7 +708,7 @@ template <uint32_t CC>
 static hipError_t launch_router_staged(hipStream_t s, const uint16_t *router, uint32_t hidden,
                                        uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                        float *logits, uint32_t *ids, float *probabilities,
-                                       uint32_t *non_finite, uint32_t *host_ids, float *host_probs,
+                                       BadFlag non_finite, uint32_t *host_ids, float *host_probs,
                                        uint32_t *host_bad) {
     const size_t lds = 2 * (((size_t)experts * (CC * 2 + 16) + CC * 4 + 15) & ~(size_t)15);
     // the largest slot ring, once per device
@@ -724,7 +724,7 @@ static hipError_t launch_router_staged(hipStream_t s, const uint16_t *router, ui
 hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
-                               uint32_t *non_finite, uint32_t *host_ids, float *host_probs, uint32_t *tickets,
+                               BadFlag non_finite, uint32_t *host_ids, float *host_probs, uint32_t *tickets,
                                uint32_t *host_bad) {
     if (host_ids && (!host_probs || !host_bad)) return hipErrorInvalidValue;
     const bool staged = experts <= 256 && hidden % 8 == 0 && (uint64_t)experts * hidden * 2 < (1ull << 30) && ((uintptr_t)router & 15u) == 0 &&
@@ -745,6 +745,12 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
     if (staged)
         return launch_router_staged<64>(s, router, hidden, experts, k, batch, x, logits, ids, probabilities,
                                         non_finite, host_ids, host_probs, host_bad);
+    // This kernel reports through the shared word only, which host_bad[0]
+    // receives: cleared first, so it holds this call's mark or zero.
+    if (host_ids) {
+        hipError_t e0 = launch_fill_u32(s, non_finite.word, 1, 0);
+        if (e0 != hipSuccess) return e0;
+    }
     hipLaunchKernelGGL(router_top_k_kernel, dim3(batch), dim3(256), experts * sizeof(float), s,
                        router, hidden, experts,
                        k, x, logits, ids, probabilities, non_finite);
@@ -755,7 +761,7 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
     e = hipMemcpyAsync(host_probs, probabilities, (size_t)batch * k * 4, hipMemcpyDeviceToHost, s);
     if (e != hipSuccess) return e;
     // this kernel only sets the shared flag: it stands for every token
-    return hipMemcpyAsync(host_bad, non_finite, 4, hipMemcpyDeviceToHost, s);
+    return hipMemcpyAsync(host_bad, non_finite.word, 4, hipMemcpyDeviceToHost, s);
 }
 
 __global__ void fill_u32_kernel(uint32_t *p, uint32_t n, uint32_t value) {

@@ -90,6 +90,7 @@ struct dmhip_ctx {
     size_t aux_lent_bytes = 0;
     dm::ArgmaxState *argmax_state = nullptr;  // device
     uint32_t *router_tickets = nullptr;       // device, kRouterTickets counters, zero between launches
+    uint32_t router_mark = 0;                 // mark of the last router call (BadFlag), never 0 once set
     uint32_t *argmax_ticket = nullptr;        // device, zero between launches: ticket, then (at +8) the best key
     uint32_t *argmax_index = nullptr;         // device
     uint32_t *flags = nullptr;                // device: [0] non-finite

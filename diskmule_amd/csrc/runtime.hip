@@ -661,7 +661,7 @@ int dmhip_top_k_softmax(dmhip_ctx *ctx, const float *logits, size_t logits_len, 
     float *dp = (float *)(dids + k);
     DM_HIP(hipMemcpyAsync(ctx->in.ptr, logits, bytes, hipMemcpyHostToDevice, ctx->stream));
     DM_HIP(launch_top_k(ctx->stream, (const float *)ctx->in.ptr, 1, (uint32_t)logits_len,
-                        (uint32_t)k, dids, dp, ctx->flags));
+                        (uint32_t)k, dids, dp, BadFlag{ctx->flags + 2, 1}));  // checked on the host first
     uint32_t ids[kMaxTopK];
     DM_HIP(hipMemcpyAsync(ids, dids, k * 4, hipMemcpyDeviceToHost, ctx->stream));
     DM_HIP(hipMemcpyAsync(probabilities, dp, k * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -911,11 +911,13 @@ int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_
     DM_CHECK(count_u32(hidden));
     if (batch == 0) return DMHIP_OK;
     DM_CHECK(set_device(ctx));
-    DM_HIP(launch_fill_u32(ctx->stream, ctx->flags, 1, 0));
+    // A new mark per call: the word needs no clearing launch.
+    ctx->router_mark = ctx->router_mark + 1 ? ctx->router_mark + 1 : 1;
     ctx->router_pending = true;
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                (uint32_t)k, (uint32_t)batch, x, logits, ids, probabilities,
-                               ctx->flags, nullptr, nullptr, batch <= kRouterTickets ? ctx->router_tickets : nullptr));
+                               BadFlag{ctx->flags, ctx->router_mark}, nullptr, nullptr,
+                               batch <= kRouterTickets ? ctx->router_tickets : nullptr));
     return DMHIP_OK;
 }
 
@@ -928,7 +930,7 @@ int dmhip_router_result(dmhip_ctx *ctx) {
     DM_HIP(hipMemcpyAsync(&flag, ctx->flags, 4, hipMemcpyDeviceToHost, ctx->stream));
     DM_HIP(hipStreamSynchronize(ctx->stream));
     ctx->router_pending = false;
-    if (flag) return fail_non_finite("top-k softmax");
+    if (flag == ctx->router_mark) return fail_non_finite("top-k softmax");
     return DMHIP_OK;
 }
 

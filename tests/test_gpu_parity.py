@@ -667,13 +667,14 @@ def _moe_setup(hidden=2048, width=768, experts=128):
 @pytest.mark.parametrize("batch,hidden,experts,k", [(1, 2048, 128, 8), (5, 2048, 128, 8), (2, 1000, 60, 4),
                                                     (3, 2824, 128, 8), (2, 4096, 256, 8), (2, 1016, 200, 6),
                                                     (1, 2050, 128, 8), (1, 512, 300, 8), (2, 1024, 12, 4),
-                                                    (33, 2048, 128, 8), (4100, 256, 16, 2)])
+                                                    (33, 2048, 128, 8), (4100, 256, 16, 2), (2, 24576, 128, 8),
+                                                    (3, 4104, 64, 4)])
 def test_router_top_k_is_bit_exact(ctx, batch, hidden, experts, k):
     """The bf16 router fold (src/cpu.rs:384-397 order) and top-k: logits bit
     for bit, ids exact.  Covers the expert-parallel fold (8 experts per
-    workgroup, 512-column chunks, partial last chunks and workgroups; above
-    4096 tokens the selection runs as a second launch), the LDS-staged
-    one-workgroup kernel (fewer than 16 experts), and the
+    workgroup, 512-column chunks, partial last chunks and workgroups, long
+    rows; above 4096 tokens the selection runs as a second launch), the
+    LDS-staged one-workgroup kernel (fewer than 16 experts), and the
     unstaged kernel (hidden % 8 != 0, more than 256 experts)."""
     print(f"router batch={batch} hidden={hidden} experts={experts} k={k}", flush=True)
     router = synth.to_bf16_bits(synth.normal(synth.weight_seed(6, hidden), experts * hidden) * np.float32(0.02))

@@ -482,7 +482,7 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ6_K> &raw, const i32x4 *
 // workgroup's LDS allows on a C2-sized row; a tighter budget makes the
 // compiler wait for each prefetch right after issuing it.
 // ---------------------------------------------------------------------------
-template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W>
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W, bool PC = false>
 __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
                                           uint32_t rows, uint32_t columns, uint32_t row_bytes,
                                           uint32_t total_bytes, const float *__restrict__ x, int x_stride,
@@ -491,6 +491,7 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
                                           const ArgmaxFinish finish, uint64_t *__restrict__ trace) {
     constexpr uint32_t WAVES = W;
     static_assert(W % S == 0, "a workgroup holds whole tiles");
+    static_assert(!PC || (S == (int)W && S > 1), "a cooperative workgroup splits each tile over all its waves");
     constexpr int NM = MODE == 2 ? 2 : 1;  // weight matrices streamed
     // Activation blocks of each wave loaded ahead of the weights: what a
     // wave's share of a 4096-column row is (16 blocks over W waves), so that
@@ -536,6 +537,10 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
         t_end = (uint32_t)((uint64_t)(blockIdx.x + 1) * tiles / gridDim.x);
         tile = t0 + wave;
         if (threadIdx.x == 0) next_tile = t0 + WAVES;
+    } else if constexpr (PC) {
+        // persistent: the workgroup takes tiles blockIdx.x, + gridDim.x, ...
+        tile = blockIdx.x;
+        t_end = tiles;
     } else {
         tile = blockIdx.x * (WAVES / S) + wave / S;
         t_end = tile + 1 < tiles ? tile + 1 : tiles;
@@ -720,6 +725,55 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
             row_base = next_row_base;
             active = tile < t_end;
         }
+    } else if constexpr (PC) {
+        // Every wave takes block groups kpart, kpart + S, ... of the
+        // workgroup's current tile, so the workgroup requests the tile's 16
+        // rows together (whole rows: one contiguous span of the matrix); the
+        // next tile's first groups are requested before the reduction.
+        // `active` is the same in every wave of the workgroup.
+        while (active) {
+            float acc[NM][TOK];
+#pragma unroll
+            for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+                for (int tok = 0; tok < TOK; tok++) acc[mtx][tok] = 0.0f;
+            const uint32_t next = tile + gridDim.x;
+            const uint32_t rb = row_base;
+            for (uint32_t grp = kpart; grp < groups; grp += S) {
+                put_stage();
+                if (grp + S < groups) {
+                    fetch(grp + S, true);
+                } else if (next < t_end) {
+                    setup(next, true);
+                    fetch(kpart, true);
+                }
+                compute_group(grp, rb, acc);
+            }
+#pragma unroll
+            for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+                for (int tok = 0; tok < TOK; tok++) {
+                    acc[mtx][tok] += __shfl_xor(acc[mtx][tok], 16, 64);
+                    acc[mtx][tok] += __shfl_xor(acc[mtx][tok], 32, 64);
+                    red[((wave * 64 + lane) * TOK + tok) * NM + mtx] = acc[mtx][tok];
+                }
+            __syncthreads();
+            if (kpart == 0) {
+#pragma unroll
+                for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+                    for (int tok = 0; tok < TOK; tok++) {
+                        float v = 0.0f;
+                        for (int p = 0; p < S; p++) v += red[(((wave + p) * 64 + lane) * TOK + tok) * NM + mtx];
+                        acc[mtx][tok] = v;
+                    }
+                finish_row(acc, rb, tile);
+            }
+            __syncthreads();  // red is written again for the next tile
+            tile = next;
+            row_base = next_row_base;
+            active = tile < t_end;
+        }
     } else {
         float acc[NM][TOK];
 #pragma unroll
@@ -810,19 +864,19 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
 // Register budget: four waves per SIMD (128 VGPRs), or two (256) for
 // four-block fetches and for the gate/up kernels that need more (Q6_K pairs,
 // two-token two-block fetches); with less they spill to scratch.
-template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
+template <uint32_t TYPE, int MODE, int TOK, uint32_t G, bool PC = false>
 constexpr int waves_per_eu8() {
-    return (G > 2 || TOK > 2 || (MODE == 2 && (TYPE == kQ6_K || (TOK == 2 && G == 2)))) ? 2 : 4;
+    return (PC || G > 2 || TOK > 2 || (MODE == 2 && (TYPE == kQ6_K || (TOK == 2 && G == 2)))) ? 2 : 4;
 }
 
-template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W>
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W, bool PC = false>
 __global__ void __launch_bounds__(64 * W)
-    __attribute__((amdgpu_waves_per_eu(waves_per_eu8<TYPE, MODE, TOK, G>()))) qmv8_kernel(
+    __attribute__((amdgpu_waves_per_eu(waves_per_eu8<TYPE, MODE, TOK, G, PC>()))) qmv8_kernel(
     const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows, uint32_t columns,
     uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x, int normalize, float epsilon,
     float *__restrict__ y, ArgmaxPartial *__restrict__ partials, ArgmaxFinish finish, uint64_t *trace) {
-    qmv8_body<TYPE, S, MODE, TOK, G, W>(w, w2, rows, columns, row_bytes, total_bytes, x, (int)columns, normalize,
-                                        epsilon, 0, y, (int)rows, partials, finish, trace);
+    qmv8_body<TYPE, S, MODE, TOK, G, W, PC>(w, w2, rows, columns, row_bytes, total_bytes, x, (int)columns,
+                                            normalize, epsilon, 0, y, (int)rows, partials, finish, trace);
 }
 
 // Grouped launch over the routed-expert jobs of a MoE layer: job
@@ -874,7 +928,16 @@ size_t lds8_bytes(uint32_t type, uint32_t blocks, uint32_t batch, uint32_t waves
 
 struct Plan8 {
     uint32_t s = 0, g = 1;
+    bool pc = false;  // persistent workgroups whose S = 8 waves share each tile
 };
+
+// Tall Q4_K and Q8_0 matrices: persistent 8-wave workgroups that read each
+// 16-row tile together (every wave one group of the tile's rows, so the
+// workgroup requests one contiguous span), rather than waves that each
+// stream their own tile.  Measured on MI355X at 151936 x 4096, batch 1:
+// Q4_K 62.3 against 65.6 us, Q8_0 110.3 against 117.5 us (6.0 TB/s); Q6_K
+// 109 against 97 us, so Q6_K keeps per-wave tiles.
+constexpr bool kCooperativeTall = true;
 
 // Waves per workgroup of a plan with split S: eight up to S = 8 (several
 // tiles per workgroup below that), S above.
@@ -916,6 +979,12 @@ Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint
     p.g = tiles >= 2048 ? 2u : 1u;
     while (p.g > 1 && blocks < 2 * p.g) p.g /= 2;
     const uint32_t groups = (blocks + p.g - 1) / p.g;
+    if (kCooperativeTall && type != kQ6_K && tiles >= 2048 && p.g == 2 && groups >= 8 && mats == 1 && batch <= 2 &&
+        fits8(type, blocks, batch, mats, 8, p.g)) {
+        p.s = 8;
+        p.pc = true;
+        return p;
+    }
     const uint32_t s_max = mats == 2 ? 8u : kMaxWaves8;  // gate/up: see run8_s
     uint32_t s = 1;
     while (s < s_max && (size_t)tiles * s < 4096 && groups >= 2 * s) s *= 2;
@@ -942,7 +1011,7 @@ struct Args8 {
     uint64_t *trace;
 };
 
-template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, bool PC = false>
 hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
     constexpr uint32_t WAVES = waves8(S);
     const uint32_t rows = a.rows, columns = a.columns;
@@ -951,22 +1020,22 @@ hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
     const uint32_t row_bytes = blocks * kBlock8<TYPE>;
     const size_t lds = lds8_bytes(TYPE, blocks, TOK, WAVES, G, MODE == 2 ? 2u : 1u);
     uint32_t grid;
-    if (S == 1) {
+    if (S == 1 || PC) {
         // persistent: as many workgroups as fit on the device at once (the
         // register budget allows waves_per_eu8 waves per SIMD)
-        const uint32_t by_regs = 4 * waves_per_eu8<TYPE, MODE, TOK, G>() / WAVES;
+        const uint32_t by_regs = 4 * waves_per_eu8<TYPE, MODE, TOK, G, PC>() / WAVES;
         uint32_t by_lds = (uint32_t)(kMaxLds8 / (lds + 4096));
         uint32_t per_cu = by_regs < by_lds ? by_regs : by_lds;
         if (per_cu == 0) per_cu = 1;
         const uint32_t cus = ctx->compute_units > 0 ? (uint32_t)ctx->compute_units : 256u;
-        const uint32_t need = (tiles + WAVES - 1) / WAVES;
+        const uint32_t need = PC ? tiles : (tiles + WAVES - 1) / WAVES;
         grid = cus * per_cu < need ? cus * per_cu : need;
     } else {
         const uint32_t per = WAVES / S;
         grid = (tiles + per - 1) / per;
     }
     if (a.count) *a.count = grid;
-    auto kernel = qmv8_kernel<TYPE, S, MODE, TOK, G, WAVES>;
+    auto kernel = qmv8_kernel<TYPE, S, MODE, TOK, G, WAVES, PC>;
     if (lds > 64 * 1024) {
         static LdsLimit limit;
         hipError_t e = limit.ensure((const void *)kernel, lds);
@@ -994,6 +1063,11 @@ hipError_t run8_s(dmhip_ctx *ctx, uint32_t s, const Args8 &a) {
 
 template <uint32_t TYPE, int MODE, int TOK>
 hipError_t run8_g(dmhip_ctx *ctx, const Plan8 &p, const Args8 &a) {
+    if constexpr (TYPE != kQ6_K && MODE != 2 && TOK <= 2) {
+        if (p.pc) return p.g == 2 && p.s == 8 ? run8<TYPE, 8, MODE, TOK, 2, true>(ctx, a) : hipErrorInvalidValue;
+    } else {
+        if (p.pc) return hipErrorInvalidValue;  // plan8 plans no cooperative Q6_K or gate/up launch
+    }
     if constexpr (MODE != 2 && TOK <= 2) {
         if (p.g == 4) return run8_s<TYPE, MODE, TOK, 4>(ctx, p.s, a);
     } else {

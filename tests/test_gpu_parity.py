@@ -416,12 +416,14 @@ def test_output_head_q6_k_with_argmax(ctx):
 
 
 @pytest.mark.parametrize("kind,rows,cols,batch", [(Q4_K, 70000, 4096, 1), (Q6_K, 66001, 2048, 2),
-                                                 (Q6_K, 65600, 768, 1), (Q4_K, 66000, 12288, 1)])
-def test_tall_matvec_line_aligned_staging(ctx, kind, rows, cols, batch):
-    """Tall matrices take the persistent plan, whose waves fetch whole
-    128-byte lines one block at a time and keep each fetch's last line for
-    the next block of the row: Q6_K rows start anywhere in a line, row counts
-    that end mid-tile, three-block rows, two tokens."""
+                                                 (Q6_K, 65600, 768, 1), (Q4_K, 66000, 12288, 1),
+                                                 (Q4_K, 40007, 4096, 2), (Q8_0, 36001, 2048, 2),
+                                                 (Q8_0, 33000, 12288, 1)])
+def test_tall_matvec_persistent_plans(ctx, kind, rows, cols, batch):
+    """Tall matrices take the persistent plans: waves that each stream their
+    own tiles (Q6_K) and workgroups whose 8 waves share each tile (Q4_K,
+    Q8_0).  Row counts that end mid-tile, three-block and wide rows, two
+    tokens."""
     print(f"tall type={kind} {rows}x{cols} batch={batch}", flush=True)
     w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(60, rows))
     x = synth.normal(synth.activation_seed(60, rows), batch * cols).reshape(batch, cols)

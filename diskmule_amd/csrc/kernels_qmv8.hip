@@ -866,7 +866,10 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
 // two-token two-block fetches); with less they spill to scratch.
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G, bool PC = false>
 constexpr int waves_per_eu8() {
-    return (PC || G > 2 || TOK > 2 || (MODE == 2 && (TYPE == kQ6_K || (TOK == 2 && G == 2)))) ? 2 : 4;
+    // cooperative: the Q8_0 form gets 256 registers (one 8-wave workgroup
+    // per CU); the Q4_K form fits 128 (two per CU)
+    return ((PC && TYPE == kQ8_0) || G > 2 || TOK > 2 || (MODE == 2 && (TYPE == kQ6_K || (TOK == 2 && G == 2)))) ? 2
+                                                                                                            : 4;
 }
 
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W, bool PC = false>
@@ -931,13 +934,17 @@ struct Plan8 {
     bool pc = false;  // persistent workgroups whose S = 8 waves share each tile
 };
 
-// Tall Q4_K and Q8_0 matrices: persistent 8-wave workgroups that read each
-// 16-row tile together (every wave one group of the tile's rows, so the
-// workgroup requests one contiguous span), rather than waves that each
-// stream their own tile.  Measured on MI355X at 151936 x 4096, batch 1:
-// Q4_K 62.3 against 65.6 us, Q8_0 110.3 against 117.5 us (6.0 TB/s); Q6_K
-// 109 against 97 us, so Q6_K keeps per-wave tiles.
+// Very tall Q4_K and Q8_0 matrices (output heads): persistent 8-wave
+// workgroups that read each 16-row tile together (every wave one group of
+// the tile's rows, so the workgroup requests one contiguous span), rather
+// than waves that each stream their own tile.  Measured on MI355X at
+// 151936 x 4096, batch 1: Q4_K 61.5 against 65.5 us (with the argmax 63.2
+// against 69.0), Q8_0 111.2 against 116.5 us.  Below about 8192 tiles it
+// loses (Q4_K 65536 x 2048: 17.1 against 16.3 us), and Q6_K gains nothing
+// (a 16-wave form: 95.9 against 95.6 us at C2, slower below), so those keep
+// per-wave tiles.
 constexpr bool kCooperativeTall = true;
+constexpr uint32_t kCooperativeTiles = 8192;
 
 // Waves per workgroup of a plan with split S: eight up to S = 8 (several
 // tiles per workgroup below that), S above.
@@ -979,8 +986,8 @@ Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint
     p.g = tiles >= 2048 ? 2u : 1u;
     while (p.g > 1 && blocks < 2 * p.g) p.g /= 2;
     const uint32_t groups = (blocks + p.g - 1) / p.g;
-    if (kCooperativeTall && type != kQ6_K && tiles >= 2048 && p.g == 2 && groups >= 8 && mats == 1 && batch <= 2 &&
-        fits8(type, blocks, batch, mats, 8, p.g)) {
+    if (kCooperativeTall && type != kQ6_K && tiles >= kCooperativeTiles && p.g == 2 && groups >= 8 && mats == 1 &&
+        batch <= 2 && fits8(type, blocks, batch, mats, 8, p.g)) {
         p.s = 8;
         p.pc = true;
         return p;

@@ -418,12 +418,13 @@ def test_output_head_q6_k_with_argmax(ctx):
 @pytest.mark.parametrize("kind,rows,cols,batch", [(Q4_K, 70000, 4096, 1), (Q6_K, 66001, 2048, 2),
                                                  (Q6_K, 65600, 768, 1), (Q4_K, 66000, 12288, 1),
                                                  (Q4_K, 40007, 4096, 2), (Q8_0, 36001, 2048, 2),
-                                                 (Q8_0, 33000, 12288, 1)])
+                                                 (Q8_0, 33000, 12288, 1), (Q4_K, 140001, 2048, 2),
+                                                 (Q8_0, 131089, 4096, 1)])
 def test_tall_matvec_persistent_plans(ctx, kind, rows, cols, batch):
     """Tall matrices take the persistent plans: waves that each stream their
-    own tiles (Q6_K) and workgroups whose 8 waves share each tile (Q4_K,
-    Q8_0).  Row counts that end mid-tile, three-block and wide rows, two
-    tokens."""
+    own tiles, and for 8192 tiles or more of Q4_K and Q8_0 workgroups whose
+    8 waves share each tile.  Row counts that end mid-tile, three-block and
+    wide rows, two tokens."""
     print(f"tall type={kind} {rows}x{cols} batch={batch}", flush=True)
     w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(60, rows))
     x = synth.normal(synth.activation_seed(60, rows), batch * cols).reshape(batch, cols)
@@ -486,12 +487,13 @@ def test_q8_0_gemv_matches_oracle(ctx, rows, cols, batch):
         assert_close(got[b], want[b], f"Q8_0 {rows}x{cols} token {b}")
 
 
-@pytest.mark.parametrize("kind", [Q6_K, Q4_K])
-def test_fused_argmax_ties_resolve_to_the_lowest_row(ctx, kind):
-    """Rows repeat with period 97, so the maximum appears in about 500 rows
+@pytest.mark.parametrize("kind,rows", [(Q6_K, 48000), (Q4_K, 48000), (Q4_K, 140000), (Q8_0, 140000)])
+def test_fused_argmax_ties_resolve_to_the_lowest_row(ctx, kind, rows):
+    """Rows repeat with period 97, so the maximum appears in hundreds of rows
     spread over many workgroups: the device-wide key maximum must return the
-    first of them (src/cpu.rs:275-293 keeps the first maximum)."""
-    rows, cols, period = 48000, 4096, 97
+    first of them (src/cpu.rs:275-293 keeps the first maximum).  140000 rows
+    take the workgroups that share each tile (Q4_K, Q8_0)."""
+    cols, period = 4096, 97
     base = synth.quantized_matrix(kind, period, cols, synth.weight_seed(97, kind))
     rb = base.size // period
     w = np.concatenate([base.reshape(period, rb)] * (rows // period + 1))[:rows].reshape(-1)

@@ -15,6 +15,7 @@ from .hip import (  # noqa: F401
     MappedBuffer,
     ExpertCache,
     ExpertLayerLayout,
+    KvLayer,
     BackendSelection,
     library_path,
     load_library,

@@ -84,6 +84,7 @@ struct dmhip_ctx {
     int compute_units = 0;
     dm::Scratch in, out, enc, aux;          // host-slice staging
     dm::Scratch partials;                    // per-wave argmax candidates
+    dm::Scratch attn;                        // attention chunk partials
     // Device memory an allocation-free call lends the fp16 path in place of
     // `aux` for its duration (null otherwise).
     void *aux_lent = nullptr;
@@ -91,11 +92,13 @@ struct dmhip_ctx {
     dm::ArgmaxState *argmax_state = nullptr;  // device
     uint32_t *router_tickets = nullptr;       // device, kRouterTickets counters, zero between launches
     uint32_t router_mark = 0;                 // mark of the last router call (BadFlag), never 0 once set
+    uint32_t attn_mark = 0;                   // mark of the last attention call (flags[kAttnFlagWord])
     uint32_t *argmax_ticket = nullptr;        // device, zero between launches: ticket, then (at +8) the best key
     uint32_t *argmax_index = nullptr;         // device
-    uint32_t *flags = nullptr;                // device: [0] non-finite
+    uint32_t *flags = nullptr;                // device: [0] router, [2] top-k, [kAttnFlagWord] attention non-finite
     bool argmax_pending = false;
     bool router_pending = false;  // a dmhip_router_top_k_device awaits dmhip_router_result
+    bool attn_pending = false;    // a dmhip_attention_cached_device awaits dmhip_attention_result
     uint32_t *argmax_user_index = nullptr;
     // Measurement: start/stop event pairs around the dominant kernels, and
     // a pool of idle events (created without a system-scope fence) reused
@@ -129,6 +132,7 @@ struct dmhip_buf {
 };
 
 namespace dm {
+constexpr uint32_t kAttnFlagWord = 4;
 // Enqueue y = W x on the context stream, choosing the fastest kernel that
 // takes the shape.  Arguments are already validated.
 int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, const void *w,

@@ -27,6 +27,7 @@ VARIANTS = {
     12: "Overflow", 13: "InvalidInputLength", 14: "InvalidOutputLength", 15: "InvalidTopK",
     16: "MappedRange", 17: "Command", 18: "NoSlots", 19: "InvalidLayer", 20: "InvalidExpert",
     21: "AllSlotsPinned", 22: "Cancelled", 23: "InvalidLayout", 24: "InvalidArgument", 25: "Io",
+    26: "InvalidAttentionShape", 27: "KvPosition", 28: "KvWidth", 29: "KvContext",
 }
 
 # Every function include/dmhip.h declares (checked against the header by tests).
@@ -48,6 +49,11 @@ EXPORTED_SYMBOLS = [
     "dmhip_expert_cache_stats_get",
     "dmhip_expert_cache_slots_per_layer", "dmhip_expert_acquire", "dmhip_expert_release",
     "dmhip_moe_layer",
+    "dmhip_new_kv_layer", "dmhip_kv_layer_free", "dmhip_kv_layer_position", "dmhip_kv_layer_capacity",
+    "dmhip_kv_layer_allocated_bytes", "dmhip_kv_layer_clear", "dmhip_kv_layer_truncate",
+    "dmhip_kv_layer_width", "dmhip_kv_layer_keys", "dmhip_kv_layer_values", "dmhip_append_kv",
+    "dmhip_append_kv_device", "dmhip_attention_cached", "dmhip_attention_cached_device",
+    "dmhip_attention_result", "dmhip_attention",
 ]
 
 F32, F16, Q5_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 6, 8, 12, 14, 30
@@ -88,7 +94,8 @@ class _Detail(ctypes.Structure):
                 ("argument", ctypes.c_char_p), ("kind", ctypes.c_char_p)] + \
                [(n, ctypes.c_uint64) for n in ("expected", "actual", "offset", "end", "length", "left", "right",
                                                "output", "elements", "block_elements", "k", "bytes", "layer",
-                                               "expert", "count")]
+                                               "expert", "count", "position", "limit")] + \
+               [("reason", ctypes.c_char_p)]
 
     # the fields each variant carries (include/dmhip.h)
     FIELDS = {
@@ -96,7 +103,8 @@ class _Detail(ctypes.Structure):
         6: ("operation", "argument", "expected", "actual"), 7: ("operation",), 8: ("operation",), 9: ("kind",),
         10: ("kind", "elements", "block_elements"), 11: ("kind", "expected", "actual"), 13: ("expected", "actual"),
         14: ("expected", "actual"), 15: ("k", "length"), 16: ("offset", "end", "length"), 19: ("layer", "count"),
-        20: ("layer", "expert", "count"), 21: ("layer",), 25: ("os_error",),
+        20: ("layer", "expert", "count"), 21: ("layer",), 25: ("os_error",), 26: ("reason",),
+        27: ("expected", "actual"), 28: ("expected", "actual"), 29: ("position", "limit"),
     }
 
     def as_dict(self) -> dict:
@@ -190,6 +198,23 @@ def load_library() -> ctypes.CDLL:
         "dmhip_expert_release": ([_vp, _sz, _sz], ctypes.c_int),
         "dmhip_moe_layer": ([_vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _u32, _u32, _vp, _vp,
                              ctypes.POINTER(ctypes.c_uint32), _f32p], ctypes.c_int),
+        "dmhip_new_kv_layer": ([_vp, _sz, _sz, ctypes.c_int, _sz, ctypes.POINTER(_vp)], ctypes.c_int),
+        "dmhip_kv_layer_free": ([_vp], None),
+        "dmhip_kv_layer_position": ([_vp], _sz),
+        "dmhip_kv_layer_capacity": ([_vp], _sz),
+        "dmhip_kv_layer_allocated_bytes": ([_vp], _sz),
+        "dmhip_kv_layer_clear": ([_vp], None),
+        "dmhip_kv_layer_truncate": ([_vp, _sz], None),
+        "dmhip_kv_layer_width": ([_vp], _sz),
+        "dmhip_kv_layer_keys": ([_vp], _vp),
+        "dmhip_kv_layer_values": ([_vp], _vp),
+        "dmhip_append_kv": ([_vp, _vp, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_append_kv_device": ([_vp, _vp, _sz, _vp, _sz, _vp, _sz], ctypes.c_int),
+        "dmhip_attention_cached": ([_vp, _f32p, _sz, _vp, _sz, _sz, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_attention_cached_device": ([_vp, _vp, _sz, _vp, _sz, _sz, _sz, _vp, _sz], ctypes.c_int),
+        "dmhip_attention_result": ([_vp], ctypes.c_int),
+        "dmhip_attention": ([_vp, _f32p, _sz, _f32p, _sz, _f32p, _sz, _sz, _sz, _sz, ctypes.c_int, _sz,
+                             _f32p, _sz], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -520,6 +545,42 @@ class HipContext:
     def event_free(ev: int) -> None:
         load_library().dmhip_event_free(_vp(ev))
 
+    # -- attention over a KV ring (src/metal.rs:1196-1511) --------------------
+    def new_kv_layer(self, width: int, max_context: int, sliding_window: int | None) -> "KvLayer":
+        h = _vp()
+        _check(load_library().dmhip_new_kv_layer(self._h, width, max_context, int(sliding_window is not None),
+                                                  sliding_window or 0, ctypes.byref(h)))
+        return KvLayer(self, h.value)
+
+    def append_kv(self, layer: "KvLayer", position: int, key, value) -> None:
+        k, v = _f32(key), _f32(value)
+        _check(load_library().dmhip_append_kv(self._h, layer.handle, position, _fp(k), k.size, _fp(v), v.size))
+
+    def append_kv_device(self, layer: "KvLayer", position: int, key_ptr, key_len, value_ptr, value_len) -> None:
+        _check(load_library().dmhip_append_kv_device(self._h, layer.handle, position, key_ptr, key_len,
+                                                     value_ptr, value_len))
+
+    def attention_cached(self, query, cache: "KvLayer", query_heads: int, kv_heads: int, head_dimension: int,
+                         output: np.ndarray) -> None:
+        q = _f32(query)
+        _check(load_library().dmhip_attention_cached(self._h, _fp(q), q.size, cache.handle, query_heads,
+                                                     kv_heads, head_dimension, _fp(output), output.size))
+
+    def attention_cached_device(self, q_ptr, query_len, cache: "KvLayer", query_heads, kv_heads, head_dimension,
+                                out_ptr, output_len) -> None:
+        _check(load_library().dmhip_attention_cached_device(self._h, q_ptr, query_len, cache.handle, query_heads,
+                                                            kv_heads, head_dimension, out_ptr, output_len))
+
+    def attention_result(self) -> None:
+        _check(load_library().dmhip_attention_result(self._h))
+
+    def attention(self, query, keys, values, query_heads: int, kv_heads: int, head_dimension: int,
+                  window: int | None, output: np.ndarray) -> None:
+        q, k, v = _f32(query), _f32(keys), _f32(values)
+        _check(load_library().dmhip_attention(self._h, _fp(q), q.size, _fp(k), k.size, _fp(v), v.size,
+                                              query_heads, kv_heads, head_dimension, int(window is not None),
+                                              window or 0, _fp(output), output.size))
+
     # -- routed experts -------------------------------------------------------
     def moe_layer(self, cache: "ExpertCache", layer, batch, hidden, width, experts, k, router_ptr,
                   gate_up_type, down_type, x_ptr, y_ptr):
@@ -530,6 +591,54 @@ class HipContext:
                                               ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
                                               _fp(probs)))
         return ids.reshape(batch, k).astype(np.int64), probs.reshape(batch, k)
+
+
+class KvLayer:
+    """MetalKvLayer (src/metal.rs:245-277): a device KV ring of one layer."""
+
+    def __init__(self, ctx: HipContext, handle: int):
+        self._ctx = ctx
+        self._h = _vp(handle)
+        ctx._children.add(self)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def position(self) -> int:
+        return load_library().dmhip_kv_layer_position(self._h)
+
+    def capacity(self) -> int:
+        return load_library().dmhip_kv_layer_capacity(self._h)
+
+    def allocated_bytes(self) -> int:
+        return load_library().dmhip_kv_layer_allocated_bytes(self._h)
+
+    def clear(self) -> None:
+        load_library().dmhip_kv_layer_clear(self._h)
+
+    def truncate(self, position: int) -> None:
+        load_library().dmhip_kv_layer_truncate(self._h, position)
+
+    def width(self) -> int:
+        return load_library().dmhip_kv_layer_width(self._h)
+
+    def keys_ptr(self) -> int:
+        return load_library().dmhip_kv_layer_keys(self._h)
+
+    def values_ptr(self) -> int:
+        return load_library().dmhip_kv_layer_values(self._h)
+
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            load_library().dmhip_kv_layer_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class PinnedHostBuffer:

@@ -64,7 +64,11 @@ typedef enum dmhip_status {
     DMHIP_ERR_CANCELLED = 22,            /* ExpertCacheError::Cancelled */
     DMHIP_ERR_INVALID_LAYOUT = 23,       /* ExpertCacheError::InvalidLayout */
     DMHIP_ERR_INVALID_ARGUMENT = 24,     /* a null handle or pointer, or a C-API misuse */
-    DMHIP_ERR_IO = 25                    /* ExpertCacheError::Io (a failed or short pread) */
+    DMHIP_ERR_IO = 25,                   /* ExpertCacheError::Io (a failed or short pread) */
+    DMHIP_ERR_INVALID_ATTENTION_SHAPE = 26, /* MetalError::InvalidAttentionShape */
+    DMHIP_ERR_KV_POSITION = 27,          /* MetalError::KvPosition */
+    DMHIP_ERR_KV_WIDTH = 28,             /* MetalError::KvWidth */
+    DMHIP_ERR_KV_CONTEXT = 29            /* MetalError::KvContext */
 } dmhip_status;
 
 /* The payload of the calling thread's last failure: the fields of the
@@ -89,6 +93,9 @@ typedef enum dmhip_status {
      InvalidExpert               layer, expert, count
      AllSlotsPinned              layer
      Io                          os_error (an errno value; 0: unexpected end of file)
+     InvalidAttentionShape       reason (the reference's static message)
+     KvPosition, KvWidth         expected, actual
+     KvContext                   position, limit
      Command, InvalidLayout      the message (dmhip_last_error) */
 typedef struct dmhip_error_detail {
     int32_t status;
@@ -103,6 +110,8 @@ typedef struct dmhip_error_detail {
     uint64_t k;
     uint64_t bytes;
     uint64_t layer, expert, count;
+    uint64_t position, limit;
+    const char *reason;
 } dmhip_error_detail;
 
 /* ggml tensor type ids accepted by the matvec entry points. */
@@ -119,6 +128,7 @@ enum {
 typedef struct dmhip_ctx dmhip_ctx;
 typedef struct dmhip_buf dmhip_buf;
 typedef struct dmhip_expert_cache dmhip_expert_cache;
+typedef struct dmhip_kv_layer dmhip_kv_layer;
 
 /* ---------------------------------------------------------------------- */
 /* Context, errors, device                                                 */
@@ -359,6 +369,77 @@ int dmhip_matvec_phase_trace(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, si
    choose it. */
 int dmhip_matvec_valu_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
                              const void *weights, const float *x, float *y);
+
+/* ---------------------------------------------------------------------- */
+/* Decode attention over a KV ring (src/metal.rs:245-277, :1196-1511)      */
+/* ---------------------------------------------------------------------- */
+
+/* MetalContext::new_kv_layer (src/metal.rs:1196-1217): two device rings of
+   capacity x width floats, capacity = min(sliding_window, max_context) when
+   has_window, else max_context.  InvalidAttentionShape for a zero width or
+   capacity, Overflow when width * capacity does not fit. */
+int dmhip_new_kv_layer(dmhip_ctx *ctx, size_t width, size_t max_context, int has_window,
+                       size_t sliding_window, dmhip_kv_layer **out);
+/* Waits for the context's stream, then frees both rings. */
+void dmhip_kv_layer_free(dmhip_kv_layer *layer);
+/* MetalKvLayer::position / capacity / allocated_bytes / clear / truncate
+   (src/metal.rs:255-277): host-side bookkeeping, no device work. */
+size_t dmhip_kv_layer_position(const dmhip_kv_layer *layer);
+size_t dmhip_kv_layer_capacity(const dmhip_kv_layer *layer);
+size_t dmhip_kv_layer_allocated_bytes(const dmhip_kv_layer *layer);
+void dmhip_kv_layer_clear(dmhip_kv_layer *layer);
+void dmhip_kv_layer_truncate(dmhip_kv_layer *layer, size_t position);
+/* The layer's width (kv_heads * head_dimension) and the device addresses of
+   its rings ([capacity][width] f32, position p in slot p % capacity). */
+size_t dmhip_kv_layer_width(const dmhip_kv_layer *layer);
+void *dmhip_kv_layer_keys(const dmhip_kv_layer *layer);
+void *dmhip_kv_layer_values(const dmhip_kv_layer *layer);
+
+/* MetalContext::append_kv (src/metal.rs:1219-1268): KvPosition unless
+   `position` is the layer's position, KvContext when it reaches max_context,
+   KvWidth unless both slices hold `width` floats; then slot position %
+   capacity takes the key and value and the position advances.  The _device
+   form copies from device addresses on the stream (the lengths are the
+   caller's statement of what they hold). */
+int dmhip_append_kv(dmhip_ctx *ctx, dmhip_kv_layer *layer, size_t position, const float *key,
+                    size_t key_len, const float *value, size_t value_len);
+int dmhip_append_kv_device(dmhip_ctx *ctx, dmhip_kv_layer *layer, size_t position,
+                           const float *key_device, size_t key_len, const float *value_device,
+                           size_t value_len);
+
+/* MetalContext::attention_cached (src/metal.rs:1270-1323): one query token
+   ([query_heads][head_dimension]) against the layer's last min(position,
+   capacity) positions; query head h reads KV head h / (query_heads /
+   kv_heads).  Scores are the sequential fma of the reference's fold
+   (unscaled), softmax over the window, output [query_heads][head_dimension].
+   Checks, in order: InvalidAttentionShape (heads), Overflow, InvalidAttention-
+   Shape (query/output lengths), KvWidth (layer width != kv_heads *
+   head_dimension), EmptyInput "attention" (position 0).  A non-finite score
+   (NaN or +inf) or a window whose scores are all -inf returns NonFinite
+   "softmax", as the CPU softmax does (src/cpu.rs:196-225). */
+int dmhip_attention_cached(dmhip_ctx *ctx, const float *query, size_t query_len,
+                           const dmhip_kv_layer *layer, size_t query_heads, size_t kv_heads,
+                           size_t head_dimension, float *output, size_t output_len);
+/* The same from and to device memory, enqueued on the stream; the
+   non-finite check is read by dmhip_attention_result. */
+int dmhip_attention_cached_device(dmhip_ctx *ctx, const float *query_device, size_t query_len,
+                                  const dmhip_kv_layer *layer, size_t query_heads, size_t kv_heads,
+                                  size_t head_dimension, float *output_device, size_t output_len);
+/* Waits for the last dmhip_attention_cached_device and returns NonFinite
+   "softmax" when its scores held a non-finite value (its output is then not
+   meaningful). */
+int dmhip_attention_result(dmhip_ctx *ctx);
+
+/* MetalContext::attention (src/metal.rs:1325-1385): keys and values are host
+   caches of whole positions (keys_len == values_len, a multiple of kv_heads *
+   head_dimension); with has_window the last `window` positions are attended.
+   Checks as attention_cached, then InvalidAttentionShape "key/value caches
+   must have equal whole-position lengths", EmptyInput "attention" (no
+   position), EmptyInput "attention window" (window 0). */
+int dmhip_attention(dmhip_ctx *ctx, const float *query, size_t query_len, const float *keys,
+                    size_t keys_len, const float *values, size_t values_len, size_t query_heads,
+                    size_t kv_heads, size_t head_dimension, int has_window, size_t window,
+                    float *output, size_t output_len);
 
 /* ---------------------------------------------------------------------- */
 /* Routed-expert residency (src/expert.rs)                                 */

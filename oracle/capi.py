@@ -90,6 +90,7 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_moe_layer.argtypes = [_sz, _sz, _sz, _sz, _sz, _u16p, ctypes.c_uint32, _u8p,
                                 ctypes.c_uint32, _u8p, _f32p, _szp, _f32p, _f32p, ctypes.c_int]
     l.orc_gemm_tokenwise.argtypes = [ctypes.c_uint32, _sz, _sz, _sz, _u16p, _u8p, _f32p, ctypes.c_int]
+    l.orc_attention.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f32p]
     l.orc_lru_new.argtypes = [_sz, _szp, _sz, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_void_p)]
     l.orc_lru_free.argtypes = [ctypes.c_void_p]
     l.orc_lru_free.restype = None
@@ -283,6 +284,29 @@ def gemm_tokenwise(ggml_type, m, n, k, a_bits, encoded, threads=None) -> np.ndar
     out = np.zeros((m, n), dtype=np.float32)
     _check(lib().orc_gemm_tokenwise(ggml_type, m, n, k, _p(a, _u16p), _p(enc, _u8p), _p(out, _f32p),
                                     threads or threads_default()), "gemm_tokenwise")
+    return out
+
+
+def attention_status(query, keys, values, capacity: int, width: int, query_heads: int, kv_heads: int,
+                     head_dimension: int, start: int, visible: int):
+    """(status, output) of one decode-attention step over a KV ring of
+    `capacity` slots of `width` floats (src/gemma4/cpu.rs:900-946)."""
+    q = _c(query, np.float32).ravel()
+    k = _c(keys, np.float32).ravel()
+    v = _c(values, np.float32).ravel()
+    assert q.size == query_heads * head_dimension and width == kv_heads * head_dimension
+    assert k.size == v.size == capacity * width and visible <= capacity
+    out = np.zeros(query_heads * head_dimension, dtype=np.float32)
+    status = lib().orc_attention(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p), capacity, width, query_heads,
+                                 kv_heads, head_dimension, start, visible, _p(out, _f32p))
+    return status, out
+
+
+def attention(query, keys, values, capacity: int, width: int, query_heads: int, kv_heads: int,
+              head_dimension: int, start: int, visible: int) -> np.ndarray:
+    status, out = attention_status(query, keys, values, capacity, width, query_heads, kv_heads,
+                                   head_dimension, start, visible)
+    _check(status, "attention")
     return out
 
 

@@ -664,3 +664,42 @@ void orc_lru_stats(const orc_lru *c, uint64_t *hits, uint64_t *misses, uint64_t 
     *hits = c->hits; *misses = c->misses; *evictions = c->evictions;
     *reads = c->reads; *bytes_read = c->bytes_read; *resident_bytes = c->resident_bytes;
 }
+
+/* src/gemma4/cpu.rs:900-946  attend, with the ring addressing of
+   metal/kernels.metal:486-578 (slot = position % capacity). */
+int orc_attention(const float *query, const float *keys, const float *values, size_t capacity,
+                  size_t width, size_t query_heads, size_t kv_heads, size_t head_dimension,
+                  size_t start, size_t visible, float *output)
+{
+    if (visible == 0) return ORC_EMPTY_INPUT;
+    size_t group_size = query_heads / kv_heads;
+    float *scores = (float *)malloc(visible * sizeof(float));
+    if (!scores) return ORC_OVERFLOW;
+    for (size_t i = 0; i < query_heads * head_dimension; i++) output[i] = 0.0f;
+    for (size_t query_head = 0; query_head < query_heads; query_head++) {
+        size_t kv_head = query_head / group_size;
+        const float *q = query + query_head * head_dimension;
+        for (size_t s = 0; s < visible; s++) {
+            size_t slot = (start + s) % capacity;
+            const float *k = keys + slot * width + kv_head * head_dimension;
+            float sum = 0.0f;
+            /* query.mul_add(key, sum), d ascending */
+            for (size_t d = 0; d < head_dimension; d++) sum = fmaf(q[d], k[d], sum);
+            scores[s] = sum;
+        }
+        int status = orc_softmax_in_place(scores, visible);
+        if (status != ORC_OK) {
+            free(scores);
+            return status;
+        }
+        float *o = output + query_head * head_dimension;
+        for (size_t s = 0; s < visible; s++) {
+            size_t slot = (start + s) % capacity;
+            const float *v = values + slot * width + kv_head * head_dimension;
+            /* value.mul_add(probability, output), positions ascending */
+            for (size_t d = 0; d < head_dimension; d++) o[d] = fmaf(v[d], scores[s], o[d]);
+        }
+    }
+    free(scores);
+    return ORC_OK;
+}

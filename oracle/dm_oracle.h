@@ -28,6 +28,10 @@
  *   orc_dense_ffn / orc_moe_layer / orc_gemm_tokenwise
  *                            compositions of the functions above, checked by
  *                            recomposing them from the pinned parts in numpy
+ *   orc_attention            src/gemma4/cpu.rs:967-985 and src/metal.rs:2499-2570
+ *                            known answers; float64 closed form from the same
+ *                            fp32 scores; equal-value and one-hot invariants;
+ *                            ring-rotation invariance (bit-exact)
  */
 #ifndef DM_ORACLE_H
 #define DM_ORACLE_H
@@ -105,6 +109,16 @@ int orc_moe_layer(size_t batch, size_t hidden, size_t expert_width, size_t exper
 int orc_gemm_tokenwise(uint32_t ggml_type, size_t m, size_t n, size_t k,
                        const uint16_t *activations_bf16, const uint8_t *encoded, float *output,
                        int threads);
+
+/* Decode attention of one query token over a KV ring, src/gemma4/cpu.rs:900-946
+   (`attend`) with the ring addressing of metal/kernels.metal:486-578: position
+   p lives in slot p % capacity of keys/values ([capacity][width] row-major,
+   width = kv_heads * head_dimension), and the query attends positions
+   [start, start + visible).  Output is [query_heads][head_dimension].
+   EmptyInput when visible is 0; NonFinite from softmax_in_place. */
+int orc_attention(const float *query, const float *keys, const float *values, size_t capacity,
+                  size_t width, size_t query_heads, size_t kv_heads, size_t head_dimension,
+                  size_t start, size_t visible, float *output);
 
 /* src/expert.rs:44-229 bookkeeping, without the byte movement. */
 typedef struct orc_lru orc_lru;

@@ -20,7 +20,6 @@
 #![allow(clippy::too_many_arguments)]
 
 use std::{
-    convert::Infallible,
     ffi::{CStr, c_char, c_int},
     fmt, io,
     os::fd::AsRawFd,
@@ -56,6 +55,10 @@ pub mod ffi {
     pub struct dmhip_expert_cache {
         _opaque: [u8; 0],
     }
+    #[repr(C)]
+    pub struct dmhip_kv_layer {
+        _opaque: [u8; 0],
+    }
 
     pub const DMHIP_OK: c_int = 0;
     pub const DMHIP_ERR_NO_DEVICE: c_int = 1;
@@ -83,6 +86,10 @@ pub mod ffi {
     pub const DMHIP_ERR_INVALID_LAYOUT: c_int = 23;
     pub const DMHIP_ERR_INVALID_ARGUMENT: c_int = 24;
     pub const DMHIP_ERR_IO: c_int = 25;
+    pub const DMHIP_ERR_INVALID_ATTENTION_SHAPE: c_int = 26;
+    pub const DMHIP_ERR_KV_POSITION: c_int = 27;
+    pub const DMHIP_ERR_KV_WIDTH: c_int = 28;
+    pub const DMHIP_ERR_KV_CONTEXT: c_int = 29;
 
     #[repr(C)]
     #[derive(Clone, Copy)]
@@ -107,6 +114,9 @@ pub mod ffi {
         pub layer: u64,
         pub expert: u64,
         pub count: u64,
+        pub position: u64,
+        pub limit: u64,
+        pub reason: *const c_char,
     }
 
     impl dmhip_error_detail {
@@ -132,6 +142,9 @@ pub mod ffi {
                 layer: 0,
                 expert: 0,
                 count: 0,
+                position: 0,
+                limit: 0,
+                reason: std::ptr::null(),
             }
         }
     }
@@ -470,6 +483,82 @@ pub mod ffi {
             ids: *mut u32,
             probabilities: *mut f32,
         ) -> c_int;
+
+        // decode attention over a KV ring
+        pub fn dmhip_new_kv_layer(
+            ctx: *mut dmhip_ctx,
+            width: usize,
+            max_context: usize,
+            has_window: c_int,
+            sliding_window: usize,
+            out: *mut *mut dmhip_kv_layer,
+        ) -> c_int;
+        pub fn dmhip_kv_layer_free(layer: *mut dmhip_kv_layer);
+        pub fn dmhip_kv_layer_position(layer: *const dmhip_kv_layer) -> usize;
+        pub fn dmhip_kv_layer_capacity(layer: *const dmhip_kv_layer) -> usize;
+        pub fn dmhip_kv_layer_allocated_bytes(layer: *const dmhip_kv_layer) -> usize;
+        pub fn dmhip_kv_layer_clear(layer: *mut dmhip_kv_layer);
+        pub fn dmhip_kv_layer_truncate(layer: *mut dmhip_kv_layer, position: usize);
+        pub fn dmhip_kv_layer_width(layer: *const dmhip_kv_layer) -> usize;
+        pub fn dmhip_kv_layer_keys(layer: *const dmhip_kv_layer) -> *mut c_void;
+        pub fn dmhip_kv_layer_values(layer: *const dmhip_kv_layer) -> *mut c_void;
+        pub fn dmhip_append_kv(
+            ctx: *mut dmhip_ctx,
+            layer: *mut dmhip_kv_layer,
+            position: usize,
+            key: *const f32,
+            key_len: usize,
+            value: *const f32,
+            value_len: usize,
+        ) -> c_int;
+        pub fn dmhip_append_kv_device(
+            ctx: *mut dmhip_ctx,
+            layer: *mut dmhip_kv_layer,
+            position: usize,
+            key_device: *const f32,
+            key_len: usize,
+            value_device: *const f32,
+            value_len: usize,
+        ) -> c_int;
+        pub fn dmhip_attention_cached(
+            ctx: *mut dmhip_ctx,
+            query: *const f32,
+            query_len: usize,
+            layer: *const dmhip_kv_layer,
+            query_heads: usize,
+            kv_heads: usize,
+            head_dimension: usize,
+            output: *mut f32,
+            output_len: usize,
+        ) -> c_int;
+        pub fn dmhip_attention_cached_device(
+            ctx: *mut dmhip_ctx,
+            query_device: *const f32,
+            query_len: usize,
+            layer: *const dmhip_kv_layer,
+            query_heads: usize,
+            kv_heads: usize,
+            head_dimension: usize,
+            output_device: *mut f32,
+            output_len: usize,
+        ) -> c_int;
+        pub fn dmhip_attention_result(ctx: *mut dmhip_ctx) -> c_int;
+        pub fn dmhip_attention(
+            ctx: *mut dmhip_ctx,
+            query: *const f32,
+            query_len: usize,
+            keys: *const f32,
+            keys_len: usize,
+            values: *const f32,
+            values_len: usize,
+            query_heads: usize,
+            kv_heads: usize,
+            head_dimension: usize,
+            has_window: c_int,
+            window: usize,
+            output: *mut f32,
+            output_len: usize,
+        ) -> c_int;
     }
 }
 
@@ -560,6 +649,19 @@ fn metal_error(code: c_int) -> MetalError {
             offset: field(d.offset),
             end: field(d.end),
             length: field(d.length),
+        },
+        ffi::DMHIP_ERR_INVALID_ATTENTION_SHAPE => MetalError::InvalidAttentionShape(static_str(d.reason)),
+        ffi::DMHIP_ERR_KV_POSITION => MetalError::KvPosition {
+            expected: field(d.expected),
+            actual: field(d.actual),
+        },
+        ffi::DMHIP_ERR_KV_WIDTH => MetalError::KvWidth {
+            expected: field(d.expected),
+            actual: field(d.actual),
+        },
+        ffi::DMHIP_ERR_KV_CONTEXT => MetalError::KvContext {
+            position: field(d.position),
+            limit: field(d.limit),
         },
         // DMHIP_ERR_COMMAND (a HIP runtime error), DMHIP_ERR_INVALID_ARGUMENT
         // (a null handle: unreachable through this module) and an
@@ -687,11 +789,12 @@ pub struct MetalOwnedBuffer {
     owned: bool,
 }
 
-/// MetalKvLayer (src/metal.rs:245-278). The HIP backend does not provide the
-/// KV cache or attention yet (`new_kv_layer` returns an error), so no value
-/// of this type exists.
+/// MetalKvLayer (src/metal.rs:245-278): the key and value rings of one
+/// layer in HBM, `capacity` slots of `width` floats each, with the position
+/// kept by the library.
 pub struct MetalKvLayer {
-    never: Infallible,
+    context: Rc<Context>,
+    raw: NonNull<ffi::dmhip_kv_layer>,
 }
 
 impl fmt::Debug for MetalContext {
@@ -716,8 +819,19 @@ impl fmt::Debug for MetalOwnedBuffer {
 }
 
 impl fmt::Debug for MetalKvLayer {
-    fn fmt(&self, _: &mut fmt::Formatter<'_>) -> fmt::Result {
-        match self.never {}
+    fn fmt(&self, f: &mut fmt::Formatter<'_>) -> fmt::Result {
+        f.debug_struct("MetalKvLayer")
+            .field("position", &self.position())
+            .field("capacity", &self.capacity())
+            .finish()
+    }
+}
+
+impl Drop for MetalKvLayer {
+    fn drop(&mut self) {
+        // SAFETY: the layer is live and its context outlives it (Rc); the
+        // library waits for the context's stream before freeing the rings.
+        unsafe { ffi::dmhip_kv_layer_free(self.raw.as_ptr()) }
     }
 }
 
@@ -794,23 +908,24 @@ impl MetalOwnedBuffer {
 
 impl MetalKvLayer {
     pub fn position(&self) -> usize {
-        match self.never {}
+        // SAFETY: the layer is live (all five are host-side bookkeeping).
+        unsafe { ffi::dmhip_kv_layer_position(self.raw.as_ptr()) }
     }
 
     pub fn capacity(&self) -> usize {
-        match self.never {}
+        unsafe { ffi::dmhip_kv_layer_capacity(self.raw.as_ptr()) }
     }
 
     pub fn allocated_bytes(&self) -> usize {
-        match self.never {}
+        unsafe { ffi::dmhip_kv_layer_allocated_bytes(self.raw.as_ptr()) }
     }
 
     pub fn clear(&mut self) {
-        match self.never {}
+        unsafe { ffi::dmhip_kv_layer_clear(self.raw.as_ptr()) }
     }
 
-    pub fn truncate(&mut self, _position: usize) {
-        match self.never {}
+    pub fn truncate(&mut self, position: usize) {
+        unsafe { ffi::dmhip_kv_layer_truncate(self.raw.as_ptr(), position) }
     }
 }
 
@@ -1050,9 +1165,9 @@ impl MetalContext {
     }
 
     // The rest of the MetalContext surface is outside the library's
-    // quantized-matrix path. These methods keep the graphs compiling and
-    // fail with a Command error naming the operation; the Qwen3.5 graph
-    // (src/qwen35/metal.rs) calls none of them.
+    // quantized-matrix and attention paths. These methods keep the graphs
+    // compiling and fail with a Command error naming the operation; the
+    // Qwen3.5 graph (src/qwen35/metal.rs) calls none of them.
 
     pub fn add(&self, _left: &[f32], _right: &[f32], _output: &mut [f32]) -> Result<(), MetalError> {
         Err(not_provided("add"))
@@ -1108,47 +1223,106 @@ impl MetalContext {
 
     pub fn new_kv_layer(
         &self,
-        _width: usize,
-        _max_context: usize,
-        _sliding_window: Option<usize>,
+        width: usize,
+        max_context: usize,
+        sliding_window: Option<usize>,
     ) -> Result<MetalKvLayer, MetalError> {
-        Err(not_provided("the KV cache"))
+        let mut raw = ptr::null_mut();
+        // SAFETY: `raw` is a valid out-pointer; the context is live.
+        check(unsafe {
+            ffi::dmhip_new_kv_layer(
+                self.context.raw(),
+                width,
+                max_context,
+                c_int::from(sliding_window.is_some()),
+                sliding_window.unwrap_or(0),
+                &mut raw,
+            )
+        })?;
+        let raw = NonNull::new(raw).ok_or(MetalError::BufferAllocation { bytes: 0 })?;
+        Ok(MetalKvLayer {
+            context: Rc::clone(&self.context),
+            raw,
+        })
     }
 
     pub fn append_kv(
         &self,
         layer: &mut MetalKvLayer,
-        _position: usize,
-        _key: &[f32],
-        _value: &[f32],
+        position: usize,
+        key: &[f32],
+        value: &[f32],
     ) -> Result<(), MetalError> {
-        match layer.never {}
+        // SAFETY: the slices are valid for their lengths; the library checks
+        // them against the layer's width before copying.
+        check(unsafe {
+            ffi::dmhip_append_kv(
+                self.context.raw(),
+                layer.raw.as_ptr(),
+                position,
+                key.as_ptr(),
+                key.len(),
+                value.as_ptr(),
+                value.len(),
+            )
+        })
     }
 
     pub fn attention_cached(
         &self,
-        _query: &[f32],
+        query: &[f32],
         cache: &MetalKvLayer,
-        _query_heads: usize,
-        _kv_heads: usize,
-        _head_dimension: usize,
-        _output: &mut [f32],
+        query_heads: usize,
+        kv_heads: usize,
+        head_dimension: usize,
+        output: &mut [f32],
     ) -> Result<(), MetalError> {
-        match cache.never {}
+        // SAFETY: as for append_kv; the layer belongs to a live context.
+        check(unsafe {
+            ffi::dmhip_attention_cached(
+                self.context.raw(),
+                query.as_ptr(),
+                query.len(),
+                cache.raw.as_ptr(),
+                query_heads,
+                kv_heads,
+                head_dimension,
+                output.as_mut_ptr(),
+                output.len(),
+            )
+        })
     }
 
     pub fn attention(
         &self,
-        _query: &[f32],
-        _keys: &[f32],
-        _values: &[f32],
-        _query_heads: usize,
-        _kv_heads: usize,
-        _head_dimension: usize,
-        _window: Option<usize>,
-        _output: &mut [f32],
+        query: &[f32],
+        keys: &[f32],
+        values: &[f32],
+        query_heads: usize,
+        kv_heads: usize,
+        head_dimension: usize,
+        window: Option<usize>,
+        output: &mut [f32],
     ) -> Result<(), MetalError> {
-        Err(not_provided("attention"))
+        // SAFETY: the slices are valid for their lengths.
+        check(unsafe {
+            ffi::dmhip_attention(
+                self.context.raw(),
+                query.as_ptr(),
+                query.len(),
+                keys.as_ptr(),
+                keys.len(),
+                values.as_ptr(),
+                values.len(),
+                query_heads,
+                kv_heads,
+                head_dimension,
+                c_int::from(window.is_some()),
+                window.unwrap_or(0),
+                output.as_mut_ptr(),
+                output.len(),
+            )
+        })
     }
 }
 

@@ -146,7 +146,7 @@ def test_rust_status_constants_match_the_header():
     c = dict((n, int(v)) for n, v in re.findall(r"(DMHIP_(?:OK|ERR_\w+)) = (\d+)", text))
     rust = dict((n, int(v)) for n, v in re.findall(r"pub const (DMHIP_(?:OK|ERR_\w+)): c_int = (\d+);",
                                                    _rust_source()))
-    assert rust == c and len(c) == 26
+    assert rust == c and len(c) == 30
 
 
 def test_rust_structs_have_the_header_field_order():
@@ -175,3 +175,14 @@ def test_gguf_writer_places_tensors_where_the_reference_parser_would():
     for t, (_, dims, kind, raw) in zip(infos, data):
         assert t.absolute_offset % 64 == 0 and t.dimensions == dims and t.kind == kind
         assert blob[t.absolute_offset:t.absolute_offset + t.byte_len] == raw
+
+
+def test_every_status_has_a_variant_in_both_bindings():
+    text = open(os.path.join(ROOT, "include", "dmhip.h")).read()
+    statuses = dict((n, int(v)) for n, v in re.findall(r"(DMHIP_(?:OK|ERR_\w+)) = (\d+)", text))
+    from diskmule_amd import hip
+    assert sorted(hip.VARIANTS) == sorted(statuses.values())
+    src = _rust_source()
+    # Command and InvalidArgument fall through to MetalError::Command by design
+    for name in set(statuses) - {"DMHIP_OK", "DMHIP_ERR_COMMAND", "DMHIP_ERR_INVALID_ARGUMENT"}:
+        assert re.search(r"ffi::%s\b[^=]*=>" % name, src), name

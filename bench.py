@@ -23,7 +23,7 @@ measured the same way, a Q8_0 GEMV entry (the third k-quant of the north
 star, which no configuration uses) and F16 / F32 / Q5_0 GEMV entries (the
 other row types of a Gemma-class GGUF).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|dense|copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|dense|attn|copy]
 """
 from __future__ import annotations
 
@@ -452,6 +452,70 @@ def bench_c5(ctx, synth, steps, warmup):
     return out
 
 
+def bench_attn(ctx, synth, steps, warmup):
+    """Decode attention over a KV ring (src/metal.rs:1270-1323) at the Gemma 4
+    26B shapes (src/gemma4.rs:150-230): full layers (16 query heads over 2 KV
+    heads of 512 dims) at 32768 and 131072 positions, and sliding layers (16
+    query heads over 8 KV heads of 256 dims, 1024-position window, ring
+    wrapped) rotating over 24 layers (403 MB, more than the MALL) as a decode
+    step does.  Algorithmic bytes per call: the visible keys and values
+    (2 x visible x width x 4) plus query and output.  cpu_port_ms: one call
+    of the oracle's restatement of src/gemma4/cpu.rs:900-946 on one thread."""
+    from oracle import capi
+    out = {}
+    configs = (("full_32k", 16, 2, 512, 32768, None, 32768, 1),
+               ("full_128k", 16, 2, 512, 131072, None, 131072, 1),
+               ("sliding_1k", 16, 8, 256, 8192, 1024, 4096, 24))
+    for key, qh, kvh, hd, max_ctx, window, positions, nlayers in configs:
+        width, pool = kvh * hd, 1024
+        kpool = synth.normal(synth.activation_seed(40, hd), pool * width)
+        vpool = synth.normal(synth.activation_seed(41, hd), pool * width)
+        kb, vb = upload(ctx, kpool), upload(ctx, vpool)
+        layers = [ctx.new_kv_layer(width, max_ctx, window) for _ in range(nlayers)]
+        for layer in layers:
+            for p in range(positions):
+                j = (p % pool) * width * 4
+                ctx.append_kv_device(layer, p, kb.device_ptr + j, width, vb.device_ptr + j, width)
+        ctx.synchronize()
+        q = (synth.normal(synth.activation_seed(42, hd), qh * hd) / np.sqrt(hd)).astype(np.float32)
+        qb, ob = upload(ctx, q), ctx.new_owned_buffer(qh * hd * 4)
+        cap = layers[0].capacity()
+        visible = min(positions, cap)
+        step_bytes = 2 * visible * width * 4 + 2 * qh * hd * 4
+
+        def call(i):
+            ctx.attention_cached_device(qb.device_ptr, qh * hd, layers[i % nlayers], qh, kvh, hd, ob.device_ptr,
+                                        qh * hd)
+
+        for i in range(warmup):
+            call(i)
+        n = max(steps, 2 * nlayers)
+        wall, kern, launches = timed_loop(ctx, call, n)
+        ctx.attention_result()
+        ms, kms = wall / n, kern / n
+        res = {"qh": qh, "kvh": kvh, "head_dim": hd, "visible": visible, "bytes_per_call": step_bytes,
+               "call_ms": ms, "kernels_ms": kms, "launches_per_call": launches / n,
+               "gbps_call": step_bytes / (ms * 1e-3) / 1e9, "gbps_kernels": step_bytes / (kms * 1e-3) / 1e9,
+               "frac_of_peak": step_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        if positions <= 32768:
+            ring_k = np.zeros((cap, width), dtype=np.float32)
+            ring_v = np.zeros((cap, width), dtype=np.float32)
+            kp2, vp2 = kpool.reshape(pool, width), vpool.reshape(pool, width)
+            for p in range(positions - visible, positions):
+                ring_k[p % cap], ring_v[p % cap] = kp2[p % pool], vp2[p % pool]
+            t0 = time.perf_counter()
+            want = capi.attention(q, ring_k, ring_v, cap, width, qh, kvh, hd, positions - visible, visible)
+            res["cpu_port_ms"] = (time.perf_counter() - t0) * 1e3
+            got = ob.read(0, qh * hd * 4, np.float32)
+            res["max_abs_diff_vs_port"] = float(np.abs(got - want).max())
+        out[key] = res
+        log(f"attention {key}: {ms * 1e3:.1f} us per call, kernels {kms * 1e3:.1f} us "
+            f"({res['gbps_kernels']:.0f} GB/s)")
+        for b in layers + [kb, vb, qb, ob]:
+            b.free()
+    return out
+
+
 def bench_copy(ctx, synth, steps, warmup):
     """A plain device copy of known size (512 MiB read + 512 MiB written):
     the calibration kernel for the FETCH_SIZE/WRITE_SIZE counter runs."""
@@ -562,7 +626,7 @@ def main() -> int:
     log("device:", ctx.device_name())
     if args.only:
         fn = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-              "q8": bench_q8, "dense": bench_dense, "copy": bench_copy}[args.only]
+              "q8": bench_q8, "dense": bench_dense, "attn": bench_attn, "copy": bench_copy}[args.only]
         res = fn(ctx, synth, args.steps, args.warmup)
         print(json.dumps(res[0] if isinstance(res, tuple) else res))
         return 0
@@ -570,7 +634,7 @@ def main() -> int:
     c2, (w2, x2) = bench_c2(ctx, synth, args.steps, args.warmup)
     details = {"C2": c2}
     for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5), ("Q8_0", bench_q8),
-                     ("dense", bench_dense)):
+                     ("dense", bench_dense), ("attention", bench_attn)):
         details[name] = fn(ctx, synth, max(3, args.steps // 2), args.warmup)
     log("CPU baseline")
     cpu = cpu_baseline(w2, x2, args.cpu_seconds)

@@ -35,16 +35,22 @@ namespace dm {
 
 constexpr uint32_t kAttnThreads = 256;
 constexpr uint32_t kAttnRows = 64;        // positions per scoring pass (one per lane)
-constexpr uint32_t kAttnTile = 64;        // key dims staged per pass
+// key dims staged per pass: 128 (512-byte row segments) for 16-byte loads,
+// 64 for element loads
+template <bool KV4>
+constexpr uint32_t key_tile() { return KV4 ? 128 : 64; }
+template <bool KV4>
+constexpr uint32_t key_stride() { return key_tile<KV4>() + (KV4 ? 4 : 1); }
 constexpr uint32_t kAttnScores = 4096;    // LDS scores: heads per group x chunk
 constexpr uint32_t kAttnMaxChunk = 512;
 constexpr uint32_t kCombineBlock = 2048;  // chunk weights staged per combine pass
+constexpr uint32_t kAttnQueryLds = 8192;  // query floats a workgroup stages in LDS
 
 template <bool KV4>
 struct KeyStage {
-    // KV4: four 16-byte units per thread (64 rows x 16 units); else sixteen
+    // KV4: eight 16-byte units per thread (64 rows x 32 units); else sixteen
     // floats (64 rows x 64 columns).
-    float v[16];
+    float v[KV4 ? key_tile<true>() / 4 : 16];
 };
 
 template <bool KV4>
@@ -52,12 +58,13 @@ __device__ __forceinline__ void attn_load_keys(KeyStage<KV4> &st, const float *_
                                                uint64_t capacity, uint64_t width, uint64_t head_off,
                                                uint64_t slot0, uint32_t row0, uint32_t n, uint32_t dim0,
                                                uint32_t head_dim) {
+    constexpr uint32_t units = key_tile<KV4>() / (KV4 ? 4 : 1);  // per row
     const uint32_t t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < (KV4 ? 4 : 16); i++) {
+    for (int i = 0; i < (KV4 ? (int)key_tile<true>() / 16 : 16); i++) {
         const uint32_t u = t + kAttnThreads * i;
-        const uint32_t row = KV4 ? (u >> 4) : (u >> 6);
-        const uint32_t col = KV4 ? (u & 15u) * 4 : (u & 63u);
+        const uint32_t row = u / units;
+        const uint32_t col = (u % units) * (KV4 ? 4 : 1);
         const uint32_t r = row0 + row;
         const uint32_t d = dim0 + col;
         uint64_t slot = slot0 + r;
@@ -78,13 +85,14 @@ __device__ __forceinline__ void attn_load_keys(KeyStage<KV4> &st, const float *_
 
 template <bool KV4>
 __device__ __forceinline__ void attn_store_keys(const KeyStage<KV4> &st, float *ktile) {
-    constexpr uint32_t stride = kAttnTile + (KV4 ? 4 : 1);
+    constexpr uint32_t stride = key_stride<KV4>();
+    constexpr uint32_t units = key_tile<KV4>() / (KV4 ? 4 : 1);
     const uint32_t t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < (KV4 ? 4 : 16); i++) {
+    for (int i = 0; i < (KV4 ? (int)key_tile<true>() / 16 : 16); i++) {
         const uint32_t u = t + kAttnThreads * i;
         if constexpr (KV4) {
-            const uint32_t row = u >> 4, col = (u & 15u) * 4;
+            const uint32_t row = u / units, col = (u % units) * 4;
             *(float4 *)&ktile[row * stride + col] =
                 make_float4(st.v[4 * i], st.v[4 * i + 1], st.v[4 * i + 2], st.v[4 * i + 3]);
         } else {
@@ -95,18 +103,23 @@ __device__ __forceinline__ void attn_store_keys(const KeyStage<KV4> &st, float *
 
 // GT: query heads per workgroup (a power of two >= the heads it takes);
 // KV4: head_dim % 4 == 0 with 16-byte aligned rows and query; VV: value
-// dims per thread per pass (hd % VV == 0).
-template <int GT, bool KV4, int VV>
+// dims per thread per pass (hd % VV == 0); QL: the workgroup's query rows
+// are staged in LDS (dynamic, GT * head_dim floats), else read through the
+// scalar cache.
+template <int GT, bool KV4, int VV, bool QL>
 __global__ void __launch_bounds__(256)
 attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ keys,
                   const float *__restrict__ values, uint64_t capacity, uint64_t width, uint32_t group,
                   uint32_t head_dim, uint64_t start, uint32_t visible, uint32_t chunk, uint32_t chunks,
                   float *__restrict__ part_o, float2 *__restrict__ part_ml, BadFlag bad) {
     constexpr int CH = GT >= 4 ? GT / 4 : 1;  // score chains per lane
-    constexpr uint32_t stride = kAttnTile + (KV4 ? 4 : 1);
+    constexpr int VU = VV == 4 ? 8 : 16;       // value rows in flight per thread
+    constexpr uint32_t stride = key_stride<KV4>();
+    constexpr uint32_t kAttnTile = key_tile<KV4>();
     __shared__ __attribute__((aligned(16))) float ktile[kAttnRows * stride];
     __shared__ __attribute__((aligned(16))) float sc[kAttnScores];
     __shared__ float s_m[GT], s_l[GT];
+    extern __shared__ __attribute__((aligned(16))) float qs[];
 
     const uint32_t t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -122,6 +135,12 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
     // ---- scores: lane = position, chains over d ascending ----
     // Wave w scores heads w, w+4, ... (GT >= 4) or head w (GT < 4); a chain
     // past the workgroup's heads reads a valid head and is dropped.
+    // LDS reads keep every wait on the LDS counter short; scalar loads of
+    // the query would share that counter and hold each wait for an L2 trip.
+    if constexpr (QL) {
+        const float *src = query + qbase * head_dim;
+        for (uint32_t i = t; i < gz * head_dim; i += kAttnThreads) qs[i] = src[i];
+    }
     const float *qrow[CH];
     int chain_head[CH];
     bool chain_on[CH];
@@ -129,29 +148,31 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
     for (int ch = 0; ch < CH; ch++) {
         chain_head[ch] = (int)wave + 4 * ch;
         chain_on[ch] = (uint32_t)chain_head[ch] < gz;
-        qrow[ch] = query + (qbase + min((uint32_t)chain_head[ch], gz - 1)) * head_dim;
+        const uint32_t h = min((uint32_t)chain_head[ch], gz - 1);
+        qrow[ch] = QL ? qs + h * head_dim : query + (qbase + h) * head_dim;
     }
     const uint32_t subs = (n + kAttnRows - 1) / kAttnRows;
     const uint32_t tiles = (head_dim + kAttnTile - 1) / kAttnTile;
-    KeyStage<KV4> st;
-    attn_load_keys<KV4>(st, keys, capacity, width, head_off, slot0, 0, n, 0, head_dim);
+    // Two register stages: the keys of step s + 2 are in flight while step s
+    // is scored.
+    const uint32_t steps = subs * tiles;
     float acc[CH];
-    uint32_t sub = 0, tile = 0;
-    for (uint32_t step = 0, steps = subs * tiles; step < steps; step++) {
+    auto load_step = [&](KeyStage<KV4> &stage, uint32_t step) {
+        const uint32_t sb = step / tiles, tl = step - sb * tiles;
+        attn_load_keys<KV4>(stage, keys, capacity, width, head_off, slot0, sb * kAttnRows, n, tl * kAttnTile,
+                            head_dim);
+    };
+    auto run_step = [&](KeyStage<KV4> &stage, uint32_t step) {
         __syncthreads();
-        attn_store_keys<KV4>(st, ktile);
+        attn_store_keys<KV4>(stage, ktile);
         __syncthreads();
-        if (step + 1 < steps) {
-            const uint32_t nsub = tile + 1 == tiles ? sub + 1 : sub;
-            const uint32_t ntile = tile + 1 == tiles ? 0 : tile + 1;
-            attn_load_keys<KV4>(st, keys, capacity, width, head_off, slot0, nsub * kAttnRows, n,
-                                ntile * kAttnTile, head_dim);
-        }
-        if (tile == 0) {
+        if (step + 2 < steps) load_step(stage, step + 2);
+        const uint32_t sb = step / tiles, tl = step - sb * tiles;
+        if (tl == 0) {
 #pragma unroll
             for (int ch = 0; ch < CH; ch++) acc[ch] = 0.0f;
         }
-        const uint32_t dim0 = tile * kAttnTile;
+        const uint32_t dim0 = tl * kAttnTile;
         const uint32_t dmax = min(kAttnTile, head_dim - dim0);
         const float *krow = ktile + lane * stride;
         if constexpr (KV4) {
@@ -174,16 +195,19 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
                 for (int ch = 0; ch < CH; ch++) acc[ch] = __builtin_fmaf(qrow[ch][dim0 + dd], k, acc[ch]);
             }
         }
-        if (tile + 1 == tiles) {
-            const uint32_t r = sub * kAttnRows + lane;
+        if (tl + 1 == tiles) {
+            const uint32_t r = sb * kAttnRows + lane;
 #pragma unroll
             for (int ch = 0; ch < CH; ch++)
                 if (chain_on[ch]) sc[chain_head[ch] * chunk + r] = r < n ? acc[ch] : -INFINITY;
-            tile = 0;
-            sub++;
-        } else {
-            tile++;
         }
+    };
+    KeyStage<KV4> st0, st1;
+    load_step(st0, 0);
+    if (steps > 1) load_step(st1, 1);
+    for (uint32_t step = 0; step < steps; step += 2) {
+        run_step(st0, step);
+        if (step + 1 < steps) run_step(st1, step + 1);
     }
     // positions of the last pass past the chunk's end (chunk is a multiple of 64)
     __syncthreads();
@@ -224,10 +248,10 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
         for (int g = 0; g < GT; g++)
 #pragma unroll
             for (int k = 0; k < VV; k++) o[g][k] = 0.0f;
-        for (uint32_t j = 0; j < n; j += 8) {
-            float v[8][VV];
+        for (uint32_t j = 0; j < n; j += VU) {
+            float v[VU][VV];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
+            for (int i = 0; i < VU; i++) {
                 uint64_t slot = slot0 + j + i;
                 if (slot >= capacity) slot -= capacity;
                 const float *src = values + slot * width + head_off + d;
@@ -245,13 +269,16 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
 #pragma unroll
             for (int g = 0; g < GT; g++) {
                 if ((uint32_t)g >= gz) break;
-                const float4 e0 = *(const float4 *)&sc[g * chunk + j];
-                const float4 e1 = *(const float4 *)&sc[g * chunk + j + 4];
-                const float e[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
 #pragma unroll
-                for (int i = 0; i < 8; i++)
+                for (int i0 = 0; i0 < VU; i0 += 4) {
+                    const float4 e = *(const float4 *)&sc[g * chunk + j + i0];
+                    const float ev[4] = {e.x, e.y, e.z, e.w};
 #pragma unroll
-                    for (int k = 0; k < VV; k++) o[g][k] = __builtin_fmaf(v[i][k], e[i], o[g][k]);
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int k = 0; k < VV; k++)
+                            o[g][k] = __builtin_fmaf(v[i0 + i][k], ev[i], o[g][k]);
+                }
             }
         }
         if (active) {
@@ -268,17 +295,27 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
 }
 
 // out[h][d] = sum_c w_c o_c[d] / sum_c w_c l_c, w_c = exp(m_c - max_c m_c).
+// Workgroup (query head, 64 dims, split s) sums the chunks of split s, in
+// chunk order per wave and a fixed tree across the four waves.  With more
+// than one split each workgroup publishes its sums and takes a ticket of its
+// (head, dims) counter; the one that draws the last ticket adds the splits
+// in split order, writes the output and resets the counter to zero.
 __global__ void __launch_bounds__(256)
 attn_combine_kernel(const float *__restrict__ part_o, const float2 *__restrict__ part_ml, uint32_t group,
-                    uint32_t head_dim, uint32_t chunks, float *__restrict__ out, BadFlag bad) {
+                    uint32_t head_dim, uint32_t chunks, uint32_t per, float *__restrict__ stage_o,
+                    float *__restrict__ stage_l, uint32_t *__restrict__ tickets, float *__restrict__ out,
+                    BadFlag bad) {
     __shared__ float wts[kCombineBlock];
     __shared__ float red[4 * 64];
+    __shared__ uint32_t s_ticket;
     const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    const uint32_t head = blockIdx.x;
+    const uint32_t head = blockIdx.x, block = blockIdx.y, split = blockIdx.z;
+    const uint32_t splits = gridDim.z, blocks = gridDim.y;
     const uint32_t kh = head / group, gg = head % group;
-    const uint32_t d = blockIdx.y * 64 + lane;
+    const uint32_t d = block * 64 + lane;
     const uint64_t row0 = (uint64_t)kh * chunks * group + gg;  // chunk c at row0 + c * group
     const uint64_t rstride = group;
+    const uint32_t c0 = split * per, cn = min(per, chunks - c0);
 
     float mx = -INFINITY;
     for (uint32_t c = t; c < chunks; c += 256) mx = fmaxf(mx, part_ml[row0 + c * rstride].x);
@@ -287,50 +324,95 @@ attn_combine_kernel(const float *__restrict__ part_o, const float2 *__restrict__
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
+    if (mx == -INFINITY) {
+        // every score -inf (or NaN): no ticket is taken
+        if (t == 0) *bad.word = bad.mark;
+        if (wave == 0 && d < head_dim) out[(uint64_t)head * head_dim + d] = NAN;
+        return;
+    }
     float l = 0.0f;
-    for (uint32_t c = t; c < chunks; c += 256) {
-        const float2 ml = part_ml[row0 + c * rstride];
-        if (ml.x != -INFINITY) l = __builtin_fmaf(expf(ml.x - mx), ml.y, l);
+    for (uint32_t i = t; i < cn; i += 256) {
+        const float2 ml = part_ml[row0 + (uint64_t)(c0 + i) * rstride];
+        const float w = ml.x != -INFINITY ? expf(ml.x - mx) : 0.0f;
+        wts[i] = w;
+        l = __builtin_fmaf(w, ml.y, l);
     }
     l = wave_sum(l);
     if (lane == 0) red[wave] = l;
     __syncthreads();
     l = (red[0] + red[1]) + (red[2] + red[3]);
     __syncthreads();
-    if (mx == -INFINITY) {
-        if (t == 0) *bad.word = bad.mark;
-        if (wave == 0 && d < head_dim) out[(uint64_t)head * head_dim + d] = NAN;
-        return;
-    }
 
     float acc = 0.0f;
-    for (uint32_t cb = 0; cb < chunks; cb += kCombineBlock) {
-        const uint32_t cn = min(kCombineBlock, chunks - cb);
-        for (uint32_t i = t; i < cn; i += 256) {
-            const float m = part_ml[row0 + (uint64_t)(cb + i) * rstride].x;
-            wts[i] = m != -INFINITY ? expf(m - mx) : 0.0f;
+    if (d < head_dim) {
+        const float *src = part_o + (row0 + (uint64_t)c0 * rstride) * head_dim + d;
+        const uint64_t step = rstride * head_dim;
+        uint32_t i = wave;
+        for (; i + 28 < cn; i += 32) {
+            float a[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) a[u] = src[(i + 4 * u) * step];
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = __builtin_fmaf(a[u], wts[i + 4 * u], acc);
         }
-        __syncthreads();
-        if (d < head_dim) {
-            const float *src = part_o + (row0 + (uint64_t)cb * rstride) * head_dim + d;
-            const uint64_t step = rstride * head_dim;
-            uint32_t i = wave;
-            for (; i + 12 < cn; i += 16) {
-                const float a0 = src[i * step], a1 = src[(i + 4) * step];
-                const float a2 = src[(i + 8) * step], a3 = src[(i + 12) * step];
-                acc = __builtin_fmaf(a0, wts[i], acc);
-                acc = __builtin_fmaf(a1, wts[i + 4], acc);
-                acc = __builtin_fmaf(a2, wts[i + 8], acc);
-                acc = __builtin_fmaf(a3, wts[i + 12], acc);
-            }
-            for (; i < cn; i += 4) acc = __builtin_fmaf(src[i * step], wts[i], acc);
-        }
-        __syncthreads();
+        for (; i < cn; i += 4) acc = __builtin_fmaf(src[i * step], wts[i], acc);
     }
     red[wave * 64 + lane] = acc;
     __syncthreads();
-    if (wave == 0 && d < head_dim)
-        out[(uint64_t)head * head_dim + d] = ((red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane])) / l;
+    const float sum = (red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane]);
+    if (splits == 1) {
+        if (wave == 0 && d < head_dim) out[(uint64_t)head * head_dim + d] = sum / l;
+        return;
+    }
+    const uint64_t slot = ((uint64_t)head * blocks + block) * splits;
+    // Publish with device-scope exchanges (no cache flush), wait until they
+    // have completed, then take the ticket.
+    if (wave == 0) {
+        float old = 0.0f;
+        if (d < head_dim)
+            old = __hip_atomic_exchange(&stage_o[(slot + split) * 64 + lane], sum, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+            old += __hip_atomic_exchange(&stage_l[slot + split], l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"(old) : "memory");
+    }
+    __syncthreads();
+    if (t == 0) s_ticket = atomicAdd(&tickets[(uint64_t)head * blocks + block], 1u);
+    __syncthreads();
+    if (s_ticket != splits - 1) return;
+    // The last workgroup adds the splits: wave w takes splits w, w+4, ...
+    // in order (loads issued eight at a time), then a fixed tree across the
+    // waves; the split sums of l likewise, one per thread.
+    float o = 0.0f;
+    for (uint32_t s0 = wave; s0 < splits; s0 += 32) {
+        float a[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t s2 = s0 + 4 * u;
+            a[u] = s2 < splits && d < head_dim
+                       ? __hip_atomic_load(&stage_o[(slot + s2) * 64 + lane], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT)
+                       : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) o += a[u];
+    }
+    float lt = 0.0f;
+    for (uint32_t s2 = t; s2 < splits; s2 += 256)
+        lt += __hip_atomic_load(&stage_l[slot + s2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lt = wave_sum(lt);
+    __syncthreads();
+    red[wave * 64 + lane] = o;
+    if (lane == 0) wts[wave] = lt;
+    __syncthreads();
+    if (wave == 0) {
+        const float ot = (red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane]);
+        const float lsum = (wts[0] + wts[1]) + (wts[2] + wts[3]);
+        if (d < head_dim) out[(uint64_t)head * head_dim + d] = ot / lsum;
+        if (lane == 0)
+            __hip_atomic_store(&tickets[(uint64_t)head * blocks + block], 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 template <int GT, bool KV4, int VV>
@@ -338,8 +420,12 @@ static hipError_t launch_chunk(dmhip_ctx *ctx, dim3 grid, const float *q, const 
                                uint64_t capacity, uint64_t width, uint32_t group, uint32_t hd,
                                uint64_t start, uint32_t visible, uint32_t chunk, uint32_t chunks,
                                float *po, float2 *pml, BadFlag bad) {
-    return launch_kernel(ctx, attn_chunk_kernel<GT, KV4, VV>, grid, dim3(kAttnThreads), 0, q, k, v, capacity,
-                         width, group, hd, start, visible, chunk, chunks, po, pml, bad);
+    if ((size_t)GT * hd <= kAttnQueryLds)
+        return launch_kernel(ctx, attn_chunk_kernel<GT, KV4, VV, true>, grid, dim3(kAttnThreads),
+                             (uint32_t)(GT * hd * 4), q, k, v, capacity, width, group, hd, start, visible, chunk,
+                             chunks, po, pml, bad);
+    return launch_kernel(ctx, attn_chunk_kernel<GT, KV4, VV, false>, grid, dim3(kAttnThreads), 0, q, k, v,
+                         capacity, width, group, hd, start, visible, chunk, chunks, po, pml, bad);
 }
 
 template <int GT>
@@ -358,6 +444,7 @@ struct AttnPlan {
     uint32_t gt, chunk, chunks, zgroups;
     bool kv4;
     int vv;
+    uint32_t splits, per;  // combine: chunks per split, splits per (head, 64 dims)
     size_t part_o_floats, part_ml_pairs;
 };
 
@@ -366,7 +453,7 @@ static AttnPlan attn_plan(size_t kv_heads, size_t group, size_t hd, size_t visib
     p.gt = group > 8 ? 16 : group > 4 ? 8 : group > 2 ? 4 : (uint32_t)group;
     p.zgroups = (uint32_t)((group + p.gt - 1) / p.gt);
     const uint32_t max_chunk = std::min<uint32_t>(kAttnMaxChunk, kAttnScores / p.gt);
-    // enough workgroups to cover the chip twice: chunk = 64 k positions
+    // about two workgroups per CU: chunk = 64 k positions
     size_t k = visible * kv_heads * p.zgroups / ((size_t)kAttnRows * 512);
     k = std::max<size_t>(1, std::min<size_t>(k, max_chunk / kAttnRows));
     p.chunk = (uint32_t)(k * kAttnRows);
@@ -374,6 +461,11 @@ static AttnPlan attn_plan(size_t kv_heads, size_t group, size_t hd, size_t visib
     p.kv4 = hd % 4 == 0 && aligned16;
     // four value dims per thread only up to 8 heads (16 x 4 accumulators spill)
     p.vv = p.kv4 && hd >= 1024 && p.gt <= 8 ? 4 : (p.kv4 && hd >= 512 ? 2 : 1);
+    // about 32 chunks per combine workgroup, at most kCombineBlock
+    p.splits = std::max<uint32_t>((p.chunks + 31) / 32, (p.chunks + kCombineBlock - 1) / kCombineBlock);
+    p.splits = std::min<uint32_t>(p.splits, 32768);
+    p.per = (p.chunks + p.splits - 1) / p.splits;
+    p.splits = (p.chunks + p.per - 1) / p.per;
     p.part_o_floats = kv_heads * (size_t)p.chunks * group * hd;
     p.part_ml_pairs = kv_heads * (size_t)p.chunks * group;
     return p;
@@ -387,10 +479,29 @@ static int enqueue_attention(dmhip_ctx *ctx, const float *query, const float *ke
     const size_t group = query_heads / kv_heads;
     const bool aligned16 = (((uintptr_t)query | (uintptr_t)keys | (uintptr_t)values) & 15u) == 0;
     const AttnPlan p = attn_plan(kv_heads, group, hd, visible, aligned16);
-    const size_t part_bytes = p.part_o_floats * 4 + 256 + p.part_ml_pairs * 8;
-    DM_CHECK_STATUS(ctx->attn.ensure(part_bytes));
-    float *po = (float *)ctx->attn.ptr;
-    float2 *pml = (float2 *)((uint8_t *)ctx->attn.ptr + ((p.part_o_floats * 4 + 255) & ~(size_t)255));
+    const size_t blocks = (hd + 63) / 64;
+    const size_t stage_o_floats = p.splits > 1 ? query_heads * blocks * p.splits * 64 : 0;
+    const size_t stage_l_floats = p.splits > 1 ? query_heads * blocks * p.splits : 0;
+    auto round256 = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t o_bytes = round256(p.part_o_floats * 4), ml_bytes = round256(p.part_ml_pairs * 8);
+    const size_t so_bytes = round256(stage_o_floats * 4);
+    DM_CHECK_STATUS(ctx->attn.ensure(o_bytes + ml_bytes + so_bytes + stage_l_floats * 4));
+    uint8_t *base = (uint8_t *)ctx->attn.ptr;
+    float *po = (float *)base;
+    float2 *pml = (float2 *)(base + o_bytes);
+    float *so = (float *)(base + o_bytes + ml_bytes);
+    float *sl = (float *)(base + o_bytes + ml_bytes + so_bytes);
+    uint32_t *tickets = nullptr;
+    if (p.splits > 1) {
+        const size_t need = query_heads * blocks;
+        if (need > ctx->attn_ticket_count) {
+            // counters start at zero and every call leaves them at zero
+            DM_CHECK_STATUS(ctx->attn_tickets.ensure(need * 4));
+            DM_HIP(launch_fill_u32(ctx->stream, (uint32_t *)ctx->attn_tickets.ptr, (uint32_t)need, 0));
+            ctx->attn_ticket_count = need;
+        }
+        tickets = (uint32_t *)ctx->attn_tickets.ptr;
+    }
     const dim3 grid(p.chunks, (uint32_t)kv_heads, p.zgroups);
     hipError_t e;
     switch (p.gt) {
@@ -401,8 +512,9 @@ static int enqueue_attention(dmhip_ctx *ctx, const float *query, const float *ke
     default: e = launch_chunk_gt<16>(ctx, p.kv4, p.vv, grid, query, keys, values, capacity, width, (uint32_t)group, (uint32_t)hd, start, (uint32_t)visible, p.chunk, p.chunks, po, pml, bad); break;
     }
     if (e != hipSuccess) return hip_fail(e, "attention chunk kernel");
-    e = launch_kernel(ctx, attn_combine_kernel, dim3((uint32_t)query_heads, (uint32_t)((hd + 63) / 64)), dim3(256), 0,
-                      (const float *)po, (const float2 *)pml, (uint32_t)group, (uint32_t)hd, p.chunks, output, bad);
+    e = launch_kernel(ctx, attn_combine_kernel, dim3((uint32_t)query_heads, (uint32_t)blocks, p.splits), dim3(256),
+                      0, (const float *)po, (const float2 *)pml, (uint32_t)group, (uint32_t)hd, p.chunks, p.per, so,
+                      sl, tickets, output, bad);
     if (e != hipSuccess) return hip_fail(e, "attention combine kernel");
     return DMHIP_OK;
 }

@@ -85,6 +85,8 @@ struct dmhip_ctx {
     dm::Scratch in, out, enc, aux;          // host-slice staging
     dm::Scratch partials;                    // per-wave argmax candidates
     dm::Scratch attn;                        // attention chunk partials
+    dm::Scratch attn_tickets;                // attention combine counters, zero between calls
+    size_t attn_ticket_count = 0;            // counters in attn_tickets already zeroed
     // Device memory an allocation-free call lends the fp16 path in place of
     // `aux` for its duration (null otherwise).
     void *aux_lent = nullptr;

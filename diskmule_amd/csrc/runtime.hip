@@ -359,7 +359,8 @@ int dmhip_context_new(int device, dmhip_ctx **out) {
         dmhip_context_free(ctx);
         return fail(DMHIP_ERR_COMMAND, "could not create the HIP streams of device %d", device);
     }
-    for (Scratch *sc : {&ctx->in, &ctx->out, &ctx->enc, &ctx->aux, &ctx->partials, &ctx->attn}) sc->stream = ctx->stream;
+    for (Scratch *sc : {&ctx->in, &ctx->out, &ctx->enc, &ctx->aux, &ctx->partials, &ctx->attn, &ctx->attn_tickets})
+        sc->stream = ctx->stream;
     const int resolved = noalloc_resolve(device);
     if (resolved != DMHIP_OK) {
         dmhip_context_free(ctx);
@@ -381,6 +382,7 @@ void dmhip_context_free(dmhip_ctx *ctx) {
     ctx->aux.release();
     ctx->partials.release();
     ctx->attn.release();
+    ctx->attn_tickets.release();
     if (ctx->argmax_state) (void)hipFree(ctx->argmax_state);
     if (ctx->argmax_ticket) (void)hipFree(ctx->argmax_ticket);
     if (ctx->router_tickets) (void)hipFree(ctx->router_tickets);

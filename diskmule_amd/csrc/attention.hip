@@ -248,8 +248,9 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
         for (int g = 0; g < GT; g++)
 #pragma unroll
             for (int k = 0; k < VV; k++) o[g][k] = 0.0f;
-        for (uint32_t j = 0; j < n; j += VU) {
-            float v[VU][VV];
+        // two register batches: the rows of batch b + 1 are in flight while
+        // batch b is accumulated
+        auto load_rows = [&](float (&v)[VU][VV], uint32_t j) {
 #pragma unroll
             for (int i = 0; i < VU; i++) {
                 uint64_t slot = slot0 + j + i;
@@ -266,6 +267,8 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
                     v[i][0] = ok ? *src : 0.0f;
                 }
             }
+        };
+        auto add_rows = [&](const float (&v)[VU][VV], uint32_t j) {
 #pragma unroll
             for (int g = 0; g < GT; g++) {
                 if ((uint32_t)g >= gz) break;
@@ -280,6 +283,15 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
                             o[g][k] = __builtin_fmaf(v[i0 + i][k], ev[i], o[g][k]);
                 }
             }
+        };
+        float va[VU][VV], vb[VU][VV];
+        load_rows(va, 0);
+        for (uint32_t j = 0; j < n; j += 2 * VU) {
+            if (j + VU < n) load_rows(vb, j + VU);
+            add_rows(va, j);
+            if (j + VU >= n) break;
+            if (j + 2 * VU < n) load_rows(va, j + 2 * VU);
+            add_rows(vb, j + VU);
         }
         if (active) {
 #pragma unroll

@@ -23,7 +23,7 @@ measured the same way, a Q8_0 GEMV entry (the third k-quant of the north
 star, which no configuration uses) and F16 / F32 / Q5_0 GEMV entries (the
 other row types of a Gemma-class GGUF).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|dense|attn|copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|dense|attn|attn_host|copy]
 """
 from __future__ import annotations
 
@@ -516,6 +516,20 @@ def bench_attn(ctx, synth, steps, warmup):
     return out
 
 
+def bench_attn_host(ctx, synth, steps, warmup):
+    """Three calls of host-cache attention (`dmhip_attention`) at the Gemma 4
+    full-layer shape, 32768 positions: a short program for the HBM counter
+    passes (no per-position append copies in the dispatch list)."""
+    qh, kvh, hd, seq = 16, 2, 512, 32768
+    keys = synth.normal(synth.activation_seed(43), seq * kvh * hd)
+    values = synth.normal(synth.activation_seed(44), seq * kvh * hd)
+    q = (synth.normal(synth.activation_seed(45), qh * hd) / np.sqrt(hd)).astype(np.float32)
+    out = np.zeros(qh * hd, dtype=np.float32)
+    for _ in range(3):
+        ctx.attention(q, keys, values, qh, kvh, hd, None, out)
+    return {"calls": 3, "bytes_per_call": 2 * seq * kvh * hd * 4 + 2 * qh * hd * 4}
+
+
 def bench_copy(ctx, synth, steps, warmup):
     """A plain device copy of known size (512 MiB read + 512 MiB written):
     the calibration kernel for the FETCH_SIZE/WRITE_SIZE counter runs."""
@@ -626,7 +640,8 @@ def main() -> int:
     log("device:", ctx.device_name())
     if args.only:
         fn = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-              "q8": bench_q8, "dense": bench_dense, "attn": bench_attn, "copy": bench_copy}[args.only]
+              "q8": bench_q8, "dense": bench_dense, "attn": bench_attn, "attn_host": bench_attn_host,
+              "copy": bench_copy}[args.only]
         res = fn(ctx, synth, args.steps, args.warmup)
         print(json.dumps(res[0] if isinstance(res, tuple) else res))
         return 0

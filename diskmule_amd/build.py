@@ -18,7 +18,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libdmhip.so")
 SOURCES = ["runtime.hip", "dispatch.hip", "kernels_simple.hip", "kernels_qmv.hip", "kernels_qmv8.hip", "kernels_qmv_valu.hip",
-           "kernels_gemm.hip", "expert_cache.hip", "kernels_dense.hip", "attention.hip"]
+           "kernels_gemm.hip", "expert_cache.hip", "kernels_dense.hip", "attention.hip",
+           "kernels_safetensor.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -531,6 +531,9 @@ static int enqueue_attention(dmhip_ctx *ctx, const float *query, const float *ke
     return DMHIP_OK;
 }
 
+// A kernel of this file: resolving it loads the file's code object.
+const void *module_anchor_attention() { return (const void *)attn_combine_kernel; }
+
 // ---- validation, same checks in the same order as src/metal.rs ----
 
 static int fail_shape(const char *reason) {

@@ -27,7 +27,7 @@ int noalloc_resolve(int device) {
     // allocation-free call.
     for (const void *anchor : {module_anchor_simple(), module_anchor_qmv(), module_anchor_qmv8(),
                                module_anchor_qmv_valu(), module_anchor_gemm(), module_anchor_expert(),
-                               module_anchor_dense()}) {
+                               module_anchor_dense(), module_anchor_attention(), module_anchor_safetensor()}) {
         hipFuncAttributes attr;
         DM_HIP(hipFuncGetAttributes(&attr, anchor));
     }

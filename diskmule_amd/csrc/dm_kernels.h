@@ -55,6 +55,18 @@ bool dense_supported(uint32_t type, size_t rows, size_t columns, const void *w, 
 hipError_t launch_dense_gemv(hipStream_t s, int cus, uint32_t type, const void *w, uint32_t rows, uint32_t columns,
                              size_t row_bytes, uint32_t batch, const float *x, float *y);
 const void *module_anchor_expert();
+const void *module_anchor_attention();
+const void *module_anchor_safetensor();
+
+// GLM safetensors GEMV formats (kernels_safetensor.hip).
+constexpr uint32_t kStBf16 = 0, kStF8 = 1, kStI8 = 2, kStI4 = 3;
+// The wide-load form: 16-byte aligned W and x, whole 16-byte chunks per row,
+// at most 16384 columns (the activation in LDS), INT4 groups of 16 or a
+// multiple of 32.
+bool st_wide_supported(uint32_t fmt, size_t rows, size_t columns, size_t group, const void *w, const float *x);
+hipError_t launch_st_gemv(hipStream_t s, int cus, uint32_t fmt, const void *w, uint32_t rows, uint32_t columns,
+                          const float *scales, uint32_t scale_columns, uint32_t group, const float *x, float *y,
+                          bool wide);
 
 hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t n);
 // Launch-floor probes: an empty kernel; a read of n bytes (16-byte aligned

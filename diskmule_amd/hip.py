@@ -54,9 +54,14 @@ EXPORTED_SYMBOLS = [
     "dmhip_kv_layer_width", "dmhip_kv_layer_keys", "dmhip_kv_layer_values", "dmhip_append_kv",
     "dmhip_append_kv_device", "dmhip_attention_cached", "dmhip_attention_cached_device",
     "dmhip_attention_result", "dmhip_attention",
+    "dmhip_matvec_safetensor_mapped", "dmhip_matvec_safetensor", "dmhip_matvec_safetensor_device",
 ]
 
 F32, F16, Q5_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 6, 8, 12, 14, 30
+
+# SafeDtype (src/safetensors.rs:171-187) ids of the safetensors entry points
+SAFE = {"BOOL": 0, "U8": 1, "I8": 2, "U16": 3, "I16": 4, "F16": 5, "BF16": 6, "U32": 7, "I32": 8, "F32": 9,
+        "U64": 10, "I64": 11, "F64": 12, "F8_E4M3": 13, "F8_E5M2": 14}
 
 
 class HipError(RuntimeError):
@@ -215,6 +220,11 @@ def load_library() -> ctypes.CDLL:
         "dmhip_attention_result": ([_vp], ctypes.c_int),
         "dmhip_attention": ([_vp, _f32p, _sz, _f32p, _sz, _f32p, _sz, _sz, _sz, _sz, ctypes.c_int, _sz,
                              _f32p, _sz], ctypes.c_int),
+        "dmhip_matvec_safetensor_mapped": ([_vp, _u32, _sz, _sz, _vp, _sz, _sz, _vp, _sz, _sz, _f32p, _sz, _f32p,
+                                            _sz], ctypes.c_int),
+        "dmhip_matvec_safetensor": ([_vp, _u32, _sz, _sz, _u8p, _sz, _f32p, _sz, _f32p, _sz, _f32p, _sz],
+                                    ctypes.c_int),
+        "dmhip_matvec_safetensor_device": ([_vp, _u32, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -544,6 +554,30 @@ class HipContext:
     @staticmethod
     def event_free(ev: int) -> None:
         load_library().dmhip_event_free(_vp(ev))
+
+    # -- GLM safetensors matrices (src/metal.rs:738-1146) ---------------------
+    def matvec_safetensor_mapped(self, dtype: str, rows: int, columns: int, mapping: MappedBuffer, offset: int,
+                                 length: int, scale, input, output: np.ndarray) -> None:
+        """`scale` is None or (MappedBuffer, offset, length)."""
+        x = _f32(input)
+        sm, so, sl = (None, 0, 0) if scale is None else (scale[0].handle, scale[1], scale[2])
+        _check(load_library().dmhip_matvec_safetensor_mapped(self._h, SAFE[dtype], rows, columns, mapping.handle,
+                                                             offset, length, sm, so, sl, _fp(x), x.size,
+                                                             _fp(output), output.size))
+
+    def matvec_safetensor(self, dtype: str, rows: int, columns: int, encoded, scales, input,
+                          output: np.ndarray) -> None:
+        enc = np.ascontiguousarray(encoded, dtype=np.uint8)
+        sc = None if scales is None else _f32(scales)
+        x = _f32(input)
+        _check(load_library().dmhip_matvec_safetensor(
+            self._h, SAFE[dtype], rows, columns, enc.ctypes.data_as(_u8p) if enc.size else None, enc.size,
+            None if sc is None else (_fp(sc) if sc.size else ctypes.cast(ctypes.c_void_p(8), _f32p)),
+            0 if sc is None else sc.size, _fp(x), x.size, _fp(output), output.size))
+
+    def matvec_safetensor_device(self, dtype: str, rows, columns, w_ptr, w_len, s_ptr, s_len, x_ptr, y_ptr) -> None:
+        _check(load_library().dmhip_matvec_safetensor_device(self._h, SAFE[dtype], rows, columns, w_ptr, w_len,
+                                                             s_ptr, s_len, x_ptr, y_ptr))
 
     # -- attention over a KV ring (src/metal.rs:1196-1511) --------------------
     def new_kv_layer(self, width: int, max_context: int, sliding_window: int | None) -> "KvLayer":

@@ -371,6 +371,61 @@ int dmhip_matvec_valu_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, si
                              const void *weights, const float *x, float *y);
 
 /* ---------------------------------------------------------------------- */
+/* GLM safetensors matrices (src/metal.rs:738-1146)                        */
+/* ---------------------------------------------------------------------- */
+
+/* SafeDtype (src/safetensors.rs:171-187), in declaration order. */
+enum {
+    DMHIP_SAFE_BOOL = 0,
+    DMHIP_SAFE_U8 = 1,
+    DMHIP_SAFE_I8 = 2,
+    DMHIP_SAFE_U16 = 3,
+    DMHIP_SAFE_I16 = 4,
+    DMHIP_SAFE_F16 = 5,
+    DMHIP_SAFE_BF16 = 6,
+    DMHIP_SAFE_U32 = 7,
+    DMHIP_SAFE_I32 = 8,
+    DMHIP_SAFE_F32 = 9,
+    DMHIP_SAFE_U64 = 10,
+    DMHIP_SAFE_I64 = 11,
+    DMHIP_SAFE_F64 = 12,
+    DMHIP_SAFE_F8_E4M3 = 13,
+    DMHIP_SAFE_F8_E5M2 = 14
+};
+
+/* MetalContext::matvec_safetensor_mapped (src/metal.rs:738-881): y = W x for
+   a safetensors matrix inside a mapped buffer.  F32 / F16 are
+   dmhip_matvec_mapped.  BF16: rows x columns little-endian bf16.  F8_E4M3:
+   bytes plus an f32 scale per 128 x 128 block ([ceil(rows/128)]
+   [ceil(columns/128)] in `scale_mapping`).  U8: row INT8 (one f32 scale per
+   row) or grouped INT4 (ceil(columns/2) bytes per row, low nibble first,
+   value (n - 8) * scale), the layout inferred from the byte lengths as
+   u8_matrix_encoding does (src/metal.rs:1893-1942).  scale_mapping NULL is
+   the reference's None.  Errors and their order as the reference's:
+   UnsupportedTensorType "safetensors dtype", InvalidInputLength,
+   InvalidOutputLength, Overflow, InvalidByteLength ("BF16", "F8_E4M3FN",
+   "F8_E4M3FN scale", "U8 quantized matrix", "U8 quantization scales"),
+   MappedRange, EmptyInput ("safetensors matvec", "safetensors U8 matvec"). */
+int dmhip_matvec_safetensor_mapped(dmhip_ctx *ctx, uint32_t safe_dtype, size_t rows, size_t columns,
+                                   const dmhip_buf *mapping, size_t encoded_offset, size_t encoded_length,
+                                   const dmhip_buf *scale_mapping, size_t scale_offset, size_t scale_length,
+                                   const float *input, size_t input_len, float *output, size_t output_len);
+
+/* MetalContext::matvec_safetensor (src/metal.rs:883-993, :1070-1146): the
+   same from host bytes, with the scales as an f32 slice (NULL for None;
+   InvalidVectorLength "safetensors U8 matvec" / "F8_E4M3FN matvec" "scales"
+   when missing or of the wrong count). */
+int dmhip_matvec_safetensor(dmhip_ctx *ctx, uint32_t safe_dtype, size_t rows, size_t columns,
+                            const uint8_t *encoded, size_t encoded_len, const float *scales, size_t scales_len,
+                            const float *input, size_t input_len, float *output, size_t output_len);
+
+/* The same with the matrix, scales, x and y in device memory, enqueued on
+   the stream (checks as dmhip_matvec_safetensor; one token). */
+int dmhip_matvec_safetensor_device(dmhip_ctx *ctx, uint32_t safe_dtype, size_t rows, size_t columns,
+                                   const void *weights, size_t weights_len, const float *scales,
+                                   size_t scales_len, const float *x, float *y);
+
+/* ---------------------------------------------------------------------- */
 /* Decode attention over a KV ring (src/metal.rs:245-277, :1196-1511)      */
 /* ---------------------------------------------------------------------- */
 

@@ -91,6 +91,11 @@ def _declare(l: ctypes.CDLL) -> None:
                                 ctypes.c_uint32, _u8p, _f32p, _szp, _f32p, _f32p, ctypes.c_int]
     l.orc_gemm_tokenwise.argtypes = [ctypes.c_uint32, _sz, _sz, _sz, _u16p, _u8p, _f32p, ctypes.c_int]
     l.orc_attention.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f32p]
+    l.orc_st_decode_f8_e4m3fn.argtypes = [ctypes.c_uint8, _f32p]
+    l.orc_st_u8_encoding.argtypes = [_sz, _sz, _sz, _sz, ctypes.POINTER(ctypes.c_int), _szp, _szp, _szp, _szp,
+                                     ctypes.POINTER(ctypes.c_int)]
+    l.orc_st_matvec.argtypes = [ctypes.c_int, _sz, _sz, _u8p, _f32p, _sz, _f32p, _f32p]
+    l.orc_st_dequantize_row.argtypes = [ctypes.c_int, _sz, _sz, _u8p, _f32p, _sz, _sz, _f32p]
     l.orc_lru_new.argtypes = [_sz, _szp, _sz, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_void_p)]
     l.orc_lru_free.argtypes = [ctypes.c_void_p]
     l.orc_lru_free.restype = None
@@ -285,6 +290,46 @@ def gemm_tokenwise(ggml_type, m, n, k, a_bits, encoded, threads=None) -> np.ndar
     _check(lib().orc_gemm_tokenwise(ggml_type, m, n, k, _p(a, _u16p), _p(enc, _u8p), _p(out, _f32p),
                                     threads or threads_default()), "gemm_tokenwise")
     return out
+
+
+ST_BF16, ST_F8_E4M3, ST_INT8_ROW, ST_INT4_GROUPED = 0, 1, 2, 3
+
+
+def st_decode_f8(bits: int):
+    """decode_f8_e4m3fn: the value, or None for the NaN patterns."""
+    v = ctypes.c_float()
+    return v.value if lib().orc_st_decode_f8_e4m3fn(bits, ctypes.byref(v)) == OK else None
+
+
+def st_u8_encoding(rows: int, columns: int, encoded_len: int, scale_len: int) -> dict:
+    """u8_matrix_encoding: {"format", "group_size", "scale_columns"} or
+    {"error": status, "expected", "actual", "scales"}."""
+    g, sc, e, a = (ctypes.c_size_t() for _ in range(4))
+    fmt, bad = ctypes.c_int(), ctypes.c_int()
+    r = lib().orc_st_u8_encoding(rows, columns, encoded_len, scale_len, ctypes.byref(fmt), ctypes.byref(g),
+                                 ctypes.byref(sc), ctypes.byref(e), ctypes.byref(a), ctypes.byref(bad))
+    if r == OK:
+        return {"format": fmt.value, "group_size": g.value, "scale_columns": sc.value}
+    return {"error": r, "expected": e.value, "actual": a.value, "scales": bool(bad.value)}
+
+
+def st_matvec(fmt: int, rows: int, columns: int, encoded, scales, input, group_size: int = 0) -> np.ndarray:
+    enc = _c(encoded, np.uint8)
+    sc = _c(scales if scales is not None else np.zeros(1), np.float32)
+    x = _c(input, np.float32)
+    out = np.zeros(max(rows, 1), dtype=np.float32)
+    _check(lib().orc_st_matvec(fmt, rows, columns, _p(enc, _u8p), _p(sc, _f32p), group_size, _p(x, _f32p),
+                               _p(out, _f32p)), "st_matvec")
+    return out[:rows]
+
+
+def st_dequantize_row(fmt: int, rows: int, columns: int, encoded, scales, row: int, group_size: int = 0):
+    enc = _c(encoded, np.uint8)
+    sc = _c(scales if scales is not None else np.zeros(1), np.float32)
+    out = np.zeros(max(columns, 1), dtype=np.float32)
+    _check(lib().orc_st_dequantize_row(fmt, rows, columns, _p(enc, _u8p), _p(sc, _f32p), group_size, row,
+                                       _p(out, _f32p)), "st_dequantize_row")
+    return out[:columns]
 
 
 def attention_status(query, keys, values, capacity: int, width: int, query_heads: int, kv_heads: int,

@@ -703,3 +703,133 @@ int orc_attention(const float *query, const float *keys, const float *values, si
     free(scores);
     return ORC_OK;
 }
+
+/* src/glm52/cpu.rs:1397-1410  decode_f8_e4m3fn */
+int orc_st_decode_f8_e4m3fn(uint8_t bits, float *value)
+{
+    float sign = (bits & 0x80) == 0 ? 1.0f : -1.0f;
+    unsigned exponent = (bits >> 3) & 0x0f;
+    unsigned fraction = bits & 0x07;
+    if (exponent == 0x0f && fraction == 0x07) return ORC_NON_FINITE;
+    float magnitude = exponent == 0 ? (float)fraction * ldexpf(1.0f, -9)
+                                    : (1.0f + (float)fraction / 8.0f) * ldexpf(1.0f, (int)exponent - 7);
+    *value = sign * magnitude;
+    return ORC_OK;
+}
+
+/* src/metal.rs:1893-1942  u8_matrix_encoding */
+int orc_st_u8_encoding(size_t rows, size_t columns, size_t encoded_len, size_t scale_len, int *format,
+                       size_t *group_size, size_t *scale_columns, size_t *expected, size_t *actual,
+                       int *scales_bad)
+{
+    size_t int8_bytes, row_scale_bytes, int4_bytes;
+    *scales_bad = 0;
+    if (__builtin_mul_overflow(rows, columns, &int8_bytes)) return ORC_OVERFLOW;
+    if (__builtin_mul_overflow(rows, (size_t)4, &row_scale_bytes)) return ORC_OVERFLOW;
+    if (encoded_len == int8_bytes && scale_len == row_scale_bytes) {
+        *format = ORC_ST_INT8_ROW;
+        *group_size = 0;
+        *scale_columns = 1;
+        return ORC_OK;
+    }
+    if (__builtin_mul_overflow(rows, (columns + 1) / 2, &int4_bytes)) return ORC_OVERFLOW;
+    if (encoded_len != int4_bytes) {
+        *expected = int4_bytes;
+        *actual = encoded_len;
+        return ORC_INVALID_BYTE_LENGTH;
+    }
+    if (scale_len == row_scale_bytes) {
+        *format = ORC_ST_INT4_GROUPED;
+        *group_size = columns > 0 ? columns : 1;
+        *scale_columns = 1;
+        return ORC_OK;
+    }
+    static const size_t sizes[8] = {16, 32, 48, 64, 96, 128, 192, 256};
+    for (int i = 0; i < 8; i++) {
+        if (sizes[i] > columns) break;
+        size_t sc = (columns + sizes[i] - 1) / sizes[i], want;
+        if (__builtin_mul_overflow(rows, sc, &want) || __builtin_mul_overflow(want, (size_t)4, &want))
+            return ORC_OVERFLOW;
+        if (scale_len == want) {
+            *format = ORC_ST_INT4_GROUPED;
+            *group_size = sizes[i];
+            *scale_columns = sc;
+            return ORC_OK;
+        }
+    }
+    *scales_bad = 1;
+    *expected = row_scale_bytes;
+    *actual = scale_len;
+    return ORC_INVALID_BYTE_LENGTH;
+}
+
+/* read_dense_values (BF16), read_fp8_row, read_quantized_row:
+   src/glm52/cpu.rs:1224-1270, :1278-1337, :1339-1394 */
+int orc_st_dequantize_row(int format, size_t rows, size_t columns, const uint8_t *encoded, const float *scales,
+                          size_t group_size, size_t row, float *output)
+{
+    (void)rows;
+    switch (format) {
+    case ORC_ST_BF16: {
+        const uint8_t *p = encoded + row * columns * 2;
+        for (size_t c = 0; c < columns; c++) {
+            uint32_t bits = (uint32_t)(p[2 * c] | (p[2 * c + 1] << 8)) << 16;
+            memcpy(&output[c], &bits, 4);
+        }
+        return ORC_OK;
+    }
+    case ORC_ST_F8_E4M3: {
+        const uint8_t *p = encoded + row * columns;
+        size_t scale_columns = (columns + 127) / 128;
+        const float *s = scales + (row / 128) * scale_columns;
+        for (size_t c = 0; c < columns; c++) {
+            float d;
+            if (orc_st_decode_f8_e4m3fn(p[c], &d) != ORC_OK) return ORC_NON_FINITE;
+            output[c] = d * s[c / 128];
+        }
+        return ORC_OK;
+    }
+    case ORC_ST_INT8_ROW: {
+        const uint8_t *p = encoded + row * columns;
+        for (size_t c = 0; c < columns; c++) output[c] = (float)(int8_t)p[c] * scales[row];
+        return ORC_OK;
+    }
+    case ORC_ST_INT4_GROUPED: {
+        size_t row_bytes = (columns + 1) / 2;
+        size_t scale_columns = (columns + group_size - 1) / group_size;
+        const uint8_t *p = encoded + row * row_bytes;
+        const float *s = scales + row * scale_columns;
+        for (size_t c = 0; c < columns; c++) {
+            uint8_t byte = p[c / 2];
+            uint8_t nibble = (c % 2 == 0) ? (byte & 0x0f) : (byte >> 4);
+            output[c] = ((float)nibble - 8.0f) * s[c / group_size];
+        }
+        return ORC_OK;
+    }
+    default:
+        return ORC_UNSUPPORTED_TYPE;
+    }
+}
+
+/* src/glm52/cpu.rs:1180-1190  row, then sum of products */
+int orc_st_matvec(int format, size_t rows, size_t columns, const uint8_t *encoded, const float *scales,
+                  size_t group_size, const float *input, float *output)
+{
+    float *row = (float *)malloc((columns ? columns : 1) * sizeof(float));
+    if (!row) return ORC_OVERFLOW;
+    for (size_t r = 0; r < rows; r++) {
+        int status = orc_st_dequantize_row(format, rows, columns, encoded, scales, group_size, r, row);
+        if (status != ORC_OK) {
+            free(row);
+            return status;
+        }
+        float sum = 0.0f;
+        for (size_t c = 0; c < columns; c++) {
+            float product = row[c] * input[c];
+            sum = sum + product;
+        }
+        output[r] = sum;
+    }
+    free(row);
+    return ORC_OK;
+}

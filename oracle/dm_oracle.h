@@ -28,6 +28,10 @@
  *   orc_dense_ffn / orc_moe_layer / orc_gemm_tokenwise
  *                            compositions of the functions above, checked by
  *                            recomposing them from the pinned parts in numpy
+ *   orc_st_*                 src/glm52/cpu.rs:1551-1606 and src/metal.rs:2315-2486
+ *                            known answers; all 256 E4M3FN patterns against the
+ *                            OCP formula and its landmark values; exact-rational
+ *                            brute force of the product-then-sum fold
  *   orc_attention            src/gemma4/cpu.rs:967-985 and src/metal.rs:2499-2570
  *                            known answers; float64 closed form from the same
  *                            fp32 scores; equal-value and one-hot invariants;
@@ -109,6 +113,31 @@ int orc_moe_layer(size_t batch, size_t hidden, size_t expert_width, size_t exper
 int orc_gemm_tokenwise(uint32_t ggml_type, size_t m, size_t n, size_t k,
                        const uint16_t *activations_bf16, const uint8_t *encoded, float *output,
                        int threads);
+
+/* GLM safetensors matrices (src/glm52/cpu.rs:1180-1420, src/metal.rs:1893-1942).
+   Formats: BF16 rows; F8_E4M3FN rows with one f32 scale per 128 x 128 block
+   (scales [ceil(rows/128)][ceil(columns/128)]); U8 row-INT8 (one scale per
+   row); U8 grouped INT4 (two codes per byte, low nibble first, (n - 8) *
+   scale[row][column / group_size], rows of ceil(columns / 2) bytes). */
+enum { ORC_ST_BF16 = 0, ORC_ST_F8_E4M3 = 1, ORC_ST_INT8_ROW = 2, ORC_ST_INT4_GROUPED = 3 };
+/* decode_f8_e4m3fn (src/glm52/cpu.rs:1397-1410): returns 0 and sets *value,
+   or ORC_NON_FINITE for the NaN patterns 0x7f / 0xff. */
+int orc_st_decode_f8_e4m3fn(uint8_t bits, float *value);
+/* u8_matrix_encoding (src/metal.rs:1893-1942): ORC_OK with *format
+   ORC_ST_INT8_ROW or ORC_ST_INT4_GROUPED (and *group_size / *scale_columns),
+   else ORC_INVALID_BYTE_LENGTH (with *expected / *actual, and *scales_bad = 1
+   when the scale length is what failed) or ORC_OVERFLOW. */
+int orc_st_u8_encoding(size_t rows, size_t columns, size_t encoded_len, size_t scale_len, int *format,
+                       size_t *group_size, size_t *scale_columns, size_t *expected, size_t *actual,
+                       int *scales_bad);
+/* One row dequantized (matrix_row_into_untracked / read_quantized_row /
+   read_fp8_row / read_dense_values), then y[r] = sum_c w[c] * x[c] as a
+   product followed by a sequential add (src/glm52/cpu.rs:1180-1190).
+   group_size is used by ORC_ST_INT4_GROUPED only. */
+int orc_st_matvec(int format, size_t rows, size_t columns, const uint8_t *encoded, const float *scales,
+                  size_t group_size, const float *input, float *output);
+int orc_st_dequantize_row(int format, size_t rows, size_t columns, const uint8_t *encoded, const float *scales,
+                          size_t group_size, size_t row, float *output);
 
 /* Decode attention of one query token over a KV ring, src/gemma4/cpu.rs:900-946
    (`attend`) with the ring addressing of metal/kernels.metal:486-578: position

@@ -36,6 +36,7 @@ use crate::{
     expert::{ExpertCacheError, ExpertCacheStats, ExpertLayerLayout},
     gguf::TensorType,
     metal::MetalError,
+    safetensors::SafeDtype,
 };
 
 /// One-to-one transcription of `include/dmhip.h`.
@@ -178,6 +179,22 @@ pub mod ffi {
     pub const DMHIP_TYPE_Q4_K: u32 = 12;
     pub const DMHIP_TYPE_Q6_K: u32 = 14;
     pub const DMHIP_TYPE_BF16: u32 = 30;
+
+    pub const DMHIP_SAFE_BOOL: u32 = 0;
+    pub const DMHIP_SAFE_U8: u32 = 1;
+    pub const DMHIP_SAFE_I8: u32 = 2;
+    pub const DMHIP_SAFE_U16: u32 = 3;
+    pub const DMHIP_SAFE_I16: u32 = 4;
+    pub const DMHIP_SAFE_F16: u32 = 5;
+    pub const DMHIP_SAFE_BF16: u32 = 6;
+    pub const DMHIP_SAFE_U32: u32 = 7;
+    pub const DMHIP_SAFE_I32: u32 = 8;
+    pub const DMHIP_SAFE_F32: u32 = 9;
+    pub const DMHIP_SAFE_U64: u32 = 10;
+    pub const DMHIP_SAFE_I64: u32 = 11;
+    pub const DMHIP_SAFE_F64: u32 = 12;
+    pub const DMHIP_SAFE_F8_E4M3: u32 = 13;
+    pub const DMHIP_SAFE_F8_E5M2: u32 = 14;
 
     #[link(name = "dmhip")]
     unsafe extern "C" {
@@ -484,6 +501,50 @@ pub mod ffi {
             probabilities: *mut f32,
         ) -> c_int;
 
+        // GLM safetensors matrices
+        pub fn dmhip_matvec_safetensor_mapped(
+            ctx: *mut dmhip_ctx,
+            safe_dtype: u32,
+            rows: usize,
+            columns: usize,
+            mapping: *const dmhip_buf,
+            encoded_offset: usize,
+            encoded_length: usize,
+            scale_mapping: *const dmhip_buf,
+            scale_offset: usize,
+            scale_length: usize,
+            input: *const f32,
+            input_len: usize,
+            output: *mut f32,
+            output_len: usize,
+        ) -> c_int;
+        pub fn dmhip_matvec_safetensor(
+            ctx: *mut dmhip_ctx,
+            safe_dtype: u32,
+            rows: usize,
+            columns: usize,
+            encoded: *const u8,
+            encoded_len: usize,
+            scales: *const f32,
+            scales_len: usize,
+            input: *const f32,
+            input_len: usize,
+            output: *mut f32,
+            output_len: usize,
+        ) -> c_int;
+        pub fn dmhip_matvec_safetensor_device(
+            ctx: *mut dmhip_ctx,
+            safe_dtype: u32,
+            rows: usize,
+            columns: usize,
+            weights: *const c_void,
+            weights_len: usize,
+            scales: *const f32,
+            scales_len: usize,
+            x: *const f32,
+            y: *mut f32,
+        ) -> c_int;
+
         // decode attention over a KV ring
         pub fn dmhip_new_kv_layer(
             ctx: *mut dmhip_ctx,
@@ -732,6 +793,27 @@ fn ggml_id(kind: TensorType) -> u32 {
         TensorType::I64 => 27,
         TensorType::F64 => 28,
         TensorType::Bf16 => 30,
+    }
+}
+
+/// SafeDtype id of the safetensors entry points (src/safetensors.rs:171-187).
+fn safe_id(dtype: SafeDtype) -> u32 {
+    match dtype {
+        SafeDtype::Bool => ffi::DMHIP_SAFE_BOOL,
+        SafeDtype::U8 => ffi::DMHIP_SAFE_U8,
+        SafeDtype::I8 => ffi::DMHIP_SAFE_I8,
+        SafeDtype::U16 => ffi::DMHIP_SAFE_U16,
+        SafeDtype::I16 => ffi::DMHIP_SAFE_I16,
+        SafeDtype::F16 => ffi::DMHIP_SAFE_F16,
+        SafeDtype::Bf16 => ffi::DMHIP_SAFE_BF16,
+        SafeDtype::U32 => ffi::DMHIP_SAFE_U32,
+        SafeDtype::I32 => ffi::DMHIP_SAFE_I32,
+        SafeDtype::F32 => ffi::DMHIP_SAFE_F32,
+        SafeDtype::U64 => ffi::DMHIP_SAFE_U64,
+        SafeDtype::I64 => ffi::DMHIP_SAFE_I64,
+        SafeDtype::F64 => ffi::DMHIP_SAFE_F64,
+        SafeDtype::F8E4M3 => ffi::DMHIP_SAFE_F8_E4M3,
+        SafeDtype::F8E5M2 => ffi::DMHIP_SAFE_F8_E5M2,
     }
 }
 
@@ -1164,10 +1246,10 @@ impl MetalContext {
         })
     }
 
-    // The rest of the MetalContext surface is outside the library's
-    // quantized-matrix and attention paths. These methods keep the graphs
-    // compiling and fail with a Command error naming the operation; the
-    // Qwen3.5 graph (src/qwen35/metal.rs) calls none of them.
+    // The rest of the MetalContext surface (add, RoPE, gelu_mul, softmax) is
+    // outside the library. These methods keep the graphs compiling and fail
+    // with a Command error naming the operation; the Qwen3.5 graph
+    // (src/qwen35/metal.rs) calls none of them.
 
     pub fn add(&self, _left: &[f32], _right: &[f32], _output: &mut [f32]) -> Result<(), MetalError> {
         Err(not_provided("add"))
@@ -1195,30 +1277,71 @@ impl MetalContext {
 
     pub fn matvec_safetensor_mapped(
         &self,
-        _dtype: crate::safetensors::SafeDtype,
-        _rows: usize,
-        _columns: usize,
-        _mapping: &MetalMappedBuffer,
-        _encoded_offset: usize,
-        _encoded_length: usize,
-        _scale: Option<(&MetalMappedBuffer, usize, usize)>,
-        _input: &[f32],
-        _output: &mut [f32],
+        dtype: SafeDtype,
+        rows: usize,
+        columns: usize,
+        mapping: &MetalMappedBuffer,
+        encoded_offset: usize,
+        encoded_length: usize,
+        scale: Option<(&MetalMappedBuffer, usize, usize)>,
+        input: &[f32],
+        output: &mut [f32],
     ) -> Result<(), MetalError> {
-        Err(not_provided("safetensors matvec"))
+        let (scale_raw, scale_offset, scale_length) = match scale {
+            Some((buffer, offset, length)) => (buffer.raw.as_ptr().cast_const(), offset, length),
+            None => (ptr::null(), 0, 0),
+        };
+        // SAFETY: the buffers belong to live contexts; the library checks
+        // both ranges against their mappings and the slices' lengths.
+        check(unsafe {
+            ffi::dmhip_matvec_safetensor_mapped(
+                self.context.raw(),
+                safe_id(dtype),
+                rows,
+                columns,
+                mapping.raw.as_ptr(),
+                encoded_offset,
+                encoded_length,
+                scale_raw,
+                scale_offset,
+                scale_length,
+                input.as_ptr(),
+                input.len(),
+                output.as_mut_ptr(),
+                output.len(),
+            )
+        })
     }
 
     pub fn matvec_safetensor(
         &self,
-        _dtype: crate::safetensors::SafeDtype,
-        _rows: usize,
-        _columns: usize,
-        _encoded: &[u8],
-        _scales: Option<&[f32]>,
-        _input: &[f32],
-        _output: &mut [f32],
+        dtype: SafeDtype,
+        rows: usize,
+        columns: usize,
+        encoded: &[u8],
+        scales: Option<&[f32]>,
+        input: &[f32],
+        output: &mut [f32],
     ) -> Result<(), MetalError> {
-        Err(not_provided("safetensors matvec"))
+        // None is a null pointer; Some(&[]) keeps its non-null dangling one
+        let (scales_ptr, scales_len) = scales.map_or((ptr::null(), 0), |s| (s.as_ptr(), s.len()));
+        // SAFETY: the slices are valid for their lengths.
+        check(unsafe {
+            ffi::dmhip_matvec_safetensor(
+                self.context.raw(),
+                safe_id(dtype),
+                rows,
+                columns,
+                encoded.as_ptr(),
+                encoded.len(),
+                scales_ptr,
+                scales_len,
+                input.as_ptr(),
+                input.len(),
+                output.as_mut_ptr(),
+                output.len(),
+            )
+        })
     }
 
     pub fn new_kv_layer(

@@ -186,3 +186,12 @@ def test_every_status_has_a_variant_in_both_bindings():
     # Command and InvalidArgument fall through to MetalError::Command by design
     for name in set(statuses) - {"DMHIP_OK", "DMHIP_ERR_COMMAND", "DMHIP_ERR_INVALID_ARGUMENT"}:
         assert re.search(r"ffi::%s\b[^=]*=>" % name, src), name
+
+
+def test_rust_safe_dtype_ids_match_the_header_and_the_python_binding():
+    text = open(os.path.join(ROOT, "include", "dmhip.h")).read()
+    c = dict((n, int(v)) for n, v in re.findall(r"(DMHIP_SAFE_\w+) = (\d+)", text))
+    rust = dict((n, int(v)) for n, v in re.findall(r"pub const (DMHIP_SAFE_\w+): u32 = (\d+);", _rust_source()))
+    assert rust == c and len(c) == 15
+    from diskmule_amd import hip
+    assert {f"DMHIP_SAFE_{k}": v for k, v in hip.SAFE.items()} == c

@@ -23,7 +23,7 @@ measured the same way, a Q8_0 GEMV entry (the third k-quant of the north
 star, which no configuration uses) and F16 / F32 / Q5_0 GEMV entries (the
 other row types of a Gemma-class GGUF).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|dense|attn|attn_host|copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|dense|st|attn|attn_host|copy]
 """
 from __future__ import annotations
 
@@ -452,6 +452,61 @@ def bench_c5(ctx, synth, steps, warmup):
     return out
 
 
+def bench_st(ctx, synth, steps, warmup):
+    """GLM safetensors GEMV (src/metal.rs:738-1146; no BASELINE config):
+    12288 x 6144 in BF16, F8_E4M3FN (128 x 128 block scales), row INT8 and
+    grouped INT4 (group 32), and an INT4 expert-sized 2048 x 6144, batch 1,
+    over rotating copies (more than the 256 MB MALL), back-to-back launches.
+    Algorithmic bytes: weights + scales + 4 columns + 4 rows."""
+    out = {}
+    rng = np.random.default_rng(61)
+    configs = (("BF16", 12288, 6144, 0), ("F8_E4M3", 12288, 6144, 0), ("I8", 12288, 6144, 0),
+               ("I4_g32", 12288, 6144, 32), ("I4_g32", 2048, 6144, 32))
+    for tag, rows, cols, group in configs:
+        if tag == "BF16":
+            w = (synth.normal(synth.activation_seed(50), rows * cols) * 0.05).view(np.uint32) >> 16
+            w = w.astype("<u2").view(np.uint8)
+            scales, dtype = None, "BF16"
+        elif tag == "F8_E4M3":
+            w = rng.integers(0, 0x7F, rows * cols, dtype=np.uint8) | (rng.integers(0, 2, rows * cols, dtype=np.uint8) << 7)
+            scales, dtype = rng.uniform(1e-3, 4e-3, (rows // 128) * (cols // 128)).astype(np.float32), "F8_E4M3"
+        elif tag == "I8":
+            w = rng.integers(0, 256, rows * cols, dtype=np.uint8)
+            scales, dtype = rng.uniform(1e-3, 1e-2, rows).astype(np.float32), "U8"
+        else:
+            w = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+            scales, dtype = rng.uniform(1e-3, 1e-2, rows * (cols // group)).astype(np.float32), "U8"
+        x = synth.normal(synth.activation_seed(51), cols)
+        step_bytes = w.size + (0 if scales is None else scales.nbytes) + 4 * cols + 4 * rows
+        copies = max(2, -(-300_000_000 // step_bytes))
+        wbs = [upload(ctx, w)]
+        for _ in range(copies - 1):
+            b = ctx.new_owned_buffer(w.size)
+            ctx.copy_device(b.device_ptr, wbs[0].device_ptr, w.size)
+            wbs.append(b)
+        sbs = [None] * copies if scales is None else [upload(ctx, scales) for _ in range(copies)]
+        xb, yb = upload(ctx, x), ctx.new_owned_buffer(rows * 4)
+
+        def call(i):
+            sb = sbs[i % copies]
+            ctx.matvec_safetensor_device(dtype, rows, cols, wbs[i % copies].device_ptr, w.size,
+                                         None if sb is None else sb.device_ptr, 0 if scales is None else scales.size,
+                                         xb.device_ptr, yb.device_ptr)
+
+        for i in range(warmup):
+            call(i)
+        n = max(steps, 2 * copies)
+        wall, kern, _ = timed_loop(ctx, call, n)
+        ms = wall / n
+        key = f"{tag}_{rows}x{cols}"
+        out[key] = {"ms": ms, "bytes": step_bytes, "gbps": step_bytes / (ms * 1e-3) / 1e9,
+                    "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "kernel_ms": kern / n}
+        log(f"safetensors {key}: {ms * 1e3:.1f} us per launch ({out[key]['gbps']:.0f} GB/s)")
+        for b in wbs + [xb, yb] + [b for b in sbs if b is not None]:
+            b.free()
+    return out
+
+
 def bench_attn(ctx, synth, steps, warmup):
     """Decode attention over a KV ring (src/metal.rs:1270-1323) at the Gemma 4
     26B shapes (src/gemma4.rs:150-230): full layers (16 query heads over 2 KV
@@ -640,7 +695,7 @@ def main() -> int:
     log("device:", ctx.device_name())
     if args.only:
         fn = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-              "q8": bench_q8, "dense": bench_dense, "attn": bench_attn, "attn_host": bench_attn_host,
+              "q8": bench_q8, "dense": bench_dense, "st": bench_st, "attn": bench_attn, "attn_host": bench_attn_host,
               "copy": bench_copy}[args.only]
         res = fn(ctx, synth, args.steps, args.warmup)
         print(json.dumps(res[0] if isinstance(res, tuple) else res))
@@ -649,7 +704,7 @@ def main() -> int:
     c2, (w2, x2) = bench_c2(ctx, synth, args.steps, args.warmup)
     details = {"C2": c2}
     for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5), ("Q8_0", bench_q8),
-                     ("dense", bench_dense), ("attention", bench_attn)):
+                     ("dense", bench_dense), ("safetensors", bench_st), ("attention", bench_attn)):
         details[name] = fn(ctx, synth, max(3, args.steps // 2), args.warmup)
     log("CPU baseline")
     cpu = cpu_baseline(w2, x2, args.cpu_seconds)

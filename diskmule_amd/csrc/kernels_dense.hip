@@ -55,13 +55,17 @@ __global__ void __launch_bounds__(64 * kDenseWaves) dense_gemv_kernel(const uint
                                                                       uint32_t columns, size_t row_bytes,
                                                                       const float *__restrict__ x,
                                                                       float *__restrict__ y, uint32_t y_stride) {
-    constexpr uint32_t E = kPerChunk<TYPE>;
-    extern __shared__ float xs[];  // [TOK][columns]
+    constexpr uint32_t E = kPerChunk<TYPE>, XP = E + 4;  // LDS floats per chunk
+    // [TOK][chunks][E + 4]: lanes reading consecutive chunks start 4 banks
+    // apart, so a 16-byte read of 16 lanes touches all 64 banks once.
+    extern __shared__ __attribute__((aligned(16))) float xs[];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    for (uint32_t i = threadIdx.x; i < TOK * columns / 4; i += 64 * kDenseWaves)
-        ((floatx4 *)xs)[i] = ((const floatx4 *)x)[i];
-    __syncthreads();
     const uint32_t chunks = columns / E;  // per row
+    for (uint32_t i = threadIdx.x; i < TOK * columns / 4; i += 64 * kDenseWaves) {
+        const uint32_t t = i / (columns / 4), k = i % (columns / 4);
+        *(floatx4 *)&xs[(t * chunks + k / (E / 4)) * XP + 4 * (k % (E / 4))] = ((const floatx4 *)x)[i];
+    }
+    __syncthreads();
     const uint32_t step = gridDim.x * kDenseWaves * kRows;
     for (uint32_t r0 = (blockIdx.x * kDenseWaves + wave) * kRows; r0 < rows; r0 += step) {
         float acc[kRows][TOK];
@@ -89,7 +93,7 @@ __global__ void __launch_bounds__(64 * kDenseWaves) dense_gemv_kernel(const uint
                 for (int t = 0; t < TOK; t++)
 #pragma unroll
                     for (uint32_t q = 0; q < E / 4; q++) {
-                        const floatx4 f = *(const floatx4 *)&xs[t * columns + c * E + 4 * q];
+                        const floatx4 f = *(const floatx4 *)&xs[(t * chunks + c) * XP + 4 * q];
 #pragma unroll
                         for (int e = 0; e < 4; e++) xv[t][4 * q + e] = f[e];
                     }
@@ -239,7 +243,7 @@ namespace {
 template <uint32_t TYPE, int TOK>
 hipError_t launch_dense_t(hipStream_t s, int cus, const uint8_t *w, uint32_t rows, uint32_t columns, size_t row_bytes,
                           const float *x, float *y, uint32_t y_stride) {
-    const uint32_t lds = TOK * columns * 4;
+    const uint32_t lds = TOK * (columns / kPerChunk<TYPE>) * (kPerChunk<TYPE> + 4) * 4;
     static LdsLimit limit;
     hipError_t e = limit.ensure((const void *)dense_gemv_kernel<TYPE, TOK>, lds);
     if (e != hipSuccess) return e;

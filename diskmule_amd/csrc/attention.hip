@@ -67,18 +67,22 @@ __device__ __forceinline__ void attn_load_keys(KeyStage<KV4> &st, const float *_
         const uint32_t col = (u % units) * (KV4 ? 4 : 1);
         const uint32_t r = row0 + row;
         const uint32_t d = dim0 + col;
-        uint64_t slot = slot0 + r;
+        // Every lane loads, from a row and column clamped into the chunk: no
+        // branch and no use of the value before it is stored, so waiting for
+        // one register stage leaves the next in flight.  A row past the
+        // chunk's end scores garbage that is replaced by -inf; a column past
+        // head_dim is never read.
+        uint64_t slot = slot0 + min(r, n - 1);
         if (slot >= capacity) slot -= capacity;
-        const bool ok = r < n && d < head_dim;
-        const float *src = keys + slot * width + head_off + d;
+        const float *src = keys + slot * width + head_off + min(d, head_dim - (KV4 ? 4 : 1));
         if constexpr (KV4) {
-            float4 k = ok ? *(const float4 *)src : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 k = *(const float4 *)src;
             st.v[4 * i + 0] = k.x;
             st.v[4 * i + 1] = k.y;
             st.v[4 * i + 2] = k.z;
             st.v[4 * i + 3] = k.w;
         } else {
-            st.v[i] = ok ? *src : 0.0f;
+            st.v[i] = *src;
         }
     }
 }
@@ -158,6 +162,9 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
     const uint32_t steps = subs * tiles;
     float acc[CH];
     auto load_step = [&](KeyStage<KV4> &stage, uint32_t step) {
+        // past the last step: reload the last tile (the loads stay
+        // unconditional, so the waits count them exactly)
+        step = min(step, steps - 1);
         const uint32_t sb = step / tiles, tl = step - sb * tiles;
         attn_load_keys<KV4>(stage, keys, capacity, width, head_off, slot0, sb * kAttnRows, n, tl * kAttnTile,
                             head_dim);
@@ -166,7 +173,7 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
         __syncthreads();
         attn_store_keys<KV4>(stage, ktile);
         __syncthreads();
-        if (step + 2 < steps) load_step(stage, step + 2);
+        load_step(stage, step + 2);
         const uint32_t sb = step / tiles, tl = step - sb * tiles;
         if (tl == 0) {
 #pragma unroll
@@ -195,19 +202,24 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
                 for (int ch = 0; ch < CH; ch++) acc[ch] = __builtin_fmaf(qrow[ch][dim0 + dd], k, acc[ch]);
             }
         }
-        if (tl + 1 == tiles) {
+        if (tl + 1 == tiles && sb < subs) {
             const uint32_t r = sb * kAttnRows + lane;
 #pragma unroll
             for (int ch = 0; ch < CH; ch++)
                 if (chain_on[ch]) sc[chain_head[ch] * chunk + r] = r < n ? acc[ch] : -INFINITY;
         }
     };
+    // An odd step count runs one extra step over the last tile again; it
+    // writes no scores (sb == subs).
     KeyStage<KV4> st0, st1;
     load_step(st0, 0);
-    if (steps > 1) load_step(st1, 1);
+    // keep stage 0's loads issued before stage 1's, as in the loop, so the
+    // wait before the first store leaves stage 1 in flight
+    __builtin_amdgcn_sched_barrier(0);
+    load_step(st1, 1);
     for (uint32_t step = 0; step < steps; step += 2) {
         run_step(st0, step);
-        if (step + 1 < steps) run_step(st1, step + 1);
+        run_step(st1, step + 1);
     }
     // positions of the last pass past the chunk's end (chunk is a multiple of 64)
     __syncthreads();
@@ -248,27 +260,32 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
         for (int g = 0; g < GT; g++)
 #pragma unroll
             for (int k = 0; k < VV; k++) o[g][k] = 0.0f;
-        // two register batches: the rows of batch b + 1 are in flight while
-        // batch b is accumulated
+        // Loads are unconditional (rows clamped into the chunk) and a row past
+        // the chunk's end is zeroed where it is used, not where it is
+        // loaded, so accumulating one batch waits only for that batch.
         auto load_rows = [&](float (&v)[VU][VV], uint32_t j) {
 #pragma unroll
             for (int i = 0; i < VU; i++) {
-                uint64_t slot = slot0 + j + i;
+                uint64_t slot = slot0 + min(j + i, n - 1);
                 if (slot >= capacity) slot -= capacity;
-                const float *src = values + slot * width + head_off + d;
-                const bool ok = active && j + i < n;
+                const float *src = values + slot * width + head_off + min(d, head_dim - VV);
                 if constexpr (VV == 4) {
-                    const float4 x = ok ? *(const float4 *)src : make_float4(0.f, 0.f, 0.f, 0.f);
+                    const float4 x = *(const float4 *)src;
                     v[i][0] = x.x, v[i][1] = x.y, v[i][2] = x.z, v[i][3] = x.w;
                 } else if constexpr (VV == 2) {
-                    const float2 x = ok ? *(const float2 *)src : make_float2(0.f, 0.f);
+                    const float2 x = *(const float2 *)src;
                     v[i][0] = x.x, v[i][1] = x.y;
                 } else {
-                    v[i][0] = ok ? *src : 0.0f;
+                    v[i][0] = *src;
                 }
             }
         };
         auto add_rows = [&](const float (&v)[VU][VV], uint32_t j) {
+            float u[VU][VV];
+#pragma unroll
+            for (int i = 0; i < VU; i++)
+#pragma unroll
+                for (int k = 0; k < VV; k++) u[i][k] = active && j + i < n ? v[i][k] : 0.0f;
 #pragma unroll
             for (int g = 0; g < GT; g++) {
                 if ((uint32_t)g >= gz) break;
@@ -280,18 +297,20 @@ attn_chunk_kernel(const float *__restrict__ query, const float *__restrict__ key
                     for (int i = 0; i < 4; i++)
 #pragma unroll
                         for (int k = 0; k < VV; k++)
-                            o[g][k] = __builtin_fmaf(v[i0 + i][k], ev[i], o[g][k]);
+                            o[g][k] = __builtin_fmaf(u[i0 + i][k], ev[i], o[g][k]);
                 }
             }
         };
+        // two register batches: the rows of batch b + 1 are in flight while
+        // batch b is accumulated
         float va[VU][VV], vb[VU][VV];
         load_rows(va, 0);
+        __builtin_amdgcn_sched_barrier(0);
         for (uint32_t j = 0; j < n; j += 2 * VU) {
-            if (j + VU < n) load_rows(vb, j + VU);
+            load_rows(vb, j + VU);
             add_rows(va, j);
-            if (j + VU >= n) break;
-            if (j + 2 * VU < n) load_rows(va, j + 2 * VU);
-            add_rows(vb, j + VU);
+            load_rows(va, j + 2 * VU);
+            if (j + VU < n) add_rows(vb, j + VU);
         }
         if (active) {
 #pragma unroll

@@ -195,6 +195,26 @@ def test_repeated_calls_are_deterministic(ctx):
         assert np.array_equal(again.view(np.uint32), first.view(np.uint32))
 
 
+def test_many_chunks_combined_in_splits(ctx):
+    # 16 query heads on one KV head at 70,000 positions: 547 chunks of 128,
+    # combined in 18 splits that publish their sums, the last of which adds
+    # them in split order
+    print("split combine: qh=16 kvh=1 hd=64 positions=70000", flush=True)
+    rng = np.random.default_rng(37)
+    qh, kvh, hd, seq = 16, 1, 64, 70000
+    width = kvh * hd
+    keys = rng.standard_normal((seq, width)).astype(np.float32)
+    values = rng.standard_normal((seq, width)).astype(np.float32)
+    q = (rng.standard_normal(qh * hd) * 0.125).astype(np.float32)
+    out = np.zeros(qh * hd, dtype=np.float32)
+    ctx.attention(q, keys, values, qh, kvh, hd, None, out)
+    exact, w, w2, _ = attention_exact(q, keys, values, seq, width, qh, kvh, hd, 0, seq)
+    assert_attention_close(out, exact, w, w2, seq, "split combine")
+    again = np.zeros(qh * hd, dtype=np.float32)
+    ctx.attention(q, keys, values, qh, kvh, hd, None, again)
+    assert np.array_equal(again.view(np.uint32), out.view(np.uint32))
+
+
 # ---- non-finite scores ---------------------------------------------------------------
 
 def test_non_finite_scores_are_rejected(ctx):

@@ -110,6 +110,11 @@ hipError_t launch_rms_norm(hipStream_t s, const float *in, uint32_t batch, uint3
                            const float *weight, float eps, float *out);
 hipError_t launch_silu_mul(hipStream_t s, const float *gate, const float *up, size_t n, float *out);
 hipError_t launch_softcap(hipStream_t s, const float *in, size_t n, float cap, float *out);
+hipError_t launch_add(hipStream_t s, const float *a, const float *b, size_t n, float *out);
+hipError_t launch_gelu_mul(hipStream_t s, const float *gate, const float *up, size_t n, float *out);
+hipError_t launch_softmax(hipStream_t s, const float *in, uint32_t n, float *out);
+hipError_t launch_rope_neox(hipStream_t s, float *v, size_t heads, uint32_t head_dim, uint32_t pairs,
+                            uint32_t position, float theta);
 hipError_t launch_moe_combine(hipStream_t s, const float *expert_out, const float *p, uint32_t batch,
                               uint32_t k, uint32_t hidden, float *y);
 hipError_t launch_silu_mul_glm_pairs(hipStream_t s, const float *gate_up, uint32_t pairs,

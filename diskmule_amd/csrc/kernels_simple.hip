@@ -805,6 +805,118 @@ hipError_t launch_softcap(hipStream_t s, const float *in, size_t n, float cap, f
     return hipGetLastError();
 }
 
+// ---- Gemma 4 / GLM glue: vector add, GELU multiply, softmax, NeoX RoPE ----
+
+// output = left + right (src/metal.rs:404-432, metal/kernels.metal:34-43).
+__global__ void add_kernel(const float *__restrict__ a, const float *__restrict__ b, size_t n,
+                           float *__restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = a[i] + b[i];
+}
+
+hipError_t launch_add(hipStream_t s, const float *a, const float *b, size_t n, float *out) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(add_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, a, b, n, out);
+    return hipGetLastError();
+}
+
+// Gemma 4's gelu_pytorch_tanh in the CPU's order (src/cpu.rs:144-149):
+// 0.5 v (1 + tanh(0.7978846 (v + 0.044715 (v v) v))), each operation
+// rounded once.
+__device__ __forceinline__ float gelu_tanh(float v) {
+    const float cubic = (v * v) * v;
+    const float inner = 0.7978846f * (v + 0.044715f * cubic);
+    return (0.5f * v) * (1.0f + tanhf(inner));
+}
+
+// gelu_tanh(gate) * up (src/metal.rs:530-552, src/gemma4/cpu.rs).
+__global__ void gelu_mul_kernel(const float *__restrict__ gate, const float *__restrict__ up, size_t n,
+                                float *__restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = gelu_tanh(gate[i]) * up[i];
+}
+
+hipError_t launch_gelu_mul(hipStream_t s, const float *gate, const float *up, size_t n, float *out) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(gelu_mul_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, gate, up, n, out);
+    return hipGetLastError();
+}
+
+// Softmax of one finite vector (src/metal.rs:578-598; src/cpu.rs:196-225):
+// the maximum, e_i = exp(x_i - max), their sum, then e_i / sum.  One
+// workgroup of 1024 threads: thread t takes i = t, t + 1024, ...; the sum
+// is a fixed tree (in-thread, then the wave, then the 16 waves in order).
+__global__ void __launch_bounds__(1024) softmax_kernel(const float *__restrict__ in, uint32_t n,
+                                                       float *__restrict__ out) {
+    __shared__ float red[16];
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    float mx = -INFINITY;
+    for (uint32_t i = t; i < n; i += 1024) mx = fmaxf(mx, in[i]);
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int w = 1; w < 16; w++) mx = fmaxf(mx, red[w]);
+    __syncthreads();
+    float sum = 0.0f;
+    for (uint32_t i = t; i < n; i += 1024) {
+        const float e = expf(in[i] - mx);
+        out[i] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    sum = red[0];
+    for (int w = 1; w < 16; w++) sum += red[w];
+    // each thread divides the values it wrote
+    for (uint32_t i = t; i < n; i += 1024) out[i] = out[i] / sum;
+}
+
+hipError_t launch_softmax(hipStream_t s, const float *in, uint32_t n, float *out) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(1024), 0, s, in, n, out);
+    return hipGetLastError();
+}
+
+// NeoX rotary embedding in place (src/cpu.rs:151-193,
+// metal/kernels.metal:74-94): for head h and pair p < rotated_pairs,
+// (x[p], x[p + hd/2]) of the head turns by
+// angle = position * theta^(-2p / hd); the division, powf, the product,
+// sinf, cosf, the four products and the two sums each round once, in the
+// CPU's order (no contraction).
+__global__ void rope_neox_kernel(float *__restrict__ v, size_t heads, uint32_t head_dim, uint32_t pairs,
+                                 uint32_t position, float theta) {
+    const size_t total = heads * pairs;
+    const uint32_t half = head_dim / 2;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const size_t head = idx / pairs;
+        const uint32_t pair = (uint32_t)(idx - head * pairs);
+        const float exponent = -(float)(2 * pair) / (float)head_dim;
+        const float angle = (float)position * powf(theta, exponent);
+        const float sine = sinf(angle), cosine = cosf(angle);
+        float *x = v + head * head_dim;
+        const float first = x[pair], second = x[half + pair];
+        x[pair] = first * cosine - second * sine;
+        x[half + pair] = first * sine + second * cosine;
+    }
+}
+
+hipError_t launch_rope_neox(hipStream_t s, float *v, size_t heads, uint32_t head_dim, uint32_t pairs,
+                            uint32_t position, float theta) {
+    size_t blocks = (heads * pairs + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_neox_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, v, heads, head_dim, pairs,
+                       position, theta);
+    return hipGetLastError();
+}
+
 hipError_t launch_moe_combine(hipStream_t s, const float *expert_out, const float *p, uint32_t batch,
                               uint32_t k, uint32_t hidden, float *y) {
     size_t total = (size_t)batch * hidden;

@@ -295,6 +295,45 @@ static bool all_finite(const float *v, size_t n) {
     return true;
 }
 
+// MetalError::VectorLength (src/metal.rs:29-34).
+static int fail_vector_lengths(size_t left, size_t right, size_t output) {
+    fail(DMHIP_ERR_VECTOR_LENGTH, "HIP vector lengths differ: left=%zu, right=%zu, output=%zu", left, right,
+         output);
+    g_last_detail.left = left;
+    g_last_detail.right = right;
+    g_last_detail.output = output;
+    return DMHIP_ERR_VECTOR_LENGTH;
+}
+
+// rope_neox_in_place's checks in src/metal.rs:487-509's order, up to the
+// no-op case: *noop is set when there is nothing to rotate.
+static int check_rope(size_t values_len, size_t heads, size_t head_dimension, size_t rotated_pairs,
+                      size_t position, float theta, bool *noop) {
+    size_t length = 0;
+    if (__builtin_mul_overflow(heads, head_dimension, &length) || length != values_len) {
+        fail(DMHIP_ERR_INVALID_ROPE_SHAPE,
+             "NeoX RoPE input length %zu does not match %zu heads of dimension %zu", values_len, heads,
+             head_dimension);
+        g_last_detail.length = values_len;
+        g_last_detail.heads = heads;
+        g_last_detail.head_dimension = head_dimension;
+        return DMHIP_ERR_INVALID_ROPE_SHAPE;
+    }
+    if (head_dimension % 2 != 0 || rotated_pairs > head_dimension / 2)
+        return fail(DMHIP_ERR_INVALID_ROPE_PAIRS,
+                    "NeoX RoPE requires an even head dimension and at most half its dimensions as pairs");
+    if (const int e = require_positive("NeoX RoPE theta", theta); e != DMHIP_OK) return e;
+    *noop = rotated_pairs == 0 || heads == 0;
+    if (*noop) return DMHIP_OK;
+    size_t pairs = 0;
+    if (__builtin_mul_overflow(heads, rotated_pairs, &pairs))
+        return fail(DMHIP_ERR_VECTOR_TOO_LARGE, "HIP vector length exceeds the 32-bit kernel limit");
+    if (const int e = count_u32(head_dimension); e != DMHIP_OK) return e;
+    if (const int e = count_u32(rotated_pairs); e != DMHIP_OK) return e;
+    if (const int e = count_u32(position); e != DMHIP_OK) return e;
+    return DMHIP_OK;
+}
+
 }  // namespace dm
 
 using namespace dm;
@@ -622,6 +661,89 @@ int dmhip_softcap(dmhip_ctx *ctx, const float *input, size_t input_len, float ca
     return DMHIP_OK;
 }
 
+int dmhip_add(dmhip_ctx *ctx, const float *left, size_t left_len, const float *right, size_t right_len,
+              float *output, size_t output_len) {
+    DM_REQUIRE(ctx);
+    if (left_len != right_len || left_len != output_len) return fail_vector_lengths(left_len, right_len, output_len);
+    if (left_len == 0) return DMHIP_OK;
+    DM_CHECK(count_u32(left_len));
+    DM_REQUIRE(left);
+    DM_REQUIRE(right);
+    DM_REQUIRE(output);
+    DM_CHECK(set_device(ctx));
+    size_t bytes = left_len * sizeof(float);
+    DM_CHECK(ctx->in.ensure(2 * bytes));
+    DM_CHECK(ctx->out.ensure(bytes));
+    float *da = (float *)ctx->in.ptr, *db = da + left_len;
+    DM_HIP(hipMemcpyAsync(da, left, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(hipMemcpyAsync(db, right, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(launch_add(ctx->stream, da, db, left_len, (float *)ctx->out.ptr));
+    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_gelu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const float *up, size_t up_len,
+                   float *output, size_t output_len) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(require_nonempty("GELU multiply", gate_len));
+    DM_CHECK(validate_vector_length("GELU multiply", "up", gate_len, up_len));
+    DM_CHECK(validate_vector_length("GELU multiply", "output", gate_len, output_len));
+    DM_CHECK(count_u32(gate_len));
+    DM_REQUIRE(gate);
+    DM_REQUIRE(up);
+    DM_REQUIRE(output);
+    DM_CHECK(set_device(ctx));
+    size_t bytes = gate_len * sizeof(float);
+    DM_CHECK(ctx->in.ensure(2 * bytes));
+    DM_CHECK(ctx->out.ensure(bytes));
+    float *dg = (float *)ctx->in.ptr, *du = dg + gate_len;
+    DM_HIP(hipMemcpyAsync(dg, gate, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(hipMemcpyAsync(du, up, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(launch_gelu_mul(ctx->stream, dg, du, gate_len, (float *)ctx->out.ptr));
+    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_softmax(dmhip_ctx *ctx, const float *input, size_t input_len, float *output, size_t output_len) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(require_nonempty("softmax", input_len));
+    DM_CHECK(validate_vector_length("softmax", "output", input_len, output_len));
+    DM_REQUIRE(input);
+    DM_REQUIRE(output);
+    if (!all_finite(input, input_len)) return fail_non_finite("softmax");
+    DM_CHECK(count_u32(input_len));
+    DM_CHECK(set_device(ctx));
+    size_t bytes = input_len * sizeof(float);
+    DM_CHECK(ctx->in.ensure(bytes));
+    DM_CHECK(ctx->out.ensure(bytes));
+    DM_HIP(hipMemcpyAsync(ctx->in.ptr, input, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(launch_softmax(ctx->stream, (const float *)ctx->in.ptr, (uint32_t)input_len, (float *)ctx->out.ptr));
+    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
+int dmhip_rope_neox_in_place(dmhip_ctx *ctx, float *values, size_t values_len, size_t heads,
+                             size_t head_dimension, size_t rotated_pairs, size_t position, float theta) {
+    DM_REQUIRE(ctx);
+    bool noop = false;
+    DM_CHECK(check_rope(values_len, heads, head_dimension, rotated_pairs, position, theta, &noop));
+    if (noop) return DMHIP_OK;
+    DM_REQUIRE(values);
+    DM_CHECK(set_device(ctx));
+    size_t bytes = values_len * sizeof(float);
+    DM_CHECK(ctx->in.ensure(bytes));
+    float *dv = (float *)ctx->in.ptr;
+    DM_HIP(hipMemcpyAsync(dv, values, bytes, hipMemcpyHostToDevice, ctx->stream));
+    DM_HIP(launch_rope_neox(ctx->stream, dv, heads, (uint32_t)head_dimension, (uint32_t)rotated_pairs,
+                            (uint32_t)position, theta));
+    DM_HIP(hipMemcpyAsync(values, dv, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    return DMHIP_OK;
+}
+
 int dmhip_argmax(dmhip_ctx *ctx, const float *input, size_t input_len, size_t *index) {
     DM_REQUIRE(ctx);
     DM_REQUIRE(index);
@@ -893,6 +1015,43 @@ int dmhip_softcap_device(dmhip_ctx *ctx, size_t count, const float *input, float
     DM_REQUIRE(output);
     DM_CHECK(set_device(ctx));
     DM_HIP(launch_softcap(ctx->stream, input, count, cap, output));
+    return DMHIP_OK;
+}
+
+int dmhip_add_device(dmhip_ctx *ctx, size_t count, const float *left, const float *right, float *output) {
+    DM_REQUIRE(ctx);
+    if (count == 0) return DMHIP_OK;
+    DM_CHECK(count_u32(count));
+    DM_REQUIRE(left);
+    DM_REQUIRE(right);
+    DM_REQUIRE(output);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_add(ctx->stream, left, right, count, output));
+    return DMHIP_OK;
+}
+
+int dmhip_gelu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const float *up, float *output) {
+    DM_REQUIRE(ctx);
+    DM_CHECK(require_nonempty("GELU multiply", count));
+    DM_CHECK(count_u32(count));
+    DM_REQUIRE(gate);
+    DM_REQUIRE(up);
+    DM_REQUIRE(output);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_gelu_mul(ctx->stream, gate, up, count, output));
+    return DMHIP_OK;
+}
+
+int dmhip_rope_neox_device(dmhip_ctx *ctx, float *values, size_t values_len, size_t heads,
+                           size_t head_dimension, size_t rotated_pairs, size_t position, float theta) {
+    DM_REQUIRE(ctx);
+    bool noop = false;
+    DM_CHECK(check_rope(values_len, heads, head_dimension, rotated_pairs, position, theta, &noop));
+    if (noop) return DMHIP_OK;
+    DM_REQUIRE(values);
+    DM_CHECK(set_device(ctx));
+    DM_HIP(launch_rope_neox(ctx->stream, values, heads, (uint32_t)head_dimension, (uint32_t)rotated_pairs,
+                            (uint32_t)position, theta));
     return DMHIP_OK;
 }
 

@@ -28,6 +28,7 @@ VARIANTS = {
     16: "MappedRange", 17: "Command", 18: "NoSlots", 19: "InvalidLayer", 20: "InvalidExpert",
     21: "AllSlotsPinned", 22: "Cancelled", 23: "InvalidLayout", 24: "InvalidArgument", 25: "Io",
     26: "InvalidAttentionShape", 27: "KvPosition", 28: "KvWidth", 29: "KvContext",
+    30: "InvalidRopeShape", 31: "InvalidRopePairs",
 }
 
 # Every function include/dmhip.h declares (checked against the header by tests).
@@ -55,6 +56,8 @@ EXPORTED_SYMBOLS = [
     "dmhip_append_kv_device", "dmhip_attention_cached", "dmhip_attention_cached_device",
     "dmhip_attention_result", "dmhip_attention",
     "dmhip_matvec_safetensor_mapped", "dmhip_matvec_safetensor", "dmhip_matvec_safetensor_device",
+    "dmhip_add", "dmhip_gelu_mul", "dmhip_softmax", "dmhip_rope_neox_in_place", "dmhip_add_device",
+    "dmhip_gelu_mul_device", "dmhip_rope_neox_device",
 ]
 
 F32, F16, Q5_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 6, 8, 12, 14, 30
@@ -100,7 +103,7 @@ class _Detail(ctypes.Structure):
                [(n, ctypes.c_uint64) for n in ("expected", "actual", "offset", "end", "length", "left", "right",
                                                "output", "elements", "block_elements", "k", "bytes", "layer",
                                                "expert", "count", "position", "limit")] + \
-               [("reason", ctypes.c_char_p)]
+               [("reason", ctypes.c_char_p), ("heads", ctypes.c_uint64), ("head_dimension", ctypes.c_uint64)]
 
     # the fields each variant carries (include/dmhip.h)
     FIELDS = {
@@ -110,6 +113,7 @@ class _Detail(ctypes.Structure):
         14: ("expected", "actual"), 15: ("k", "length"), 16: ("offset", "end", "length"), 19: ("layer", "count"),
         20: ("layer", "expert", "count"), 21: ("layer",), 25: ("os_error",), 26: ("reason",),
         27: ("expected", "actual"), 28: ("expected", "actual"), 29: ("position", "limit"),
+        30: ("length", "heads", "head_dimension"),
     }
 
     def as_dict(self) -> dict:
@@ -156,6 +160,10 @@ def load_library() -> ctypes.CDLL:
         "dmhip_rms_norm": ([_vp, _f32p, _sz, _f32p, _sz, ctypes.c_float, _f32p, _sz], ctypes.c_int),
         "dmhip_silu_mul": ([_vp, _f32p, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
         "dmhip_softcap": ([_vp, _f32p, _sz, ctypes.c_float, _f32p, _sz], ctypes.c_int),
+        "dmhip_add": ([_vp, _f32p, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_gelu_mul": ([_vp, _f32p, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_softmax": ([_vp, _f32p, _sz, _f32p, _sz], ctypes.c_int),
+        "dmhip_rope_neox_in_place": ([_vp, _f32p, _sz, _sz, _sz, _sz, _sz, ctypes.c_float], ctypes.c_int),
         "dmhip_argmax": ([_vp, _f32p, _sz, _szp], ctypes.c_int),
         "dmhip_top_k_softmax": ([_vp, _f32p, _sz, _sz, _szp, _f32p], ctypes.c_int),
         "dmhip_matvec": ([_vp, _u32, _sz, _sz, _u8p, _sz, _f32p, _sz, _f32p, _sz], ctypes.c_int),
@@ -170,6 +178,9 @@ def load_library() -> ctypes.CDLL:
         "dmhip_rms_norm_device": ([_vp, _sz, _sz, _vp, _vp, ctypes.c_float, _vp], ctypes.c_int),
         "dmhip_silu_mul_device": ([_vp, _sz, _vp, _vp, _vp], ctypes.c_int),
         "dmhip_softcap_device": ([_vp, _sz, _vp, ctypes.c_float, _vp], ctypes.c_int),
+        "dmhip_add_device": ([_vp, _sz, _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_gelu_mul_device": ([_vp, _sz, _vp, _vp, _vp], ctypes.c_int),
+        "dmhip_rope_neox_device": ([_vp, _vp, _sz, _sz, _sz, _sz, _sz, ctypes.c_float], ctypes.c_int),
         "dmhip_ffn_workspace_bytes": ([_sz, _sz, _sz], _sz),
         "dmhip_ffn_device": ([_vp, _sz, _sz, _sz, _u32, _vp, _u32, _vp, _u32, _vp, ctypes.c_float,
                               _vp, _vp, _vp, _sz], ctypes.c_int),
@@ -406,6 +417,29 @@ class HipContext:
         x = _f32(input)
         _check(load_library().dmhip_softcap(self._h, _fp(x), x.size, cap, _fp(output), output.size))
 
+    def add(self, left, right, output: np.ndarray) -> None:
+        """MetalContext::add (src/metal.rs:404-432)."""
+        a, b = _f32(left), _f32(right)
+        _check(load_library().dmhip_add(self._h, _fp(a), a.size, _fp(b), b.size, _fp(output), output.size))
+
+    def gelu_mul(self, gate, up, output: np.ndarray) -> None:
+        """MetalContext::gelu_mul (src/metal.rs:530-552)."""
+        g, u = _f32(gate), _f32(up)
+        _check(load_library().dmhip_gelu_mul(self._h, _fp(g), g.size, _fp(u), u.size, _fp(output), output.size))
+
+    def softmax(self, input, output: np.ndarray) -> None:
+        """MetalContext::softmax (src/metal.rs:578-598)."""
+        x = _f32(input)
+        _check(load_library().dmhip_softmax(self._h, _fp(x), x.size, _fp(output), output.size))
+
+    def rope_neox_in_place(self, values: np.ndarray, heads: int, head_dimension: int, rotated_pairs: int,
+                           position: int, theta: float) -> None:
+        """MetalContext::rope_neox_in_place (src/metal.rs:478-528): `values`
+        (float32, contiguous) is rotated in place."""
+        assert values.dtype == np.float32 and values.flags.c_contiguous
+        _check(load_library().dmhip_rope_neox_in_place(self._h, _fp(values), values.size, heads, head_dimension,
+                                                       rotated_pairs, position, theta))
+
     def argmax(self, input) -> int:
         x = _f32(input)
         idx = ctypes.c_size_t()
@@ -472,6 +506,16 @@ class HipContext:
 
     def softcap_device(self, count, in_ptr, cap, out_ptr) -> None:
         _check(load_library().dmhip_softcap_device(self._h, count, in_ptr, cap, out_ptr))
+
+    def add_device(self, count, a_ptr, b_ptr, out_ptr) -> None:
+        _check(load_library().dmhip_add_device(self._h, count, a_ptr, b_ptr, out_ptr))
+
+    def gelu_mul_device(self, count, g_ptr, u_ptr, out_ptr) -> None:
+        _check(load_library().dmhip_gelu_mul_device(self._h, count, g_ptr, u_ptr, out_ptr))
+
+    def rope_neox_device(self, v_ptr, values_len, heads, head_dimension, rotated_pairs, position, theta) -> None:
+        _check(load_library().dmhip_rope_neox_device(self._h, v_ptr, values_len, heads, head_dimension,
+                                                     rotated_pairs, position, theta))
 
     def ffn_workspace_bytes(self, batch, hidden, ffn) -> int:
         return int(load_library().dmhip_ffn_workspace_bytes(batch, hidden, ffn))

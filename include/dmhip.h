@@ -7,8 +7,9 @@
  * its expert residency (src/expert.rs) for the operators on the quantized
  * path.  A Rust `hip` module binds these symbols 1:1 (an `extern "C"` block
  * over this header) so the graph code keeps calling `matvec_mapped`,
- * `matvec_owned`, `argmax`, `top_k_softmax`, `rms_norm`, `silu_mul` and
- * `ExpertCache::with_expert` by name.
+ * `matvec_owned`, `argmax`, `top_k_softmax`, `rms_norm`, `silu_mul`, `add`,
+ * `gelu_mul`, `softmax`, `rope_neox_in_place`, the attention and KV-cache
+ * methods and `ExpertCache::with_expert` by name.
  *
  * Conventions (kept from src/metal.rs):
  *  - Every entry point validates its arguments before any device work and
@@ -68,7 +69,9 @@ typedef enum dmhip_status {
     DMHIP_ERR_INVALID_ATTENTION_SHAPE = 26, /* MetalError::InvalidAttentionShape */
     DMHIP_ERR_KV_POSITION = 27,          /* MetalError::KvPosition */
     DMHIP_ERR_KV_WIDTH = 28,             /* MetalError::KvWidth */
-    DMHIP_ERR_KV_CONTEXT = 29            /* MetalError::KvContext */
+    DMHIP_ERR_KV_CONTEXT = 29,           /* MetalError::KvContext */
+    DMHIP_ERR_INVALID_ROPE_SHAPE = 30,   /* MetalError::InvalidRopeShape */
+    DMHIP_ERR_INVALID_ROPE_PAIRS = 31    /* MetalError::InvalidRopePairs */
 } dmhip_status;
 
 /* The payload of the calling thread's last failure: the fields of the
@@ -96,6 +99,7 @@ typedef enum dmhip_status {
      InvalidAttentionShape       reason (the reference's static message)
      KvPosition, KvWidth         expected, actual
      KvContext                   position, limit
+     InvalidRopeShape            length, heads, head_dimension
      Command, InvalidLayout      the message (dmhip_last_error) */
 typedef struct dmhip_error_detail {
     int32_t status;
@@ -112,6 +116,7 @@ typedef struct dmhip_error_detail {
     uint64_t layer, expert, count;
     uint64_t position, limit;
     const char *reason;
+    uint64_t heads, head_dimension;
 } dmhip_error_detail;
 
 /* ggml tensor type ids accepted by the matvec entry points. */
@@ -202,6 +207,33 @@ int dmhip_silu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const flo
 int dmhip_softcap(dmhip_ctx *ctx, const float *input, size_t input_len, float cap, float *output,
                   size_t output_len);
 
+/* MetalContext::add (src/metal.rs:404-432): output = left + right.  The
+   three lengths must agree (VectorLength); empty vectors are a no-op. */
+int dmhip_add(dmhip_ctx *ctx, const float *left, size_t left_len, const float *right, size_t right_len,
+              float *output, size_t output_len);
+
+/* MetalContext::gelu_mul (src/metal.rs:530-552): output =
+   gelu_tanh(gate) * up with Gemma 4's gelu_pytorch_tanh (src/cpu.rs:144-149).
+   Checks: EmptyInput, InvalidVectorLength (up, then output). */
+int dmhip_gelu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const float *up, size_t up_len,
+                   float *output, size_t output_len);
+
+/* MetalContext::softmax (src/metal.rs:578-598): the stable softmax of
+   src/cpu.rs:196-225.  Checks: EmptyInput, InvalidVectorLength (output),
+   NonFinite "softmax" for any non-finite input. */
+int dmhip_softmax(dmhip_ctx *ctx, const float *input, size_t input_len, float *output, size_t output_len);
+
+/* MetalContext::rope_neox_in_place (src/metal.rs:478-528): NeoX rotary
+   embedding of `heads` contiguous heads of `head_dimension` values; pair p <
+   rotated_pairs of each head, (x[p], x[p + head_dimension / 2]), turns by
+   position * theta^(-2p / head_dimension) (src/cpu.rs:151-193).  Checks in
+   the reference's order: InvalidRopeShape (heads * head_dimension !=
+   values_len), InvalidRopePairs (odd head_dimension or rotated_pairs >
+   head_dimension / 2), InvalidPositiveParameter "NeoX RoPE theta"; no
+   rotated pairs or no heads is a no-op; then VectorTooLarge. */
+int dmhip_rope_neox_in_place(dmhip_ctx *ctx, float *values, size_t values_len, size_t heads,
+                             size_t head_dimension, size_t rotated_pairs, size_t position, float theta);
+
 /* MetalContext::argmax (src/metal.rs:624-644): first maximum, lowest index on
    ties, non-finite input rejected. */
 int dmhip_argmax(dmhip_ctx *ctx, const float *input, size_t input_len, size_t *index);
@@ -274,6 +306,19 @@ int dmhip_silu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const
 /* Logit softcap over `count` device values (src/cpu.rs:263-273), as
    dmhip_softcap; input and output may be the same buffer. */
 int dmhip_softcap_device(dmhip_ctx *ctx, size_t count, const float *input, float cap, float *output);
+
+/* output = left + right over `count` device values, as dmhip_add; output may
+   be either input. */
+int dmhip_add_device(dmhip_ctx *ctx, size_t count, const float *left, const float *right, float *output);
+
+/* output = gelu_tanh(gate) * up over `count` device values, as
+   dmhip_gelu_mul. */
+int dmhip_gelu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const float *up, float *output);
+
+/* NeoX RoPE in place over device values, with dmhip_rope_neox_in_place's
+   checks (values_len is the number of floats at `values`). */
+int dmhip_rope_neox_device(dmhip_ctx *ctx, float *values, size_t values_len, size_t heads,
+                           size_t head_dimension, size_t rotated_pairs, size_t position, float theta);
 
 /* Dense gated FFN at decode for `batch` tokens (src/qwen35/cpu.rs:415-427):
    y = down(silu(gate(n)) * up(n)) with n = rms_norm(h, eps), unit weight.

@@ -30,6 +30,8 @@ INVALID_LAYER = 12
 INVALID_EXPERT = 13
 ALL_SLOTS_PINNED = 14
 NO_SLOTS = 15
+INVALID_ROPE_SHAPE = 16
+INVALID_ROPE_PAIRS = 17
 
 
 class OracleError(RuntimeError):
@@ -81,6 +83,11 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_rms_norm.argtypes = [_f32p, _sz, _f32p, _sz, ctypes.c_float, _f32p, _sz]
     l.orc_silu.argtypes = [ctypes.c_float]
     l.orc_softcap_in_place.argtypes = [_f32p, _sz, ctypes.c_float]
+    l.orc_gelu_tanh.argtypes = [ctypes.c_float]
+    l.orc_gelu_tanh.restype = ctypes.c_float
+    l.orc_gelu_mul.argtypes = [_f32p, _f32p, _sz, _f32p]
+    l.orc_gelu_mul.restype = None
+    l.orc_rope_neox_in_place.argtypes = [_f32p, _sz, _sz, _sz, _sz, _sz, ctypes.c_float]
     l.orc_softcap_in_place.restype = ctypes.c_int
     l.orc_silu.restype = ctypes.c_float
     l.orc_silu_mul_glm.argtypes = [_f32p, _f32p, _sz, _f32p]
@@ -247,6 +254,33 @@ def softcap(values, cap: float) -> np.ndarray:
 def softcap_status(values, cap: float) -> int:
     out = np.array(values, dtype=np.float32, copy=True).ravel()
     return lib().orc_softcap_in_place(_p(out, _f32p), out.size, cap)
+
+
+def gelu_tanh(value: float) -> float:
+    return float(np.float32(lib().orc_gelu_tanh(value)))
+
+
+def gelu_mul(gate, up) -> np.ndarray:
+    g = _c(gate, np.float32)
+    u = _c(up, np.float32)
+    out = np.zeros_like(g)
+    lib().orc_gelu_mul(_p(g, _f32p), _p(u, _f32p), g.size, _p(out, _f32p))
+    return out
+
+
+def rope_neox_status(values, heads: int, head_dimension: int, rotated_pairs: int, position: int,
+                     theta: float) -> tuple[int, np.ndarray]:
+    v = np.array(values, dtype=np.float32, copy=True).ravel()
+    status = lib().orc_rope_neox_in_place(_p(v, _f32p), v.size, heads, head_dimension, rotated_pairs, position,
+                                          theta)
+    return status, v
+
+
+def rope_neox(values, heads: int, head_dimension: int, rotated_pairs: int, position: int,
+              theta: float) -> np.ndarray:
+    status, v = rope_neox_status(values, heads, head_dimension, rotated_pairs, position, theta)
+    _check(status, "rope_neox")
+    return v
 
 
 def silu_mul_glm(gate, up) -> np.ndarray:

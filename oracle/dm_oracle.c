@@ -460,6 +460,50 @@ int orc_softcap_in_place(float *values, size_t count, float cap)
     return ORC_OK;
 }
 
+/* src/cpu.rs:144-149  Gemma 4's gelu_pytorch_tanh,
+   0.5 v (1 + tanh(0.7978846 (v + 0.044715 v^3))): Rust's powi(3) multiplies
+   (v v) v, f32::tanh is the C library's tanhf, each operation rounds once. */
+float orc_gelu_tanh(float value)
+{
+    float cubic = (value * value) * value;
+    float inner = 0.7978846f * (value + 0.044715f * cubic);
+    return (0.5f * value) * (1.0f + tanhf(inner));
+}
+
+/* gelu_tanh(gate) * up, as the reference's Metal test states the CPU side
+   of MetalContext::gelu_mul (src/metal.rs:2201-2209). */
+void orc_gelu_mul(const float *gate, const float *up, size_t count, float *output)
+{
+    for (size_t i = 0; i < count; i++) output[i] = orc_gelu_tanh(gate[i]) * up[i];
+}
+
+/* src/cpu.rs:151-193  NeoX rotary embedding in place: for each head and
+   pair p < rotated_pairs, angle = position * powf(theta, -(2p) / hd) (f32
+   division, powf, product), (sin, cos) = (sinf, cosf)(angle) (Rust's
+   f32::sin_cos), then first' = first cos - second sin, second' = first sin +
+   second cos, no fused operations. */
+int orc_rope_neox_in_place(float *values, size_t count, size_t heads, size_t head_dimension,
+                           size_t rotated_pairs, size_t position, float theta)
+{
+    size_t length;
+    if (__builtin_mul_overflow(heads, head_dimension, &length) || length != count) return ORC_INVALID_ROPE_SHAPE;
+    if (head_dimension % 2 != 0 || rotated_pairs > head_dimension / 2) return ORC_INVALID_ROPE_PAIRS;
+    if (!isfinite(theta) || theta <= 0.0f) return ORC_INVALID_POSITIVE_PARAMETER;
+    size_t half = head_dimension / 2;
+    for (size_t h = 0; h < heads; h++) {
+        float *head = values + h * head_dimension;
+        for (size_t pair = 0; pair < rotated_pairs; pair++) {
+            float exponent = -(float)(2 * pair) / (float)head_dimension;
+            float angle = (float)position * powf(theta, exponent);
+            float sine = sinf(angle), cosine = cosf(angle);
+            float first = head[pair], second = head[half + pair];
+            head[pair] = first * cosine - second * sine;
+            head[half + pair] = first * sine + second * cosine;
+        }
+    }
+    return ORC_OK;
+}
+
 /* src/glm52/expert.rs:260-267  (gate / (1 + exp(-gate))) * up */
 void orc_silu_mul_glm(const float *gate, const float *up, size_t count, float *output)
 {

@@ -64,7 +64,9 @@ enum {
     ORC_INVALID_LAYER = 12,
     ORC_INVALID_EXPERT = 13,
     ORC_ALL_SLOTS_PINNED = 14,
-    ORC_NO_SLOTS = 15
+    ORC_NO_SLOTS = 15,
+    ORC_INVALID_ROPE_SHAPE = 16,
+    ORC_INVALID_ROPE_PAIRS = 17
 };
 
 /* ggml type ids, src/gguf.rs:295-318. */
@@ -98,6 +100,10 @@ float orc_silu(float value);
 /* src/cpu.rs:263-273: values[i] = cap * tanh(values[i] / cap) in place;
    InvalidPositiveParameter unless cap is finite and > 0. */
 int orc_softcap_in_place(float *values, size_t count, float cap);
+float orc_gelu_tanh(float value);
+void orc_gelu_mul(const float *gate, const float *up, size_t count, float *output);
+int orc_rope_neox_in_place(float *values, size_t count, size_t heads, size_t head_dimension,
+                           size_t rotated_pairs, size_t position, float theta);
 void orc_silu_mul_glm(const float *gate, const float *up, size_t count, float *output);
 
 int orc_dense_ffn(size_t batch, size_t hidden, size_t ffn, uint32_t gate_type,

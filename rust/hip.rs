@@ -91,6 +91,8 @@ pub mod ffi {
     pub const DMHIP_ERR_KV_POSITION: c_int = 27;
     pub const DMHIP_ERR_KV_WIDTH: c_int = 28;
     pub const DMHIP_ERR_KV_CONTEXT: c_int = 29;
+    pub const DMHIP_ERR_INVALID_ROPE_SHAPE: c_int = 30;
+    pub const DMHIP_ERR_INVALID_ROPE_PAIRS: c_int = 31;
 
     #[repr(C)]
     #[derive(Clone, Copy)]
@@ -118,6 +120,8 @@ pub mod ffi {
         pub position: u64,
         pub limit: u64,
         pub reason: *const c_char,
+        pub heads: u64,
+        pub head_dimension: u64,
     }
 
     impl dmhip_error_detail {
@@ -146,6 +150,8 @@ pub mod ffi {
                 position: 0,
                 limit: 0,
                 reason: std::ptr::null(),
+                heads: 0,
+                head_dimension: 0,
             }
         }
     }
@@ -265,6 +271,65 @@ pub mod ffi {
             cap: f32,
             output: *mut f32,
             output_len: usize,
+        ) -> c_int;
+        pub fn dmhip_add(
+            ctx: *mut dmhip_ctx,
+            left: *const f32,
+            left_len: usize,
+            right: *const f32,
+            right_len: usize,
+            output: *mut f32,
+            output_len: usize,
+        ) -> c_int;
+        pub fn dmhip_gelu_mul(
+            ctx: *mut dmhip_ctx,
+            gate: *const f32,
+            gate_len: usize,
+            up: *const f32,
+            up_len: usize,
+            output: *mut f32,
+            output_len: usize,
+        ) -> c_int;
+        pub fn dmhip_softmax(
+            ctx: *mut dmhip_ctx,
+            input: *const f32,
+            input_len: usize,
+            output: *mut f32,
+            output_len: usize,
+        ) -> c_int;
+        pub fn dmhip_rope_neox_in_place(
+            ctx: *mut dmhip_ctx,
+            values: *mut f32,
+            values_len: usize,
+            heads: usize,
+            head_dimension: usize,
+            rotated_pairs: usize,
+            position: usize,
+            theta: f32,
+        ) -> c_int;
+        pub fn dmhip_add_device(
+            ctx: *mut dmhip_ctx,
+            count: usize,
+            left: *const f32,
+            right: *const f32,
+            output: *mut f32,
+        ) -> c_int;
+        pub fn dmhip_gelu_mul_device(
+            ctx: *mut dmhip_ctx,
+            count: usize,
+            gate: *const f32,
+            up: *const f32,
+            output: *mut f32,
+        ) -> c_int;
+        pub fn dmhip_rope_neox_device(
+            ctx: *mut dmhip_ctx,
+            values: *mut f32,
+            values_len: usize,
+            heads: usize,
+            head_dimension: usize,
+            rotated_pairs: usize,
+            position: usize,
+            theta: f32,
         ) -> c_int;
         pub fn dmhip_argmax(ctx: *mut dmhip_ctx, input: *const f32, input_len: usize, index: *mut usize) -> c_int;
         pub fn dmhip_top_k_softmax(
@@ -724,6 +789,12 @@ fn metal_error(code: c_int) -> MetalError {
             position: field(d.position),
             limit: field(d.limit),
         },
+        ffi::DMHIP_ERR_INVALID_ROPE_SHAPE => MetalError::InvalidRopeShape {
+            length: field(d.length),
+            heads: field(d.heads),
+            head_dimension: field(d.head_dimension),
+        },
+        ffi::DMHIP_ERR_INVALID_ROPE_PAIRS => MetalError::InvalidRopePairs,
         // DMHIP_ERR_COMMAND (a HIP runtime error), DMHIP_ERR_INVALID_ARGUMENT
         // (a null handle: unreachable through this module) and an
         // expert-cache status reaching a context method: the message names
@@ -1010,11 +1081,6 @@ impl MetalKvLayer {
         unsafe { ffi::dmhip_kv_layer_truncate(self.raw.as_ptr(), position) }
     }
 }
-
-fn not_provided(operation: &str) -> MetalError {
-    MetalError::Command(format!("{operation} is not provided by the HIP backend"))
-}
-
 impl MetalContext {
     /// MetalContext::new (src/metal.rs:291-346) on HIP device 0 (the first
     /// device HIP_VISIBLE_DEVICES leaves visible). No device: NoDevice.
@@ -1246,33 +1312,70 @@ impl MetalContext {
         })
     }
 
-    // The rest of the MetalContext surface (add, RoPE, gelu_mul, softmax) is
-    // outside the library. These methods keep the graphs compiling and fail
-    // with a Command error naming the operation; the Qwen3.5 graph
-    // (src/qwen35/metal.rs) calls none of them.
-
-    pub fn add(&self, _left: &[f32], _right: &[f32], _output: &mut [f32]) -> Result<(), MetalError> {
-        Err(not_provided("add"))
+    /// MetalContext::add (src/metal.rs:404-432).
+    pub fn add(&self, left: &[f32], right: &[f32], output: &mut [f32]) -> Result<(), MetalError> {
+        // SAFETY: the slices are valid for their lengths for the call; the
+        // library checks the lengths before it touches them.
+        check(unsafe {
+            ffi::dmhip_add(
+                self.raw(),
+                left.as_ptr(),
+                left.len(),
+                right.as_ptr(),
+                right.len(),
+                output.as_mut_ptr(),
+                output.len(),
+            )
+        })
     }
 
+    /// MetalContext::rope_neox_in_place (src/metal.rs:478-528).
     pub fn rope_neox_in_place(
         &self,
-        _values: &mut [f32],
-        _heads: usize,
-        _head_dimension: usize,
-        _rotated_pairs: usize,
-        _position: usize,
-        _theta: f32,
+        values: &mut [f32],
+        heads: usize,
+        head_dimension: usize,
+        rotated_pairs: usize,
+        position: usize,
+        theta: f32,
     ) -> Result<(), MetalError> {
-        Err(not_provided("NeoX RoPE"))
+        // SAFETY: as above.
+        check(unsafe {
+            ffi::dmhip_rope_neox_in_place(
+                self.raw(),
+                values.as_mut_ptr(),
+                values.len(),
+                heads,
+                head_dimension,
+                rotated_pairs,
+                position,
+                theta,
+            )
+        })
     }
 
-    pub fn gelu_mul(&self, _gate: &[f32], _up: &[f32], _output: &mut [f32]) -> Result<(), MetalError> {
-        Err(not_provided("gelu_mul"))
+    /// MetalContext::gelu_mul (src/metal.rs:530-552).
+    pub fn gelu_mul(&self, gate: &[f32], up: &[f32], output: &mut [f32]) -> Result<(), MetalError> {
+        // SAFETY: as above.
+        check(unsafe {
+            ffi::dmhip_gelu_mul(
+                self.raw(),
+                gate.as_ptr(),
+                gate.len(),
+                up.as_ptr(),
+                up.len(),
+                output.as_mut_ptr(),
+                output.len(),
+            )
+        })
     }
 
-    pub fn softmax(&self, _input: &[f32], _output: &mut [f32]) -> Result<(), MetalError> {
-        Err(not_provided("softmax"))
+    /// MetalContext::softmax (src/metal.rs:578-598).
+    pub fn softmax(&self, input: &[f32], output: &mut [f32]) -> Result<(), MetalError> {
+        // SAFETY: as above.
+        check(unsafe {
+            ffi::dmhip_softmax(self.raw(), input.as_ptr(), input.len(), output.as_mut_ptr(), output.len())
+        })
     }
 
     pub fn matvec_safetensor_mapped(

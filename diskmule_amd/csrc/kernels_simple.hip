@@ -145,15 +145,15 @@ __device__ bool block_top_k(const float *logits, uint32_t count, uint32_t k, uin
     __shared__ float values[kMaxTopK];
     uint32_t tid = threadIdx.x, nthreads = blockDim.x;
     uint32_t bad = 0;
-    for (uint32_t i = tid; i < count; i += nthreads)
+    for (size_t i = tid; i < count; i += nthreads)
         if (!__builtin_isfinite(logits[i])) bad = 1;
     if (bad) *non_finite.word = non_finite.mark;  // every writer stores the same value
     const bool row_bad = __syncthreads_or((int)bad) != 0;
     uint64_t previous = ~0ull;
     for (uint32_t s = 0; s < k; s++) {
         uint64_t best = 0;
-        for (uint32_t i = tid; i < count; i += nthreads) {
-            uint64_t key = argmax_key(logits[i], i);
+        for (size_t i = tid; i < count; i += nthreads) {
+            uint64_t key = argmax_key(logits[i], (uint32_t)i);
             if (key < previous && key > best) best = key;
         }
         best = wave_max_u64(best);
@@ -531,7 +531,7 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const float *__restrict__
     const float *row = in + (size_t)blockIdx.x * n;
     float *orow = out + (size_t)blockIdx.x * n;
     float s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) s = __builtin_fmaf(row[i], row[i], s);
+    for (size_t i = threadIdx.x; i < n; i += blockDim.x) s = __builtin_fmaf(row[i], row[i], s);
     s = wave_sum(s);
     if ((threadIdx.x & 63u) == 0) partial[threadIdx.x >> 6] = s;
     __syncthreads();
@@ -539,7 +539,7 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const float *__restrict__
     for (uint32_t w = 0; w < blockDim.x / 64; w++) total += partial[w];
     // (sum / n + eps).sqrt().recip(): two correctly rounded steps.
     float inverse_rms = 1.0f / __builtin_sqrtf(total / (float)n + eps);
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
+    for (size_t i = threadIdx.x; i < n; i += blockDim.x)
         orow[i] = weight ? row[i] * weight[i] * inverse_rms : row[i] * inverse_rms;
 }
 
@@ -765,7 +765,8 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
 }
 
 __global__ void fill_u32_kernel(uint32_t *p, uint32_t n, uint32_t value) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = value;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = value;
 }
 
 hipError_t launch_fill_u32(hipStream_t s, uint32_t *p, uint32_t n, uint32_t value) {
@@ -855,7 +856,7 @@ __global__ void __launch_bounds__(1024) softmax_kernel(const float *__restrict__
     __shared__ float red[16];
     const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
     float mx = -INFINITY;
-    for (uint32_t i = t; i < n; i += 1024) mx = fmaxf(mx, in[i]);
+    for (size_t i = t; i < n; i += 1024) mx = fmaxf(mx, in[i]);
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
@@ -863,7 +864,7 @@ __global__ void __launch_bounds__(1024) softmax_kernel(const float *__restrict__
     for (int w = 1; w < 16; w++) mx = fmaxf(mx, red[w]);
     __syncthreads();
     float sum = 0.0f;
-    for (uint32_t i = t; i < n; i += 1024) {
+    for (size_t i = t; i < n; i += 1024) {
         const float e = expf(in[i] - mx);
         out[i] = e;
         sum += e;
@@ -874,7 +875,7 @@ __global__ void __launch_bounds__(1024) softmax_kernel(const float *__restrict__
     sum = red[0];
     for (int w = 1; w < 16; w++) sum += red[w];
     // each thread divides the values it wrote
-    for (uint32_t i = t; i < n; i += 1024) out[i] = out[i] / sum;
+    for (size_t i = t; i < n; i += 1024) out[i] = out[i] / sum;
 }
 
 hipError_t launch_softmax(hipStream_t s, const float *in, uint32_t n, float *out) {

@@ -801,7 +801,9 @@ int dmhip_attention_cached_device(dmhip_ctx *ctx, const float *query_device, siz
     const size_t start = layer->position - visible;
     DM_CHECK_STATUS(check_kernel_limits(query_heads, kv_heads, head_dimension, visible));
     DM_CHECK_STATUS(set_device(ctx));
-    const uint32_t mark = next_mark(ctx);
+    // the device calls between two results share one mark, so the result
+    // reports a non-finite score in any of them
+    const uint32_t mark = ctx->attn_pending ? ctx->attn_mark : next_mark(ctx);
     DM_CHECK_STATUS(enqueue_attention(ctx, query_device, layer->keys, layer->values, layer->capacity,
                                       layer->width, query_heads, kv_heads, head_dimension, start, visible,
                                       output_device, BadFlag{ctx->flags + kAttnFlagWord, mark}));

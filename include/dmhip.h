@@ -525,9 +525,10 @@ int dmhip_attention_cached(dmhip_ctx *ctx, const float *query, size_t query_len,
 int dmhip_attention_cached_device(dmhip_ctx *ctx, const float *query_device, size_t query_len,
                                   const dmhip_kv_layer *layer, size_t query_heads, size_t kv_heads,
                                   size_t head_dimension, float *output_device, size_t output_len);
-/* Waits for the last dmhip_attention_cached_device and returns NonFinite
-   "softmax" when its scores held a non-finite value (its output is then not
-   meaningful). */
+/* Waits for the dmhip_attention_cached_device calls made since the previous
+   result (or since a host-slice attention call, which ends that period) and
+   returns NonFinite "softmax" when any of them met a non-finite score (its
+   output is then not meaningful). */
 int dmhip_attention_result(dmhip_ctx *ctx);
 
 /* MetalContext::attention (src/metal.rs:1325-1385): keys and values are host

@@ -233,7 +233,15 @@ def test_non_finite_scores_are_rejected(ctx):
     expect_error("NonFinite", ctx.attention_result)
     with pytest.raises(HipError):
         ctx.attention_result()  # nothing pending
-    for b in (qb, ob, layer):
+    # one result covers every device call since the previous one: a NaN in
+    # the first of two calls is still reported after a clean second call
+    good = ctx.device_array(np.array([1.0, 0.0], dtype=np.float32))
+    ctx.attention_cached_device(qb.device_ptr, 2, layer, 1, 1, 2, ob.device_ptr, 2)
+    ctx.attention_cached_device(good.device_ptr, 2, layer, 1, 1, 2, ob.device_ptr, 2)
+    expect_error("NonFinite", ctx.attention_result)
+    ctx.attention_cached_device(good.device_ptr, 2, layer, 1, 1, 2, ob.device_ptr, 2)
+    ctx.attention_result()  # a new period starts clean
+    for b in (qb, ob, good, layer):
         b.free()
 
 

@@ -564,10 +564,9 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     // The previous call has finished (it ends with a synchronisation): the
     // per-token words can be cleared from here.
     memset(sel_bad, 0, 16 * 4);
-    ctx->router_mark = ctx->router_mark + 1 ? ctx->router_mark + 1 : 1;
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs,
-                               BadFlag{ctx->flags, ctx->router_mark}, sel_ids, sel_probs,
+                               BadFlag{ctx->flags + kMoeFlagWord, 1}, sel_ids, sel_probs,
                                batch <= kRouterTickets ? ctx->router_tickets : nullptr, sel_bad));
     DM_HIP(hipStreamSynchronize(ctx->stream));
     // top_k_softmax rejects non-finite logits (src/cpu.rs:240-245); nothing

@@ -93,11 +93,11 @@ struct dmhip_ctx {
     size_t aux_lent_bytes = 0;
     dm::ArgmaxState *argmax_state = nullptr;  // device
     uint32_t *router_tickets = nullptr;       // device, kRouterTickets counters, zero between launches
-    uint32_t router_mark = 0;                 // mark of the last router call (BadFlag), never 0 once set
+    uint32_t router_mark = 0;                 // mark of the pending device router calls (BadFlag), never 0 once set
     uint32_t attn_mark = 0;                   // mark of the last attention call (flags[kAttnFlagWord])
     uint32_t *argmax_ticket = nullptr;        // device, zero between launches: ticket, then (at +8) the best key
     uint32_t *argmax_index = nullptr;         // device
-    uint32_t *flags = nullptr;                // device: [0] router, [2] top-k, [kAttnFlagWord] attention non-finite
+    uint32_t *flags = nullptr;                // device: [0] router, [1] read probe, [2] top-k, [3] MoE router, [4] attention
     bool argmax_pending = false;
     bool router_pending = false;  // a dmhip_router_top_k_device awaits dmhip_router_result
     bool attn_pending = false;    // a dmhip_attention_cached_device awaits dmhip_attention_result
@@ -135,6 +135,9 @@ struct dmhip_buf {
 
 namespace dm {
 constexpr uint32_t kAttnFlagWord = 4;
+// flags word the MoE layer's router writes (a sink: the layer reads its
+// per-token words on the host), apart from the device router's word 0
+constexpr uint32_t kMoeFlagWord = 3;
 // Enqueue y = W x on the context stream, choosing the fastest kernel that
 // takes the shape.  Arguments are already validated.
 int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, const void *w,

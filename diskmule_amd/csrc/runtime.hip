@@ -1074,7 +1074,9 @@ int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_
     if (batch == 0) return DMHIP_OK;
     DM_CHECK(set_device(ctx));
     // A new mark per call: the word needs no clearing launch.
-    ctx->router_mark = ctx->router_mark + 1 ? ctx->router_mark + 1 : 1;
+    // the calls between two results share one mark, so the result reports
+    // a non-finite logit in any of them
+    if (!ctx->router_pending) ctx->router_mark = ctx->router_mark + 1 ? ctx->router_mark + 1 : 1;
     ctx->router_pending = true;
     DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                (uint32_t)k, (uint32_t)batch, x, logits, ids, probabilities,

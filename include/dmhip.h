@@ -355,10 +355,10 @@ int dmhip_ffn_device_noalloc(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t
 int dmhip_router_top_k_device(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t experts,
                               size_t k, const uint16_t *router_bf16, const float *x,
                               float *logits, uint32_t *ids, float *probabilities);
-/* Waits for the last dmhip_router_top_k_device and returns NonFinite when
-   any token's logits held a non-finite value (top_k_softmax rejects them,
-   src/cpu.rs:240-245); the ids and probabilities of such a call are not
-   meaningful. */
+/* Waits for the dmhip_router_top_k_device calls made since the previous
+   result and returns NonFinite when any token's logits in any of them held a
+   non-finite value (top_k_softmax rejects them, src/cpu.rs:240-245); the ids
+   and probabilities of such a call are not meaningful. */
 int dmhip_router_result(dmhip_ctx *ctx);
 
 /* Prefill GEMM: C[m][n] = sum_k A[m][k] * W[n][k], A bf16 [m][k] row-major,

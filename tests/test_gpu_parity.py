@@ -700,8 +700,8 @@ def test_router_top_k_is_bit_exact(ctx, batch, hidden, experts, k):
 
 def test_router_rejects_non_finite_logits(ctx):
     """top_k_softmax rejects non-finite logits (src/cpu.rs:240-245): an Inf in
-    a token makes dmhip_router_result report NonFinite, and the next clean
-    call reports nothing (the flag is cleared per call)."""
+    a token makes dmhip_router_result report NonFinite, the next clean call
+    reports nothing, and a result covers every call since the previous one."""
     batch, hidden, experts, k = 3, 2048, 128, 8
     router = synth.to_bf16_bits(synth.normal(synth.weight_seed(6, 1), experts * hidden) * np.float32(0.02))
     x = synth.normal(synth.activation_seed(6, 1), batch * hidden).reshape(batch, hidden)
@@ -723,6 +723,15 @@ def test_router_rejects_non_finite_logits(ctx):
     for t in range(batch):
         want = capi.top_k_softmax(capi.matvec_bf16(experts, hidden, router, x[t]), k)
         assert ids[t].tolist() == [i for i, _ in want]
+    # one result covers every call since the previous result: the bad call
+    # first, then a clean one, is still reported
+    xbad = dev(ctx, bad)
+    for buf in (xbad, xb):
+        ctx.router_top_k_device(batch, hidden, experts, k, rb.device_ptr, buf.device_ptr, lb.device_ptr,
+                                ib.device_ptr, pb.device_ptr)
+    with pytest.raises(HipError) as e:
+        ctx.router_result()
+    assert e.value.variant == "NonFinite"
 
 
 @pytest.mark.parametrize("experts,hidden", [(128, 2048), (12, 1024), (300, 512)])

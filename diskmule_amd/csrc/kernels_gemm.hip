@@ -613,7 +613,7 @@ gemm_kernel(const half8 *__restrict__ a16, uint32_t a_bytes, const float *__rest
 #pragma unroll
                     for (int e = 0; e < 4; e++) acc[r][t][4 * g + e] *= rs[g][e];
         }
-        // round 1: rows of the other half to region `wave`
+        // first exchange: rows of the other half to region `wave`
 #pragma unroll
         for (uint32_t r = 0; r < kRM; r++) {
             if (r / 2 == keep_half) continue;
@@ -640,7 +640,7 @@ gemm_kernel(const half8 *__restrict__ a16, uint32_t a_bytes, const float *__rest
 #pragma unroll
                     for (int e = 0; e < 4; e++) acc[r][t][4 * g + e] += o[t][g][e];
         }
-        // round 2: the other 32 rows of the kept half to region wave ^ 2
+        // second exchange: the other 32 rows of the kept half to region wave ^ 2
 #pragma unroll
         for (uint32_t r = 0; r < kRM; r++) {
             if (r / 2 != keep_half || r % 2 == keep_quarter) continue;

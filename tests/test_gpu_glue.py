@@ -41,6 +41,21 @@ def test_add_known_answer_and_exactness(ctx):
     assert np.array_equal(out.view(np.uint32), (a + b).view(np.uint32))  # one IEEE rounding each
 
 
+def test_add_device_in_place(ctx):
+    # the device form may write over either input
+    rng = np.random.default_rng(4)
+    a = rng.standard_normal(70_000).astype(np.float32)
+    b = rng.standard_normal(a.size).astype(np.float32)
+    da, db = ctx.device_array(a), ctx.device_array(b)
+    ctx.add_device(a.size, da.device_ptr, db.device_ptr, da.device_ptr)
+    ctx.add_device(a.size, da.device_ptr, db.device_ptr, db.device_ptr)
+    assert np.array_equal(da.read(0, a.nbytes, np.float32), a + b)
+    assert np.array_equal(db.read(0, a.nbytes, np.float32), (a + b) + b)
+    ctx.add_device(0, 0, 0, 0)  # nothing to add
+    for x in (da, db):
+        x.free()
+
+
 def test_add_checks(ctx):
     out = np.zeros(3, np.float32)
     expect_error("VectorLength", ctx.add, [1.0, 2.0], [1.0, 2.0, 3.0], out, left=2, right=3, output=3)

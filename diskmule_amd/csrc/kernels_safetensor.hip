@@ -239,7 +239,9 @@ template <uint32_t FMT>
 hipError_t launch_st_t(hipStream_t s, int cus, const uint8_t *w, uint32_t rows, uint32_t columns, size_t row_bytes,
                        const float *scales, uint32_t scale_columns, uint32_t group, const float *x, float *y) {
     // (4 rows x 4 chunks for rows of at most 4 chunks per lane measured slower:
-    // INT4 12288 x 6144 in 19.3 against 16.5 us, fewer workgroups)
+    // INT4 12288 x 6144 in 19.3 against 16.5 us, fewer workgroups; so did
+    // 3 rows x 8 chunks for every format, e.g. INT4 18.0 against 16.3 us and
+    // F8 18.7 against 17.0 us)
     return launch_st_rc<FMT, 2, 8>(s, cus, w, rows, columns, row_bytes, scales, scale_columns, group, x, y);
 }
 

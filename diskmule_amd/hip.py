@@ -436,7 +436,8 @@ class HipContext:
                            position: int, theta: float) -> None:
         """MetalContext::rope_neox_in_place (src/metal.rs:478-528): `values`
         (float32, contiguous) is rotated in place."""
-        assert values.dtype == np.float32 and values.flags.c_contiguous
+        if not (isinstance(values, np.ndarray) and values.dtype == np.float32 and values.flags.c_contiguous):
+            raise TypeError("rope_neox_in_place rotates a contiguous float32 array in place")
         _check(load_library().dmhip_rope_neox_in_place(self._h, _fp(values), values.size, heads, head_dimension,
                                                        rotated_pairs, position, theta))
 

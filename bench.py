@@ -49,18 +49,15 @@ def log(*a):
 
 
 class Timed:
-    """Wall time on the compute stream (events) and, with kernels=True, the
-    library's per-launch timing of the dominant kernels (an event pair around
-    each of them on the same stream)."""
+    """Wall time of the enclosed work on the compute stream: an event before
+    and after it, nothing else recorded.  Kernel durations come from the
+    rocprofv3 kernel traces in profiles/, not from this program."""
 
-    def __init__(self, ctx, kernels=True):
+    def __init__(self, ctx):
         self.ctx = ctx
-        self.kernels = kernels
 
     def __enter__(self):
         self.ctx.synchronize()
-        self.ctx.kernel_timing_read()  # drop anything recorded before
-        self.ctx.kernel_timing_enable(self.kernels)
         self.start = self.ctx.event_record()
         return self
 
@@ -68,27 +65,16 @@ class Timed:
         stop = self.ctx.event_record()
         self.ctx.synchronize()
         self.wall_ms = self.ctx.event_elapsed_ms(self.start, stop)
-        self.kernel_ms, self.launches = self.ctx.kernel_timing_read()
-        self.ctx.kernel_timing_enable(False)
         self.ctx.event_free(self.start)
         self.ctx.event_free(stop)
 
 
 def timed_loop(ctx, body, steps):
-    """(wall ms, kernel ms, launches) of `steps` calls of body(i).  The wall
-    time comes from a pass with nothing but the work on the stream; the
-    kernel times from a second, identical pass in which the library attaches
-    start/stop events to each dominant kernel's dispatch.  The start event
-    is stamped when the dispatch is processed, before the barrier on the
-    preceding kernel clears, so these durations run a few percent above a
-    kernel trace's."""
-    with Timed(ctx, kernels=False) as wall:
+    """Wall ms on the compute stream of `steps` calls of body(i)."""
+    with Timed(ctx) as wall:
         for i in range(steps):
             body(i)
-    with Timed(ctx) as kern:
-        for i in range(steps):
-            body(i)
-    return wall.wall_ms, kern.kernel_ms, kern.launches
+    return wall.wall_ms
 
 
 def upload(ctx, arr):
@@ -110,7 +96,7 @@ def bench_c2(ctx, synth, steps, warmup):
     # The box slows by several percent within milliseconds of sustained load:
     # each timed pass starts after the same short idle period.
     time.sleep(0.2)
-    with Timed(ctx, kernels=False) as t:
+    with Timed(ctx) as t:
         for _ in range(steps):
             ctx.matvec_argmax_device(Q6_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr, ib.device_ptr)
     ms = t.wall_ms / steps
@@ -122,7 +108,7 @@ def bench_c2(ctx, synth, steps, warmup):
     ctx.matvec_device(Q6_K, rows, cols, wb.device_ptr, 1, xb.device_ptr, yb.device_ptr)
     ctx.synchronize()
     time.sleep(0.2)
-    with Timed(ctx, kernels=False) as k:
+    with Timed(ctx) as k:
         for _ in range(steps):
             ctx.matvec_device(Q6_K, rows, cols, wb.device_ptr, 1, xb.device_ptr, yb.device_ptr)
     kms = k.wall_ms / steps
@@ -153,13 +139,12 @@ def bench_c1(ctx, synth, steps, warmup):
             ctx.matvec_device(Q4_K, rows, cols, bufs[i % len(bufs)].device_ptr, 1, xb.device_ptr, yb.device_ptr)
         # one GEMV launch per step, back to back: the region time per launch
         # is the kernel's average launch duration
-        with Timed(ctx, kernels=False) as t:
+        with Timed(ctx) as t:
             for i in range(n):
                 ctx.matvec_device(Q4_K, rows, cols, bufs[i % len(bufs)].device_ptr, 1, xb.device_ptr, yb.device_ptr)
-        ms = kms = t.wall_ms / n
-        out[mode] = {"ms_per_step": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9, "kernel_ms": kms,
-                     "kernel_gbps": step_bytes / (kms * 1e-3) / 1e9,
-                     "kernel_frac_of_peak": step_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        ms = t.wall_ms / n
+        out[mode] = {"ms_per_step": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9,
+                     "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     # Sustained: 8 distinct cold matrices sharing x in one grouped launch
     # (matvec_batch_device), so the ~2.4 us launch floor is paid once per 8
     # matvecs.  Time and bytes are reported per matrix.
@@ -169,63 +154,49 @@ def bench_c1(ctx, synth, steps, warmup):
     for i in range(warmup + 1):
         ctx.matvec_batch_device(Q4_K, rows, cols, sets[i % len(sets)], xb.device_ptr, 0, yg.device_ptr, rows)
     n = max(steps, 2 * len(sets))
-    with Timed(ctx, kernels=False) as t:
+    with Timed(ctx) as t:
         for i in range(n):
             ctx.matvec_batch_device(Q4_K, rows, cols, sets[i % len(sets)], xb.device_ptr, 0, yg.device_ptr, rows)
     ms = t.wall_ms / (n * group)
     per = w.size + rows * 4 + cols * 4 / group
     out["sustained"] = {"matrices_per_launch": group, "ms_per_matrix": ms, "bytes_per_matrix": per,
                         "gbps": per / (ms * 1e-3) / 1e9, "frac_of_peak": per / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
-    log(f"C1: cold kernel {out['cold']['kernel_ms'] * 1e3:.2f} us ({out['cold']['kernel_gbps']:.0f} GB/s); "
+    log(f"C1: cold {out['cold']['ms_per_step'] * 1e3:.2f} us per launch ({out['cold']['gbps']:.0f} GB/s); "
         f"sustained {ms * 1e3:.2f} us per matrix ({out['sustained']['gbps']:.0f} GB/s)")
-    out["floor"] = c1_floor(ctx, wbs, xb, yb, rows, cols, w.size, step_bytes, steps)
+    out["floor"] = c1_floor(ctx, wbs, w.size, step_bytes, steps)
     return out
 
 
-def c1_floor(ctx, wbs, xb, yb, rows, cols, wbytes, step_bytes, steps):
+def c1_floor(ctx, wbs, wbytes, step_bytes, steps):
     """What bounds a single C1 launch: back-to-back durations of an empty
-    kernel (256 x 256, the GEMV's grid), of a kernel that only reads the same
-    9.4 MB (cold: rotating copies; warm: one copy), and of the VALU form of
-    the GEMV; plus the GEMV's phase stamps (s_memrealtime, 100 MHz) over a
-    few cold launches."""
+    kernel (256 x 256, the GEMV's grid) and of a kernel that only reads the
+    same 9.4 MB (cold: rotating copies; warm: one copy), from the launch-floor
+    probes of libdmhip_diag.so (include/dmhip_diag.h).  None when that
+    library is not built."""
+    import ctypes
+    path = os.path.join(ROOT, "diskmule_amd", "libdmhip_diag.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.dmhip_diag_time_empty.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_size_t,
+                                          ctypes.POINTER(ctypes.c_double)]
+    lib.dmhip_diag_time_read.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_size_t,
+                                         ctypes.c_size_t, ctypes.POINTER(ctypes.c_double)]
     n = max(steps, 2 * len(wbs))
+    ctx.synchronize()
 
-    def per_launch(body):
-        for i in range(3):
-            body(i)
-        ctx.synchronize()
-        time.sleep(0.05)
-        with Timed(ctx, kernels=False) as t:
-            for i in range(n):
-                body(i)
-        return t.wall_ms / n * 1e3
+    def read(bufs):
+        us = ctypes.c_double()
+        srcs = (ctypes.c_void_p * len(bufs))(*[b.device_ptr for b in bufs])
+        assert lib.dmhip_diag_time_read(srcs, len(bufs), wbytes - wbytes % 16, n, ctypes.byref(us)) == 0
+        return us.value
 
-    res = {"empty_kernel_us": per_launch(lambda i: ctx.probe_empty(256, 256)),
-           "read_only_cold_us": per_launch(lambda i: ctx.probe_read(wbs[i % len(wbs)].device_ptr, wbytes)),
-           "read_only_warm_us": per_launch(lambda i: ctx.probe_read(wbs[0].device_ptr, wbytes)),
-           "valu_gemv_cold_us": per_launch(lambda i: ctx.matvec_valu_device(Q4_K, rows, cols, wbs[i % len(wbs)].device_ptr,
-                                                                        xb.device_ptr, yb.device_ptr)),
-           "valu_gemv_warm_us": per_launch(lambda i: ctx.matvec_valu_device(Q4_K, rows, cols, wbs[0].device_ptr,
-                                                                        xb.device_ptr, yb.device_ptr))}
+    empty = ctypes.c_double()
+    assert lib.dmhip_diag_time_empty(256, 256, n, ctypes.byref(empty)) == 0
+    res = {"empty_kernel_us": empty.value, "read_only_cold_us": read(wbs), "read_only_warm_us": read(wbs[:1])}
     res["read_only_cold_gbps"] = step_bytes / (res["read_only_cold_us"] * 1e-6) / 1e9
-    spans, spread, rec, first, tail = [], [], [], [], []
-    for i in range(8):
-        ctx.synchronize()
-        time.sleep(0.002)
-        st = ctx.matvec_phase_trace(Q4_K, rows, cols, wbs[(3 + i) % len(wbs)].device_ptr, xb.device_ptr, yb.device_ptr)
-        t0 = st[:, 0].min()
-        spans.append((st[:, 3].max() - t0) * 0.01)
-        spread.append((st[:, 0].max() - t0) * 0.01)
-        rec.append(float(np.mean(st[:, 1] - st[:, 0])) * 0.01)
-        first.append(float(np.mean(st[:, 2] - st[:, 0])) * 0.01)
-        tail.append(float(np.mean(st[:, 3] - st[:, 2])) * 0.01)
-    med = lambda v: float(np.median(v))
-    res["phases_us"] = {"workgroups": int(st.shape[0]), "span": med(spans), "entry_spread": med(spread),
-                        "entry_to_records_built": med(rec), "entry_to_first_weights": med(first),
-                        "first_weights_to_end": med(tail),
-                        "note": "medians over 8 cold launches of per-workgroup means; the 100 MHz counter"}
     log(f"C1 floor: empty {res['empty_kernel_us']:.2f} us, read-only cold {res['read_only_cold_us']:.2f} / warm "
-        f"{res['read_only_warm_us']:.2f} us, VALU GEMV cold {res['valu_gemv_cold_us']:.2f} us; phases {res['phases_us']}")
+        f"{res['read_only_warm_us']:.2f} us")
     return res
 
 
@@ -242,7 +213,7 @@ def bench_q8(ctx, synth, steps, warmup):
             ctx.matvec_device(Q8_0, rows, cols, wb.device_ptr, 1, xb.device_ptr, yb.device_ptr)
         ctx.synchronize()
         time.sleep(0.2)
-        with Timed(ctx, kernels=False) as t:
+        with Timed(ctx) as t:
             for _ in range(steps):
                 ctx.matvec_device(Q8_0, rows, cols, wb.device_ptr, 1, xb.device_ptr, yb.device_ptr)
         ms = t.wall_ms / steps
@@ -276,7 +247,7 @@ def bench_dense(ctx, synth, steps, warmup):
                 ctx.matvec_device(kind, rows, cols, wbs[i % copies].device_ptr, 1, xb.device_ptr, yb.device_ptr)
             ctx.synchronize()
             time.sleep(0.2)
-            with Timed(ctx, kernels=False) as t:
+            with Timed(ctx) as t:
                 for i in range(n):
                     ctx.matvec_device(kind, rows, cols, wbs[i % copies].device_ptr, 1, xb.device_ptr, yb.device_ptr)
             ms = t.wall_ms / n
@@ -323,11 +294,10 @@ def bench_c3(ctx, synth, steps, warmup):
             for i in range(warmup):
                 call(i, sets)
             n = max(steps, 2 * len(sets))
-            wall, kern, _ = timed_loop(ctx, lambda i: call(i, sets), n)
-            ms = wall / n
+            ms = timed_loop(ctx, lambda i: call(i, sets), n) / n
             res[mode] = {"layer_ms": ms, "gbps": step_bytes / (ms * 1e-3) / 1e9,
                          "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                         "tok_per_s": batch / (ms * 1e-3), "matvec_kernel_ms": kern / n}
+                         "tok_per_s": batch / (ms * 1e-3)}
         out[f"B{batch}"] = res
         log(f"C3 B={batch}: {res['cold']['layer_ms'] * 1e3:.1f} us/layer cold, "
             f"{res['warm']['layer_ms'] * 1e3:.1f} us warm")
@@ -355,8 +325,8 @@ def bench_c4(ctx, synth, steps, warmup):
         for i in range(warmup):
             ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
                           xs[i].device_ptr, yb.device_ptr)
-        # Wall-time pass with nothing else recorded (per-dispatch timing
-        # events slow these short launches and their upload waits).
+        # Wall time of the layer calls (host clock: each call ends with the
+        # host reading the router's selection).
         s0 = cache.stats()
         t0 = time.perf_counter()
         for i in range(warmup, warmup + steps):
@@ -367,19 +337,10 @@ def bench_c4(ctx, synth, steps, warmup):
         misses = s1["misses"] - s0["misses"]
         hits = s1["hits"] - s0["hits"]
         up_bytes = s1["bytes_read"] - s0["bytes_read"]
-        # Kernel pass: the same tokens again with the expert kernels timed.
-        uniq = 0
-        with Timed(ctx) as t:
-            for i in range(warmup, warmup + steps):
-                ids, _ = ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K,
-                                       Q6_K, xs[i].device_ptr, yb.device_ptr)
-                uniq += len(set(ids.ravel().tolist()))
-        kernel_bytes = uniq * (gu_bytes + dn_bytes)
         layer = {
             "layer_ms": wall / steps * 1e3, "hits": hits, "misses": misses,
             "evictions": s1["evictions"] - s0["evictions"],
             "upload_bytes": up_bytes, "upload_gbps_wall": up_bytes / wall / 1e9,
-            "expert_kernel_gbps": kernel_bytes / (t.kernel_ms * 1e-3) / 1e9 if t.kernel_ms else None,
         }
         cache.free()
         # All-resident layer: a cache with a slot for every expert, warmed
@@ -391,19 +352,13 @@ def bench_c4(ctx, synth, steps, warmup):
             ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
                           xs[0].device_ptr, yb.device_ptr)
         r0 = cache.stats()["misses"]
-        with Timed(ctx, kernels=False) as hot_wall:
-            ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
-                          xs[0].device_ptr, yb.device_ptr)
-        with Timed(ctx) as hot:
+        with Timed(ctx) as hot_wall:
             ids, _ = ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
                                    xs[0].device_ptr, yb.device_ptr)
         assert cache.stats()["misses"] == r0, "the all-resident pass loaded an expert"
-        hot_bytes = len(set(ids.ravel().tolist())) * (gu_bytes + dn_bytes)
         layer.update({
             "all_resident_layer_ms": hot_wall.wall_ms,
             "all_resident_experts": len(set(ids.ravel().tolist())),
-            "all_resident_expert_kernel_gbps":
-                hot_bytes / (hot.kernel_ms * 1e-3) / 1e9 if hot.kernel_ms else None,
         })
         out[f"B{batch}"] = layer
         log(f"C4 B={batch}: {wall / steps * 1e3:.2f} ms/layer, misses {misses}, hits {hits}; all-resident "
@@ -423,8 +378,8 @@ def bench_c4(ctx, synth, steps, warmup):
 def bench_c5(ctx, synth, steps, warmup):
     """C5: 512-token prefill GEMM at K = 4096, N = 4096 and 12288, for Q4_K
     (the headline) and the other two quantized types of the path.  `ms` is
-    the whole call (A preparation + GEMM); `kernel_ms_per_step` the GEMM
-    kernel alone (events on its dispatch)."""
+    the whole call (A preparation + GEMM); the GEMM kernel alone is in the
+    kernel trace of profiles/c5_gemm_kernel_stats.md."""
     m, k = 512, 4096
     a = synth.to_bf16_bits(synth.normal(synth.activation_seed(5), m * k))
     ab = upload(ctx, a)
@@ -438,13 +393,10 @@ def bench_c5(ctx, synth, steps, warmup):
                                            len(ws))
             for _ in range(warmup):
                 call()
-            wall, kern, _ = timed_loop(ctx, lambda i: call(), steps)
-            ms = wall / steps
+            ms = timed_loop(ctx, lambda i: call(), steps) / steps
             flops = 2.0 * m * n * k
             out[f"N{n}{tag}"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
-                                 "frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
-                                 "kernel_ms_per_step": kern / steps,
-                                 "kernel_tflops": flops / (kern / steps * 1e-3) / 1e12 if kern else None}
+                                 "frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
             log(f"C5{tag} N={n}: {ms * 1e3:.1f} us, {out[f'N{n}{tag}']['tflops']:.1f} TFLOP/s")
             wb.free()
             cb.free()
@@ -496,11 +448,10 @@ def bench_st(ctx, synth, steps, warmup):
         for i in range(warmup):
             call(i)
         n = max(steps, 2 * copies)
-        wall, kern, _ = timed_loop(ctx, call, n)
-        ms = wall / n
+        ms = timed_loop(ctx, call, n) / n
         key = f"{tag}_{rows}x{cols}"
         out[key] = {"ms": ms, "bytes": step_bytes, "gbps": step_bytes / (ms * 1e-3) / 1e9,
-                    "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "kernel_ms": kern / n}
+                    "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         log(f"safetensors {key}: {ms * 1e3:.1f} us per launch ({out[key]['gbps']:.0f} GB/s)")
         for b in wbs + [xb, yb] + [b for b in sbs if b is not None]:
             b.free()
@@ -545,13 +496,11 @@ def bench_attn(ctx, synth, steps, warmup):
         for i in range(warmup):
             call(i)
         n = max(steps, 2 * nlayers)
-        wall, kern, launches = timed_loop(ctx, call, n)
+        ms = timed_loop(ctx, call, n) / n
         ctx.attention_result()
-        ms, kms = wall / n, kern / n
         res = {"qh": qh, "kvh": kvh, "head_dim": hd, "visible": visible, "bytes_per_call": step_bytes,
-               "call_ms": ms, "kernels_ms": kms, "launches_per_call": launches / n,
-               "gbps_call": step_bytes / (ms * 1e-3) / 1e9, "gbps_kernels": step_bytes / (kms * 1e-3) / 1e9,
-               "frac_of_peak": step_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+               "call_ms": ms, "gbps_call": step_bytes / (ms * 1e-3) / 1e9,
+               "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         if positions <= 32768:
             ring_k = np.zeros((cap, width), dtype=np.float32)
             ring_v = np.zeros((cap, width), dtype=np.float32)
@@ -564,8 +513,7 @@ def bench_attn(ctx, synth, steps, warmup):
             got = ob.read(0, qh * hd * 4, np.float32)
             res["max_abs_diff_vs_port"] = float(np.abs(got - want).max())
         out[key] = res
-        log(f"attention {key}: {ms * 1e3:.1f} us per call, kernels {kms * 1e3:.1f} us "
-            f"({res['gbps_kernels']:.0f} GB/s)")
+        log(f"attention {key}: {ms * 1e3:.1f} us per call ({res['gbps_call']:.0f} GB/s)")
         for b in layers + [kb, vb, qb, ob]:
             b.free()
     return out
@@ -592,7 +540,7 @@ def bench_copy(ctx, synth, steps, warmup):
     src, dst = ctx.new_owned_buffer(n), ctx.new_owned_buffer(n)
     for _ in range(warmup):
         ctx.copy_device(dst.device_ptr, src.device_ptr, n)
-    with Timed(ctx, kernels=False) as t:
+    with Timed(ctx) as t:
         for _ in range(steps):
             ctx.copy_device(dst.device_ptr, src.device_ptr, n)
     ms = t.wall_ms / steps

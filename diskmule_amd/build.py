@@ -1,4 +1,6 @@
-"""Build the gfx950 library ``libdmhip.so`` from ``csrc/`` with hipcc.
+"""Build the gfx950 library ``libdmhip.so`` from ``csrc/`` with hipcc, and
+the measurement-only ``libdmhip_diag.so`` (launch-floor probes,
+``include/dmhip_diag.h``) from ``csrc/diag/``.
 
 Every HIP source is compiled for gfx950 only, with FMA contraction off (all
 fused multiply-adds in the kernels are explicit) and without packed-FP32
@@ -17,9 +19,11 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libdmhip.so")
-SOURCES = ["runtime.hip", "dispatch.hip", "kernels_simple.hip", "kernels_qmv.hip", "kernels_qmv8.hip", "kernels_qmv_valu.hip",
+DIAG_LIB = os.path.join(HERE, "libdmhip_diag.so")
+SOURCES = ["runtime.hip", "dispatch.hip", "kernels_simple.hip", "kernels_qmv.hip", "kernels_qmv8.hip",
            "kernels_gemm.hip", "expert_cache.hip", "kernels_dense.hip", "attention.hip",
            "kernels_safetensor.hip"]
+DIAG_SOURCES = ["diag/probes.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -31,24 +35,23 @@ SOURCE_FLAGS: dict = {}
 
 def build(verbose: bool = False, jobs: int = 6) -> str:
     objdir = os.path.join(HERE, "_build")
-    os.makedirs(objdir, exist_ok=True)
+    os.makedirs(os.path.join(objdir, "diag"), exist_ok=True)
     procs = []
-    objs = []
-    for src in SOURCES:
-        path = os.path.join(CSRC, src)
-        if not os.path.exists(path):
-            continue
-        obj = os.path.join(objdir, src + ".o")
-        objs.append(obj)
-        cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-c", path, "-o", obj]
-        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
-        if len(procs) >= jobs:
-            _drain(procs, verbose)
+    objs = {LIB: [], DIAG_LIB: []}
+    for lib, sources in ((LIB, SOURCES), (DIAG_LIB, DIAG_SOURCES)):
+        for src in sources:
+            path = os.path.join(CSRC, src)
+            obj = os.path.join(objdir, src + ".o")
+            objs[lib].append(obj)
+            cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-c", path, "-o", obj]
+            procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+            if len(procs) >= jobs:
+                _drain(procs, verbose)
     _drain(procs, verbose)
-    tmp = LIB + ".tmp"
-    subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs],
-                   check=True)
-    os.replace(tmp, LIB)
+    for lib, lib_objs in objs.items():
+        tmp = lib + ".tmp"
+        subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *lib_objs], check=True)
+        os.replace(tmp, lib)
     return LIB
 
 

@@ -621,6 +621,13 @@ static uint32_t next_mark(dmhip_ctx *ctx) {
     return ctx->attn_mark;
 }
 
+// The mark of a host-slice call: it ends the period of device calls awaiting
+// a result, so while one is open it shares that period's mark and reports a
+// non-finite score met by any of them, as dmhip_attention_result would.
+static uint32_t host_call_mark(dmhip_ctx *ctx) {
+    return ctx->attn_pending ? ctx->attn_mark : next_mark(ctx);
+}
+
 static int attention_finish_host(dmhip_ctx *ctx, float *output, const float *dout, size_t query_width) {
     uint32_t flag = 0;
     DM_HIP(hipMemcpyAsync(output, dout, query_width * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -781,7 +788,7 @@ int dmhip_attention_cached(dmhip_ctx *ctx, const float *query, size_t query_len,
     DM_CHECK_STATUS(ctx->out.ensure(bytes));
     float *dq = (float *)ctx->in.ptr, *dout = (float *)ctx->out.ptr;
     DM_HIP(hipMemcpyAsync(dq, query, bytes, hipMemcpyHostToDevice, ctx->stream));
-    const uint32_t mark = next_mark(ctx);
+    const uint32_t mark = host_call_mark(ctx);
     DM_CHECK_STATUS(enqueue_attention(ctx, dq, layer->keys, layer->values, layer->capacity, layer->width,
                                       query_heads, kv_heads, head_dimension, start, visible, dout,
                                       BadFlag{ctx->flags + kAttnFlagWord, mark}));
@@ -855,7 +862,7 @@ int dmhip_attention(dmhip_ctx *ctx, const float *query, size_t query_len, const 
     DM_HIP(hipMemcpyAsync(dq, query, q_bytes, hipMemcpyHostToDevice, ctx->stream));
     DM_HIP(hipMemcpyAsync(dk, keys + start * cache_width, kv_bytes, hipMemcpyHostToDevice, ctx->stream));
     DM_HIP(hipMemcpyAsync(dv, values + start * cache_width, kv_bytes, hipMemcpyHostToDevice, ctx->stream));
-    const uint32_t mark = next_mark(ctx);
+    const uint32_t mark = host_call_mark(ctx);
     DM_CHECK_STATUS(enqueue_attention(ctx, dq, dk, dv, visible, cache_width, query_heads, kv_heads,
                                       head_dimension, 0, visible, dout, BadFlag{ctx->flags + kAttnFlagWord, mark}));
     return attention_finish_host(ctx, output, dout, query_len);

@@ -26,8 +26,8 @@ int noalloc_resolve(int device) {
     // one of its kernels is first resolved, which must not happen inside an
     // allocation-free call.
     for (const void *anchor : {module_anchor_simple(), module_anchor_qmv(), module_anchor_qmv8(),
-                               module_anchor_qmv_valu(), module_anchor_gemm(), module_anchor_expert(),
-                               module_anchor_dense(), module_anchor_attention(), module_anchor_safetensor()}) {
+                               module_anchor_gemm(), module_anchor_expert(), module_anchor_dense(),
+                               module_anchor_attention(), module_anchor_safetensor()}) {
         hipFuncAttributes attr;
         DM_HIP(hipFuncGetAttributes(&attr, anchor));
     }
@@ -63,7 +63,6 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
         }
         return DMHIP_OK;
     }
-    KernelTimer timer(ctx);
     if (dense_supported(type, rows, columns, w, x, batch)) {
         DM_HIP(launch_dense_gemv(ctx->stream, ctx->compute_units, type, w, (uint32_t)rows, (uint32_t)columns,
                                  (size_t)row_bytes, (uint32_t)batch, x, y));
@@ -118,13 +117,14 @@ int dmhip_ffn_device_noalloc(dmhip_ctx *ctx, size_t batch, size_t hidden, size_t
     if (batch < 1 || batch > 16)
         return fail(DMHIP_ERR_INVALID_ARGUMENT, "batch %zu is outside 1..=16", batch);
     const size_t ws = dmhip_ffn_workspace_bytes(batch, hidden, ffn);
-    // batches above 2 prepare activation fragments of h (gate/up) and of the
-    // activation rows (down); the larger of the two regions is lent
+    // batches above 2 prepare activation fragments of h (gate and up, whose
+    // types may differ and need different fragment sets) and of the
+    // activation rows (down); the largest of the three regions is lent
     size_t lend = 0;
     if (batch > 2) {
-        const uint32_t types[2] = {gate_type, down_type};
-        const size_t cols[2] = {hidden, ffn};
-        for (int i = 0; i < 2; i++) {
+        const uint32_t types[3] = {gate_type, up_type, down_type};
+        const size_t cols[3] = {hidden, hidden, ffn};
+        for (int i = 0; i < 3; i++) {
             const size_t b = qmv_prepare_bytes(types[i], cols[i], batch);
             lend = b > lend ? b : lend;
         }

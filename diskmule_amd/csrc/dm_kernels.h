@@ -45,7 +45,6 @@ struct ArgmaxState {
 const void *module_anchor_simple();
 const void *module_anchor_qmv();
 const void *module_anchor_qmv8();
-const void *module_anchor_qmv_valu();
 const void *module_anchor_gemm();
 const void *module_anchor_dense();
 // GEMV over F32 / F16 rows (whole 16-byte chunks, 16-byte aligned) and Q5_0
@@ -69,10 +68,6 @@ hipError_t launch_st_gemv(hipStream_t s, int cus, uint32_t fmt, const void *w, u
                           bool wide);
 
 hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t n);
-// Launch-floor probes: an empty kernel; a read of n bytes (16-byte aligned
-// src; bytes past the last whole 16 are not read).
-hipError_t launch_probe_empty(hipStream_t s, uint32_t workgroups, uint32_t threads);
-hipError_t launch_probe_read(hipStream_t s, const void *src, size_t n, uint32_t *sink);
 hipError_t launch_dequantize(hipStream_t s, uint32_t type, const uint8_t *enc, uint32_t be,
                              uint32_t bb, size_t elements, float *out);
 hipError_t launch_gemv_exact(hipStream_t s, uint32_t type, uint32_t be, uint32_t bb, uint32_t rows,

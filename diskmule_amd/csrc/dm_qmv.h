@@ -30,19 +30,13 @@ struct ArgmaxFinish {
 // the caller has already checked qmv_supported.
 bool qmv8_supported(uint32_t type, size_t rows, size_t columns, size_t batch);
 
-// y[b][r] = W[r] . x[b] with the int8-MFMA kernels.  With `trace` (a
-// measurement hook) thread 0 of workgroup i writes four s_memrealtime stamps
-// (100 MHz) to trace[4i..4i+3]: entry, activation records built, first weight
-// group landed, end.  force_s / force_g (both nonzero) pin the split and the
-// blocks per fetch (measurement); the call fails when that plan does not fit.
-// With `partials` the
+// y[b][r] = W[r] . x[b] with the int8-MFMA kernels.  With `partials` the
 // epilogue also writes one ArgmaxPartial per workgroup (batch 1) and *count
 // receives the number written; with a `finish` ticket the kernel reduces
 // them itself into finish.state / finish.index.
 hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
                        uint32_t batch, const float *x, float *y, ArgmaxPartial *partials,
-                       uint32_t *count, ArgmaxFinish finish = ArgmaxFinish{nullptr, nullptr, nullptr, nullptr},
-                       uint64_t *trace = nullptr, uint32_t force_s = 0, uint32_t force_g = 0);
+                       uint32_t *count, ArgmaxFinish finish = ArgmaxFinish{nullptr, nullptr, nullptr, nullptr});
 
 // The int8-MFMA gate/up pair: act[b][r] = silu(gate[r] . n[b]) * (up[r] . n[b])
 // with n = RMSNorm(x) (unit weight) when `normalize`, else n = x.
@@ -96,14 +90,5 @@ hipError_t launch_qmv(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t col
 hipError_t launch_qmv_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns,
                               const void *gate, const void *up, uint32_t batch, const float *x,
                               float *act, int normalize, float epsilon);
-
-// True when the VALU batch-1 GEMV takes this shape: Q4_K rows of 1, 2, 4, 8
-// or 16 super-blocks, weights and x 16-byte aligned, weights under 4 GiB.
-bool qmv_valu_supported(uint32_t type, size_t rows, size_t columns, const void *w, const float *x,
-                        size_t batch);
-
-// y = W x (batch 1) with the VALU kernel.
-hipError_t launch_qmv_valu(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
-                           const float *x, float *y);
 
 }  // namespace dm

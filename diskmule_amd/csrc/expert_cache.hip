@@ -76,10 +76,8 @@ struct Slot {
     dmhip_buf *down_buf = nullptr;     // cache-owned, len = down_bytes
     void *gate_up = nullptr;           // their device addresses
     void *down = nullptr;
-    hipEvent_t upload_start = nullptr;  // start of the last upload (memory source: timed)
-    hipEvent_t ready = nullptr;         // end of the last upload into the slot
-    bool uploaded = false;              // ready has been recorded
-    bool timing_pending = false;        // upload_start..ready not yet added to io_wait
+    hipEvent_t ready = nullptr;  // end of the last upload into the slot
+    bool uploaded = false;       // ready has been recorded
     // End of the last compute that read it: an event of the cache's ring,
     // shared by the slots released together.  Once the ring wraps the event
     // may be recorded again later on the same stream, which only makes a
@@ -92,6 +90,14 @@ struct Layer {
     dmhip_expert_layer_layout layout;
     std::vector<Slot> slots;
     uint64_t clock = 0;
+};
+
+// Memory source: the device time of one upload, a (start, end) pair of
+// timing events from a ring.  io_wait adds the durations of finished
+// uploads; nothing on the acquire path waits for an upload to finish.
+struct TimedUpload {
+    hipEvent_t start = nullptr, end = nullptr;
+    bool pending = false;  // recorded, not yet added to io_wait
 };
 
 // One pinned host buffer of the file source's staging ring.
@@ -112,6 +118,8 @@ struct dmhip_expert_cache {
     int fd = -1;
     std::vector<dm::Staging> staging;
     size_t next_staging = 0;
+    std::vector<dm::TimedUpload> timed;  // memory source
+    size_t next_timed = 0;
     std::vector<dm::Layer> layers;
     dmhip_expert_cache_stats stats = {};
     // MoE workspace (device): grows on demand.
@@ -130,6 +138,10 @@ constexpr size_t kSelectionPairs = 16 * dm::kMaxTopK;  // batch <= 16
 constexpr size_t kSelectionBytes = kSelectionPairs * 8 + 16 * 4;  // ids, probabilities, per-token flags
 constexpr size_t kReleaseEvents = 64;
 constexpr size_t kStagingEntries = 4;  // file source: experts in flight from storage
+// Memory source: uploads whose timing is kept until it is read.  The ring is
+// reused oldest first, so a wait at reuse only ever meets an upload issued
+// 64 uploads earlier.
+constexpr size_t kTimedUploads = 64;
 }
 
 using namespace dm;
@@ -154,21 +166,21 @@ int read_exact_at(int fd, uint64_t offset, uint8_t *dst, size_t n) {
     return -1;  // complete
 }
 
-// Adds the device-measured duration of finished uploads into io_wait (the
+// Adds the device-measured duration of a finished upload into io_wait (the
 // memory source: the host never waits for its asynchronous copies, so the
 // time the bytes took to arrive is what io_wait reports).  `wait` waits for
-// uploads still in flight.
+// an upload still in flight; otherwise one in flight is left for later.
+void account_upload(dmhip_expert_cache *c, TimedUpload &t, bool wait) {
+    if (!t.pending) return;
+    if (!wait && hipEventQuery(t.end) != hipSuccess) return;
+    float ms = 0.0f;
+    if (hipEventSynchronize(t.end) == hipSuccess && hipEventElapsedTime(&ms, t.start, t.end) == hipSuccess)
+        c->stats.io_wait_ns += (uint64_t)((double)ms * 1e6);
+    t.pending = false;
+}
+
 void account_uploads(dmhip_expert_cache *c, bool wait) {
-    for (Layer &layer : c->layers)
-        for (Slot &s : layer.slots) {
-            if (!s.timing_pending) continue;
-            if (!wait && hipEventQuery(s.ready) != hipSuccess) continue;
-            float ms = 0.0f;
-            if (hipEventSynchronize(s.ready) == hipSuccess &&
-                hipEventElapsedTime(&ms, s.upload_start, s.ready) == hipSuccess)
-                c->stats.io_wait_ns += (uint64_t)((double)ms * 1e6);
-            s.timing_pending = false;
-        }
+    for (TimedUpload &t : c->timed) account_upload(c, t, wait);
 }
 
 // Copies expert `expert` of the layer into slot s on an upload stream that
@@ -201,15 +213,20 @@ int upload_expert(dmhip_expert_cache *c, const dmhip_expert_layer_layout &L, siz
     hipStream_t up = (c->ctx->upload_next++ & 1u) ? c->ctx->upload2 : c->ctx->upload;
     if (s.released_recorded) DM_HIP(hipStreamWaitEvent(up, s.released, 0));
     if (s.uploaded) DM_HIP(hipStreamWaitEvent(up, s.ready, 0));
+    TimedUpload *timer = nullptr;
     if (c->fd < 0) {
-        if (s.timing_pending) account_uploads(c, true);
-        DM_HIP(hipEventRecord(s.upload_start, up));
+        timer = &c->timed[c->next_timed++ % c->timed.size()];
+        account_upload(c, *timer, true);  // the oldest pair of the ring
+        DM_HIP(hipEventRecord(timer->start, up));
     }
     DM_HIP(hipMemcpyAsync(s.gate_up, gu_src, gu_bytes, hipMemcpyHostToDevice, up));
     DM_HIP(hipMemcpyAsync(s.down, dn_src, dn_bytes, hipMemcpyHostToDevice, up));
     DM_HIP(hipEventRecord(s.ready, up));
     s.uploaded = true;
-    s.timing_pending = c->fd < 0;
+    if (timer) {
+        DM_HIP(hipEventRecord(timer->end, up));
+        timer->pending = true;
+    }
     if (entry) {
         DM_HIP(hipEventRecord(entry->done, up));
         entry->busy = true;
@@ -310,8 +327,12 @@ void destroy(dmhip_expert_cache *c) {
             free_slot_buffer(s.gate_up_buf);
             free_slot_buffer(s.down_buf);
             if (s.ready) (void)hipEventDestroy(s.ready);
-            if (s.upload_start) (void)hipEventDestroy(s.upload_start);
         }
+    for (TimedUpload &t : c->timed) {
+        if (t.pending) (void)hipEventSynchronize(t.end);
+        if (t.start) (void)hipEventDestroy(t.start);
+        if (t.end) (void)hipEventDestroy(t.end);
+    }
     for (hipEvent_t ev : c->release_events)
         if (ev) (void)hipEventDestroy(ev);
     for (Staging &e : c->staging) {
@@ -345,12 +366,16 @@ int build_cache(dmhip_ctx *ctx, const dmhip_expert_layer_layout *layouts, size_t
                 return fail_alloc(!s.gate_up_buf ? layer.layout.gate_up_bytes : layer.layout.down_bytes);
             s.gate_up = s.gate_up_buf->dev;
             s.down = s.down_buf->dev;
-            if (hipEventCreate(&s.ready) != hipSuccess || hipEventCreate(&s.upload_start) != hipSuccess)
+            if (hipEventCreate(&s.ready) != hipSuccess)
                 return fail(DMHIP_ERR_COMMAND, "could not create the expert slot events");
             resident += layer.layout.gate_up_bytes + layer.layout.down_bytes;
         }
     }
     c->stats.resident_bytes = resident;
+    c->timed.resize(kTimedUploads);
+    for (TimedUpload &t : c->timed)
+        if (hipEventCreate(&t.start) != hipSuccess || hipEventCreate(&t.end) != hipSuccess)
+            return fail(DMHIP_ERR_COMMAND, "could not create the upload timing events");
     c->release_events.assign(kReleaseEvents, nullptr);
     for (hipEvent_t &ev : c->release_events)
         if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {

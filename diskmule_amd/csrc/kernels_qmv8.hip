@@ -488,7 +488,7 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
                                           uint32_t total_bytes, const float *__restrict__ x, int x_stride,
                                           int normalize, float epsilon, int glm, float *__restrict__ y,
                                           int y_stride, ArgmaxPartial *__restrict__ partials,
-                                          const ArgmaxFinish finish, uint64_t *__restrict__ trace) {
+                                          const ArgmaxFinish finish) {
     constexpr uint32_t WAVES = W;
     static_assert(W % S == 0, "a workgroup holds whole tiles");
     static_assert(!PC || (S == (int)W && S > 1), "a cooperative workgroup splits each tile over all its waves");
@@ -509,11 +509,6 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     __shared__ unsigned long long wg_key[WAVES];
     __shared__ uint32_t wg_bad[WAVES];
 
-    // Phase stamps of the workgroup (measurement only): entry, activation
-    // records built, first weight group landed, last output written.
-    const bool stamp = trace != nullptr && threadIdx.x == 0;
-    uint64_t t_entry = 0, t_records = 0, t_weights = 0;
-    if (stamp) t_entry = __builtin_amdgcn_s_memrealtime();
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t kpart = wave % S;
@@ -589,7 +584,6 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
         build_records8<TYPE, TOK, WAVES, false, XP>(x, x_stride, columns, (uint8_t *)lds8, red_ss, xpre);
     for (uint32_t i = threadIdx.x; i < kZero8 / 16; i += 64 * WAVES) lds8[rec_bytes / 16 + i] = i32x4{0, 0, 0, 0};
     __syncthreads();
-    if (stamp) t_records = __builtin_amdgcn_s_memrealtime();
     // Output scale per token: 1, or the RMSNorm factor (unit weight)
     // inv = (ss/n + eps).sqrt().recip() (src/cpu.rs:98-142) folded in.
     float tscale[TOK];
@@ -623,7 +617,6 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
                 if constexpr (MODE == 2) stage2[j * 64 + lane] = st2[j];
             }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        if (stamp && t_weights == 0) t_weights = __builtin_amdgcn_s_memrealtime();
     };
     // acc[m][tok]: matrix m (gate, up) of token tok
     auto compute_group = [&](uint32_t grp, uint32_t rb, float (&acc)[NM][TOK]) {
@@ -809,13 +802,6 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
         }
     }
 
-    if (stamp) {
-        uint64_t *t = trace + 4 * (size_t)blockIdx.x;
-        t[0] = t_entry;
-        t[1] = t_records;
-        t[2] = t_weights;
-        t[3] = __builtin_amdgcn_s_memrealtime();
-    }
     if constexpr (MODE == 1) {
         best = wave_max_u64(best);
         bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
@@ -877,9 +863,9 @@ __global__ void __launch_bounds__(64 * W)
     __attribute__((amdgpu_waves_per_eu(waves_per_eu8<TYPE, MODE, TOK, G, PC>()))) qmv8_kernel(
     const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2, uint32_t rows, uint32_t columns,
     uint32_t row_bytes, uint32_t total_bytes, const float *__restrict__ x, int normalize, float epsilon,
-    float *__restrict__ y, ArgmaxPartial *__restrict__ partials, ArgmaxFinish finish, uint64_t *trace) {
+    float *__restrict__ y, ArgmaxPartial *__restrict__ partials, ArgmaxFinish finish) {
     qmv8_body<TYPE, S, MODE, TOK, G, W, PC>(w, w2, rows, columns, row_bytes, total_bytes, x, (int)columns,
-                                            normalize, epsilon, 0, y, (int)rows, partials, finish, trace);
+                                            normalize, epsilon, 0, y, (int)rows, partials, finish);
 }
 
 // Grouped launch over the routed-expert jobs of a MoE layer: job
@@ -905,7 +891,7 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     const uint8_t *w = (const uint8_t *)j.w;
     qmv8_body<TYPE, S, MODE, TOK, G, (S > 8 ? S : 8)>(w, w + w2_offset, rows, columns, row_bytes, total_bytes, x + j.x_off,
                                      j.x_stride, 0, 0.0f, glm, y + j.y_off, j.y_stride, nullptr,
-                                     ArgmaxFinish{nullptr, nullptr, nullptr, nullptr}, nullptr);
+                                     ArgmaxFinish{nullptr, nullptr, nullptr, nullptr});
 }
 
 // ---------------------------------------------------------------------------
@@ -967,22 +953,10 @@ bool fits8(uint32_t type, uint32_t blocks, uint32_t batch, uint32_t mats, uint32
 // 16 waves of one block per tile against 6.2 us with one 4-wave workgroup of
 // four-block fetches per tile, and 4096 x 2048 runs 4.2 us with 8 waves
 // against 5.2 us with four of two-block fetches.
-// force_s / force_g (both nonzero) pin the plan when it fits (measurement).
 // s == 0: no plan.
-Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t mats, uint32_t force_s = 0,
-            uint32_t force_g = 0) {
+Plan8 plan8(uint32_t type, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t mats) {
     Plan8 p;
     const uint32_t tiles = (rows + 15) / 16, blocks = columns / 256;
-    if (force_s || force_g) {
-        const bool ok_s = force_s == 1 || force_s == 2 || force_s == 4 || force_s == 8 || force_s == 16;
-        const bool ok_g = force_g == 1 || force_g == 2 || force_g == 4;
-        const bool pair_ok = (mats == 1 || (force_s <= 8 && force_g <= 2)) && (force_s <= 8 || force_g <= 2);
-        if (ok_s && ok_g && pair_ok && force_g <= blocks && fits8(type, blocks, batch, mats, force_s, force_g)) {
-            p.s = force_s;
-            p.g = force_g;
-        }
-        return p;
-    }
     p.g = tiles >= 2048 ? 2u : 1u;
     while (p.g > 1 && blocks < 2 * p.g) p.g /= 2;
     const uint32_t groups = (blocks + p.g - 1) / p.g;
@@ -1015,7 +989,6 @@ struct Args8 {
     ArgmaxPartial *partials;
     uint32_t *count;
     ArgmaxFinish finish;
-    uint64_t *trace;
 };
 
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, bool PC = false>
@@ -1050,7 +1023,7 @@ hipError_t run8(dmhip_ctx *ctx, const Args8 &a) {
     }
     return launch_kernel(ctx, kernel, dim3(grid), dim3(64 * WAVES), lds, (const uint8_t *)a.w,
                          (const uint8_t *)a.w2, rows, columns, row_bytes, row_bytes * rows, a.x, a.normalize,
-                         a.epsilon, a.y, a.partials, a.finish, a.trace);
+                         a.epsilon, a.y, a.partials, a.finish);
 }
 
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
@@ -1159,9 +1132,8 @@ hipError_t run8_grouped_s(dmhip_ctx *ctx, const Plan8 &p, uint32_t rows, uint32_
 }
 
 template <uint32_t TYPE>
-hipError_t launch8(dmhip_ctx *ctx, uint32_t batch, int mode, const Args8 &a, uint32_t force_s = 0,
-                   uint32_t force_g = 0) {
-    const Plan8 p = plan8(TYPE, a.rows, a.columns, batch, mode == 2 ? 2u : 1u, force_s, force_g);
+hipError_t launch8(dmhip_ctx *ctx, uint32_t batch, int mode, const Args8 &a) {
+    const Plan8 p = plan8(TYPE, a.rows, a.columns, batch, mode == 2 ? 2u : 1u);
     if (p.s == 0) return hipErrorInvalidValue;
     if (mode == 1) return run8_g<TYPE, 1, 1>(ctx, p, a);
     if (mode == 2) {
@@ -1208,19 +1180,19 @@ bool qmv8_gate_up_supported(uint32_t type, size_t rows, size_t columns, size_t b
 
 hipError_t launch_qmv8(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, const void *w,
                        uint32_t batch, const float *x, float *y, ArgmaxPartial *partials, uint32_t *count,
-                       ArgmaxFinish finish, uint64_t *trace, uint32_t force_s, uint32_t force_g) {
-    const Args8 a{rows, columns, w, w, x, 0, 0.0f, y, partials, count, finish, trace};
+                       ArgmaxFinish finish) {
+    const Args8 a{rows, columns, w, w, x, 0, 0.0f, y, partials, count, finish};
     const int mode = partials ? 1 : 0;
-    if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, mode, a, force_s, force_g);
-    if (type == kQ8_0) return launch8<kQ8_0>(ctx, batch, mode, a, force_s, force_g);
-    return launch8<kQ6_K>(ctx, batch, mode, a, force_s, force_g);
+    if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, mode, a);
+    if (type == kQ8_0) return launch8<kQ8_0>(ctx, batch, mode, a);
+    return launch8<kQ6_K>(ctx, batch, mode, a);
 }
 
 hipError_t launch_qmv8_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns,
                                const void *gate, const void *up, uint32_t batch, const float *x, float *act,
                                int normalize, float epsilon) {
     const Args8 a{rows, columns, gate, up, x, normalize, epsilon, act, nullptr, nullptr,
-                  ArgmaxFinish{nullptr, nullptr, nullptr, nullptr}, nullptr};
+                  ArgmaxFinish{nullptr, nullptr, nullptr, nullptr}};
     if (type == kQ4_K) return launch8<kQ4_K>(ctx, batch, 2, a);
     return launch8<kQ6_K>(ctx, batch, 2, a);
 }

@@ -390,7 +390,6 @@ int st_enqueue(dmhip_ctx *ctx, uint32_t fmt, size_t rows, size_t columns, const 
         scales = (const float *)ctx->aux.ptr;
     }
     const bool wide = st_wide_supported(fmt, rows, columns, group, w, x);
-    KernelTimer timer(ctx);
     DM_HIP(launch_st_gemv(ctx->stream, ctx->compute_units, fmt, w, (uint32_t)rows, (uint32_t)columns, scales,
                           (uint32_t)scale_columns, (uint32_t)std::min<size_t>(group, 0xffffffffu), x, y, wide));
     return DMHIP_OK;

@@ -555,8 +555,9 @@ __device__ __forceinline__ float silu_stable(float v) {
     return v * sigmoid;
 }
 
-__global__ void silu_mul_kernel(const float *__restrict__ gate, const float *__restrict__ up,
-                                size_t n, float *__restrict__ out) {
+// No __restrict__ on the elementwise kernels: the output may be either
+// input (each element is read by the thread that writes it).
+__global__ void silu_mul_kernel(const float *gate, const float *up, size_t n, float *out) {
     size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
         out[i] = silu_stable(gate[i]) * up[i];
@@ -607,46 +608,7 @@ __global__ void __launch_bounds__(256) copy_bytes_kernel(uint8_t *__restrict__ d
     }
 }
 
-// ---- launch-floor probes (measurement) ----------------------------------
-// An empty kernel, and a kernel that only reads: each 256-thread workgroup
-// streams 16 KB with four 16-byte loads per lane issued before any use, and
-// writes only if the checksum equals `magic` (never, in practice), so the
-// loads cannot be dropped.  Their durations bound what a GEMV of the same
-// bytes can reach.
-__global__ void probe_empty_kernel() {}
-
-__global__ void __launch_bounds__(256) probe_read_kernel(const u32x4 *__restrict__ src, size_t n16,
-                                                         uint32_t magic, uint32_t *sink) {
-    const size_t base = (size_t)blockIdx.x * 1024 + threadIdx.x;
-    u32x4 v[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const size_t i = base + 256 * j;
-        v[j] = i < n16 ? src[i] : u32x4{0, 0, 0, 0};
-    }
-    uint32_t h = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) h += v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3];
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) h ^= __shfl_xor(h, m, 64);
-    if (h == magic) sink[0] = h;
-}
-
 // ---- host-side launchers -------------------------------------------------
-
-hipError_t launch_probe_empty(hipStream_t s, uint32_t workgroups, uint32_t threads) {
-    hipLaunchKernelGGL(probe_empty_kernel, dim3(workgroups), dim3(threads), 0, s);
-    return hipGetLastError();
-}
-
-hipError_t launch_probe_read(hipStream_t s, const void *src, size_t n, uint32_t *sink) {
-    const size_t n16 = n / 16;
-    const size_t groups = (n16 + 1023) / 1024;
-    if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL(probe_read_kernel, dim3((uint32_t)groups), dim3(256), 0, s, (const u32x4 *)src, n16,
-                       0x9e3779b9u, sink);
-    return hipGetLastError();
-}
 
 hipError_t launch_copy_bytes(hipStream_t s, void *dst, const void *src, size_t n) {
     size_t blocks = (n / 16 + 255) / 256;
@@ -791,7 +753,7 @@ hipError_t launch_silu_mul(hipStream_t s, const float *gate, const float *up, si
 
 // Logit softcap, src/cpu.rs:263-273: cap * tanh(value / cap), fp32 (the
 // division, tanh and product each round once).
-__global__ void softcap_kernel(const float *__restrict__ in, size_t n, float cap, float *__restrict__ out) {
+__global__ void softcap_kernel(const float *in, size_t n, float cap, float *out) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
         const float q = in[i] / cap;
         out[i] = cap * tanhf(q);
@@ -809,8 +771,7 @@ hipError_t launch_softcap(hipStream_t s, const float *in, size_t n, float cap, f
 // ---- Gemma 4 / GLM glue: vector add, GELU multiply, softmax, NeoX RoPE ----
 
 // output = left + right (src/metal.rs:404-432, metal/kernels.metal:34-43).
-__global__ void add_kernel(const float *__restrict__ a, const float *__restrict__ b, size_t n,
-                           float *__restrict__ out) {
+__global__ void add_kernel(const float *a, const float *b, size_t n, float *out) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         out[i] = a[i] + b[i];
 }
@@ -833,8 +794,7 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 }
 
 // gelu_tanh(gate) * up (src/metal.rs:530-552, src/gemma4/cpu.rs).
-__global__ void gelu_mul_kernel(const float *__restrict__ gate, const float *__restrict__ up, size_t n,
-                                float *__restrict__ out) {
+__global__ void gelu_mul_kernel(const float *gate, const float *up, size_t n, float *out) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         out[i] = gelu_tanh(gate[i]) * up[i];
 }

@@ -102,26 +102,7 @@ struct dmhip_ctx {
     bool router_pending = false;  // a dmhip_router_top_k_device awaits dmhip_router_result
     bool attn_pending = false;    // a dmhip_attention_cached_device awaits dmhip_attention_result
     uint32_t *argmax_user_index = nullptr;
-    // Measurement: start/stop event pairs around the dominant kernels, and
-    // a pool of idle events (created without a system-scope fence) reused
-    // across measurements.
-    bool kernel_timing = false;
-    std::vector<hipEvent_t> timing_events;
-    std::vector<hipEvent_t> timing_pool;
 };
-
-// An idle timing event from the context's pool (nullptr when none can be
-// created).
-inline hipEvent_t timing_event(dmhip_ctx *ctx) {
-    if (!ctx->timing_pool.empty()) {
-        hipEvent_t e = ctx->timing_pool.back();
-        ctx->timing_pool.pop_back();
-        return e;
-    }
-    hipEvent_t e = nullptr;
-    if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
-    return e;
-}
 
 struct dmhip_buf {
     dmhip_ctx *ctx = nullptr;
@@ -149,36 +130,10 @@ int set_device(dmhip_ctx *ctx);
 // the allocation-free FFN's scratch array.
 int noalloc_resolve(int device);
 
-// While ctx->kernel_timing is set, records an event on the compute stream
-// when constructed (before a launch) and another when destroyed (after it).
-struct KernelTimer {
-    dmhip_ctx *ctx;
-    explicit KernelTimer(dmhip_ctx *c);
-    ~KernelTimer();
-};
-
-// Launches `kernel` on the context's stream.  While ctx->kernel_timing is
-// set the dispatch itself carries a start/stop event pair (the timestamps a
-// kernel trace reports for it), kept for dmhip_kernel_timing_read.
+// Launches `kernel` on the context's stream.
 template <typename F, typename... Args>
 hipError_t launch_kernel(dmhip_ctx *ctx, F kernel, dim3 grid, dim3 block, uint32_t lds, Args... args) {
-    hipEvent_t start = nullptr, stop = nullptr;
-    if (ctx->kernel_timing) {
-        start = timing_event(ctx);
-        stop = start ? timing_event(ctx) : nullptr;
-        if (!stop && start) {
-            ctx->timing_pool.push_back(start);
-            start = nullptr;
-        }
-    }
-    if (!start) {
-        hipLaunchKernelGGL(kernel, grid, block, lds, ctx->stream, args...);
-        return hipGetLastError();
-    }
-    hipExtLaunchKernelGGL(kernel, grid, block, lds, ctx->stream, start, stop, 0, args...);
-    const hipError_t e = hipGetLastError();
-    ctx->timing_events.push_back(start);
-    ctx->timing_events.push_back(stop);
-    return e;
+    hipLaunchKernelGGL(kernel, grid, block, lds, ctx->stream, args...);
+    return hipGetLastError();
 }
 }  // namespace dm

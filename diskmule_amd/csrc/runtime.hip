@@ -227,26 +227,6 @@ int set_device(dmhip_ctx *ctx) {
     return DMHIP_OK;
 }
 
-static void timing_mark(dmhip_ctx *ctx) {
-    hipEvent_t e = timing_event(ctx);
-    if (!e) return;
-    if (hipEventRecord(e, ctx->stream) != hipSuccess) {
-        ctx->timing_pool.push_back(e);
-        return;
-    }
-    ctx->timing_events.push_back(e);
-}
-
-KernelTimer::KernelTimer(dmhip_ctx *c) : ctx(c) {
-    if (ctx->kernel_timing) timing_mark(ctx);
-}
-
-KernelTimer::~KernelTimer() {
-    // Pairs stay aligned: a failed start leaves an odd count, which the
-    // reader drops.
-    if (ctx->kernel_timing && (ctx->timing_events.size() & 1)) timing_mark(ctx);
-}
-
 static bool matvec_kind_supported(uint32_t type) {
     // The pipelines of MetalContext::prepare_matvec (src/metal.rs:1534-1542).
     return type == 0 || type == 1 || type == 6 || type == 8 || type == 12 || type == 14;
@@ -427,8 +407,6 @@ void dmhip_context_free(dmhip_ctx *ctx) {
     if (ctx->router_tickets) (void)hipFree(ctx->router_tickets);
     if (ctx->argmax_index) (void)hipFree(ctx->argmax_index);
     if (ctx->flags) (void)hipFree(ctx->flags);
-    for (hipEvent_t e : ctx->timing_events) (void)hipEventDestroy(e);
-    for (hipEvent_t e : ctx->timing_pool) (void)hipEventDestroy(e);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     if (ctx->upload) (void)hipStreamDestroy(ctx->upload);
     if (ctx->upload2) (void)hipStreamDestroy(ctx->upload2);
@@ -1098,35 +1076,6 @@ int dmhip_router_result(dmhip_ctx *ctx) {
     return DMHIP_OK;
 }
 
-int dmhip_kernel_timing_enable(dmhip_ctx *ctx, int enable) {
-    DM_REQUIRE(ctx);
-    ctx->kernel_timing = enable != 0;
-    return DMHIP_OK;
-}
-
-int dmhip_kernel_timing_read(dmhip_ctx *ctx, double *total_ms, uint64_t *launches) {
-    DM_REQUIRE(ctx);
-    DM_REQUIRE(total_ms);
-    DM_REQUIRE(launches);
-    DM_CHECK(set_device(ctx));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    double total = 0.0;
-    uint64_t count = 0;
-    std::vector<hipEvent_t> &ev = ctx->timing_events;
-    for (size_t i = 0; i + 1 < ev.size(); i += 2) {
-        float ms = 0.0f;
-        if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess) {
-            total += ms;
-            count += 1;
-        }
-    }
-    ctx->timing_pool.insert(ctx->timing_pool.end(), ev.begin(), ev.end());
-    ev.clear();
-    *total_ms = total;
-    *launches = count;
-    return DMHIP_OK;
-}
-
 int dmhip_copy_device(dmhip_ctx *ctx, void *dst, const void *src, size_t n) {
     DM_REQUIRE(ctx);
     if (n == 0) return DMHIP_OK;
@@ -1134,63 +1083,6 @@ int dmhip_copy_device(dmhip_ctx *ctx, void *dst, const void *src, size_t n) {
     DM_REQUIRE(src);
     DM_CHECK(set_device(ctx));
     DM_HIP(launch_copy_bytes(ctx->stream, dst, src, n));
-    return DMHIP_OK;
-}
-
-int dmhip_probe_empty(dmhip_ctx *ctx, uint32_t workgroups, uint32_t threads) {
-    DM_REQUIRE(ctx);
-    if (workgroups == 0 || threads == 0 || threads > 1024 || threads % 64)
-        return fail(DMHIP_ERR_INVALID_ARGUMENT, "probe grid %u x %u is not a launchable shape", workgroups,
-                    threads);
-    DM_CHECK(set_device(ctx));
-    DM_HIP(launch_probe_empty(ctx->stream, workgroups, threads));
-    return DMHIP_OK;
-}
-
-int dmhip_probe_read(dmhip_ctx *ctx, const void *src, size_t n) {
-    DM_REQUIRE(ctx);
-    if (n == 0) return DMHIP_OK;
-    DM_REQUIRE(src);
-    if (((uintptr_t)src & 15u) || (n & 15u))
-        return fail(DMHIP_ERR_INVALID_ARGUMENT, "probe_read needs a 16-byte aligned source and length");
-    DM_CHECK(set_device(ctx));
-    DM_HIP(launch_probe_read(ctx->stream, src, n, ctx->flags + 1));
-    return DMHIP_OK;
-}
-
-int dmhip_matvec_phase_trace(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, const void *weights,
-                             const float *x, float *y, uint64_t *stamps, size_t capacity, size_t *workgroups) {
-    DM_REQUIRE(ctx);
-    DM_REQUIRE(weights);
-    DM_REQUIRE(x);
-    DM_REQUIRE(y);
-    DM_REQUIRE(stamps);
-    DM_REQUIRE(workgroups);
-    DM_CHECK(validate_device_matvec(type, rows, columns, 1));
-    if (!qmv_supported(type, rows, columns, weights, 1) || !qmv8_supported(type, rows, columns, 1))
-        return fail_unsupported(type, "the int8 decode GEMV at this shape");
-    if (capacity / 4 < (rows + 15) / 16)
-        return fail(DMHIP_ERR_INVALID_ARGUMENT, "phase trace needs %zu stamps, got room for %zu",
-                    4 * ((rows + 15) / 16), capacity);
-    DM_CHECK(set_device(ctx));
-    uint32_t count = 0;
-    DM_HIP(launch_qmv8(ctx, type, (uint32_t)rows, (uint32_t)columns, weights, 1, x, y, nullptr, &count,
-                       ArgmaxFinish{nullptr, nullptr, nullptr, nullptr}, stamps));
-    *workgroups = count;
-    return DMHIP_OK;
-}
-
-int dmhip_matvec_valu_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, const void *weights,
-                             const float *x, float *y) {
-    DM_REQUIRE(ctx);
-    DM_REQUIRE(weights);
-    DM_REQUIRE(x);
-    DM_REQUIRE(y);
-    DM_CHECK(validate_device_matvec(type, rows, columns, 1));
-    if (!qmv_valu_supported(type, rows, columns, weights, x, 1))
-        return fail_unsupported(type, "the VALU decode GEMV at this shape");
-    DM_CHECK(set_device(ctx));
-    DM_HIP(launch_qmv_valu(ctx, type, (uint32_t)rows, (uint32_t)columns, weights, x, y));
     return DMHIP_OK;
 }
 

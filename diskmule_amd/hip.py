@@ -44,8 +44,7 @@ EXPORTED_SYMBOLS = [
     "dmhip_ffn_noalloc_scratch_bytes", "dmhip_ffn_device_noalloc",
     "dmhip_router_top_k_device", "dmhip_router_result", "dmhip_gemm_workspace_bytes", "dmhip_gemm_device",
     "dmhip_event_record", "dmhip_event_elapsed_ms", "dmhip_event_free",
-    "dmhip_kernel_timing_enable", "dmhip_kernel_timing_read", "dmhip_copy_device",
-    "dmhip_probe_empty", "dmhip_probe_read", "dmhip_matvec_phase_trace", "dmhip_matvec_valu_device",
+    "dmhip_copy_device",
     "dmhip_expert_cache_new", "dmhip_expert_cache_new_file", "dmhip_expert_cache_free",
     "dmhip_expert_cache_stats_get",
     "dmhip_expert_cache_slots_per_layer", "dmhip_expert_acquire", "dmhip_expert_release",
@@ -194,14 +193,7 @@ def load_library() -> ctypes.CDLL:
         "dmhip_event_record": ([_vp, ctypes.POINTER(_vp)], ctypes.c_int),
         "dmhip_event_elapsed_ms": ([_vp, _vp, ctypes.POINTER(ctypes.c_float)], ctypes.c_int),
         "dmhip_event_free": ([_vp], None),
-        "dmhip_kernel_timing_enable": ([_vp, ctypes.c_int], ctypes.c_int),
-        "dmhip_kernel_timing_read": ([_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint64)],
-                                     ctypes.c_int),
         "dmhip_copy_device": ([_vp, _vp, _vp, _sz], ctypes.c_int),
-        "dmhip_probe_empty": ([_vp, _u32, _u32], ctypes.c_int),
-        "dmhip_probe_read": ([_vp, _vp, _sz], ctypes.c_int),
-        "dmhip_matvec_phase_trace": ([_vp, _u32, _sz, _sz, _vp, _vp, _vp, _vp, _sz, _szp], ctypes.c_int),
-        "dmhip_matvec_valu_device": ([_vp, _u32, _sz, _sz, _vp, _vp, _vp], ctypes.c_int),
         "dmhip_expert_cache_new": ([_vp, _vp, _sz, ctypes.POINTER(_Layout), _sz, _sz, ctypes.POINTER(_vp)],
                                    ctypes.c_int),
         "dmhip_expert_cache_new_file": ([_vp, ctypes.c_int, ctypes.POINTER(_Layout), _sz, _sz,
@@ -562,39 +554,8 @@ class HipContext:
         _check(load_library().dmhip_event_elapsed_ms(_vp(start), _vp(stop), ctypes.byref(ms)))
         return ms.value
 
-    def kernel_timing_enable(self, enable: bool) -> None:
-        _check(load_library().dmhip_kernel_timing_enable(self._h, int(enable)))
-
-    def kernel_timing_read(self) -> tuple[float, int]:
-        ms = ctypes.c_double()
-        n = ctypes.c_uint64()
-        _check(load_library().dmhip_kernel_timing_read(self._h, ctypes.byref(ms), ctypes.byref(n)))
-        return ms.value, n.value
-
     def copy_device(self, dst_ptr: int, src_ptr: int, nbytes: int) -> None:
         _check(load_library().dmhip_copy_device(self._h, dst_ptr, src_ptr, nbytes))
-
-    # -- measurement hooks ----------------------------------------------------
-    def probe_empty(self, workgroups: int, threads: int) -> None:
-        _check(load_library().dmhip_probe_empty(self._h, workgroups, threads))
-
-    def probe_read(self, src_ptr: int, nbytes: int) -> None:
-        _check(load_library().dmhip_probe_read(self._h, src_ptr, nbytes))
-
-    def matvec_phase_trace(self, kind, rows, columns, w_ptr, x_ptr, y_ptr) -> np.ndarray:
-        """One int8 GEMV launch with per-workgroup s_memrealtime stamps (100 MHz):
-        returns int64 [workgroups, 4] = entry, records built, first weights, end."""
-        cap = 4 * ((rows + 15) // 16)
-        buf = self.new_owned_buffer(8 * cap)
-        wg = ctypes.c_size_t()
-        _check(load_library().dmhip_matvec_phase_trace(self._h, kind, rows, columns, w_ptr, x_ptr, y_ptr,
-                                                       buf.device_ptr, cap, ctypes.byref(wg)))
-        stamps = buf.read(0, 8 * 4 * wg.value, np.uint64).reshape(wg.value, 4).astype(np.int64)
-        buf.free()
-        return stamps
-
-    def matvec_valu_device(self, kind, rows, columns, w_ptr, x_ptr, y_ptr) -> None:
-        _check(load_library().dmhip_matvec_valu_device(self._h, kind, rows, columns, w_ptr, x_ptr, y_ptr))
 
     @staticmethod
     def event_free(ev: int) -> None:

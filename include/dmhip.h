@@ -299,7 +299,8 @@ int dmhip_matvec_batch_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, s
 int dmhip_rms_norm_device(dmhip_ctx *ctx, size_t batch, size_t count, const float *input,
                           const float *weight, float epsilon, float *output);
 
-/* out = silu(gate) * up, count values (src/qwen35/cpu.rs:422-424). */
+/* out = silu(gate) * up, count values (src/qwen35/cpu.rs:422-424); output
+   may be either input. */
 int dmhip_silu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const float *up,
                           float *output);
 
@@ -312,7 +313,7 @@ int dmhip_softcap_device(dmhip_ctx *ctx, size_t count, const float *input, float
 int dmhip_add_device(dmhip_ctx *ctx, size_t count, const float *left, const float *right, float *output);
 
 /* output = gelu_tanh(gate) * up over `count` device values, as
-   dmhip_gelu_mul. */
+   dmhip_gelu_mul; output may be either input. */
 int dmhip_gelu_mul_device(dmhip_ctx *ctx, size_t count, const float *gate, const float *up, float *output);
 
 /* NeoX RoPE in place over device values, with dmhip_rope_neox_in_place's
@@ -375,45 +376,9 @@ int dmhip_event_record(dmhip_ctx *ctx, void **event);
 int dmhip_event_elapsed_ms(void *start, void *stop, float *ms);
 void dmhip_event_free(void *event);
 
-/* Measurement hooks (no counterpart in the reference; used by bench.py).
-   While enabled, the library records HIP events on the compute stream
-   around every launch of its dominant kernels (the quantized matvec and GEMM
-   kernels).  _read waits for the stream, returns the summed duration in ms
-   and the number of timed launches since the previous read, and resets. */
-int dmhip_kernel_timing_enable(dmhip_ctx *ctx, int enable);
-int dmhip_kernel_timing_read(dmhip_ctx *ctx, double *total_ms, uint64_t *launches);
-
 /* Stream-ordered device-to-device copy by a plain streaming kernel (also the
    calibration kernel for HBM byte counters). */
 int dmhip_copy_device(dmhip_ctx *ctx, void *dst, const void *src, size_t n);
-
-/* Launch-floor probes (measurement hooks, no counterpart in the reference):
-   an empty kernel of `workgroups` x `threads` (threads a multiple of 64,
-   at most 1024), and a kernel that reads the n bytes at `src` (a 16-byte
-   aligned device address; n a multiple of 16) with 16-byte loads, four per
-   lane, and keeps nothing.  Their durations bound what a GEMV over the same
-   bytes can reach. */
-int dmhip_probe_empty(dmhip_ctx *ctx, uint32_t workgroups, uint32_t threads);
-int dmhip_probe_read(dmhip_ctx *ctx, const void *src, size_t n);
-
-/* The batch-1 int8 decode GEMV that dmhip_matvec_device runs for Q4_K, Q6_K
-   and Q8_0 rows, with phase stamps (measurement hook): thread 0 of workgroup
-   i writes four values of the 100 MHz s_memrealtime counter to
-   stamps[4i .. 4i+3]: entry, activation records built, first weight group
-   landed, end.  `capacity` counts uint64 elements and must be at least
-   4 * ceil(rows / 16); *workgroups receives the number of workgroups. */
-int dmhip_matvec_phase_trace(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
-                             const void *weights, const float *x, float *y, uint64_t *stamps,
-                             size_t capacity, size_t *workgroups);
-
-/* The VALU form of the batch-1 Q4_K decode GEMV (measurement hook): per
-   weight a v_cvt_f32_ubyte of the masked nibble and an fma, activations held
-   in registers, cross-lane butterflies for the row sums; rows of 1, 2, 4, 8
-   or 16 super-blocks, 16-byte aligned weights and x.  Measured slower than
-   the int8-MFMA kernel at every shape tried, so dmhip_matvec_device does not
-   choose it. */
-int dmhip_matvec_valu_device(dmhip_ctx *ctx, uint32_t ggml_type, size_t rows, size_t columns,
-                             const void *weights, const float *x, float *y);
 
 /* ---------------------------------------------------------------------- */
 /* GLM safetensors matrices (src/metal.rs:738-1146)                        */
@@ -528,7 +493,10 @@ int dmhip_attention_cached_device(dmhip_ctx *ctx, const float *query_device, siz
 /* Waits for the dmhip_attention_cached_device calls made since the previous
    result (or since a host-slice attention call, which ends that period) and
    returns NonFinite "softmax" when any of them met a non-finite score (its
-   output is then not meaningful). */
+   output is then not meaningful).  A host-slice attention call made while
+   device calls await their result reports for them too: it returns
+   NonFinite "softmax" when it or any of them met a non-finite score, and
+   the period then has no result left to read. */
 int dmhip_attention_result(dmhip_ctx *ctx);
 
 /* MetalContext::attention (src/metal.rs:1325-1385): keys and values are host

@@ -506,15 +506,11 @@ pub mod ffi {
             workspace_len: usize,
         ) -> c_int;
 
-        // events and measurement hooks
+        // events and device copies
         pub fn dmhip_event_record(ctx: *mut dmhip_ctx, event: *mut *mut c_void) -> c_int;
         pub fn dmhip_event_elapsed_ms(start: *mut c_void, stop: *mut c_void, ms: *mut f32) -> c_int;
         pub fn dmhip_event_free(event: *mut c_void);
-        pub fn dmhip_kernel_timing_enable(ctx: *mut dmhip_ctx, enable: c_int) -> c_int;
-        pub fn dmhip_kernel_timing_read(ctx: *mut dmhip_ctx, total_ms: *mut f64, launches: *mut u64) -> c_int;
         pub fn dmhip_copy_device(ctx: *mut dmhip_ctx, dst: *mut c_void, src: *const c_void, n: usize) -> c_int;
-        pub fn dmhip_probe_empty(ctx: *mut dmhip_ctx, workgroups: u32, threads: u32) -> c_int;
-        pub fn dmhip_probe_read(ctx: *mut dmhip_ctx, src: *const c_void, n: usize) -> c_int;
 
         // routed-expert residency
         pub fn dmhip_expert_cache_new(

@@ -33,6 +33,17 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert exported == set(header_functions())
 
 
+def test_diagnostics_library_exports_exactly_its_header():
+    """The launch-floor probes live in their own library
+    (include/dmhip_diag.h), not in the product's exports."""
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "dmhip_diag.h")).read(), flags=re.S)
+    declared = set(re.findall(r"\b(dmhip_[a-z0-9_]+)\s*\(", text))
+    path = os.path.join(ROOT, "diskmule_amd", "libdmhip_diag.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    assert set(re.findall(r" T (dmhip_\w+)", out)) == declared == {"dmhip_diag_time_empty", "dmhip_diag_time_read"}
+    assert not declared & set(header_functions())
+
+
 def test_library_is_built_for_gfx950_only():
     # The offload bundle of our own build names its target triples.
     blob = open(hip.library_path(), "rb").read()
@@ -136,9 +147,7 @@ def _rust_struct_fields(name):
 def test_rust_ffi_declares_every_header_function():
     block = _rust_source().split("unsafe extern \"C\" {", 1)[1].split("\n    }\n", 1)[0]
     declared = sorted(set(re.findall(r"pub fn (dmhip_\w+)\(", block)))
-    # the two measurement hooks for one kernel variant each are C-only
-    c_only = {"dmhip_matvec_phase_trace", "dmhip_matvec_valu_device"}
-    assert declared == sorted(set(header_functions()) - c_only)
+    assert declared == sorted(set(header_functions()))
 
 
 def test_rust_status_constants_match_the_header():

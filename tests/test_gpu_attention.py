@@ -241,6 +241,18 @@ def test_non_finite_scores_are_rejected(ctx):
     expect_error("NonFinite", ctx.attention_result)
     ctx.attention_cached_device(good.device_ptr, 2, layer, 1, 1, 2, ob.device_ptr, 2)
     ctx.attention_result()  # a new period starts clean
+    # a host-slice call ends an open period and reports its device calls: a
+    # NaN met by a pending device call makes the clean host call fail, and no
+    # result is left to read afterwards
+    host_out = np.zeros(2, dtype=np.float32)
+    ctx.attention_cached_device(qb.device_ptr, 2, layer, 1, 1, 2, ob.device_ptr, 2)
+    expect_error("NonFinite", ctx.attention_cached, [1.0, 0.0], layer, 1, 1, 2, host_out, operation="softmax")
+    assert host_out.tolist() == [3.0, 4.0]  # the host call's own output is written
+    with pytest.raises(HipError):
+        ctx.attention_result()
+    ctx.attention_cached_device(good.device_ptr, 2, layer, 1, 1, 2, ob.device_ptr, 2)
+    ctx.attention_cached([1.0, 0.0], layer, 1, 1, 2, host_out)  # clean device call, clean host call
+    ctx.attention_cached([1.0, 0.0], layer, 1, 1, 2, host_out)  # and a host call with nothing pending
     for b in (qb, ob, good, layer):
         b.free()
 

@@ -92,6 +92,18 @@ def test_gelu_mul_random_and_device_form(ctx):
     g, u, o = ctx.device_array(gate), ctx.device_array(up), ctx.new_owned_buffer(gate.nbytes)
     ctx.gelu_mul_device(gate.size, g.device_ptr, u.device_ptr, o.device_ptr)
     assert np.array_equal(o.read(0, gate.nbytes, np.float32), out)
+    # in place: the output may be either input
+    ctx.gelu_mul_device(gate.size, g.device_ptr, u.device_ptr, g.device_ptr)
+    assert np.array_equal(g.read(0, gate.nbytes, np.float32), out)
+    g.write(0, gate)
+    ctx.gelu_mul_device(gate.size, g.device_ptr, u.device_ptr, u.device_ptr)
+    assert np.array_equal(u.read(0, gate.nbytes, np.float32), out)
+    # silu_mul's device form, in place over the gate
+    u.write(0, up)
+    want_silu = np.zeros_like(gate)
+    ctx.silu_mul(gate, up, want_silu)
+    ctx.silu_mul_device(gate.size, g.device_ptr, u.device_ptr, g.device_ptr)
+    assert np.array_equal(g.read(0, gate.nbytes, np.float32), want_silu)
     for b in (g, u, o):
         b.free()
 

@@ -7,7 +7,8 @@ import pytest
 from diskmule_amd import ExpertCache, ExpertLayerLayout, HipError, synth
 from diskmule_amd.hip import PinnedHostBuffer
 from oracle import capi
-from tests.tolerance import assert_close, assert_metal_tolerance, top2_gap
+from tests.tolerance import (CHANNEL_TOL_GEMM, CHANNEL_TOL_GEMV, assert_channel_close, assert_close,
+                             assert_metal_tolerance, channel_err, exact_products, top2_gap)
 
 pytestmark = pytest.mark.gpu
 
@@ -180,34 +181,10 @@ def test_decode_gemv_matches_oracle(ctx, kind, rows, cols, cfg):
     ctx.matvec_device(kind, rows, cols, wb.device_ptr, 1, xb.device_ptr, yb.device_ptr)
     got = yb.read(0, rows * 4, np.float32)
     e, c = assert_close(got, want, f"{rows}x{cols}")
-    print(f"  rel_err={e:.2e} cosine={c:.9f}", flush=True)
-
-
-@pytest.mark.parametrize("rows,cols", [(4096, 4096), (1000, 2048), (37, 256), (65, 1024), (12288, 4096)])
-def test_valu_gemv_matches_oracle(ctx, rows, cols):
-    """The VALU form of the batch-1 Q4_K GEMV (a measurement hook): row counts
-    that end mid-pass, 1..16 blocks per row."""
-    w = synth.quantized_matrix(Q4_K, rows, cols, synth.weight_seed(120, rows))
-    x = synth.normal(synth.activation_seed(120, cols), cols)
-    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, rows * 4)
-    ctx.matvec_valu_device(Q4_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr)
-    assert_close(yb.read(0, rows * 4, np.float32), capi.matvec(Q4_K, rows, cols, w, x), f"VALU {rows}x{cols}")
-    with pytest.raises(HipError) as e:
-        ctx.matvec_valu_device(Q6_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr)
-    assert e.value.variant == "UnsupportedTensorType"
-
-
-def test_phase_trace_hook_runs_the_gemv(ctx):
-    """The phase-stamped launch computes the same GEMV, and every workgroup's
-    stamps are in phase order."""
-    rows, cols = 4096, 4096
-    w = synth.quantized_matrix(Q4_K, rows, cols, synth.weight_seed(1))
-    x = synth.normal(synth.activation_seed(1), cols)
-    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, rows * 4)
-    st = ctx.matvec_phase_trace(Q4_K, rows, cols, wb.device_ptr, xb.device_ptr, yb.device_ptr)
-    assert st.shape[0] >= 1 and st.shape[1] == 4
-    assert (np.diff(st, axis=1) >= 0).all()
-    assert_close(yb.read(0, rows * 4, np.float32), capi.matvec(Q4_K, rows, cols, w, x), "traced C1")
+    exact, scale = exact_products(kind, rows, cols, w, x)
+    ch = assert_channel_close(got, exact, scale, CHANNEL_TOL_GEMV, f"{rows}x{cols}")
+    print(f"  rel_err={e:.2e} cosine={c:.9f} channel={ch:.2e} (oracle {channel_err(want, exact, scale):.2e})",
+          flush=True)
 
 
 @pytest.mark.parametrize("batch", [2, 3, 4, 8, 9, 16])
@@ -223,8 +200,10 @@ def test_batched_gemv_matches_oracle(ctx, batch):
         wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, batch * rows * 4)
         ctx.matvec_device(kind, rows, cols, wb.device_ptr, batch, xb.device_ptr, yb.device_ptr)
         got = yb.read(0, batch * rows * 4, np.float32).reshape(batch, rows)
+        exact, scale = exact_products(kind, rows, cols, w, x)
         for b in range(batch):
             assert_close(got[b], want[b], f"type {kind} batch {batch} token {b}")
+            assert_channel_close(got[b], exact[b], scale[b], CHANNEL_TOL_GEMV, f"type {kind} token {b}")
 
 
 @pytest.mark.parametrize("kind,rows,cols,batch", [
@@ -248,8 +227,10 @@ def test_batched_gemv_short_and_misaligned_shapes(ctx, kind, rows, cols, batch):
     wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, batch * rows * 4)
     ctx.matvec_device(kind, rows, cols, wb.device_ptr, batch, xb.device_ptr, yb.device_ptr)
     got = yb.read(0, batch * rows * 4, np.float32).reshape(batch, rows)
+    exact, scale = exact_products(kind, rows, cols, w, x)
     for b in range(batch):
         assert_close(got[b], want[b], f"type {kind} {rows}x{cols} batch {batch} token {b}")
+        assert_channel_close(got[b], exact[b], scale[b], CHANNEL_TOL_GEMV, f"token {b}")
 
 
 @pytest.mark.parametrize("kind,rows,cols,x_stride", [(Q4_K, 1000, 2048, 0), (Q6_K, 1000, 2048, 2048),
@@ -315,14 +296,37 @@ def _int8_record_bound(kind, rows, cols, w, x):
     return wb @ xb + noise
 
 
+def _fp16_pair_bound(kind, rows, cols, w, x):
+    """The fp16 path's worst-case error per output row (batches 3-16): the
+    token is scaled by one power of two so max|x| 2^-e lies in [2^14, 2^15)
+    and split into fp16 hi + lo, so |x~ - x| <= 2^-22 |x| (two roundings of
+    half an fp16 ulp) + 2^-39 max|x| (lo below fp16's normal range).  Q4_K's
+    dmin m sum(x) term takes 32-column sums in fp32 (at most 31 roundings,
+    2^-19 of sum|x|) before the same split, and dmin m <= 63 dmin bounds its
+    factor.  The fp32 noise term is the one of the int8 bound."""
+    dense = capi.dequantize(kind, w, rows * cols).reshape(rows, cols).astype(np.float64)
+    ax = np.abs(x.astype(np.float64))
+    per_x = 2.0 ** -22 * ax + 2.0 ** -39 * ax.max()
+    bound = np.abs(dense) @ per_x
+    if kind == Q4_K:
+        blocks = w.reshape(rows, cols // 256, 144)
+        dmin = blocks[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+        sub = ax.reshape(-1, 32).sum(axis=1).reshape(cols // 256, 8).sum(axis=1)
+        bound += (63.0 * dmin * (2.0 ** -19 + 2.0 ** -22)) @ sub
+    noise = 8.0 * np.sqrt(cols) * np.finfo(np.float32).eps * (np.abs(dense) @ ax)
+    return bound + noise
+
+
 @pytest.mark.parametrize("kind,rows,cols,batch", [(Q4_K, 4096, 4096, 1), (Q6_K, 4096, 4096, 2),
                                                  (Q8_0, 4096, 4096, 1), (Q4_K, 1000, 2048, 4),
-                                                 (Q6_K, 1000, 2048, 8)])
+                                                 (Q6_K, 1000, 2048, 8), (Q4_K, 1000, 2048, 8),
+                                                 (Q4_K, 4096, 12288, 6)])
 def test_in_block_outliers_stay_within_the_bound(ctx, kind, rows, cols, batch):
     """One element 10^4 times its neighbours inside each 256-value block, and
     blocks 10^4 smaller than the rest: batches of 1-4 tokens take the int8
-    records (22 bits per block, checked against the bound derived above, and
-    the tolerance), batch 8 the fp16 path (per-token scale)."""
+    records (22 bits per block), batches 6 and 8 the fp16 path (22 bits per
+    token); each is checked against the bound derived for its path, and the
+    tolerance."""
     print(f"outliers type={kind} {rows}x{cols} batch={batch}", flush=True)
     w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(130, kind))
     x = np.stack([_outlier_activations(131 + b, cols) for b in range(batch)])
@@ -334,9 +338,11 @@ def test_in_block_outliers_stay_within_the_bound(ctx, kind, rows, cols, batch):
         e, _ = assert_close(got[b], want[b], f"outliers type {kind} token {b}")
         if batch <= 4:
             bound = _int8_record_bound(kind, rows, cols, w, x[b])
-            err = np.abs(got[b].astype(np.float64) - want[b])
-            assert (err <= bound).all(), f"token {b}: worst excess {np.max(err - bound):.3g}"
-        print(f"  token {b}: rel_err={e:.2e}", flush=True)
+        else:
+            bound = _fp16_pair_bound(kind, rows, cols, w, x[b])
+        err = np.abs(got[b].astype(np.float64) - want[b])
+        assert (err <= bound).all(), f"token {b}: worst excess {np.max(err - bound):.3g}"
+        print(f"  token {b}: rel_err={e:.2e} worst err/bound={float((err / bound).max()):.3f}", flush=True)
 
 
 @pytest.mark.parametrize("kind", [Q6_K, Q4_K])
@@ -382,6 +388,81 @@ def test_prefill_gemm_with_in_block_outliers(ctx, kind):
     print(f"  type {kind}: worst rel_err={worst:.2e}", flush=True)
 
 
+_SMALL_D = (1e-6, 1e-5, 3e-5)
+
+
+def _small_scale_matrix(kind, rows, cols, seed):
+    """Seeded blocks whose super-block scale d is replaced by 1e-6, 1e-5 or
+    3e-5 (fp16 subnormals: 17, 168 and 503 times 2^-24) on rows 4j, 4j + 1
+    and 4j + 2, and by 1e-6 on the even blocks of rows 4j + 3, beside rows
+    of the seeded scales; Q4_K's dmin becomes half the new d.  Such rows are
+    30 to 2000 times smaller than their neighbours, so the per-channel
+    measure sees them where the vector-wide one would not."""
+    w = synth.quantized_matrix(kind, rows, cols, seed).copy()
+    elems, nbytes = synth.BLOCK[kind]
+    blk = w.reshape(rows, cols // elems, nbytes)
+    d_at = {Q4_K: 0, Q6_K: 208, Q8_0: 0}[kind]
+
+    def put(part, dv):
+        part[..., d_at:d_at + 2] = np.float16([dv]).view(np.uint8)
+        if kind == Q4_K:
+            part[..., 2:4] = np.float16([dv / 2]).view(np.uint8)
+
+    for j, dv in enumerate(_SMALL_D):
+        put(blk[j::4], dv)
+    put(blk[3::4, 0::2], _SMALL_D[0])
+    return w
+
+
+@pytest.mark.parametrize("kind", [Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
+def test_small_scale_blocks_gemv(ctx, kind, batch):
+    """Super-block scales in fp16's subnormal range beside ordinary rows: the
+    int8 records (batch 1-4) and the fp16 pairs (batch 8) keep every output
+    channel within the per-channel bar, not only the vector-wide one."""
+    rows, cols = 4096, 4096
+    w = _small_scale_matrix(kind, rows, cols, synth.weight_seed(150, kind))
+    x = synth.normal(synth.activation_seed(150, batch), batch * cols).reshape(batch, cols)
+    want = np.stack([capi.matvec(kind, rows, cols, w, x[b]) for b in range(batch)])
+    wb, xb, yb = dev(ctx, w), dev(ctx, x), dev_out(ctx, batch * rows * 4)
+    ctx.matvec_device(kind, rows, cols, wb.device_ptr, batch, xb.device_ptr, yb.device_ptr)
+    got = yb.read(0, batch * rows * 4, np.float32).reshape(batch, rows)
+    exact, scale = exact_products(kind, rows, cols, w, x)
+    worst = 0.0
+    for b in range(batch):
+        assert_close(got[b], want[b], f"small scales type {kind} token {b}")
+        worst = max(worst, assert_channel_close(got[b], exact[b], scale[b], CHANNEL_TOL_GEMV,
+                                                f"small scales type {kind} token {b}"))
+        small = np.arange(rows) % 4 == 0  # the d = 1e-6 rows alone
+        assert channel_err(got[b][small], exact[b][small], scale[b][small]) <= CHANNEL_TOL_GEMV
+    print(f"  type {kind} batch {batch}: channel={worst:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("kind", [Q4_K, Q6_K, Q8_0])
+def test_small_scale_blocks_gemm(ctx, kind):
+    """The GEMM's fp16 weight factors at subnormal super-block scales: d is
+    itself an fp16 value, so d sc (Q4_K, Q6_K), dmin m and every weight
+    below 2^-14 lie on fp16's 2^-24 grid and convert exactly; above it one
+    rounding of 2^-11 applies as for any other block.  Every token's
+    channels stay within the GEMM's per-channel bar."""
+    m, n, k = 160, 256, 4096
+    a = synth.to_bf16_bits(synth.normal(synth.activation_seed(151, kind), m * k))
+    w = _small_scale_matrix(kind, n, k, synth.weight_seed(151, kind))
+    want = capi.gemm_tokenwise(kind, m, n, k, a, w)
+    ab, wb, cb = dev(ctx, a), dev(ctx, w), dev_out(ctx, m * n * 4)
+    ws = dev_out(ctx, ctx.gemm_workspace_bytes(m, k))
+    ctx.gemm_device(kind, m, n, k, ab.device_ptr, wb.device_ptr, cb.device_ptr, ws.device_ptr, len(ws))
+    got = cb.read(0, m * n * 4, np.float32).reshape(m, n)
+    for r in range(m):
+        assert_close(got[r], want[r], f"small-scale GEMM type {kind} token {r}")
+    exact, scale = exact_products(kind, n, k, w, synth.bf16_bits_to_f32(a).reshape(m, k))
+    ch = assert_channel_close(got, exact, scale, CHANNEL_TOL_GEMM, f"small-scale GEMM type {kind}")
+    small = np.arange(n) % 4 == 0
+    ch_small = channel_err(got[:, small], exact[:, small], scale[:, small])
+    assert ch_small <= CHANNEL_TOL_GEMM
+    print(f"  type {kind}: channel={ch:.2e} (d = 1e-6 rows {ch_small:.2e})", flush=True)
+
+
 def test_q6_k_large_scales_take_the_exact_split_path(ctx):
     rows, cols = 64, 1024
     w = synth.quantized_matrix(Q6_K, rows, cols, synth.weight_seed(55)).reshape(-1, 210).copy()
@@ -409,6 +490,9 @@ def test_output_head_q6_k_with_argmax(ctx):
     idx = ctx.argmax_result()
     got = yb.read(0, rows * 4, np.float32)
     assert_close(got, want, "C2 logits")
+    exact, scale = exact_products(Q6_K, rows, cols, w, x)
+    ch = assert_channel_close(got, exact, scale, CHANNEL_TOL_GEMV, "C2 logits")
+    print(f"  channel={ch:.2e} (oracle {channel_err(want, exact, scale):.2e})", flush=True)
     assert idx == capi.argmax(got)  # the fused argmax is exact on the GPU's logits
     gap = top2_gap(want)
     print(f"  argmax gpu={idx} cpu={want_idx} top2 gap={gap:.4g}", flush=True)
@@ -1043,7 +1127,10 @@ def _gemm_check(ctx, kind, m, n, k, seed, what):
     for r in range(m):
         e, _ = assert_close(got[r], want[r], f"{what} type {kind} token {r}")
         worst = max(worst, e)
-    print(f"  worst rel_err={worst:.2e}", flush=True)
+    exact, scale = exact_products(kind, n, k, w, synth.bf16_bits_to_f32(a).reshape(m, k))
+    ch = assert_channel_close(got, exact, scale, CHANNEL_TOL_GEMM, f"{what} type {kind}")
+    print(f"  worst rel_err={worst:.2e} channel={ch:.2e} (oracle {channel_err(want, exact, scale):.2e})",
+          flush=True)
     return worst
 
 

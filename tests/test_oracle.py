@@ -220,6 +220,101 @@ def test_dense_ffn_is_the_composition_of_its_parts():
         assert np.isclose(float(capi.silu(v)), v / (1.0 + np.exp(-v)), rtol=1e-6, atol=1e-12)
 
 
+# ---- GLM expert activation (src/glm52/expert.rs:260-267) --------------------
+#
+# orc_silu_mul_glm evaluates (g / (1 + exp(-g))) * u in f32: one exp, then
+# the sum, the quotient and the product each round once.  Against the exact
+# value computed in float64 its relative error is at most the exp's (glibc
+# expf: under 1 ulp; 2 allowed) plus three roundings of 2^-24, so 6 * 2^-24,
+# with two subnormal quanta of absolute slack where the product underflows.
+# Below g = -88.72 the f32 exp(-g) overflows to +inf and the quotient is -0,
+# as the reference's f32 code computes it; the float64 check stops at -88.
+
+GLM_REL = 6.0 * 2.0 ** -24
+GLM_ABS = 2.0 * 2.0 ** -149
+
+
+def _glm_activation_excess(got, gate, up) -> float:
+    """Largest |got - exact| / bound over the elements (<= 1 passes)."""
+    g = np.asarray(gate, dtype=np.float64)
+    u = np.asarray(up, dtype=np.float64)
+    exact = g / (1.0 + np.exp(-g)) * u
+    err = np.abs(np.asarray(got, dtype=np.float64) - exact)
+    return float((err / (GLM_REL * np.abs(exact) + GLM_ABS)).max())
+
+
+def _glm_inputs(seed=61, count=12000):
+    """Gates over [-88, 88] (uniform, plus a log-spread of small magnitudes
+    of both signs) and ups of magnitude 1e-3 .. 1e3 of both signs."""
+    rng = np.random.default_rng(seed)
+    g = np.concatenate([rng.uniform(-88.0, 88.0, count // 2),
+                        np.sign(rng.uniform(-1, 1, count // 2)) * 10.0 ** rng.uniform(-30, 1.9, count // 2)])
+    u = rng.standard_normal(count) * 10.0 ** rng.uniform(-3, 3, count)
+    return g.astype(np.float32), u.astype(np.float32)
+
+
+def test_glm_expert_activation_against_float64():
+    g, u = _glm_inputs()
+    got = capi.silu_mul_glm(g, u)
+    assert _glm_activation_excess(got, g, u) <= 1.0
+
+
+def test_glm_expert_activation_checks_catch_planted_mistakes():
+    """The float64 check rejects each plausible slip in a numpy f32
+    restatement of the formula: exp(+g), 1 - exp(-g), the up factor dropped,
+    the sigmoid without the gate factor, and g / exp(-g)."""
+    g, u = _glm_inputs(62, 4000)
+    gf, uf = g.astype(np.float32), u.astype(np.float32)
+    one = np.float32(1.0)
+    with np.errstate(over="ignore", divide="ignore", invalid="ignore"):
+        right = (gf / (one + np.exp(-gf))) * uf
+        slips = {
+            "exp(+g)": (gf / (one + np.exp(gf))) * uf,
+            "1 - exp(-g)": (gf / (one - np.exp(-gf))) * uf,
+            "no up": gf / (one + np.exp(-gf)),
+            "sigmoid only": (one / (one + np.exp(-gf))) * uf,
+            "no one": (gf / np.exp(-gf)) * uf,
+        }
+        assert _glm_activation_excess(right, g, u) <= 1.0
+        for name, wrong in slips.items():
+            assert not _glm_activation_excess(wrong, g, u) <= 1.0, name
+
+
+def test_glm_expert_activation_against_the_pinned_silu():
+    """Against orc_silu (pinned on its two branches) times up: the two
+    evaluation orders differ by a few roundings, never more."""
+    g, u = _glm_inputs(63, 3000)
+    keep = g >= -87.0  # orc_silu's exp(g) branch has no overflow; compare where both are finite
+    g, u = g[keep], u[keep]
+    got = capi.silu_mul_glm(g, u)
+    via_silu = np.array([capi.silu(float(a)) for a in g], dtype=np.float32) * u
+    rel = np.abs(got.astype(np.float64) - via_silu) / (np.abs(via_silu.astype(np.float64)) + GLM_ABS)
+    assert float(rel.max()) <= 12.0 * 2.0 ** -24
+
+
+def test_glm_expert_activation_special_values():
+    """Exact results where the formula leaves no rounding: g = +-0 gives a
+    signed zero; for g >= 17 the f32 exp(-g) is below half an ulp of 1, so the
+    result is the single rounding of g * u; past g = -88.72 exp(-g) overflows
+    and the result is -0 (times the sign of u); inf and NaN propagate as
+    IEEE arithmetic says."""
+    def one(gv, uv):
+        return capi.silu_mul_glm(np.float32([gv]), np.float32([uv]))[0]
+
+    assert bits(one(0.0, 1.0)) == 0 and bits(one(-0.0, 1.0)) == 0x80000000
+    assert bits(one(0.0, -2.5)) == 0x80000000
+    for gv in (17.0, 30.0, 88.0, 1e4):
+        for uv in (1.0, 0.1, -3.7, 1e-20):
+            want = np.float32(np.float32(gv) * np.float32(uv))
+            assert bits(one(gv, uv)) == bits(want), (gv, uv)
+    for gv in (-30.0, -60.0, -88.0):
+        got = one(gv, 1.5)
+        assert got < 0 and _glm_activation_excess([got], [gv], [1.5]) <= 1.0, gv
+    assert bits(one(-89.0, 2.0)) == 0x80000000 and bits(one(-1e4, -2.0)) == 0
+    assert one(float("inf"), 2.0) == float("inf") and one(float("inf"), -2.0) == float("-inf")
+    assert np.isnan(one(float("nan"), 1.0)) and np.isnan(one(float("-inf"), 1.0))
+
+
 def test_moe_layer_is_the_composition_of_its_parts():
     hidden, width, experts, k, batch = 256, 256, 16, 4, 3
     router = synth.to_bf16_bits(synth.normal(41, experts * hidden) * np.float32(0.02))

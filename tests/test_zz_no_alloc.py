@@ -70,3 +70,34 @@ def test_noalloc_ffn_matches_the_workspace_entry_point():
         assert e.value.variant == "InvalidArgument"
     finally:
         ctx.close()
+
+
+def test_noalloc_ffn_with_mixed_gate_and_up_types():
+    """An unfused FFN whose gate is Q6_K and up Q4_K at batch 8: the up
+    matrix's activation fragments (nine scale slots per block) are larger
+    than the gate's (eight) and the down input's, and the lent region is
+    sized for the largest, so the call completes and equals the workspace
+    entry point bit for bit."""
+    ctx = HipContext(0)
+    try:
+        batch, hidden, ffn, seed = 8, 4096, 1024, 21
+        g = synth.quantized_matrix(Q6_K, ffn, hidden, synth.weight_seed(seed, 0))
+        u = synth.quantized_matrix(Q4_K, ffn, hidden, synth.weight_seed(seed, 1))
+        d = synth.quantized_matrix(Q6_K, hidden, ffn, synth.weight_seed(seed, 2))
+        h = synth.normal(synth.activation_seed(seed, batch), batch * hidden).reshape(batch, hidden)
+        gb, ub, db, hb = (ctx.device_array(a) for a in (g, u, d, h))
+        yb, yw = ctx.new_owned_buffer(batch * hidden * 4), ctx.new_owned_buffer(batch * hidden * 4)
+        ws = ctx.new_owned_buffer(ctx.ffn_workspace_bytes(batch, hidden, ffn))
+        print(f"noalloc FFN mixed types batch={batch} hidden={hidden} ffn={ffn}", flush=True)
+        ctx.ffn_device_noalloc(batch, hidden, ffn, Q6_K, gb.device_ptr, Q4_K, ub.device_ptr, Q6_K, db.device_ptr,
+                               1e-6, hb.device_ptr, yb.device_ptr)
+        ctx.ffn_device(batch, hidden, ffn, Q6_K, gb.device_ptr, Q4_K, ub.device_ptr, Q6_K, db.device_ptr,
+                       1e-6, hb.device_ptr, yw.device_ptr, ws.device_ptr, len(ws))
+        got = yb.read(0, batch * hidden * 4, np.float32).reshape(batch, hidden)
+        want = yw.read(0, batch * hidden * 4, np.float32).reshape(batch, hidden)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        ref = capi.dense_ffn(batch, hidden, ffn, Q6_K, g, Q4_K, u, Q6_K, d, h)
+        for b in range(batch):
+            assert_close(got[b], ref[b], f"mixed types token {b}")
+    finally:
+        ctx.close()

@@ -23,7 +23,7 @@ measured the same way, a Q8_0 GEMV entry (the third k-quant of the north
 star, which no configuration uses) and F16 / F32 / Q5_0 GEMV entries (the
 other row types of a Gemma-class GGUF).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|dense|st|attn|attn_host|copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|q8|dense|st|attn|attn_host|host|copy]
 """
 from __future__ import annotations
 
@@ -375,6 +375,70 @@ def bench_c4(ctx, synth, steps, warmup):
     return out
 
 
+def bench_host(ctx, synth, steps, warmup):
+    """The drop-in host-slice path an unchanged graph takes (src/metal.rs:
+    1562-1604, :1801-1882: host x in, host y out, synchronous per call):
+    matvec_mapped at the C1 and C2 shapes over a mapped GGUF-like buffer, and
+    at the C4 shape one routed expert as the Gemma 4 graph runs it
+    (src/gemma4/metal.rs:1003-1031): acquire -> matvec_owned gate_up ->
+    silu_mul -> matvec_owned down -> release, all slots resident.  Host clock
+    per call, next to the device-resident kernel time of the same shape
+    (matvec_device, events, back to back)."""
+    from diskmule_amd import ExpertCache, ExpertLayerLayout
+    out = {}
+    for tag, kind, rows, cols in (("C1", Q4_K, 4096, 4096), ("C2", Q6_K, 151936, 4096)):
+        w = synth.quantized_matrix(kind, rows, cols, synth.weight_seed(1 if tag == "C1" else 2))
+        x = synth.normal(synth.activation_seed(1 if tag == "C1" else 2), cols)
+        mb = ctx.map_read_only(w)
+        y = np.zeros(rows, np.float32)
+        for _ in range(warmup + 2):
+            ctx.matvec_mapped(kind, rows, cols, mb, 0, w.size, x, y)
+        n = max(steps, 50 if tag == "C1" else 20)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            ctx.matvec_mapped(kind, rows, cols, mb, 0, w.size, x, y)
+        call_us = (time.perf_counter() - t0) / n * 1e6
+        xb, yb = upload(ctx, x), ctx.new_owned_buffer(rows * 4)
+        dev_us = timed_loop(ctx, lambda i: ctx.matvec_device(kind, rows, cols, mb.device_ptr, 1, xb.device_ptr,
+                                                              yb.device_ptr), n) / n * 1e3
+        out[tag] = {"rows": rows, "columns": cols, "call_us": call_us, "device_kernel_us": dev_us,
+                    "host_overhead_us": call_us - dev_us}
+        log(f"host-slice {tag}: matvec_mapped {call_us:.1f} us per call, device-resident {dev_us:.1f} us")
+        for b in (mb, xb, yb):
+            b.free()
+    hidden, width, experts, slots = 2048, 768, 16, 8
+    gu_bytes = 2 * width * synth.row_bytes(Q4_K, hidden)
+    dn_bytes = hidden * synth.row_bytes(Q6_K, width)
+    gu = synth.quantized_matrix(Q4_K, experts * 2 * width, hidden, synth.weight_seed(4, 0))
+    dn = synth.quantized_matrix(Q6_K, experts * hidden, width, synth.weight_seed(4, 1))
+    src = np.concatenate([gu, dn])
+    cache = ExpertCache(ctx, src, [ExpertLayerLayout(experts, 0, gu_bytes, gu.size, dn_bytes)], slots)
+    x = synth.normal(synth.activation_seed(4, 7), hidden)
+    g_u = np.zeros(2 * width, np.float32)
+    act = np.zeros(width, np.float32)
+    y = np.zeros(hidden, np.float32)
+
+    def expert(e):
+        slot, gub, dnb = cache.acquire(0, e)
+        ctx.matvec_owned(Q4_K, 2 * width, hidden, gub, 0, gu_bytes, x, g_u)
+        ctx.silu_mul(g_u[:width], g_u[width:], act)
+        ctx.matvec_owned(Q6_K, hidden, width, dnb, 0, dn_bytes, act, y)
+        cache.release(0, slot)
+
+    for e in range(slots):
+        expert(e)
+    n = max(steps, 40)
+    t0 = time.perf_counter()
+    for i in range(n):
+        expert(i % slots)
+    out["C4_expert"] = {"per_expert_us": (time.perf_counter() - t0) / n * 1e6, "calls_per_expert": 3,
+                        "note": "acquire (hit), matvec_owned gate_up 1536x2048 Q4_K, silu_mul, matvec_owned "
+                                "down 2048x768 Q6_K, release"}
+    log(f"host-slice C4 expert: {out['C4_expert']['per_expert_us']:.1f} us per expert (3 synchronous calls)")
+    cache.free()
+    return out
+
+
 def bench_c5(ctx, synth, steps, warmup):
     """C5: 512-token prefill GEMM at K = 4096, N = 4096 and 12288, for Q4_K
     (the headline) and the other two quantized types of the path.  `ms` is
@@ -644,7 +708,7 @@ def main() -> int:
     if args.only:
         fn = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
               "q8": bench_q8, "dense": bench_dense, "st": bench_st, "attn": bench_attn, "attn_host": bench_attn_host,
-              "copy": bench_copy}[args.only]
+              "host": bench_host, "copy": bench_copy}[args.only]
         res = fn(ctx, synth, args.steps, args.warmup)
         print(json.dumps(res[0] if isinstance(res, tuple) else res))
         return 0
@@ -652,7 +716,8 @@ def main() -> int:
     c2, (w2, x2) = bench_c2(ctx, synth, args.steps, args.warmup)
     details = {"C2": c2}
     for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5), ("Q8_0", bench_q8),
-                     ("dense", bench_dense), ("safetensors", bench_st), ("attention", bench_attn)):
+                     ("dense", bench_dense), ("safetensors", bench_st), ("attention", bench_attn),
+                     ("host_slice", bench_host)):
         details[name] = fn(ctx, synth, max(3, args.steps // 2), args.warmup)
     log("CPU baseline")
     cpu = cpu_baseline(w2, x2, args.cpu_seconds)

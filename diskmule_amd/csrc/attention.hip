@@ -628,11 +628,12 @@ static uint32_t host_call_mark(dmhip_ctx *ctx) {
     return ctx->attn_pending ? ctx->attn_mark : next_mark(ctx);
 }
 
-static int attention_finish_host(dmhip_ctx *ctx, float *output, const float *dout, size_t query_width) {
+static int attention_finish_host(dmhip_ctx *ctx, HostCall &hc, float *output, const float *dout,
+                                 size_t query_width) {
     uint32_t flag = 0;
-    DM_HIP(hipMemcpyAsync(output, dout, query_width * 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipMemcpyAsync(&flag, ctx->flags + kAttnFlagWord, 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
+    DM_CHECK_STATUS(hc.out(output, dout, query_width * 4));
+    DM_CHECK_STATUS(hc.out(&flag, ctx->flags + kAttnFlagWord, 4));
+    DM_CHECK_STATUS(hc.finish());
     ctx->attn_pending = false;
     if (flag == ctx->attn_mark) return fail_non_finite("softmax");
     return DMHIP_OK;
@@ -787,12 +788,14 @@ int dmhip_attention_cached(dmhip_ctx *ctx, const float *query, size_t query_len,
     DM_CHECK_STATUS(ctx->in.ensure(bytes));
     DM_CHECK_STATUS(ctx->out.ensure(bytes));
     float *dq = (float *)ctx->in.ptr, *dout = (float *)ctx->out.ptr;
-    DM_HIP(hipMemcpyAsync(dq, query, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK_STATUS(hc.begin(2 * bytes + 4));
+    DM_CHECK_STATUS(hc.in(dq, query, bytes));
     const uint32_t mark = host_call_mark(ctx);
     DM_CHECK_STATUS(enqueue_attention(ctx, dq, layer->keys, layer->values, layer->capacity, layer->width,
                                       query_heads, kv_heads, head_dimension, start, visible, dout,
                                       BadFlag{ctx->flags + kAttnFlagWord, mark}));
-    return attention_finish_host(ctx, output, dout, query_len);
+    return attention_finish_host(ctx, hc, output, dout, query_len);
 }
 
 int dmhip_attention_cached_device(dmhip_ctx *ctx, const float *query_device, size_t query_len,
@@ -859,13 +862,15 @@ int dmhip_attention(dmhip_ctx *ctx, const float *query, size_t query_len, const 
     DM_CHECK_STATUS(ctx->enc.ensure(2 * kv_span));
     float *dq = (float *)ctx->in.ptr, *dout = (float *)ctx->out.ptr;
     float *dk = (float *)ctx->enc.ptr, *dv = (float *)((uint8_t *)ctx->enc.ptr + kv_span);
-    DM_HIP(hipMemcpyAsync(dq, query, q_bytes, hipMemcpyHostToDevice, ctx->stream));
-    DM_HIP(hipMemcpyAsync(dk, keys + start * cache_width, kv_bytes, hipMemcpyHostToDevice, ctx->stream));
-    DM_HIP(hipMemcpyAsync(dv, values + start * cache_width, kv_bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK_STATUS(hc.begin(2 * q_bytes + 2 * kv_bytes + 4));
+    DM_CHECK_STATUS(hc.in(dq, query, q_bytes));
+    DM_CHECK_STATUS(hc.in(dk, keys + start * cache_width, kv_bytes));
+    DM_CHECK_STATUS(hc.in(dv, values + start * cache_width, kv_bytes));
     const uint32_t mark = host_call_mark(ctx);
     DM_CHECK_STATUS(enqueue_attention(ctx, dq, dk, dv, visible, cache_width, query_heads, kv_heads,
                                       head_dimension, 0, visible, dout, BadFlag{ctx->flags + kAttnFlagWord, mark}));
-    return attention_finish_host(ctx, output, dout, query_len);
+    return attention_finish_host(ctx, hc, output, dout, query_len);
 }
 
 }  // extern "C"

@@ -102,7 +102,7 @@ namespace {
 // issued, so activations requested after the weights could only be used
 // once the weights had arrived.
 template <int TOK, int XP> struct XPre8 {
-    floatx4 v[TOK][XP];
+    floatx4 v[TOK][XP > 0 ? XP : 1];
 };
 
 template <uint32_t TYPE, int TOK, uint32_t WAVES, int XP>
@@ -136,13 +136,16 @@ template <uint32_t later, int TOK, int XP>
 __device__ __forceinline__ void wait_x8(XPre8<TOK, XP> &pre) {
     static_assert(later < 64, "vmcnt is 6 bits");
     constexpr int N = TOK * XP;
-    static_assert(N >= 1 && N <= 4, "1 to 4 preloaded blocks");
+    static_assert(N >= 0 && N <= 4, "0 to 4 preloaded blocks");
     // preloaded block i is pre.v[i / XP][i % XP]
+    constexpr int D = XP > 0 ? XP : 1;
     floatx4 &a = pre.v[0][0];
-    floatx4 &b = pre.v[(N > 1 ? 1 : 0) / XP][(N > 1 ? 1 : 0) % XP];
-    floatx4 &c = pre.v[(N > 2 ? 2 : 0) / XP][(N > 2 ? 2 : 0) % XP];
-    floatx4 &d = pre.v[(N > 3 ? 3 : 0) / XP][(N > 3 ? 3 : 0) % XP];
-    if constexpr (N == 1) {
+    floatx4 &b = pre.v[(N > 1 ? 1 : 0) / D][(N > 1 ? 1 : 0) % D];
+    floatx4 &c = pre.v[(N > 2 ? 2 : 0) / D][(N > 2 ? 2 : 0) % D];
+    floatx4 &d = pre.v[(N > 3 ? 3 : 0) / D][(N > 3 ? 3 : 0) % D];
+    if constexpr (N == 0) {
+        // nothing preloaded
+    } else if constexpr (N == 1) {
         asm volatile("s_waitcnt vmcnt(%1)" : "+v"(a) : "n"(later) : "memory");
     } else if constexpr (N == 2) {
         asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(later) : "memory");
@@ -496,8 +499,14 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     // Activation blocks of each wave loaded ahead of the weights: what a
     // wave's share of a 4096-column row is (16 blocks over W waves), so that
     // no record is computed for a block past the end; wider rows load the
-    // rest after the weights.
-    constexpr int XP = TOK >= 2 ? 1 : (W >= 16 ? 1 : 2);
+    // rest after the weights.  None on the persistent one-tile-per-wave
+    // schedule of single matrices (S = 1, tall matrices), which requests its
+    // first weights behind a branch and builds the records after them:
+    // measured on MI355X at C2 (Q6_K 151936 x 4096 with the argmax,
+    // interleaved runs on one box) 94.0-94.2 us against 97.3-97.8 us with
+    // the preloading, branch-free prologue the split schedules use, which
+    // also read 4.7% more bytes per launch.
+    constexpr int XP = (S == 1 && !PC && MODE != 2) ? 0 : (TOK >= 2 ? 1 : (W >= 16 ? 1 : 2));
     constexpr uint32_t REC = Rec8<TYPE>::bytes;
     constexpr uint32_t BB = kBlock8<TYPE>;
     using ST = Stage8<TYPE, G>;
@@ -570,10 +579,17 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
     // requested before the records are built.
     XPre8<TOK, XP> xpre;
     preload_x8<TYPE, TOK, WAVES, XP>(x, x_stride, columns, xpre);
-    // Issued without a branch (an idle wave's loads all read past the end).
     bool active = tile < t_end;
-    setup(active ? tile : 0u, active);
-    fetch(kpart, active && kpart < groups);
+    if constexpr (XP == 0) {
+        if (active) {
+            setup(tile, true);
+            if (kpart < groups) fetch(kpart, true);
+        }
+    } else {
+        // Issued without a branch (an idle wave's loads all read past the end).
+        setup(active ? tile : 0u, active);
+        fetch(kpart, active && kpart < groups);
+    }
     wait_x8<NL * NM>(xpre);
     uint32_t row_base = next_row_base;
 

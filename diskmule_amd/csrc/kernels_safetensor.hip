@@ -501,14 +501,15 @@ int dmhip_matvec_safetensor_mapped(dmhip_ctx *ctx, uint32_t dtype, size_t rows, 
     DM_CHECK_STATUS(set_device(ctx));
     DM_CHECK_STATUS(ctx->in.ensure(columns * 4));
     DM_CHECK_STATUS(ctx->out.ensure(rows * 4));
-    DM_HIP(hipMemcpyAsync(ctx->in.ptr, input, columns * 4, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK_STATUS(hc.begin(columns * 4 + rows * 4));
+    DM_CHECK_STATUS(hc.in(ctx->in.ptr, input, columns * 4));
     const uint8_t *w = (const uint8_t *)mapping->dev + encoded_offset;
     const float *sc = fmt == kStBf16 ? nullptr : (const float *)((const uint8_t *)scale_mapping->dev + scale_offset);
     DM_CHECK_STATUS(st_enqueue(ctx, fmt, rows, columns, w, sc, scale_length / 4, group, scale_columns,
                                (const float *)ctx->in.ptr, (float *)ctx->out.ptr));
-    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, rows * 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    return DMHIP_OK;
+    DM_CHECK_STATUS(hc.out(output, ctx->out.ptr, rows * 4));
+    return hc.finish();
 }
 
 int dmhip_matvec_safetensor(dmhip_ctx *ctx, uint32_t dtype, size_t rows, size_t columns, const uint8_t *encoded,

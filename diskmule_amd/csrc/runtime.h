@@ -63,6 +63,22 @@ struct Scratch {
     void release();
 };
 
+// Pinned host memory that the synchronous host-slice calls stage their
+// inputs and outputs through: one memcpy into it and one DMA copy each way,
+// instead of the runtime's pageable copy path.  Every call that uses it waits
+// for its stream before returning, so no copy out of it is in flight when it
+// is refilled or replaced.
+struct HostBounce {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    int ensure(size_t need);
+    void release();
+};
+// Inputs and outputs of one host-slice call up to this size go through the
+// bounce buffer; larger ones (the unmapped matvec's whole matrix) keep the
+// runtime's path.
+constexpr size_t kHostBounceMax = 8u << 20;
+
 // (block elements, block bytes) of a ggml type, src/gguf.rs:321-342.
 bool type_layout(uint32_t type, uint32_t *block_elements, uint32_t *block_bytes);
 const char *type_name(uint32_t type);
@@ -83,6 +99,7 @@ struct dmhip_ctx {
     char name[256] = {0};
     int compute_units = 0;
     dm::Scratch in, out, enc, aux;          // host-slice staging
+    dm::HostBounce bounce;                   // pinned host side of the host-slice copies
     dm::Scratch partials;                    // per-wave argmax candidates
     dm::Scratch attn;                        // attention chunk partials
     dm::Scratch attn_tickets;                // attention combine counters, zero between calls
@@ -126,6 +143,36 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
 int enqueue_matvec_argmax(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
                           const void *w, const float *x, float *y, uint32_t *index_device);
 int set_device(dmhip_ctx *ctx);
+
+// The copies of one synchronous host-slice call.  begin(total) sizes the
+// call's inputs and outputs together: up to kHostBounceMax they are staged in
+// the context's pinned bounce buffer (in() copies the host data into it and
+// enqueues the DMA; out() enqueues the DMA into it and finish() copies it to
+// the caller after waiting for the stream); above that, the host pointers go
+// to the runtime directly.  finish() always waits for the stream, and a call
+// that returns early (an error after its first copy) waits in the
+// destructor, so no copy out of the bounce buffer outlives the call.
+struct HostCall {
+    dmhip_ctx *ctx;
+    bool staged = false;
+    bool open = false;
+    size_t used = 0;
+    struct Pending {
+        void *dst;
+        const void *src;
+        size_t n;
+    } pending[2];
+    int outs = 0;
+    explicit HostCall(dmhip_ctx *c) : ctx(c) {}
+    ~HostCall();
+    HostCall(const HostCall &) = delete;
+    HostCall &operator=(const HostCall &) = delete;
+    int begin(size_t total);
+    int in(void *device_dst, const void *host_src, size_t n);
+    int out(void *host_dst, const void *device_src, size_t n);
+    int finish();
+};
+
 // Resolves (once per device, with that device current) the device address of
 // the allocation-free FFN's scratch array.
 int noalloc_resolve(int device);

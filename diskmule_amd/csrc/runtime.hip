@@ -176,6 +176,73 @@ void Scratch::release() {
     bytes = 0;
 }
 
+int HostBounce::ensure(size_t need) {
+    if (need <= bytes) return DMHIP_OK;
+    release();
+    size_t grow = 64u << 10;
+    while (grow < need) grow *= 2;
+    if (hipHostMalloc(&ptr, grow, hipHostMallocDefault) != hipSuccess) {
+        ptr = nullptr;
+        return fail_alloc(need);
+    }
+    bytes = grow;
+    return DMHIP_OK;
+}
+
+void HostBounce::release() {
+    if (ptr) (void)hipHostFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+}
+
+HostCall::~HostCall() {
+    if (open) (void)hipStreamSynchronize(ctx->stream);
+}
+
+int HostCall::begin(size_t total) {
+    staged = total <= kHostBounceMax;
+    used = 0;
+    outs = 0;
+    open = true;
+    // room for the 256-byte alignment of up to four pieces
+    return staged ? ctx->bounce.ensure(total + 4 * 256) : DMHIP_OK;
+}
+
+int HostCall::in(void *device_dst, const void *host_src, size_t n) {
+    if (n == 0) return DMHIP_OK;
+    if (!staged) {
+        DM_HIP(hipMemcpyAsync(device_dst, host_src, n, hipMemcpyHostToDevice, ctx->stream));
+        return DMHIP_OK;
+    }
+    char *b = (char *)ctx->bounce.ptr + used;
+    used += (n + 255) & ~(size_t)255;
+    memcpy(b, host_src, n);
+    DM_HIP(hipMemcpyAsync(device_dst, b, n, hipMemcpyHostToDevice, ctx->stream));
+    return DMHIP_OK;
+}
+
+int HostCall::out(void *host_dst, const void *device_src, size_t n) {
+    if (n == 0) return DMHIP_OK;
+    if (!staged) {
+        DM_HIP(hipMemcpyAsync(host_dst, device_src, n, hipMemcpyDeviceToHost, ctx->stream));
+        return DMHIP_OK;
+    }
+    if (outs == 2) return fail(DMHIP_ERR_COMMAND, "a host-slice call stages at most two outputs");
+    char *b = (char *)ctx->bounce.ptr + used;
+    used += (n + 255) & ~(size_t)255;
+    DM_HIP(hipMemcpyAsync(b, device_src, n, hipMemcpyDeviceToHost, ctx->stream));
+    pending[outs++] = Pending{host_dst, b, n};
+    return DMHIP_OK;
+}
+
+int HostCall::finish() {
+    open = false;
+    DM_HIP(hipStreamSynchronize(ctx->stream));
+    for (int i = 0; i < outs; i++) memcpy(pending[i].dst, pending[i].src, pending[i].n);
+    outs = 0;
+    return DMHIP_OK;
+}
+
 bool type_layout(uint32_t type, uint32_t *be, uint32_t *bb) {
     switch (type) {
     case 0: *be = 1; *bb = 4; return true;      // F32
@@ -396,6 +463,7 @@ void dmhip_context_free(dmhip_ctx *ctx) {
     if (ctx->upload) (void)hipStreamSynchronize(ctx->upload);
     if (ctx->upload2) (void)hipStreamSynchronize(ctx->upload2);
     ctx->in.release();
+    ctx->bounce.release();
     ctx->out.release();
     ctx->enc.release();
     ctx->aux.release();
@@ -588,12 +656,13 @@ int dmhip_rms_norm(dmhip_ctx *ctx, const float *input, size_t input_len, const f
     DM_CHECK(ctx->out.ensure(bytes));
     float *din = (float *)ctx->in.ptr;
     float *dw = weight ? din + input_len : nullptr;
-    DM_HIP(hipMemcpyAsync(din, input, bytes, hipMemcpyHostToDevice, ctx->stream));
-    if (weight) DM_HIP(hipMemcpyAsync(dw, weight, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin((weight ? 3 : 2) * bytes));
+    DM_CHECK(hc.in(din, input, bytes));
+    if (weight) DM_CHECK(hc.in(dw, weight, bytes));
     DM_HIP(launch_rms_norm(ctx->stream, din, 1, (uint32_t)input_len, dw, epsilon, (float *)ctx->out.ptr));
-    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    return DMHIP_OK;
+    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    return hc.finish();
 }
 
 int dmhip_silu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const float *up,
@@ -611,12 +680,13 @@ int dmhip_silu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const flo
     DM_CHECK(ctx->in.ensure(2 * bytes));
     DM_CHECK(ctx->out.ensure(bytes));
     float *dg = (float *)ctx->in.ptr, *du = dg + gate_len;
-    DM_HIP(hipMemcpyAsync(dg, gate, bytes, hipMemcpyHostToDevice, ctx->stream));
-    DM_HIP(hipMemcpyAsync(du, up, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin(3 * bytes));
+    DM_CHECK(hc.in(dg, gate, bytes));
+    DM_CHECK(hc.in(du, up, bytes));
     DM_HIP(launch_silu_mul(ctx->stream, dg, du, gate_len, (float *)ctx->out.ptr));
-    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    return DMHIP_OK;
+    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    return hc.finish();
 }
 
 int dmhip_softcap(dmhip_ctx *ctx, const float *input, size_t input_len, float cap, float *output,
@@ -632,11 +702,12 @@ int dmhip_softcap(dmhip_ctx *ctx, const float *input, size_t input_len, float ca
     size_t bytes = input_len * sizeof(float);
     DM_CHECK(ctx->in.ensure(bytes));
     DM_CHECK(ctx->out.ensure(bytes));
-    DM_HIP(hipMemcpyAsync(ctx->in.ptr, input, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin(2 * bytes));
+    DM_CHECK(hc.in(ctx->in.ptr, input, bytes));
     DM_HIP(launch_softcap(ctx->stream, (const float *)ctx->in.ptr, input_len, cap, (float *)ctx->out.ptr));
-    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    return DMHIP_OK;
+    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    return hc.finish();
 }
 
 int dmhip_add(dmhip_ctx *ctx, const float *left, size_t left_len, const float *right, size_t right_len,
@@ -653,12 +724,13 @@ int dmhip_add(dmhip_ctx *ctx, const float *left, size_t left_len, const float *r
     DM_CHECK(ctx->in.ensure(2 * bytes));
     DM_CHECK(ctx->out.ensure(bytes));
     float *da = (float *)ctx->in.ptr, *db = da + left_len;
-    DM_HIP(hipMemcpyAsync(da, left, bytes, hipMemcpyHostToDevice, ctx->stream));
-    DM_HIP(hipMemcpyAsync(db, right, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin(3 * bytes));
+    DM_CHECK(hc.in(da, left, bytes));
+    DM_CHECK(hc.in(db, right, bytes));
     DM_HIP(launch_add(ctx->stream, da, db, left_len, (float *)ctx->out.ptr));
-    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    return DMHIP_OK;
+    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    return hc.finish();
 }
 
 int dmhip_gelu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const float *up, size_t up_len,
@@ -676,12 +748,13 @@ int dmhip_gelu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const flo
     DM_CHECK(ctx->in.ensure(2 * bytes));
     DM_CHECK(ctx->out.ensure(bytes));
     float *dg = (float *)ctx->in.ptr, *du = dg + gate_len;
-    DM_HIP(hipMemcpyAsync(dg, gate, bytes, hipMemcpyHostToDevice, ctx->stream));
-    DM_HIP(hipMemcpyAsync(du, up, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin(3 * bytes));
+    DM_CHECK(hc.in(dg, gate, bytes));
+    DM_CHECK(hc.in(du, up, bytes));
     DM_HIP(launch_gelu_mul(ctx->stream, dg, du, gate_len, (float *)ctx->out.ptr));
-    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    return DMHIP_OK;
+    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    return hc.finish();
 }
 
 int dmhip_softmax(dmhip_ctx *ctx, const float *input, size_t input_len, float *output, size_t output_len) {
@@ -696,11 +769,12 @@ int dmhip_softmax(dmhip_ctx *ctx, const float *input, size_t input_len, float *o
     size_t bytes = input_len * sizeof(float);
     DM_CHECK(ctx->in.ensure(bytes));
     DM_CHECK(ctx->out.ensure(bytes));
-    DM_HIP(hipMemcpyAsync(ctx->in.ptr, input, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin(2 * bytes));
+    DM_CHECK(hc.in(ctx->in.ptr, input, bytes));
     DM_HIP(launch_softmax(ctx->stream, (const float *)ctx->in.ptr, (uint32_t)input_len, (float *)ctx->out.ptr));
-    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, bytes, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    return DMHIP_OK;
+    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    return hc.finish();
 }
 
 int dmhip_rope_neox_in_place(dmhip_ctx *ctx, float *values, size_t values_len, size_t heads,
@@ -714,12 +788,13 @@ int dmhip_rope_neox_in_place(dmhip_ctx *ctx, float *values, size_t values_len, s
     size_t bytes = values_len * sizeof(float);
     DM_CHECK(ctx->in.ensure(bytes));
     float *dv = (float *)ctx->in.ptr;
-    DM_HIP(hipMemcpyAsync(dv, values, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin(2 * bytes));
+    DM_CHECK(hc.in(dv, values, bytes));
     DM_HIP(launch_rope_neox(ctx->stream, dv, heads, (uint32_t)head_dimension, (uint32_t)rotated_pairs,
                             (uint32_t)position, theta));
-    DM_HIP(hipMemcpyAsync(values, dv, bytes, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    return DMHIP_OK;
+    DM_CHECK(hc.out(values, dv, bytes));
+    return hc.finish();
 }
 
 int dmhip_argmax(dmhip_ctx *ctx, const float *input, size_t input_len, size_t *index) {
@@ -733,12 +808,14 @@ int dmhip_argmax(dmhip_ctx *ctx, const float *input, size_t input_len, size_t *i
     DM_CHECK(set_device(ctx));
     size_t bytes = input_len * sizeof(float);
     DM_CHECK(ctx->in.ensure(bytes));
-    DM_HIP(hipMemcpyAsync(ctx->in.ptr, input, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin(bytes + 4));
+    DM_CHECK(hc.in(ctx->in.ptr, input, bytes));
     DM_HIP(launch_argmax(ctx->stream, (const float *)ctx->in.ptr, input_len, ctx->argmax_state,
                          ctx->argmax_index));
     uint32_t result = 0;
-    DM_HIP(hipMemcpyAsync(&result, ctx->argmax_index, 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
+    DM_CHECK(hc.out(&result, ctx->argmax_index, 4));
+    DM_CHECK(hc.finish());
     *index = result;
     return DMHIP_OK;
 }
@@ -762,13 +839,15 @@ int dmhip_top_k_softmax(dmhip_ctx *ctx, const float *logits, size_t logits_len, 
     DM_CHECK(ctx->out.ensure(k * 8));
     uint32_t *dids = (uint32_t *)ctx->out.ptr;
     float *dp = (float *)(dids + k);
-    DM_HIP(hipMemcpyAsync(ctx->in.ptr, logits, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin(bytes + 8 * k));
+    DM_CHECK(hc.in(ctx->in.ptr, logits, bytes));
     DM_HIP(launch_top_k(ctx->stream, (const float *)ctx->in.ptr, 1, (uint32_t)logits_len,
                         (uint32_t)k, dids, dp, BadFlag{ctx->flags + 2, 1}));  // checked on the host first
     uint32_t ids[kMaxTopK];
-    DM_HIP(hipMemcpyAsync(ids, dids, k * 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipMemcpyAsync(probabilities, dp, k * 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
+    DM_CHECK(hc.out(ids, dids, k * 4));
+    DM_CHECK(hc.out(probabilities, dp, k * 4));
+    DM_CHECK(hc.finish());
     for (size_t i = 0; i < k; i++) indices[i] = ids[i];
     return DMHIP_OK;
 }
@@ -781,14 +860,15 @@ static int matvec_from_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t
     DM_REQUIRE(output);
     DM_CHECK(count_u32(columns));
     DM_CHECK(count_u32(rows));
-    DM_CHECK(ctx->in.ensure(columns * sizeof(float)));
-    DM_CHECK(ctx->out.ensure(rows * sizeof(float)));
-    DM_HIP(hipMemcpyAsync(ctx->in.ptr, input, columns * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
-    DM_CHECK(enqueue_matvec(ctx, type, rows, columns, w, 1, (const float *)ctx->in.ptr,
-                            (float *)ctx->out.ptr));
-    DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
-    return DMHIP_OK;
+    const size_t in_bytes = columns * sizeof(float), out_bytes = rows * sizeof(float);
+    DM_CHECK(ctx->in.ensure(in_bytes));
+    DM_CHECK(ctx->out.ensure(out_bytes));
+    HostCall hc(ctx);
+    DM_CHECK(hc.begin(in_bytes + out_bytes));
+    DM_CHECK(hc.in(ctx->in.ptr, input, in_bytes));
+    DM_CHECK(enqueue_matvec(ctx, type, rows, columns, w, 1, (const float *)ctx->in.ptr, (float *)ctx->out.ptr));
+    DM_CHECK(hc.out(output, ctx->out.ptr, out_bytes));
+    return hc.finish();
 }
 
 int dmhip_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,

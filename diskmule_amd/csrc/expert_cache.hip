@@ -11,10 +11,10 @@
 // the ring bounds the host memory the cache uses.
 //
 // Ordering is by events, never by device-wide waits:
-//   * an upload into a slot first waits for the `released` event recorded
-//     after the last compute work that read the slot, and for the `ready`
-//     event of the slot's previous upload (which may be on the other upload
-//     stream);
+//   * before an upload into a slot is issued, the host waits for the
+//     `released` event recorded after the last compute work that read the
+//     slot, and for the `ready` event of the slot's previous upload (the
+//     upload streams themselves never wait on another queue's event);
 //   * compute work that uses a freshly loaded slot waits for its `ready`
 //     event (the end of its upload);
 //   * a staging entry is refilled only after the host has waited for the
@@ -211,8 +211,14 @@ int upload_expert(dmhip_expert_cache *c, const dmhip_expert_layer_layout &L, siz
     }
     // experts alternate between the two upload streams
     hipStream_t up = (c->ctx->upload_next++ & 1u) ? c->ctx->upload2 : c->ctx->upload;
-    if (s.released_recorded) DM_HIP(hipStreamWaitEvent(up, s.released, 0));
-    if (s.uploaded) DM_HIP(hipStreamWaitEvent(up, s.ready, 0));
+    // The slot's last readers and its previous upload are waited for here,
+    // on the host, not by the upload stream: a copy queued behind a wait on
+    // an event of another queue that has not completed yet moved expert
+    // bytes at 26 GB/s against 42 GB/s for free copies (MI355X, the MoE
+    // layer at 4 tokens: 3.6-4.3 against 2.2 ms per call).  Both events are
+    // usually complete by the time a slot is reused.
+    if (s.released_recorded) DM_HIP(hipEventSynchronize(s.released));
+    if (s.uploaded) DM_HIP(hipEventSynchronize(s.ready));
     TimedUpload *timer = nullptr;
     if (c->fd < 0) {
         timer = &c->timed[c->next_timed++ % c->timed.size()];

@@ -9,6 +9,8 @@
 //  * reductions for argmax / top-k / RMSNorm, SiLU products, the exact bf16
 //    router fold and the ordered expert combine.
 #include "dm_device.h"
+
+#include <utility>
 #include "dm_kernels.h"
 
 namespace dm {
@@ -499,6 +501,147 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
     }
 }
 
+// Expert-parallel exact router for decode, operands in registers: lane e of
+// workgroup (g, t) folds router row 64 g + e of token t sequentially from
+// column 0 with fma (the reference's fold, so the logits are bit-identical to
+// the kernels above).  The dependent fma chain is the whole cost, so nothing
+// it waits on may be late.  The token's x is staged in LDS once; each step
+// of 8 columns then takes the row's 8 bf16 values from one 16-byte load
+// issued kRcAhead steps earlier (widened by one shift or mask each) and the
+// 8 values of x from two LDS reads of one address.  The N8 steps (hidden =
+// 8 N8) are unrolled into straight-line code, where every wait names exactly
+// the load it needs (a loop header makes the compiler wait for every load in
+// flight).  The selection is the ticketed finish of router_fold_kernel.
+constexpr uint32_t kRcAhead = 32;  // steps of 8 columns in flight per lane (row loads)
+constexpr uint32_t kRcXAhead = 4;  // steps of x read from LDS ahead of their use
+
+// The chain's operands and state: the row-load ring, the x ring, the sum.
+struct ChainState {
+    v4a ring[kRcAhead];
+    v4a xring[2 * kRcXAhead];
+    float wf[2][8];  // the row values of this step and the next, widened
+    float acc;
+    __amdgpu_buffer_rsrc_t rw;
+    uint32_t row;
+    const v4a *xs;
+};
+
+// Step C8 of N8: fold 8 columns, then refill the two ring slots it used.
+// Every index is a constant, so the rings stay in fixed registers.
+// The 8 row values of a step, widened from bf16 (bits << 16).
+__device__ __forceinline__ void chain_widen(const v4a w, float (&wf)[8]) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        wf[2 * q] = __uint_as_float(w[q] << 16);
+        wf[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+    }
+}
+
+template <uint32_t N8, uint32_t C8>
+__device__ __forceinline__ void chain_step(ChainState &st) {
+    constexpr uint32_t nowhere = 0x80000000u;
+    // the next step's row values are widened during this step's chain, so
+    // each fma waits only for the previous one
+    if constexpr (C8 + 1 < N8) chain_widen(st.ring[(C8 + 1) % kRcAhead], st.wf[(C8 + 1) % 2]);
+    const float *wf = st.wf[C8 % 2];
+    const v4a xa = st.xring[2 * (C8 % kRcXAhead)], xb = st.xring[2 * (C8 % kRcXAhead) + 1];
+    const float xv[8] = {__uint_as_float(xa[0]), __uint_as_float(xa[1]), __uint_as_float(xa[2]),
+                         __uint_as_float(xa[3]), __uint_as_float(xb[0]), __uint_as_float(xb[1]),
+                         __uint_as_float(xb[2]), __uint_as_float(xb[3])};
+#pragma unroll
+    for (int i = 0; i < 8; i++) st.acc = __builtin_fmaf(wf[i], xv[i], st.acc);
+    if constexpr (C8 + kRcAhead < N8)
+        st.ring[C8 % kRcAhead] = __builtin_bit_cast(
+            v4a, rsrc_load16(st.rw, st.row != nowhere ? st.row + 16 * (C8 + kRcAhead) : nowhere));
+    if constexpr (C8 + kRcXAhead < N8) {
+        st.xring[2 * (C8 % kRcXAhead)] = st.xs[2 * (C8 + kRcXAhead)];
+        st.xring[2 * (C8 % kRcXAhead) + 1] = st.xs[2 * (C8 + kRcXAhead) + 1];
+    }
+    // keep each step's loads right after its fmas, so the queues stay
+    // kRcAhead (row) and kRcXAhead (x) steps deep
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <uint32_t N8, uint32_t... C>
+__device__ __forceinline__ void chain_steps(ChainState &st, std::integer_sequence<uint32_t, C...>) {
+    (chain_step<N8, C>(st), ...);
+}
+
+template <uint32_t N8>
+__global__ void __launch_bounds__(64) router_chain_kernel(const uint16_t *__restrict__ router, uint32_t hidden,
+                                                          uint32_t experts, uint32_t k,
+                                                          const float *__restrict__ x, float *logits,
+                                                          uint32_t *tickets, uint32_t *ids, float *probabilities,
+                                                          BadFlag non_finite, uint32_t *host_ids,
+                                                          float *host_probs, uint32_t *host_bad) {
+    static_assert(N8 >= kRcAhead && N8 >= kRcXAhead, "at least one ring of steps");
+    __shared__ v4a xs[N8 * 2];
+    const uint32_t lane = threadIdx.x, e0 = blockIdx.x * 64, token = blockIdx.y;
+    const uint32_t e = e0 + lane;
+    constexpr uint32_t nowhere = 0x80000000u;  // every load from here reads zeros
+    ChainState st;
+    // rows past `experts` read zeros (buffer loads past the end)
+    st.rw = make_rsrc(router, experts * hidden * 2);
+    st.row = e < experts ? e * hidden * 2 : nowhere;
+    st.xs = xs;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)token * hidden, hidden * 4);
+    // x first (the LDS stores wait for it), then the first kRcAhead steps of
+    // the row
+    constexpr uint32_t XL = (N8 * 2 + 63) / 64;  // 16-byte pieces of x per lane
+    v4a xr[XL];
+#pragma unroll
+    for (uint32_t i = 0; i < XL; i++) {
+        const uint32_t piece = i * 64 + lane;
+        xr[i] = __builtin_bit_cast(v4a, rsrc_load16(rx, piece < N8 * 2 ? 16 * piece : nowhere));
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kRcAhead; j++)
+        st.ring[j] = __builtin_bit_cast(v4a, rsrc_load16(st.rw, st.row != nowhere ? st.row + 16 * j : nowhere));
+#pragma unroll
+    for (uint32_t i = 0; i < XL; i++)
+        if (i * 64 + lane < N8 * 2) xs[i * 64 + lane] = xr[i];
+    __syncthreads();
+#pragma unroll
+    for (uint32_t j = 0; j < kRcXAhead; j++) {
+        st.xring[2 * j] = xs[2 * j];
+        st.xring[2 * j + 1] = xs[2 * j + 1];
+    }
+    st.acc = 0.0f;
+    chain_widen(st.ring[0], st.wf[0]);
+    chain_steps<N8>(st, std::make_integer_sequence<uint32_t, N8>{});
+    const float acc = st.acc;
+    if (!tickets) {
+        if (e < experts) logits[(size_t)token * experts + e] = acc;
+        return;
+    }
+    // Fused selection, as in router_fold_kernel.
+    float old = 0.0f;
+    if (e < experts)
+        old = __hip_atomic_exchange(&logits[(size_t)token * experts + e], acc, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"(old) : "memory");
+    uint32_t drawn = 0;
+    if (lane == 0) drawn = atomicAdd(&tickets[token], 1u);
+    if (__builtin_amdgcn_readfirstlane(drawn) != gridDim.x - 1) return;
+    __shared__ float s_row[256];
+    for (uint32_t i = lane; i < experts; i += 64)
+        s_row[i] = __hip_atomic_load(&logits[(size_t)token * experts + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    uint32_t *ti = ids + (size_t)token * k;
+    float *tp = probabilities + (size_t)token * k;
+    const bool bad = block_top_k(s_row, experts, k, ti, tp, non_finite);
+    if (lane == 0) {
+        if (host_ids) {
+            for (uint32_t s = 0; s < k; s++) {
+                host_ids[(size_t)token * k + s] = ti[s];
+                host_probs[(size_t)token * k + s] = tp[s];
+            }
+            host_bad[token] = bad;
+        }
+        __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // Top-k softmax over the router logits (at most 256) of one token per
 // workgroup, with the selection also written to (pinned) host memory when
 // host_ids is set.
@@ -693,9 +836,14 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
                         ((uintptr_t)x & 15u) == 0;
     // Decode batches: the expert-parallel fold, then the selection.
     if (staged && experts >= 2 * RF_EXPERTS && (uint64_t)experts * hidden * 2 < 0x80000000ull) {
-        hipLaunchKernelGGL(router_fold_kernel, dim3((experts + RF_EXPERTS - 1) / RF_EXPERTS, batch), dim3(64), 0, s,
-                           router, hidden, experts, k, x, logits, tickets, ids, probabilities, non_finite, host_ids,
-                           host_probs, host_bad);
+        if (hidden == 2048)
+            hipLaunchKernelGGL(router_chain_kernel<256>, dim3((experts + 63) / 64, batch), dim3(64), 0, s, router, hidden,
+                               experts, k, x, logits, tickets, ids, probabilities, non_finite, host_ids, host_probs,
+                               host_bad);
+        else
+            hipLaunchKernelGGL(router_fold_kernel, dim3((experts + RF_EXPERTS - 1) / RF_EXPERTS, batch), dim3(64),
+                               0, s, router, hidden, experts, k, x, logits, tickets, ids, probabilities, non_finite,
+                               host_ids, host_probs, host_bad);
         if (!tickets)
             hipLaunchKernelGGL(top_k_host_kernel, dim3(batch), dim3(256), 0, s, logits, experts, k, ids,
                                probabilities, non_finite, host_ids, host_probs, host_bad);

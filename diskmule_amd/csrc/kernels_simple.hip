@@ -501,142 +501,210 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
     }
 }
 
-// Expert-parallel exact router for decode, operands in registers: lane e of
-// workgroup (g, t) folds router row 64 g + e of token t sequentially from
-// column 0 with fma (the reference's fold, so the logits are bit-identical to
-// the kernels above).  The dependent fma chain is the whole cost, so nothing
-// it waits on may be late.  The token's x is staged in LDS once; each step
-// of 8 columns then takes the row's 8 bf16 values from one 16-byte load
-// issued kRcAhead steps earlier (widened by one shift or mask each) and the
-// 8 values of x from two LDS reads of one address.  The N8 steps (hidden =
-// 8 N8) are unrolled into straight-line code, where every wait names exactly
-// the load it needs (a loop header makes the compiler wait for every load in
-// flight).  The selection is the ticketed finish of router_fold_kernel.
-constexpr uint32_t kRcAhead = 32;  // steps of 8 columns in flight per lane (row loads)
-constexpr uint32_t kRcXAhead = 4;  // steps of x read from LDS ahead of their use
+// Exact router for decode with the rows staged in LDS as f32.  Workgroup
+// (g, t) of four waves first loads router rows R g .. R g + R - 1 and token
+// t's x with up to 16 loads per thread in flight at once (contiguous 16-byte
+// pieces), widens the bf16 values (bits << 16, exact) and stores them in LDS,
+// so the rows cost one or two memory round trips.  R is the most rows that
+// fit in LDS beside x (16 at hidden 2048).  Rows and x are zero-padded to
+// whole rings of steps: the padding adds fma(0, 0, acc) = acc (the sum starts
+// at +0 and an exactly zero sum of +0 and -0 is +0, so it is never -0).
+// Lane e < R of wave 0 then folds row R g + e sequentially from column 0
+// with fma (the reference's fold: logits and ids are bit-identical to the
+// kernels above).  Each step of 8 columns takes the row's values and x's from
+// two 16-byte LDS reads each (x: one address for all lanes), kRlAhead steps
+// ahead, so the wave issues nothing but the chain's fmas and the reads.  The
+// loop body is one ring of steps: ring slots keep fixed registers, every
+// wait names the read it needs, and the code stays small (an unrolled chain
+// is tens of KB run once per launch, more than instruction fetch keeps up
+// with).  Rows are padded by 16 bytes in LDS, so the lanes' reads of one step
+// start 4 banks apart.  The token's last workgroup (ticket) makes the
+// selection by rank: each of up to 256 logits counts the keys above its own.
+constexpr uint32_t kRlRing = 4;   // ring slots: steps of 8 columns per loop iteration
+constexpr uint32_t kRlAhead = 3;  // steps read ahead of their use (4 LDS reads each, lgkmcnt <= 15)
 
-// The chain's operands and state: the row-load ring, the x ring, the sum.
-struct ChainState {
-    v4a ring[kRcAhead];
-    v4a xring[2 * kRcXAhead];
-    float wf[2][8];  // the row values of this step and the next, widened
+struct LdsChainState {
+    v4a wring[2 * kRlRing];  // the row's 8 values of a step, f32
+    v4a xring[2 * kRlRing];  // x's 8 values of a step
     float acc;
-    __amdgpu_buffer_rsrc_t rw;
-    uint32_t row;
-    const v4a *xs;
+    const v4a *wrow;  // this lane's row in LDS
+    const v4a *xs;    // x in LDS
 };
 
-// Step C8 of N8: fold 8 columns, then refill the two ring slots it used.
-// Every index is a constant, so the rings stay in fixed registers.
-// The 8 row values of a step, widened from bf16 (bits << 16).
-__device__ __forceinline__ void chain_widen(const v4a w, float (&wf)[8]) {
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        wf[2 * q] = __uint_as_float(w[q] << 16);
-        wf[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
-    }
+template <uint32_t C>
+__device__ __forceinline__ void lds_chain_read(LdsChainState &st, uint32_t step) {
+    st.wring[2 * C] = st.wrow[2 * step];
+    st.wring[2 * C + 1] = st.wrow[2 * step + 1];
+    st.xring[2 * C] = st.xs[2 * step];
+    st.xring[2 * C + 1] = st.xs[2 * step + 1];
 }
 
-template <uint32_t N8, uint32_t C8>
-__device__ __forceinline__ void chain_step(ChainState &st) {
-    constexpr uint32_t nowhere = 0x80000000u;
-    // the next step's row values are widened during this step's chain, so
-    // each fma waits only for the previous one
-    if constexpr (C8 + 1 < N8) chain_widen(st.ring[(C8 + 1) % kRcAhead], st.wf[(C8 + 1) % 2]);
-    const float *wf = st.wf[C8 % 2];
-    const v4a xa = st.xring[2 * (C8 % kRcXAhead)], xb = st.xring[2 * (C8 % kRcXAhead) + 1];
-    const float xv[8] = {__uint_as_float(xa[0]), __uint_as_float(xa[1]), __uint_as_float(xa[2]),
-                         __uint_as_float(xa[3]), __uint_as_float(xb[0]), __uint_as_float(xb[1]),
-                         __uint_as_float(xb[2]), __uint_as_float(xb[3])};
+// Step base + C of a ring of steps: fold 8 columns, then (C < NREAD) read the
+// operands of step base + C + kRlAhead into their slot.
+template <uint32_t C, uint32_t NREAD>
+__device__ __forceinline__ void lds_chain_step(LdsChainState &st, uint32_t base) {
+    const v4a wa = st.wring[2 * C], wb = st.wring[2 * C + 1];
+    const v4a xa = st.xring[2 * C], xb = st.xring[2 * C + 1];
 #pragma unroll
-    for (int i = 0; i < 8; i++) st.acc = __builtin_fmaf(wf[i], xv[i], st.acc);
-    if constexpr (C8 + kRcAhead < N8)
-        st.ring[C8 % kRcAhead] = __builtin_bit_cast(
-            v4a, rsrc_load16(st.rw, st.row != nowhere ? st.row + 16 * (C8 + kRcAhead) : nowhere));
-    if constexpr (C8 + kRcXAhead < N8) {
-        st.xring[2 * (C8 % kRcXAhead)] = st.xs[2 * (C8 + kRcXAhead)];
-        st.xring[2 * (C8 % kRcXAhead) + 1] = st.xs[2 * (C8 + kRcXAhead) + 1];
-    }
-    // keep each step's loads right after its fmas, so the queues stay
-    // kRcAhead (row) and kRcXAhead (x) steps deep
+    for (int i = 0; i < 4; i++) st.acc = __builtin_fmaf(__uint_as_float(wa[i]), __uint_as_float(xa[i]), st.acc);
+#pragma unroll
+    for (int i = 0; i < 4; i++) st.acc = __builtin_fmaf(__uint_as_float(wb[i]), __uint_as_float(xb[i]), st.acc);
+    if constexpr (C < NREAD) lds_chain_read<(C + kRlAhead) % kRlRing>(st, base + C + kRlAhead);
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <uint32_t N8, uint32_t... C>
-__device__ __forceinline__ void chain_steps(ChainState &st, std::integer_sequence<uint32_t, C...>) {
-    (chain_step<N8, C>(st), ...);
+template <uint32_t NREAD, uint32_t... C>
+__device__ __forceinline__ void lds_chain_ring(LdsChainState &st, uint32_t base,
+                                               std::integer_sequence<uint32_t, C...>) {
+    (lds_chain_step<C, NREAD>(st, base), ...);
 }
 
-template <uint32_t N8>
-__global__ void __launch_bounds__(64) router_chain_kernel(const uint16_t *__restrict__ router, uint32_t hidden,
-                                                          uint32_t experts, uint32_t k,
-                                                          const float *__restrict__ x, float *logits,
-                                                          uint32_t *tickets, uint32_t *ids, float *probabilities,
-                                                          BadFlag non_finite, uint32_t *host_ids,
-                                                          float *host_probs, uint32_t *host_bad) {
-    static_assert(N8 >= kRcAhead && N8 >= kRcXAhead, "at least one ring of steps");
-    __shared__ v4a xs[N8 * 2];
-    const uint32_t lane = threadIdx.x, e0 = blockIdx.x * 64, token = blockIdx.y;
-    const uint32_t e = e0 + lane;
+// Steps of 8 columns, padded to whole rings, and the LDS layout of a row:
+// f32 pieces of 16 bytes plus one padding piece.
+__host__ __device__ constexpr uint32_t router_lds_steps(uint32_t hidden) {
+    return (hidden / 8 + kRlRing - 1) / kRlRing * kRlRing;
+}
+__host__ __device__ constexpr uint32_t router_lds_row_pieces(uint32_t hidden) {
+    return 2 * router_lds_steps(hidden) + 1;
+}
+constexpr size_t router_lds_bytes(uint32_t hidden, uint32_t rows) {
+    return ((size_t)rows * router_lds_row_pieces(hidden) + 2 * router_lds_steps(hidden)) * 16;
+}
+
+__global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restrict__ router, uint32_t hidden,
+                                                         uint32_t experts, uint32_t R, uint32_t k,
+                                                         const float *__restrict__ x, float *logits,
+                                                         uint32_t *tickets, uint32_t *ids, float *probabilities,
+                                                         BadFlag non_finite, uint32_t *host_ids, float *host_probs,
+                                                         uint32_t *host_bad) {
+    constexpr uint32_t kBatch = 16;   // row loads per thread in flight
+    constexpr uint32_t kXPieces = 8;  // x loads per thread: hidden <= 8192
+    const uint32_t N8 = hidden / 8, NS = router_lds_steps(hidden), RS = router_lds_row_pieces(hidden);
+    extern __shared__ __attribute__((aligned(16))) v4a lds_rows[];  // [R][RS], then x [2 NS]
+    v4a *xs = lds_rows + R * RS;
+    const uint32_t tid = threadIdx.x, e0 = blockIdx.x * R, token = blockIdx.y;
     constexpr uint32_t nowhere = 0x80000000u;  // every load from here reads zeros
-    ChainState st;
-    // rows past `experts` read zeros (buffer loads past the end)
-    st.rw = make_rsrc(router, experts * hidden * 2);
-    st.row = e < experts ? e * hidden * 2 : nowhere;
-    st.xs = xs;
+    // rows past `experts` and columns past `hidden` read zeros (buffer loads
+    // past the end, or nowhere)
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(router, experts * hidden * 2);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)token * hidden, hidden * 4);
-    // x first (the LDS stores wait for it), then the first kRcAhead steps of
-    // the row
-    constexpr uint32_t XL = (N8 * 2 + 63) / 64;  // 16-byte pieces of x per lane
-    v4a xr[XL];
+    // x: 2 NS <= 2048 pieces of 4 floats (hidden % 8 == 0, so whole
+    // pieces), requested together with the first batch of rows
+    v4a xr[kXPieces];
 #pragma unroll
-    for (uint32_t i = 0; i < XL; i++) {
-        const uint32_t piece = i * 64 + lane;
-        xr[i] = __builtin_bit_cast(v4a, rsrc_load16(rx, piece < N8 * 2 ? 16 * piece : nowhere));
+    for (uint32_t j = 0; j < kXPieces; j++) {
+        const uint32_t piece = j * 256 + tid;
+        xr[j] = __builtin_bit_cast(v4a, rsrc_load16(rx, piece < 2 * N8 ? 16 * piece : nowhere));
     }
+    // rows: R NS bf16 pieces of 8 values, kBatch per thread at a time; piece
+    // p is (row p / NS, step p % NS), the quotient by a multiply-high (exact
+    // for p NS < 2^32)
+    const uint32_t total = R * NS, inv = (uint32_t)((0xffffffffull + NS) / NS);
+    for (uint32_t p0 = 0; p0 < total; p0 += 256 * kBatch) {
+        v4a wr[kBatch];
 #pragma unroll
-    for (uint32_t j = 0; j < kRcAhead; j++)
-        st.ring[j] = __builtin_bit_cast(v4a, rsrc_load16(st.rw, st.row != nowhere ? st.row + 16 * j : nowhere));
+        for (uint32_t j = 0; j < kBatch; j++) {
+            const uint32_t p = p0 + j * 256 + tid, row = __umulhi(p, inv), col = p - row * NS;
+            const bool real = p < total && col < N8 && e0 + row < experts;
+            wr[j] = __builtin_bit_cast(v4a, rsrc_load16(rw, real ? ((e0 + row) * N8 + col) * 16 : nowhere));
+        }
+        if (p0 == 0) {
 #pragma unroll
-    for (uint32_t i = 0; i < XL; i++)
-        if (i * 64 + lane < N8 * 2) xs[i * 64 + lane] = xr[i];
+            for (uint32_t j = 0; j < kXPieces; j++)
+                if (j * 256 + tid < 2 * NS) xs[j * 256 + tid] = xr[j];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; j++) {
+            const uint32_t p = p0 + j * 256 + tid, row = __umulhi(p, inv), col = p - row * NS;
+            if (p < total) {
+                const v4a w = wr[j];
+                lds_rows[row * RS + 2 * col] = v4a{w[0] << 16, w[0] & 0xffff0000u, w[1] << 16, w[1] & 0xffff0000u};
+                lds_rows[row * RS + 2 * col + 1] =
+                    v4a{w[2] << 16, w[2] & 0xffff0000u, w[3] << 16, w[3] & 0xffff0000u};
+            }
+        }
+    }
     __syncthreads();
-#pragma unroll
-    for (uint32_t j = 0; j < kRcXAhead; j++) {
-        st.xring[2 * j] = xs[2 * j];
-        st.xring[2 * j + 1] = xs[2 * j + 1];
+    __shared__ uint32_t s_drawn;
+    if (tid < 64) {
+        const uint32_t lane = tid, e = e0 + lane;
+        LdsChainState st;
+        st.wrow = lds_rows + (lane % R) * RS;
+        st.xs = xs;
+        lds_chain_read<0>(st, 0);
+        lds_chain_read<1>(st, 1);
+        lds_chain_read<2>(st, 2);
+        static_assert(kRlAhead == 3, "the prologue reads kRlAhead steps");
+        st.acc = 0.0f;
+        constexpr auto ring = std::make_integer_sequence<uint32_t, kRlRing>{};
+        uint32_t base = 0;
+#pragma unroll 1
+        for (; base + kRlRing < NS; base += kRlRing) lds_chain_ring<kRlRing>(st, base, ring);
+        lds_chain_ring<kRlRing - kRlAhead>(st, base, ring);
+        const float acc = st.acc;
+        const bool mine = lane < R && e < experts;
+        if (!tickets) {
+            if (mine) logits[(size_t)token * experts + e] = acc;
+        } else {
+            float old = 0.0f;
+            if (mine)
+                old = __hip_atomic_exchange(&logits[(size_t)token * experts + e], acc, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("" ::"v"(old) : "memory");
+            uint32_t drawn = 0;
+            if (lane == 0) drawn = atomicAdd(&tickets[token], 1u);
+            if (lane == 0) s_drawn = drawn;
+        }
     }
-    st.acc = 0.0f;
-    chain_widen(st.ring[0], st.wf[0]);
-    chain_steps<N8>(st, std::make_integer_sequence<uint32_t, N8>{});
-    const float acc = st.acc;
-    if (!tickets) {
-        if (e < experts) logits[(size_t)token * experts + e] = acc;
-        return;
-    }
-    // Fused selection, as in router_fold_kernel.
-    float old = 0.0f;
-    if (e < experts)
-        old = __hip_atomic_exchange(&logits[(size_t)token * experts + e], acc, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("" ::"v"(old) : "memory");
-    uint32_t drawn = 0;
-    if (lane == 0) drawn = atomicAdd(&tickets[token], 1u);
-    if (__builtin_amdgcn_readfirstlane(drawn) != gridDim.x - 1) return;
-    __shared__ float s_row[256];
-    for (uint32_t i = lane; i < experts; i += 64)
-        s_row[i] = __hip_atomic_load(&logits[(size_t)token * experts + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!tickets) return;
     __syncthreads();
-    uint32_t *ti = ids + (size_t)token * k;
-    float *tp = probabilities + (size_t)token * k;
-    const bool bad = block_top_k(s_row, experts, k, ti, tp, non_finite);
-    if (lane == 0) {
+    if (s_drawn != gridDim.x - 1) return;
+    // The token's last workgroup: the selection over every logit, by rank.
+    __shared__ uint64_t s_keys[256];
+    __shared__ uint32_t s_sel[256];
+    __shared__ float s_logit[256], s_value[256];
+    uint64_t mine = 0;
+    bool bad = false;
+    if (tid < experts) {
+        const float v =
+            __hip_atomic_load(&logits[(size_t)token * experts + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bad = !__builtin_isfinite(v);
+        mine = argmax_key(v, tid);
+        s_keys[tid] = mine;
+        s_logit[tid] = v;
+    }
+    if (bad) *non_finite.word = non_finite.mark;  // every writer stores the same value
+    const bool row_bad = __syncthreads_or((int)bad) != 0;
+    if (tid < experts) {
+        // keys are unique (value, then index), so ranks are 0 .. experts - 1
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < experts; j++) rank += s_keys[j] > mine ? 1u : 0u;
+        if (rank < k) s_sel[rank] = tid;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t *ti = ids + (size_t)token * k;
+        float *tp = probabilities + (size_t)token * k;
+        // softmax_in_place over the selected logits (src/cpu.rs:195-230):
+        // maximum, exp(v - max), sequential sum, divide.
+        float maximum = -__builtin_inff();
+        for (uint32_t s = 0; s < k; s++) {
+            const uint32_t index = s_sel[s];
+            ti[s] = index;
+            maximum = fmaxf(maximum, s_logit[index]);
+        }
+        float sum = 0.0f;
+        for (uint32_t s = 0; s < k; s++) {
+            s_value[s] = expf(s_logit[s_sel[s]] - maximum);
+            sum += s_value[s];
+        }
+        for (uint32_t s = 0; s < k; s++) tp[s] = s_value[s] / sum;
         if (host_ids) {
             for (uint32_t s = 0; s < k; s++) {
                 host_ids[(size_t)token * k + s] = ti[s];
                 host_probs[(size_t)token * k + s] = tp[s];
             }
-            host_bad[token] = bad;
+            host_bad[token] = row_bad;
         }
         __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -836,11 +904,20 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
                         ((uintptr_t)x & 15u) == 0;
     // Decode batches: the expert-parallel fold, then the selection.
     if (staged && experts >= 2 * RF_EXPERTS && (uint64_t)experts * hidden * 2 < 0x80000000ull) {
-        if (hidden == 2048)
-            hipLaunchKernelGGL(router_chain_kernel<256>, dim3((experts + 63) / 64, batch), dim3(64), 0, s, router, hidden,
-                               experts, k, x, logits, tickets, ids, probabilities, non_finite, host_ids, host_probs,
-                               host_bad);
-        else
+        // as many rows per workgroup as fit in LDS beside x and the
+        // kernel's own arrays (the rank selection's keys, ids, logits)
+        constexpr size_t kLdsBudget = 160 * 1024 - 8 * 1024;
+        const size_t row = (size_t)router_lds_row_pieces(hidden) * 16, xbytes = (size_t)router_lds_steps(hidden) * 32;
+        const uint32_t R = xbytes < kLdsBudget ? (uint32_t)std::min<size_t>(64, (kLdsBudget - xbytes) / row) : 0;
+        if (R >= 4 && router_lds_steps(hidden) <= 1024) {
+            static LdsLimit limit;
+            const size_t lds = router_lds_bytes(hidden, R);
+            hipError_t e = limit.ensure((const void *)router_lds_kernel, lds);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL(router_lds_kernel, dim3((experts + R - 1) / R, batch), dim3(256), lds, s, router,
+                               hidden, experts, R, k, x, logits, tickets, ids, probabilities, non_finite, host_ids,
+                               host_probs, host_bad);
+        } else
             hipLaunchKernelGGL(router_fold_kernel, dim3((experts + RF_EXPERTS - 1) / RF_EXPERTS, batch), dim3(64),
                                0, s, router, hidden, experts, k, x, logits, tickets, ids, probabilities, non_finite,
                                host_ids, host_probs, host_bad);

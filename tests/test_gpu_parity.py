@@ -756,10 +756,13 @@ def _moe_setup(hidden=2048, width=768, experts=128):
                                                     (3, 2824, 128, 8), (2, 4096, 256, 8), (2, 1016, 200, 6),
                                                     (1, 2050, 128, 8), (1, 512, 300, 8), (2, 1024, 12, 4),
                                                     (33, 2048, 128, 8), (4100, 256, 16, 2), (2, 24576, 128, 8),
-                                                    (3, 4104, 64, 4)])
+                                                    (3, 4104, 64, 4), (2, 2048, 200, 6), (1, 2048, 16, 2),
+                                                    (2, 2048, 256, 8), (4100, 2048, 48, 4)])
 def test_router_top_k_is_bit_exact(ctx, batch, hidden, experts, k):
     """The bf16 router fold (src/cpu.rs:384-397 order) and top-k: logits bit
-    for bit, ids exact.  Covers the expert-parallel fold (8 experts per
+    for bit, ids exact.  Covers the expert-parallel fold at hidden 2048 (32
+    rows per workgroup staged in LDS, partial last workgroups, 16 to 256
+    experts), the expert-parallel fold at other widths (8 experts per
     workgroup, 512-column chunks, partial last chunks and workgroups, long
     rows; above 4096 tokens the selection runs as a second launch), the
     LDS-staged one-workgroup kernel (fewer than 16 experts), and the

@@ -87,12 +87,27 @@ struct BadFlag {
 };
 hipError_t launch_top_k(hipStream_t s, const float *logits, uint32_t rows, uint32_t count,
                         uint32_t k, uint32_t *ids, float *probabilities, BadFlag non_finite);
+// The routed experts' slots looked up on the device, for a MoE layer call
+// of one token whose expert launches are queued behind the router: per
+// expert of the layer the device addresses of its slot's gate_up and down
+// bytes (0 when not resident); out, per selection, the addresses, and one
+// go word (device and pinned host copies): 1 when every selected expert is
+// resident and the token's logits are finite, else 0.
+struct ExpertLookup {
+    const uint64_t *gate_up_of, *down_of;
+    uint64_t *gate_up_w, *down_w;
+    uint32_t *go, *host_go;
+};
 hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
                                BadFlag non_finite, uint32_t *host_ids = nullptr,
                                float *host_probs = nullptr, uint32_t *tickets = nullptr,
-                               uint32_t *host_bad = nullptr);
+                               uint32_t *host_bad = nullptr, const ExpertLookup *lookup = nullptr);
+// True when launch_router_top_k takes a lookup for this router: one token,
+// and the router runs as one of the expert-parallel kernels whose token's
+// last workgroup makes the selection.
+bool router_takes_lookup(uint32_t hidden, uint32_t experts, uint32_t batch, const void *router, const float *x);
 // With host_ids, the selection and one word per token (nonzero when that
 // token's logits held a non-finite value; with the one-workgroup-per-token
 // fallback kernel word 0 stands for all tokens) are written to host memory.

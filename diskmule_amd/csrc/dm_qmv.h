@@ -49,6 +49,8 @@ hipError_t launch_qmv8_gate_up(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uin
 // form the gate rows, the up rows following at up_offset bytes) applied to
 // `tokens` (1 or 2) activation rows x + x_off + t * x_stride, writing
 // y + y_off + t * y_stride (offsets and strides in floats).
+constexpr uint32_t kMaxGroupedJobs = 64;  // jobs per launch of the grouped kernel
+
 struct QmvJob {
     const void *w;
     uint32_t tokens;
@@ -64,8 +66,12 @@ bool qmv8_grouped_supported(uint32_t type, size_t rows, size_t columns, uint32_t
 // All jobs in one or a few launches.  gate_up == 0: y = W x.  gate_up == 1:
 // y = (g / (1 + exp(-g))) * u with g = gate . x, u = up . x, the routed-expert
 // activation of src/glm52/expert.rs:260-267.
+// With dev_w (one-token jobs, at most 64, one launch) the job addresses are
+// read on the device from dev_w[job] and the launch does nothing when *go is
+// 0: both written by a kernel earlier on the stream (ExpertLookup).
 hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, int gate_up,
-                               uint64_t up_offset, const QmvJob *jobs, size_t count, const float *x, float *y);
+                               uint64_t up_offset, const QmvJob *jobs, size_t count, const float *x, float *y,
+                               const uint64_t *dev_w = nullptr, const uint32_t *go = nullptr);
 
 // True when the MFMA matvec takes this shape: Q4_K or Q6_K rows of whole
 // 256-value blocks, a weight base address aligned to 4 bytes (16 for Q4_K),

@@ -48,7 +48,8 @@ __global__ void gather_rows_kernel(const float *__restrict__ x, const uint32_t *
 __global__ void moe_combine_pos_kernel(const float *__restrict__ expert_out,
                                        const uint32_t *__restrict__ pos, const float *__restrict__ p,
                                        uint32_t batch, uint32_t k, uint32_t hidden,
-                                       float *__restrict__ y) {
+                                       float *__restrict__ y, const uint32_t *__restrict__ go) {
+    if (go && *go == 0) return;  // the device-side lookup found a slot missing
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < (size_t)batch * hidden;
          e += (size_t)gridDim.x * blockDim.x) {
         uint32_t t = (uint32_t)(e / hidden), i = (uint32_t)(e - (size_t)t * hidden);
@@ -59,6 +60,19 @@ __global__ void moe_combine_pos_kernel(const float *__restrict__ expert_out,
         }
         y[e] = acc;
     }
+}
+
+// Residency table of a layer (device addresses of each expert's slot bytes,
+// 0 when not resident), updated in stream order when a slot takes a new
+// expert: the previous expert's entries are cleared, the new one's set.
+__global__ void expert_table_kernel(uint64_t *gate_up_of, uint64_t *down_of, uint64_t previous, uint64_t expert,
+                                    uint64_t gate_up, uint64_t down) {
+    if (previous != ~0ull) {
+        gate_up_of[previous] = 0;
+        down_of[previous] = 0;
+    }
+    gate_up_of[expert] = gate_up;
+    down_of[expert] = down;
 }
 
 // A kernel of this file: resolving it loads the file's code object.
@@ -90,6 +104,13 @@ struct Layer {
     dmhip_expert_layer_layout layout;
     std::vector<Slot> slots;
     uint64_t clock = 0;
+    // This layer's residency table: gate_up addresses at table[0 ..
+    // expert_count), down addresses after them (device memory).
+    uint64_t *table = nullptr;
+    // Whether the next one-token MoE call tries the device-side lookup: set
+    // after a call whose experts were all resident, cleared by one that
+    // found a slot missing.
+    bool try_lookup = true;
 };
 
 // Memory source: the device time of one upload, a (start, end) pair of
@@ -131,11 +152,16 @@ struct dmhip_expert_cache {
     // Release events, used round-robin: one record per released group.
     std::vector<hipEvent_t> release_events;
     size_t next_release = 0;
+    // Device memory: every layer's residency table, then the lookup's
+    // outputs (gate_up and down addresses per selection, the go word).
+    uint64_t *tables = nullptr;
+    uint64_t *lookup_gate_up = nullptr, *lookup_down = nullptr;
+    uint32_t *lookup_go = nullptr;
 };
 
 namespace {
 constexpr size_t kSelectionPairs = 16 * dm::kMaxTopK;  // batch <= 16
-constexpr size_t kSelectionBytes = kSelectionPairs * 8 + 16 * 4;  // ids, probabilities, per-token flags
+constexpr size_t kSelectionBytes = kSelectionPairs * 8 + 16 * 4 + 16;  // ids, probabilities, per-token flags, go
 constexpr size_t kReleaseEvents = 64;
 constexpr size_t kStagingEntries = 4;  // file source: experts in flight from storage
 // Memory source: uploads whose timing is kept until it is read.  The ring is
@@ -274,6 +300,12 @@ int acquire(dmhip_expert_cache *c, size_t layer_index, size_t expert, size_t *sl
     Slot &s = layer.slots[victim];
     if (s.has) c->stats.evictions += 1;
     DM_CHECK_STATUS(upload_expert(c, layer.layout, expert, s));
+    // the residency table follows on the compute stream, behind its wait for
+    // the upload
+    hipLaunchKernelGGL(expert_table_kernel, dim3(1), dim3(1), 0, c->ctx->stream, layer.table,
+                       layer.table + layer.layout.expert_count, s.has ? (uint64_t)s.expert : ~0ull,
+                       (uint64_t)expert, (uint64_t)(uintptr_t)s.gate_up, (uint64_t)(uintptr_t)s.down);
+    DM_HIP(hipGetLastError());
     c->stats.reads += 2;
     c->stats.bytes_read += layer.layout.gate_up_bytes + layer.layout.down_bytes;
     s.has = true;
@@ -349,6 +381,7 @@ void destroy(dmhip_expert_cache *c) {
     // stream) may already be gone
     c->work.stream = nullptr;
     c->work.release();
+    if (c->tables) (void)hipFree(c->tables);
     if (c->host_selection) (void)hipHostFree(c->host_selection);
     delete c;
 }
@@ -392,6 +425,24 @@ int build_cache(dmhip_ctx *ctx, const dmhip_expert_layer_layout *layouts, size_t
         c->host_selection = nullptr;
         return fail_alloc(kSelectionBytes);
     }
+    // residency tables (all zero: nothing resident) and the lookup outputs
+    size_t entries = 0;
+    for (const Layer &layer : c->layers) entries += 2 * layer.layout.expert_count;
+    const size_t table_bytes = (entries + 2 * kMaxTopK + 1) * sizeof(uint64_t);
+    if (hipMalloc((void **)&c->tables, table_bytes) != hipSuccess) {
+        c->tables = nullptr;
+        return fail_alloc(table_bytes);
+    }
+    if (hipMemset(c->tables, 0, table_bytes) != hipSuccess)
+        return fail(DMHIP_ERR_COMMAND, "could not clear the expert residency tables");
+    size_t at = 0;
+    for (Layer &layer : c->layers) {
+        layer.table = c->tables + at;
+        at += 2 * layer.layout.expert_count;
+    }
+    c->lookup_gate_up = c->tables + at;
+    c->lookup_down = c->lookup_gate_up + kMaxTopK;
+    c->lookup_go = (uint32_t *)(c->lookup_down + kMaxTopK);
     return DMHIP_OK;
 }
 
@@ -588,17 +639,59 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     float *d_act = (float *)(w + a_act);
     float *d_eo = (float *)(w + a_eo);
 
+    // Grouped int8 path: one launch applies every slot of a phase, with the
+    // gate/up activation in its epilogue; act and expert-output rows are
+    // indexed by pair.  Slot buffers come from hipMalloc (256-byte aligned).
+    const uint64_t up_offset = (uint64_t)width * gu_row;
+    const bool grouped = qmv8_grouped_supported(gate_up_type, width, hidden, 2) &&
+                         qmv8_grouped_supported(down_type, hidden, width, 1) &&
+                         up_offset % (gate_up_type == 12 ? 16 : 4) == 0 &&  // 12: Q4_K
+                         (uint64_t)pairs * (hidden > width ? hidden : width) < (1ull << 31);
+
     // 1. Router logits (exact fold) and top-k softmax on the GPU.
     uint32_t *sel_ids = (uint32_t *)c->host_selection;
     float *sel_probs = (float *)(c->host_selection + kSelectionPairs * 4);
     uint32_t *sel_bad = (uint32_t *)(c->host_selection + kSelectionPairs * 8);
+    volatile uint32_t *sel_go = (volatile uint32_t *)(c->host_selection + kSelectionPairs * 8 + 16 * 4);
     // The previous call has finished (it ends with a synchronisation): the
     // per-token words can be cleared from here.
     memset(sel_bad, 0, 16 * 4);
-    DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
-                               (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs,
-                               BadFlag{ctx->flags + kMoeFlagWord, 1}, sel_ids, sel_probs,
-                               batch <= kRouterTickets ? ctx->router_tickets : nullptr, sel_bad));
+    Layer &Lay = c->layers[layer];
+    // One token whose experts are likely resident: the router's last
+    // workgroup looks the selected experts up in the layer's residency table
+    // and the expert launches and the combine are queued right behind it,
+    // reading the slot addresses it found; when a slot is missing (or the
+    // logits are not finite) they do nothing and the host takes the path
+    // below with the selection in hand.  Every earlier upload is already
+    // waited for on the compute stream, and every table update follows its
+    // upload there.
+    const bool lookup = Lay.try_lookup && grouped && k <= kMaxGroupedJobs &&
+                        router_takes_lookup((uint32_t)hidden, (uint32_t)experts, (uint32_t)batch, router_bf16, x);
+    if (lookup) {
+        *sel_go = 0;
+        const ExpertLookup el{Lay.table, Lay.table + L.expert_count, c->lookup_gate_up, c->lookup_down,
+                              c->lookup_go, (uint32_t *)sel_go};
+        DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts, (uint32_t)k,
+                                   1, x, d_logits, d_ids, d_probs, BadFlag{ctx->flags + kMoeFlagWord, 1}, sel_ids,
+                                   sel_probs, ctx->router_tickets, sel_bad, &el));
+        std::vector<QmvJob> gu_jobs(k), dn_jobs(k);
+        for (size_t p = 0; p < k; p++) {
+            gu_jobs[p] = QmvJob{nullptr, 1u, 0u, (uint32_t)(p * width), 0, 0};
+            dn_jobs[p] = QmvJob{nullptr, 1u, (uint32_t)(p * width), (uint32_t)(p * hidden), 0, 0};
+        }
+        DM_HIP(launch_qmv8_grouped(ctx, gate_up_type, (uint32_t)width, (uint32_t)hidden, 1, up_offset,
+                                   gu_jobs.data(), k, x, d_act, c->lookup_gate_up, c->lookup_go));
+        DM_HIP(launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(), k,
+                                   d_act, d_eo, c->lookup_down, c->lookup_go));
+        hipLaunchKernelGGL(moe_combine_pos_kernel, dim3((uint32_t)((hidden + 255) / 256)), dim3(256), 0,
+                           ctx->stream, d_eo, nullptr, d_probs, 1u, (uint32_t)k, (uint32_t)hidden, y, c->lookup_go);
+        DM_HIP(hipGetLastError());
+    } else {
+        DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
+                                   (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs,
+                                   BadFlag{ctx->flags + kMoeFlagWord, 1}, sel_ids, sel_probs,
+                                   batch <= kRouterTickets ? ctx->router_tickets : nullptr, sel_bad));
+    }
     DM_HIP(hipStreamSynchronize(ctx->stream));
     // top_k_softmax rejects non-finite logits (src/cpu.rs:240-245); nothing
     // has been acquired yet.
@@ -606,6 +699,16 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
         if (sel_bad[t]) return fail_non_finite("top-k softmax");
     memcpy(ids, sel_ids, pairs * 4);
     memcpy(probabilities, sel_probs, pairs * 4);
+    if (lookup && *sel_go) {
+        // Done on the device: the cache's bookkeeping is the reference's
+        // acquire sequence, every one a hit, then the slots' release after
+        // the work that read them.
+        std::vector<size_t> slots(k);
+        for (size_t p = 0; p < k; p++) DM_CHECK_STATUS(acquire(c, layer, ids[p], &slots[p]));
+        return record_release(c, layer, slots.data(), k);
+    }
+    if (lookup) Lay.try_lookup = false;
+    const uint64_t misses_before = c->stats.misses;
 
     // 2. Acquire in the reference's order (token by token, selection order)
     //    and cut the pairs into phases: a phase ends before an acquire whose
@@ -616,14 +719,6 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     // Host sources of the per-phase token lists stay alive until the final
     // synchronisation below.
     std::vector<std::vector<uint32_t>> phase_tokens;
-    // Grouped int8 path: one launch applies every slot of a phase, with the
-    // gate/up activation in its epilogue; act and expert-output rows are
-    // indexed by pair.  Slot buffers come from hipMalloc (256-byte aligned).
-    const uint64_t up_offset = (uint64_t)width * gu_row;
-    const bool grouped = qmv8_grouped_supported(gate_up_type, width, hidden, 2) &&
-                         qmv8_grouped_supported(down_type, hidden, width, 1) &&
-                         up_offset % (gate_up_type == 12 ? 16 : 4) == 0 &&  // 12: Q4_K
-                         (uint64_t)pairs * (hidden > width ? hidden : width) < (1ull << 31);
     std::vector<QmvJob> gu_jobs, dn_jobs;
     auto run_phase = [&](size_t p0, size_t p1) -> int {
         if (p0 == p1) return DMHIP_OK;
@@ -737,9 +832,12 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     if (!grouped) DM_HIP(hipMemcpyAsync(d_pos, pos.data(), pairs * 4, hipMemcpyHostToDevice, ctx->stream));
     hipLaunchKernelGGL(moe_combine_pos_kernel, dim3((uint32_t)((batch * hidden + 255) / 256)), dim3(256), 0,
                        ctx->stream, d_eo, grouped ? nullptr : d_pos, d_probs, (uint32_t)batch, (uint32_t)k,
-                       (uint32_t)hidden, y);
+                       (uint32_t)hidden, y, nullptr);
     DM_HIP(hipGetLastError());
     DM_HIP(hipStreamSynchronize(ctx->stream));
+    // a call whose experts were all resident lets the next one-token call
+    // try the device-side lookup again
+    if (c->stats.misses == misses_before) Lay.try_lookup = true;
     return DMHIP_OK;
 }
 

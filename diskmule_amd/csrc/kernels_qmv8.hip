@@ -893,7 +893,7 @@ struct Job8 {
     uint32_t x_off, y_off;
     int32_t x_stride, y_stride;
 };
-constexpr uint32_t kMaxJobs8 = 64;
+constexpr uint32_t kMaxJobs8 = kMaxGroupedJobs;
 struct JobTable8 {
     Job8 job[kMaxJobs8];
 };
@@ -902,9 +902,13 @@ template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
 __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     __attribute__((amdgpu_waves_per_eu(waves_per_eu8<TYPE, MODE, TOK, G>()))) qmv8_grouped_kernel(JobTable8 jobs, uint32_t rows, uint32_t columns, uint32_t row_bytes,
                         uint32_t total_bytes, uint64_t w2_offset, const float *__restrict__ x,
-                        float *__restrict__ y, int glm) {
+                        float *__restrict__ y, int glm, const uint64_t *__restrict__ dev_w,
+                        const uint32_t *__restrict__ go) {
+    // Jobs whose matrices a kernel earlier on the stream looked up: their
+    // addresses come from dev_w, and the launch does nothing when go is 0.
+    if (go && *go == 0) return;
     const Job8 j = jobs.job[blockIdx.y];
-    const uint8_t *w = (const uint8_t *)j.w;
+    const uint8_t *w = (const uint8_t *)(dev_w ? dev_w[blockIdx.y] : j.w);
     qmv8_body<TYPE, S, MODE, TOK, G, (S > 8 ? S : 8)>(w, w + w2_offset, rows, columns, row_bytes, total_bytes, x + j.x_off,
                                      j.x_stride, 0, 0.0f, glm, y + j.y_off, j.y_stride, nullptr,
                                      ArgmaxFinish{nullptr, nullptr, nullptr, nullptr});
@@ -1108,9 +1112,14 @@ Plan8 plan8_grouped(uint32_t type, uint32_t rows, uint32_t columns, uint32_t bat
     return p;
 }
 
+struct DeviceJobs {
+    const uint64_t *w;
+    const uint32_t *go;
+};
+
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
 hipError_t run8_grouped(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, uint64_t up_offset,
-                        const JobTable8 &table, uint32_t count, const float *x, float *y) {
+                        const JobTable8 &table, uint32_t count, const float *x, float *y, DeviceJobs dj) {
     constexpr uint32_t WAVES = 8;
     const uint32_t tiles = (rows + 15) / 16;
     const uint32_t blocks = columns / 256;
@@ -1126,25 +1135,26 @@ hipError_t run8_grouped(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, uint64_
         if (e != hipSuccess) return e;
     }
     return launch_kernel(ctx, kernel, dim3(grid, count), dim3(64 * WAVES), lds, table, rows, columns, row_bytes,
-                         row_bytes * rows, up_offset, x, y, MODE == 2 ? 1 : 0);
+                         row_bytes * rows, up_offset, x, y, MODE == 2 ? 1 : 0, dj.w, dj.go);
 }
 
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
 hipError_t run8_grouped_sg(dmhip_ctx *ctx, uint32_t s, uint32_t rows, uint32_t columns, uint64_t up_offset,
-                           const JobTable8 &table, uint32_t count, const float *x, float *y) {
+                           const JobTable8 &table, uint32_t count, const float *x, float *y, DeviceJobs dj) {
     switch (s) {
-    case 1: return run8_grouped<TYPE, 1, MODE, TOK, G>(ctx, rows, columns, up_offset, table, count, x, y);
-    case 2: return run8_grouped<TYPE, 2, MODE, TOK, G>(ctx, rows, columns, up_offset, table, count, x, y);
-    case 4: return run8_grouped<TYPE, 4, MODE, TOK, G>(ctx, rows, columns, up_offset, table, count, x, y);
-    default: return run8_grouped<TYPE, 8, MODE, TOK, G>(ctx, rows, columns, up_offset, table, count, x, y);
+    case 1: return run8_grouped<TYPE, 1, MODE, TOK, G>(ctx, rows, columns, up_offset, table, count, x, y, dj);
+    case 2: return run8_grouped<TYPE, 2, MODE, TOK, G>(ctx, rows, columns, up_offset, table, count, x, y, dj);
+    case 4: return run8_grouped<TYPE, 4, MODE, TOK, G>(ctx, rows, columns, up_offset, table, count, x, y, dj);
+    default: return run8_grouped<TYPE, 8, MODE, TOK, G>(ctx, rows, columns, up_offset, table, count, x, y, dj);
     }
 }
 
 template <uint32_t TYPE, int MODE, int TOK>
 hipError_t run8_grouped_s(dmhip_ctx *ctx, const Plan8 &p, uint32_t rows, uint32_t columns, uint64_t up_offset,
-                          const JobTable8 &table, uint32_t count, const float *x, float *y) {
-    if (p.g == 2) return run8_grouped_sg<TYPE, MODE, TOK, 2>(ctx, p.s, rows, columns, up_offset, table, count, x, y);
-    return run8_grouped_sg<TYPE, MODE, TOK, 1>(ctx, p.s, rows, columns, up_offset, table, count, x, y);
+                          const JobTable8 &table, uint32_t count, const float *x, float *y, DeviceJobs dj) {
+    if (p.g == 2)
+        return run8_grouped_sg<TYPE, MODE, TOK, 2>(ctx, p.s, rows, columns, up_offset, table, count, x, y, dj);
+    return run8_grouped_sg<TYPE, MODE, TOK, 1>(ctx, p.s, rows, columns, up_offset, table, count, x, y, dj);
 }
 
 template <uint32_t TYPE>
@@ -1223,8 +1233,16 @@ bool qmv8_grouped_supported(uint32_t type, size_t rows, size_t columns, uint32_t
 }
 
 hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, int gate_up,
-                               uint64_t up_offset, const QmvJob *jobs, size_t count, const float *x, float *y) {
+                               uint64_t up_offset, const QmvJob *jobs, size_t count, const float *x, float *y,
+                               const uint64_t *dev_w, const uint32_t *go) {
     const uint32_t mats = gate_up ? 2u : 1u;
+    // device-side addresses: one launch of one-token jobs, in order
+    if (dev_w) {
+        if (count > kMaxJobs8) return hipErrorInvalidValue;
+        for (size_t i = 0; i < count; i++)
+            if (jobs[i].tokens != 1) return hipErrorInvalidValue;
+    }
+    const DeviceJobs dj{dev_w, go};
     // Jobs of one and of two tokens go to separate launches, kMaxJobs8 each.
     for (uint32_t tok = 1; tok <= 2; tok++) {
         size_t i = 0;
@@ -1242,15 +1260,15 @@ hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uin
             if (p.s == 0) return hipErrorInvalidValue;
             hipError_t e;
             if (type == kQ4_K) {
-                e = gate_up ? (tok == 1 ? run8_grouped_s<kQ4_K, 2, 1>(ctx, p, rows, columns, up_offset, table, n, x, y)
-                                        : run8_grouped_s<kQ4_K, 2, 2>(ctx, p, rows, columns, up_offset, table, n, x, y))
-                            : (tok == 1 ? run8_grouped_s<kQ4_K, 0, 1>(ctx, p, rows, columns, 0, table, n, x, y)
-                                        : run8_grouped_s<kQ4_K, 0, 2>(ctx, p, rows, columns, 0, table, n, x, y));
+                e = gate_up ? (tok == 1 ? run8_grouped_s<kQ4_K, 2, 1>(ctx, p, rows, columns, up_offset, table, n, x, y, dj)
+                                        : run8_grouped_s<kQ4_K, 2, 2>(ctx, p, rows, columns, up_offset, table, n, x, y, dj))
+                            : (tok == 1 ? run8_grouped_s<kQ4_K, 0, 1>(ctx, p, rows, columns, 0, table, n, x, y, dj)
+                                        : run8_grouped_s<kQ4_K, 0, 2>(ctx, p, rows, columns, 0, table, n, x, y, dj));
             } else {
-                e = gate_up ? (tok == 1 ? run8_grouped_s<kQ6_K, 2, 1>(ctx, p, rows, columns, up_offset, table, n, x, y)
-                                        : run8_grouped_s<kQ6_K, 2, 2>(ctx, p, rows, columns, up_offset, table, n, x, y))
-                            : (tok == 1 ? run8_grouped_s<kQ6_K, 0, 1>(ctx, p, rows, columns, 0, table, n, x, y)
-                                        : run8_grouped_s<kQ6_K, 0, 2>(ctx, p, rows, columns, 0, table, n, x, y));
+                e = gate_up ? (tok == 1 ? run8_grouped_s<kQ6_K, 2, 1>(ctx, p, rows, columns, up_offset, table, n, x, y, dj)
+                                        : run8_grouped_s<kQ6_K, 2, 2>(ctx, p, rows, columns, up_offset, table, n, x, y, dj))
+                            : (tok == 1 ? run8_grouped_s<kQ6_K, 0, 1>(ctx, p, rows, columns, 0, table, n, x, y, dj)
+                                        : run8_grouped_s<kQ6_K, 0, 2>(ctx, p, rows, columns, 0, table, n, x, y, dj));
             }
             if (e != hipSuccess) return e;
         }

@@ -361,6 +361,21 @@ __global__ void __launch_bounds__(256) router_staged_kernel(
     }
 }
 
+// The selected experts' slots (MoE layer call of one token): thread 0 of
+// the token's last workgroup looks each id up and publishes the addresses
+// and the go word (ExpertLookup).
+__device__ void expert_lookup(const ExpertLookup &L, const uint32_t *ids, uint32_t k, bool bad) {
+    uint32_t go = bad ? 0u : 1u;
+    for (uint32_t s = 0; s < k; s++) {
+        const uint64_t gu = L.gate_up_of[ids[s]], dn = L.down_of[ids[s]];
+        if (gu == 0 || dn == 0) go = 0;
+        L.gate_up_w[s] = gu;
+        L.down_w[s] = dn;
+    }
+    *L.go = go;
+    *L.host_go = go;
+}
+
 // Expert-parallel form of the exact router for decode: workgroup (g, t) is
 // one wave that folds the RF_EXPERTS rows g * RF_EXPERTS .. of token t.
 // Lane e < RF_EXPERTS still folds its row sequentially from column 0 with
@@ -383,7 +398,8 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
                                                          uint32_t experts, uint32_t k, const float *__restrict__ x,
                                                          float *logits, uint32_t *tickets, uint32_t *ids,
                                                          float *probabilities, BadFlag non_finite,
-                                                         uint32_t *host_ids, float *host_probs, uint32_t *host_bad) {
+                                                         uint32_t *host_ids, float *host_probs, uint32_t *host_bad,
+                                                         ExpertLookup lookup) {
     __shared__ v4a rf_lds[2 * RF_BUF / 4];
     const uint32_t lane = threadIdx.x, e0 = blockIdx.x * RF_EXPERTS, token = blockIdx.y;
     const uint32_t chunks = (hidden + RF_CHUNK - 1) / RF_CHUNK;
@@ -497,6 +513,7 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
             }
             host_bad[token] = bad;
         }
+        if (lookup.go) expert_lookup(lookup, ti, k, bad);
         __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -576,7 +593,7 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
                                                          const float *__restrict__ x, float *logits,
                                                          uint32_t *tickets, uint32_t *ids, float *probabilities,
                                                          BadFlag non_finite, uint32_t *host_ids, float *host_probs,
-                                                         uint32_t *host_bad) {
+                                                         uint32_t *host_bad, ExpertLookup lookup) {
     constexpr uint32_t kBatch = 16;   // row loads per thread in flight
     constexpr uint32_t kXPieces = 8;  // x loads per thread: hidden <= 8192
     const uint32_t N8 = hidden / 8, NS = router_lds_steps(hidden), RS = router_lds_row_pieces(hidden);
@@ -706,6 +723,7 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
             }
             host_bad[token] = row_bad;
         }
+        if (lookup.go) expert_lookup(lookup, ti, k, row_bad);
         __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -894,16 +912,30 @@ static hipError_t launch_router_staged(hipStream_t s, const uint16_t *router, ui
     return hipGetLastError();
 }
 
+namespace {
+bool router_staged(uint32_t hidden, uint32_t experts, const void *router, const float *x) {
+    return experts <= 256 && hidden % 8 == 0 && (uint64_t)experts * hidden * 2 < (1ull << 30) &&
+           ((uintptr_t)router & 15u) == 0 && ((uintptr_t)x & 15u) == 0;
+}
+}  // namespace
+
+bool router_takes_lookup(uint32_t hidden, uint32_t experts, uint32_t batch, const void *router, const float *x) {
+    return batch == 1 && router_staged(hidden, experts, router, x) && experts >= 2 * RF_EXPERTS;
+}
+
 hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
                                BadFlag non_finite, uint32_t *host_ids, float *host_probs, uint32_t *tickets,
-                               uint32_t *host_bad) {
+                               uint32_t *host_bad, const ExpertLookup *lookup) {
     if (host_ids && (!host_probs || !host_bad)) return hipErrorInvalidValue;
-    const bool staged = experts <= 256 && hidden % 8 == 0 && (uint64_t)experts * hidden * 2 < (1ull << 30) && ((uintptr_t)router & 15u) == 0 &&
-                        ((uintptr_t)x & 15u) == 0;
+    const bool staged = router_staged(hidden, experts, router, x);
+    if (lookup && (!tickets || !router_takes_lookup(hidden, experts, batch, router, x)))
+        return hipErrorInvalidValue;
+    const ExpertLookup no_lookup{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    const ExpertLookup L = lookup ? *lookup : no_lookup;
     // Decode batches: the expert-parallel fold, then the selection.
-    if (staged && experts >= 2 * RF_EXPERTS && (uint64_t)experts * hidden * 2 < 0x80000000ull) {
+    if (staged && experts >= 2 * RF_EXPERTS) {
         // as many rows per workgroup as fit in LDS beside x and the
         // kernel's own arrays (the rank selection's keys, ids, logits)
         constexpr size_t kLdsBudget = 160 * 1024 - 8 * 1024;
@@ -916,11 +948,11 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL(router_lds_kernel, dim3((experts + R - 1) / R, batch), dim3(256), lds, s, router,
                                hidden, experts, R, k, x, logits, tickets, ids, probabilities, non_finite, host_ids,
-                               host_probs, host_bad);
+                               host_probs, host_bad, L);
         } else
             hipLaunchKernelGGL(router_fold_kernel, dim3((experts + RF_EXPERTS - 1) / RF_EXPERTS, batch), dim3(64),
                                0, s, router, hidden, experts, k, x, logits, tickets, ids, probabilities, non_finite,
-                               host_ids, host_probs, host_bad);
+                               host_ids, host_probs, host_bad, L);
         if (!tickets)
             hipLaunchKernelGGL(top_k_host_kernel, dim3(batch), dim3(256), 0, s, logits, experts, k, ids,
                                probabilities, non_finite, host_ids, host_probs, host_bad);

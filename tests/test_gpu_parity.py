@@ -1113,6 +1113,58 @@ def test_moe_layer_matches_oracle(ctx, batch):
     src.free()
 
 
+@pytest.mark.parametrize("slots", [8, 16])
+def test_moe_layer_resident_lookup_sequence(ctx, slots):
+    """One-token MoE calls that take the device-side slot lookup once their
+    experts are resident, and fall back when a slot is missing: tokens a, a,
+    a, b, b, b, a, a, a non-finite token, a.  With 8 slots token b evicts
+    token a's experts it does not share, so the later calls of a must not
+    use a slot that now holds another expert.  Every clean call equals the
+    oracle (ids, weights, output); the non-finite call returns NonFinite and
+    acquires nothing; the cache counters equal the reference LRU's for the
+    same acquire sequence."""
+    hidden, width, experts, k = 2048, 768, 128, 8
+    router, gu, dn, gu_bytes, dn_bytes = _moe_setup(hidden, width, experts)
+    src = PinnedHostBuffer(gu.size + dn.size)
+    src.array[:gu.size] = gu
+    src.array[gu.size:] = dn
+    cache = ExpertCache(ctx, src, [ExpertLayerLayout(experts, 0, gu_bytes, gu.size, dn_bytes)], slots)
+    xs = {name: synth.normal(synth.activation_seed(45, i), hidden).reshape(1, hidden)
+          for i, name in enumerate("ab")}
+    want = {name: capi.moe_layer(1, hidden, width, experts, k, router, Q4_K, gu, Q6_K, dn, x)
+            for name, x in xs.items()}
+    bad = xs["a"].copy()
+    bad[0, 100] = np.nan
+    rb, yb = dev(ctx, router), dev_out(ctx, hidden * 4)
+    dx = {name: dev(ctx, x) for name, x in xs.items()}
+    lru = capi.Lru([experts], slots, gu_bytes, dn_bytes)
+    for step, name in enumerate(["a", "a", "a", "b", "b", "b", "a", "a", "bad", "a"]):
+        print(f"slots={slots} call {step}: token {name}", flush=True)
+        if name == "bad":
+            before = cache.stats()
+            with pytest.raises(HipError) as e:
+                ctx.moe_layer(cache, 0, 1, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                              dev(ctx, bad).device_ptr, yb.device_ptr)
+            assert e.value.variant == "NonFinite"
+            after = cache.stats()
+            assert (after["hits"], after["misses"]) == (before["hits"], before["misses"])
+            continue
+        sel, wts, out = want[name]
+        ids, probs = ctx.moe_layer(cache, 0, 1, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                                   dx[name].device_ptr, yb.device_ptr)
+        assert np.array_equal(ids, sel), f"call {step}: expert ids differ"
+        assert np.allclose(probs, wts, rtol=1e-5, atol=1e-7)
+        got = yb.read(0, hidden * 4, np.float32)
+        assert_close(got, out[0], f"call {step} token {name}")
+        for e_id in sel[0]:
+            lru.acquire(0, int(e_id))
+    st, ref = cache.stats(), lru.stats()
+    for key in ("hits", "misses", "evictions", "reads", "bytes_read", "resident_bytes"):
+        assert st[key] == ref[key], key
+    cache.free()
+    src.free()
+
+
 # ---- config 5: prefill GEMM ----------------------------------------------------
 
 def _gemm_check(ctx, kind, m, n, k, seed, what):

@@ -506,9 +506,11 @@ int dmhip_matvec_safetensor_mapped(dmhip_ctx *ctx, uint32_t dtype, size_t rows, 
     DM_CHECK_STATUS(hc.in(ctx->in.ptr, input, columns * 4));
     const uint8_t *w = (const uint8_t *)mapping->dev + encoded_offset;
     const float *sc = fmt == kStBf16 ? nullptr : (const float *)((const uint8_t *)scale_mapping->dev + scale_offset);
+    // the kernel writes y straight into the pinned bounce buffer
+    float *o = (float *)hc.out_direct(output, rows * 4);
     DM_CHECK_STATUS(st_enqueue(ctx, fmt, rows, columns, w, sc, scale_length / 4, group, scale_columns,
-                               (const float *)ctx->in.ptr, (float *)ctx->out.ptr));
-    DM_CHECK_STATUS(hc.out(output, ctx->out.ptr, rows * 4));
+                               (const float *)ctx->in.ptr, o ? o : (float *)ctx->out.ptr));
+    if (!o) DM_CHECK_STATUS(hc.out(output, ctx->out.ptr, rows * 4));
     return hc.finish();
 }
 

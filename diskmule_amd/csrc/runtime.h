@@ -170,6 +170,10 @@ struct HostCall {
     int begin(size_t total);
     int in(void *device_dst, const void *host_src, size_t n);
     int out(void *host_dst, const void *device_src, size_t n);
+    // A place in the pinned bounce buffer where kernels may write an output
+    // of n bytes directly (no device-to-host copy), handed to host_dst at
+    // finish(); nullptr when the call is not staged (then use out()).
+    void *out_direct(void *host_dst, size_t n);
     int finish();
 };
 

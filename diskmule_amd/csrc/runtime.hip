@@ -235,6 +235,14 @@ int HostCall::out(void *host_dst, const void *device_src, size_t n) {
     return DMHIP_OK;
 }
 
+void *HostCall::out_direct(void *host_dst, size_t n) {
+    if (!staged || n == 0 || outs == 2) return nullptr;
+    char *b = (char *)ctx->bounce.ptr + used;
+    used += (n + 255) & ~(size_t)255;
+    pending[outs++] = Pending{host_dst, b, n};
+    return b;
+}
+
 int HostCall::finish() {
     open = false;
     DM_HIP(hipStreamSynchronize(ctx->stream));
@@ -660,8 +668,9 @@ int dmhip_rms_norm(dmhip_ctx *ctx, const float *input, size_t input_len, const f
     DM_CHECK(hc.begin((weight ? 3 : 2) * bytes));
     DM_CHECK(hc.in(din, input, bytes));
     if (weight) DM_CHECK(hc.in(dw, weight, bytes));
-    DM_HIP(launch_rms_norm(ctx->stream, din, 1, (uint32_t)input_len, dw, epsilon, (float *)ctx->out.ptr));
-    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    float *o = (float *)hc.out_direct(output, bytes);  // written by the kernel, no copy back
+    DM_HIP(launch_rms_norm(ctx->stream, din, 1, (uint32_t)input_len, dw, epsilon, o ? o : (float *)ctx->out.ptr));
+    if (!o) DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
     return hc.finish();
 }
 
@@ -684,8 +693,9 @@ int dmhip_silu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const flo
     DM_CHECK(hc.begin(3 * bytes));
     DM_CHECK(hc.in(dg, gate, bytes));
     DM_CHECK(hc.in(du, up, bytes));
-    DM_HIP(launch_silu_mul(ctx->stream, dg, du, gate_len, (float *)ctx->out.ptr));
-    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    float *o = (float *)hc.out_direct(output, bytes);
+    DM_HIP(launch_silu_mul(ctx->stream, dg, du, gate_len, o ? o : (float *)ctx->out.ptr));
+    if (!o) DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
     return hc.finish();
 }
 
@@ -705,8 +715,9 @@ int dmhip_softcap(dmhip_ctx *ctx, const float *input, size_t input_len, float ca
     HostCall hc(ctx);
     DM_CHECK(hc.begin(2 * bytes));
     DM_CHECK(hc.in(ctx->in.ptr, input, bytes));
-    DM_HIP(launch_softcap(ctx->stream, (const float *)ctx->in.ptr, input_len, cap, (float *)ctx->out.ptr));
-    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    float *o = (float *)hc.out_direct(output, bytes);
+    DM_HIP(launch_softcap(ctx->stream, (const float *)ctx->in.ptr, input_len, cap, o ? o : (float *)ctx->out.ptr));
+    if (!o) DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
     return hc.finish();
 }
 
@@ -728,8 +739,9 @@ int dmhip_add(dmhip_ctx *ctx, const float *left, size_t left_len, const float *r
     DM_CHECK(hc.begin(3 * bytes));
     DM_CHECK(hc.in(da, left, bytes));
     DM_CHECK(hc.in(db, right, bytes));
-    DM_HIP(launch_add(ctx->stream, da, db, left_len, (float *)ctx->out.ptr));
-    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    float *o = (float *)hc.out_direct(output, bytes);
+    DM_HIP(launch_add(ctx->stream, da, db, left_len, o ? o : (float *)ctx->out.ptr));
+    if (!o) DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
     return hc.finish();
 }
 
@@ -752,8 +764,9 @@ int dmhip_gelu_mul(dmhip_ctx *ctx, const float *gate, size_t gate_len, const flo
     DM_CHECK(hc.begin(3 * bytes));
     DM_CHECK(hc.in(dg, gate, bytes));
     DM_CHECK(hc.in(du, up, bytes));
-    DM_HIP(launch_gelu_mul(ctx->stream, dg, du, gate_len, (float *)ctx->out.ptr));
-    DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
+    float *o = (float *)hc.out_direct(output, bytes);
+    DM_HIP(launch_gelu_mul(ctx->stream, dg, du, gate_len, o ? o : (float *)ctx->out.ptr));
+    if (!o) DM_CHECK(hc.out(output, ctx->out.ptr, bytes));
     return hc.finish();
 }
 
@@ -866,8 +879,13 @@ static int matvec_from_device(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t
     HostCall hc(ctx);
     DM_CHECK(hc.begin(in_bytes + out_bytes));
     DM_CHECK(hc.in(ctx->in.ptr, input, in_bytes));
-    DM_CHECK(enqueue_matvec(ctx, type, rows, columns, w, 1, (const float *)ctx->in.ptr, (float *)ctx->out.ptr));
-    DM_CHECK(hc.out(output, ctx->out.ptr, out_bytes));
+    // The kernels write y straight into the pinned bounce buffer (plain
+    // stores; the rows travel to host memory while the rest is computed),
+    // so no copy follows them.
+    float *y = (float *)hc.out_direct(output, out_bytes);
+    DM_CHECK(enqueue_matvec(ctx, type, rows, columns, w, 1, (const float *)ctx->in.ptr,
+                            y ? y : (float *)ctx->out.ptr));
+    if (!y) DM_CHECK(hc.out(output, ctx->out.ptr, out_bytes));
     return hc.finish();
 }
 

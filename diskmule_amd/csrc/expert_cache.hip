@@ -62,19 +62,6 @@ __global__ void moe_combine_pos_kernel(const float *__restrict__ expert_out,
     }
 }
 
-// Residency table of a layer (device addresses of each expert's slot bytes,
-// 0 when not resident), updated in stream order when a slot takes a new
-// expert: the previous expert's entries are cleared, the new one's set.
-__global__ void expert_table_kernel(uint64_t *gate_up_of, uint64_t *down_of, uint64_t previous, uint64_t expert,
-                                    uint64_t gate_up, uint64_t down) {
-    if (previous != ~0ull) {
-        gate_up_of[previous] = 0;
-        down_of[previous] = 0;
-    }
-    gate_up_of[expert] = gate_up;
-    down_of[expert] = down;
-}
-
 // A kernel of this file: resolving it loads the file's code object.
 const void *module_anchor_expert() { return (const void *)gather_rows_kernel; }
 
@@ -104,9 +91,14 @@ struct Layer {
     dmhip_expert_layer_layout layout;
     std::vector<Slot> slots;
     uint64_t clock = 0;
-    // This layer's residency table: gate_up addresses at table[0 ..
-    // expert_count), down addresses after them (device memory).
-    uint64_t *table = nullptr;
+    // This layer's residency table: the device addresses of each expert's
+    // slot bytes (gate_up at [0, expert_count), down after them; 0 when not
+    // resident).  The host keeps the master copy in pinned memory and
+    // copies it to the device copy before a call that looks experts up,
+    // when it changed since.
+    uint64_t *table = nullptr;       // device copy
+    uint64_t *host_table = nullptr;  // pinned master
+    bool table_dirty = false;
     // Whether the next one-token MoE call tries the device-side lookup: set
     // after a call whose experts were all resident, cleared by one that
     // found a slot missing.
@@ -153,8 +145,10 @@ struct dmhip_expert_cache {
     std::vector<hipEvent_t> release_events;
     size_t next_release = 0;
     // Device memory: every layer's residency table, then the lookup's
-    // outputs (gate_up and down addresses per selection, the go word).
+    // outputs (gate_up and down addresses per selection, the go word); the
+    // tables' pinned host masters.
     uint64_t *tables = nullptr;
+    uint64_t *host_tables = nullptr;
     uint64_t *lookup_gate_up = nullptr, *lookup_down = nullptr;
     uint32_t *lookup_go = nullptr;
 };
@@ -300,12 +294,13 @@ int acquire(dmhip_expert_cache *c, size_t layer_index, size_t expert, size_t *sl
     Slot &s = layer.slots[victim];
     if (s.has) c->stats.evictions += 1;
     DM_CHECK_STATUS(upload_expert(c, layer.layout, expert, s));
-    // the residency table follows on the compute stream, behind its wait for
-    // the upload
-    hipLaunchKernelGGL(expert_table_kernel, dim3(1), dim3(1), 0, c->ctx->stream, layer.table,
-                       layer.table + layer.layout.expert_count, s.has ? (uint64_t)s.expert : ~0ull,
-                       (uint64_t)expert, (uint64_t)(uintptr_t)s.gate_up, (uint64_t)(uintptr_t)s.down);
-    DM_HIP(hipGetLastError());
+    // the residency table's master (no device reads it until it is copied,
+    // and every call that copies it has ended with a synchronisation)
+    const size_t n = layer.layout.expert_count;
+    if (s.has) layer.host_table[s.expert] = layer.host_table[n + s.expert] = 0;
+    layer.host_table[expert] = (uint64_t)(uintptr_t)s.gate_up;
+    layer.host_table[n + expert] = (uint64_t)(uintptr_t)s.down;
+    layer.table_dirty = true;
     c->stats.reads += 2;
     c->stats.bytes_read += layer.layout.gate_up_bytes + layer.layout.down_bytes;
     s.has = true;
@@ -382,6 +377,7 @@ void destroy(dmhip_expert_cache *c) {
     c->work.stream = nullptr;
     c->work.release();
     if (c->tables) (void)hipFree(c->tables);
+    if (c->host_tables) (void)hipHostFree(c->host_tables);
     if (c->host_selection) (void)hipHostFree(c->host_selection);
     delete c;
 }
@@ -435,9 +431,15 @@ int build_cache(dmhip_ctx *ctx, const dmhip_expert_layer_layout *layouts, size_t
     }
     if (hipMemset(c->tables, 0, table_bytes) != hipSuccess)
         return fail(DMHIP_ERR_COMMAND, "could not clear the expert residency tables");
+    if (entries && hipHostMalloc((void **)&c->host_tables, entries * sizeof(uint64_t), hipHostMallocDefault) != hipSuccess) {
+        c->host_tables = nullptr;
+        return fail_alloc(entries * sizeof(uint64_t));
+    }
+    if (entries) memset(c->host_tables, 0, entries * sizeof(uint64_t));
     size_t at = 0;
     for (Layer &layer : c->layers) {
         layer.table = c->tables + at;
+        layer.host_table = c->host_tables + at;
         at += 2 * layer.layout.expert_count;
     }
     c->lookup_gate_up = c->tables + at;
@@ -663,12 +665,17 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     // reading the slot addresses it found; when a slot is missing (or the
     // logits are not finite) they do nothing and the host takes the path
     // below with the selection in hand.  Every earlier upload is already
-    // waited for on the compute stream, and every table update follows its
-    // upload there.
+    // waited for on the compute stream, before the table copy and the
+    // router.
     const bool lookup = Lay.try_lookup && grouped && k <= kMaxGroupedJobs &&
                         router_takes_lookup((uint32_t)hidden, (uint32_t)experts, (uint32_t)batch, router_bf16, x);
     if (lookup) {
         *sel_go = 0;
+        if (Lay.table_dirty) {
+            DM_HIP(hipMemcpyAsync(Lay.table, Lay.host_table, 2 * L.expert_count * sizeof(uint64_t),
+                                  hipMemcpyHostToDevice, ctx->stream));
+            Lay.table_dirty = false;
+        }
         const ExpertLookup el{Lay.table, Lay.table + L.expert_count, c->lookup_gate_up, c->lookup_down,
                               c->lookup_go, (uint32_t *)sel_go};
         DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts, (uint32_t)k,

@@ -691,6 +691,9 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
         s_logit[tid] = v;
     }
     if (bad) *non_finite.word = non_finite.mark;  // every writer stores the same value
+    __shared__ float s_sum;
+    __shared__ uint32_t s_missing;
+    if (tid == 0) s_missing = 0;
     const bool row_bad = __syncthreads_or((int)bad) != 0;
     if (tid < experts) {
         // keys are unique (value, then index), so ranks are 0 .. experts - 1
@@ -699,31 +702,45 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
         if (rank < k) s_sel[rank] = tid;
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t *ti = ids + (size_t)token * k;
-        float *tp = probabilities + (size_t)token * k;
-        // softmax_in_place over the selected logits (src/cpu.rs:195-230):
-        // maximum, exp(v - max), sequential sum, divide.
+    // softmax_in_place over the selected logits (src/cpu.rs:195-230):
+    // maximum, exp(v - max), sequential sum, divide; selection s by thread s
+    // (k <= experts <= 256), the sum in selection order by thread 0.
+    uint32_t *ti = ids + (size_t)token * k;
+    float *tp = probabilities + (size_t)token * k;
+    if (tid < k) {
+        const uint32_t index = s_sel[tid];
         float maximum = -__builtin_inff();
-        for (uint32_t s = 0; s < k; s++) {
-            const uint32_t index = s_sel[s];
-            ti[s] = index;
-            maximum = fmaxf(maximum, s_logit[index]);
+        for (uint32_t j = 0; j < k; j++) maximum = fmaxf(maximum, s_logit[s_sel[j]]);
+        s_value[tid] = expf(s_logit[index] - maximum);
+        ti[tid] = index;
+        if (host_ids) host_ids[(size_t)token * k + tid] = index;
+        if (lookup.go) {
+            // the selected expert's slot (ExpertLookup)
+            const uint64_t gu = lookup.gate_up_of[index], dn = lookup.down_of[index];
+            lookup.gate_up_w[tid] = gu;
+            lookup.down_w[tid] = dn;
+            if (gu == 0 || dn == 0) s_missing = 1;  // every writer stores the same value
         }
+    }
+    __syncthreads();
+    if (tid == 0) {
         float sum = 0.0f;
-        for (uint32_t s = 0; s < k; s++) {
-            s_value[s] = expf(s_logit[s_sel[s]] - maximum);
-            sum += s_value[s];
+        for (uint32_t j = 0; j < k; j++) sum += s_value[j];
+        s_sum = sum;
+    }
+    __syncthreads();
+    if (tid < k) {
+        const float p = s_value[tid] / s_sum;
+        tp[tid] = p;
+        if (host_ids) host_probs[(size_t)token * k + tid] = p;
+    }
+    if (tid == 0) {
+        if (host_ids) host_bad[token] = row_bad;
+        if (lookup.go) {
+            const uint32_t go = row_bad || s_missing ? 0u : 1u;
+            *lookup.go = go;
+            *lookup.host_go = go;
         }
-        for (uint32_t s = 0; s < k; s++) tp[s] = s_value[s] / sum;
-        if (host_ids) {
-            for (uint32_t s = 0; s < k; s++) {
-                host_ids[(size_t)token * k + s] = ti[s];
-                host_probs[(size_t)token * k + s] = tp[s];
-            }
-            host_bad[token] = row_bad;
-        }
-        if (lookup.go) expert_lookup(lookup, ti, k, row_bad);
         __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }

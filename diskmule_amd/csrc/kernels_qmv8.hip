@@ -43,6 +43,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kStep8 = 192;  // A bytes of one MFMA step: 4 groups x 3 terms x 16
 constexpr uint32_t kZero8 = 1024;  // zeroed LDS bytes read by lanes whose A row is idle
+constexpr int kNonTemporal = 2;     // buffer load cache policy: NT (no reuse expected)
 constexpr uint32_t kMaxWaves8 = 16;
 // Tokens per launch: lane group g writes token g.  A batch's records must
 // fit the workgroup's LDS with the staging areas (plan8), which bounds the
@@ -565,13 +566,36 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
         next_row_base = (live && rw < rows) ? rw * row_bytes : nowhere;
     };
     v4u st[NL], st2[MODE == 2 ? NL : 1];
+    // Consecutive fetches of a row share the 128-byte line at their
+    // boundary, and a wave's next fetch of the row comes microseconds later:
+    // the rest of a fetch is loaded non-temporal (evicted first from the
+    // L2), the chunks in the line where the row's next fetch starts are
+    // loaded normally, so that line is still there for it (C2: 1.11 ->
+    // 1.06 times the algorithmic bytes, 95 -> 92 us).  Lines are 128-byte
+    // aligned in the address space, hence the base's low bits (the gate/up
+    // pairs' matrices share them: separate allocations, or the up rows at a
+    // multiple of 128 bytes; otherwise only the cache hint is off).
+    const uint32_t lo = (uint32_t)(uintptr_t)w & 127u;
+    constexpr bool kHint = S == 1 && !PC && TOK == 1;
     auto fetch = [&](uint32_t grp, bool live) {
 #pragma unroll
         for (uint32_t j = 0; j < NL; j++) {
-            const uint32_t off =
-                (!live || src_row[j] == nowhere) ? nowhere : ((src_row[j] + grp * G * BB) & ~3u) + src_chunk[j];
-            st[j] = __builtin_bit_cast(v4u, rsrc_load16(rsrc, off));
-            if constexpr (MODE == 2) st2[j] = __builtin_bit_cast(v4u, rsrc_load16(rsrc2, off));
+            const uint32_t cur = (src_row[j] + grp * G * BB) & ~3u;
+            const uint32_t off = (!live || src_row[j] == nowhere) ? nowhere : cur + src_chunk[j];
+            // the line where the next fetch starts (within 3 bytes: a hint);
+            // only where one wave reads a tile's groups one after another
+            // (the persistent one-tile-per-wave schedule, one token): where
+            // neighbouring waves read adjacent groups at the same time, the
+            // hint made C1, C3 and the Q8_0 head 10-14% slower
+            const bool keep = !kHint || off + 16 > ((lo + cur + G * BB) & ~127u) - lo;
+            if (keep) {
+                st[j] = __builtin_bit_cast(v4u, rsrc_load16(rsrc, off));
+                if constexpr (MODE == 2) st2[j] = __builtin_bit_cast(v4u, rsrc_load16(rsrc2, off));
+            } else {
+                st[j] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, kNonTemporal));
+                if constexpr (MODE == 2)
+                    st2[j] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsrc2, off, 0, kNonTemporal));
+            }
         }
     };
 

@@ -708,11 +708,15 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     memcpy(probabilities, sel_probs, pairs * 4);
     if (lookup && *sel_go) {
         // Done on the device: the cache's bookkeeping is the reference's
-        // acquire sequence, every one a hit, then the slots' release after
-        // the work that read them.
-        std::vector<size_t> slots(k);
-        for (size_t p = 0; p < k; p++) DM_CHECK_STATUS(acquire(c, layer, ids[p], &slots[p]));
-        return record_release(c, layer, slots.data(), k);
+        // acquire sequence, every one a hit.  The work that read the slots
+        // has finished (the synchronisation above), so a later upload into
+        // them has nothing to wait for.
+        size_t slot;
+        for (size_t p = 0; p < k; p++) DM_CHECK_STATUS(acquire(c, layer, ids[p], &slot));
+        for (size_t p = 0; p < k; p++)
+            for (Slot &sl : Lay.slots)
+                if (sl.has && sl.expert == ids[p]) sl.released_recorded = false;
+        return DMHIP_OK;
     }
     if (lookup) Lay.try_lookup = false;
     const uint64_t misses_before = c->stats.misses;

@@ -151,12 +151,14 @@ struct dmhip_expert_cache {
     uint64_t *host_tables = nullptr;
     uint64_t *lookup_gate_up = nullptr, *lookup_down = nullptr;
     uint32_t *lookup_go = nullptr;
+    uint32_t *combine_tickets = nullptr;  // kCombineTickets, zero between calls
 };
 
 namespace {
 constexpr size_t kSelectionPairs = 16 * dm::kMaxTopK;  // batch <= 16
 constexpr size_t kSelectionBytes = kSelectionPairs * 8 + 16 * 4 + 16;  // ids, probabilities, per-token flags, go
 constexpr size_t kReleaseEvents = 64;
+constexpr size_t kCombineTickets = 4096;  // row-tile workgroups of a fused down + combine launch
 constexpr size_t kStagingEntries = 4;  // file source: experts in flight from storage
 // Memory source: uploads whose timing is kept until it is read.  The ring is
 // reused oldest first, so a wait at reuse only ever meets an upload issued
@@ -424,7 +426,7 @@ int build_cache(dmhip_ctx *ctx, const dmhip_expert_layer_layout *layouts, size_t
     // residency tables (all zero: nothing resident) and the lookup outputs
     size_t entries = 0;
     for (const Layer &layer : c->layers) entries += 2 * layer.layout.expert_count;
-    const size_t table_bytes = (entries + 2 * kMaxTopK + 1) * sizeof(uint64_t);
+    const size_t table_bytes = (entries + 2 * kMaxTopK + 1) * sizeof(uint64_t) + kCombineTickets * sizeof(uint32_t);
     if (hipMalloc((void **)&c->tables, table_bytes) != hipSuccess) {
         c->tables = nullptr;
         return fail_alloc(table_bytes);
@@ -445,6 +447,7 @@ int build_cache(dmhip_ctx *ctx, const dmhip_expert_layer_layout *layouts, size_t
     c->lookup_gate_up = c->tables + at;
     c->lookup_down = c->lookup_gate_up + kMaxTopK;
     c->lookup_go = (uint32_t *)(c->lookup_down + kMaxTopK);
+    c->combine_tickets = (uint32_t *)(c->lookup_down + kMaxTopK + 1);
     return DMHIP_OK;
 }
 
@@ -688,11 +691,19 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
         }
         DM_HIP(launch_qmv8_grouped(ctx, gate_up_type, (uint32_t)width, (uint32_t)hidden, 1, up_offset,
                                    gu_jobs.data(), k, x, d_act, c->lookup_gate_up, c->lookup_go));
-        DM_HIP(launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(), k,
-                                   d_act, d_eo, c->lookup_down, c->lookup_go));
-        hipLaunchKernelGGL(moe_combine_pos_kernel, dim3((uint32_t)((hidden + 255) / 256)), dim3(256), 0,
-                           ctx->stream, d_eo, nullptr, d_probs, 1u, (uint32_t)k, (uint32_t)hidden, y, c->lookup_go);
-        DM_HIP(hipGetLastError());
+        // the down launch also makes the ordered combine when its split
+        // allows (every workgroup holds whole row tiles of every expert)
+        const QmvCombine cmb{c->combine_tickets, kCombineTickets, d_probs, y};
+        if (launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(), k, d_act,
+                                d_eo, c->lookup_down, c->lookup_go, &cmb) != hipSuccess) {
+            (void)hipGetLastError();
+            DM_HIP(launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(), k,
+                                       d_act, d_eo, c->lookup_down, c->lookup_go));
+            hipLaunchKernelGGL(moe_combine_pos_kernel, dim3((uint32_t)((hidden + 255) / 256)), dim3(256), 0,
+                               ctx->stream, d_eo, nullptr, d_probs, 1u, (uint32_t)k, (uint32_t)hidden, y,
+                               c->lookup_go);
+            DM_HIP(hipGetLastError());
+        }
     } else {
         DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                    (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs,

@@ -486,7 +486,7 @@ __device__ __forceinline__ void block_dot8(const Raw8<kQ6_K> &raw, const i32x4 *
 // workgroup's LDS allows on a C2-sized row; a tighter budget makes the
 // compiler wait for each prefetch right after issuing it.
 // ---------------------------------------------------------------------------
-template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W, bool PC = false>
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, uint32_t W, bool PC = false, bool PUB = false>
 __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
                                           uint32_t rows, uint32_t columns, uint32_t row_bytes,
                                           uint32_t total_bytes, const float *__restrict__ x, int x_stride,
@@ -713,7 +713,15 @@ __device__ __forceinline__ void qmv8_body(const uint8_t *__restrict__ w, const u
                     v = v * sig * u;
                 }
             }
-            y[(ptrdiff_t)g * y_stride + row] = v;
+            if constexpr (PUB) {
+                // published for another workgroup: performed at the memory
+                // side before this wave goes on (the fence-free pattern)
+                const float old = __hip_atomic_exchange(&y[(ptrdiff_t)g * y_stride + row], v, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+                asm volatile("" ::"v"(old) : "memory");
+            } else {
+                y[(ptrdiff_t)g * y_stride + row] = v;
+            }
             if constexpr (MODE == 1) {
                 bad |= !__builtin_isfinite(v);
                 const uint64_t key = argmax_key(v, row);
@@ -922,20 +930,54 @@ struct JobTable8 {
     Job8 job[kMaxJobs8];
 };
 
-template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
+// The ordered combine of one token's routed experts fused into their down
+// launch: y[r] = fma(out_k-1[r], p[k-1], ... fma(out_0[r], p[0], 0)) in
+// selection order, as the separate combine computes it
+// (src/gemma4/cpu.rs:608-611).  Every workgroup publishes its expert's rows
+// (PUB), then takes the ticket of its row tiles; the one that draws the
+// last (of gridDim.y = k) adds the k rows of those tiles and resets the
+// ticket.
+struct Combine8 {
+    uint32_t *tickets;  // one per blockIdx.x, zero between launches
+    const float *p;     // the token's k probabilities
+    float *y;           // the token's output
+};
+
+template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, bool PUB = false>
 __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     __attribute__((amdgpu_waves_per_eu(waves_per_eu8<TYPE, MODE, TOK, G>()))) qmv8_grouped_kernel(JobTable8 jobs, uint32_t rows, uint32_t columns, uint32_t row_bytes,
                         uint32_t total_bytes, uint64_t w2_offset, const float *__restrict__ x,
                         float *__restrict__ y, int glm, const uint64_t *__restrict__ dev_w,
-                        const uint32_t *__restrict__ go) {
+                        const uint32_t *__restrict__ go, Combine8 cb) {
     // Jobs whose matrices a kernel earlier on the stream looked up: their
     // addresses come from dev_w, and the launch does nothing when go is 0.
     if (go && *go == 0) return;
     const Job8 j = jobs.job[blockIdx.y];
     const uint8_t *w = (const uint8_t *)(dev_w ? dev_w[blockIdx.y] : j.w);
-    qmv8_body<TYPE, S, MODE, TOK, G, (S > 8 ? S : 8)>(w, w + w2_offset, rows, columns, row_bytes, total_bytes, x + j.x_off,
-                                     j.x_stride, 0, 0.0f, glm, y + j.y_off, j.y_stride, nullptr,
-                                     ArgmaxFinish{nullptr, nullptr, nullptr, nullptr});
+    constexpr uint32_t WAVES = S > 8 ? S : 8;
+    qmv8_body<TYPE, S, MODE, TOK, G, WAVES, false, PUB>(w, w + w2_offset, rows, columns, row_bytes, total_bytes,
+                                                        x + j.x_off, j.x_stride, 0, 0.0f, glm, y + j.y_off,
+                                                        j.y_stride, nullptr,
+                                                        ArgmaxFinish{nullptr, nullptr, nullptr, nullptr});
+    if constexpr (PUB) {
+        static_assert(MODE == 0 && TOK == 1 && S > 1, "the combine follows one-token split launches");
+        __shared__ uint32_t s_last;
+        __syncthreads();  // every wave's rows are published
+        if (threadIdx.x == 0) s_last = atomicAdd(&cb.tickets[blockIdx.x], 1u) == gridDim.y - 1 ? 1u : 0u;
+        __syncthreads();
+        if (!s_last) return;
+        // the rows of this workgroup's tiles (y_off of job p is p * rows)
+        const uint32_t r0 = blockIdx.x * (WAVES / S) * 16, r1 = min(r0 + (WAVES / S) * 16, rows);
+        for (uint32_t r = r0 + threadIdx.x; r < r1; r += blockDim.x) {
+            float acc = 0.0f;
+            for (uint32_t p = 0; p < gridDim.y; p++)
+                acc = __builtin_fmaf(__hip_atomic_load(&y[(size_t)p * rows + r], __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT),
+                                     cb.p[p], acc);
+            cb.y[r] = acc;
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(&cb.tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1142,6 +1184,7 @@ Plan8 plan8_grouped(uint32_t type, uint32_t rows, uint32_t columns, uint32_t bat
 struct DeviceJobs {
     const uint64_t *w;
     const uint32_t *go;
+    Combine8 cb;  // cb.tickets set: the fused combine (one-token down jobs)
 };
 
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
@@ -1156,13 +1199,16 @@ hipError_t run8_grouped(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, uint64_
     const uint32_t per = S == 1 ? WAVES : WAVES / S;
     const uint32_t grid = (tiles + per - 1) / per;
     auto kernel = qmv8_grouped_kernel<TYPE, S, MODE, TOK, G>;
+    if constexpr (MODE == 0 && TOK == 1 && S > 1) {
+        if (dj.cb.tickets) kernel = qmv8_grouped_kernel<TYPE, S, MODE, TOK, G, true>;
+    }
     if (lds > 64 * 1024) {
-        static LdsLimit limit;
-        hipError_t e = limit.ensure((const void *)kernel, lds);
+        static LdsLimit limit, limit_pub;
+        hipError_t e = (dj.cb.tickets ? limit_pub : limit).ensure((const void *)kernel, lds);
         if (e != hipSuccess) return e;
     }
     return launch_kernel(ctx, kernel, dim3(grid, count), dim3(64 * WAVES), lds, table, rows, columns, row_bytes,
-                         row_bytes * rows, up_offset, x, y, MODE == 2 ? 1 : 0, dj.w, dj.go);
+                         row_bytes * rows, up_offset, x, y, MODE == 2 ? 1 : 0, dj.w, dj.go, dj.cb);
 }
 
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
@@ -1261,15 +1307,25 @@ bool qmv8_grouped_supported(uint32_t type, size_t rows, size_t columns, uint32_t
 
 hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, int gate_up,
                                uint64_t up_offset, const QmvJob *jobs, size_t count, const float *x, float *y,
-                               const uint64_t *dev_w, const uint32_t *go) {
+                               const uint64_t *dev_w, const uint32_t *go, const QmvCombine *combine) {
     const uint32_t mats = gate_up ? 2u : 1u;
-    // device-side addresses: one launch of one-token jobs, in order
-    if (dev_w) {
+    // device-side addresses (and the fused combine): one launch of one-token
+    // jobs, in order
+    if (dev_w || combine) {
         if (count > kMaxJobs8) return hipErrorInvalidValue;
         for (size_t i = 0; i < count; i++)
             if (jobs[i].tokens != 1) return hipErrorInvalidValue;
     }
-    const DeviceJobs dj{dev_w, go};
+    DeviceJobs dj{dev_w, go, Combine8{nullptr, nullptr, nullptr}};
+    if (combine) {
+        // the combine reads job p's rows at y + p * rows, and needs a split
+        // launch (one workgroup holds whole tiles of every job)
+        for (size_t i = 0; i < count; i++)
+            if (jobs[i].y_off != i * rows) return hipErrorInvalidValue;
+        const Plan8 p = plan8_grouped(type, rows, columns, 1, mats, (uint32_t)count);
+        if (gate_up || p.s < 2 || (rows + 15) / 16 > combine->tickets_count * (8 / p.s)) return hipErrorInvalidValue;
+        dj.cb = Combine8{combine->tickets, combine->p, combine->y};
+    }
     // Jobs of one and of two tokens go to separate launches, kMaxJobs8 each.
     for (uint32_t tok = 1; tok <= 2; tok++) {
         size_t i = 0;

@@ -1138,6 +1138,7 @@ def test_moe_layer_resident_lookup_sequence(ctx, slots):
     rb, yb = dev(ctx, router), dev_out(ctx, hidden * 4)
     dx = {name: dev(ctx, x) for name, x in xs.items()}
     lru = capi.Lru([experts], slots, gu_bytes, dn_bytes)
+    first = {}
     for step, name in enumerate(["a", "a", "a", "b", "b", "b", "a", "a", "bad", "a"]):
         print(f"slots={slots} call {step}: token {name}", flush=True)
         if name == "bad":
@@ -1156,6 +1157,10 @@ def test_moe_layer_resident_lookup_sequence(ctx, slots):
         assert np.allclose(probs, wts, rtol=1e-5, atol=1e-7)
         got = yb.read(0, hidden * 4, np.float32)
         assert_close(got, out[0], f"call {step} token {name}")
+        # the host path (first call of a token) and the device lookup with the
+        # combine fused into the down launch (later calls) agree bit for bit
+        first.setdefault(name, got.copy())
+        assert np.array_equal(bits(got), bits(first[name])), f"call {step}: output differs from the token's first call"
         for e_id in sel[0]:
             lru.acquire(0, int(e_id))
     st, ref = cache.stats(), lru.stats()

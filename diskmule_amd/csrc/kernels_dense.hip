@@ -28,6 +28,7 @@ namespace dm {
 namespace {
 
 constexpr uint32_t kDenseWaves = 4, kRows = 2, kChunkGroup = 8;
+constexpr uint32_t kXU = 8;  // activation loads per thread in flight while staging
 
 // Elements of one 16-byte chunk.
 template <uint32_t TYPE> constexpr uint32_t kPerChunk = TYPE == kF32 ? 4u : 8u;
@@ -61,9 +62,21 @@ __global__ void __launch_bounds__(64 * kDenseWaves) dense_gemv_kernel(const uint
     extern __shared__ __attribute__((aligned(16))) float xs[];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t chunks = columns / E;  // per row
-    for (uint32_t i = threadIdx.x; i < TOK * columns / 4; i += 64 * kDenseWaves) {
-        const uint32_t t = i / (columns / 4), k = i % (columns / 4);
-        *(floatx4 *)&xs[(t * chunks + k / (E / 4)) * XP + 4 * (k % (E / 4))] = ((const floatx4 *)x)[i];
+    // kXU loads of each thread in flight before their stores
+    for (uint32_t i0 = 0; i0 < TOK * columns / 4; i0 += kXU * 64 * kDenseWaves) {
+        floatx4 v[kXU];
+#pragma unroll
+        for (uint32_t j = 0; j < kXU; j++) {
+            const uint32_t i = i0 + j * 64 * kDenseWaves + threadIdx.x;
+            v[j] = i < TOK * columns / 4 ? ((const floatx4 *)x)[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kXU; j++) {
+            const uint32_t i = i0 + j * 64 * kDenseWaves + threadIdx.x;
+            if (i >= TOK * columns / 4) break;
+            const uint32_t t = i / (columns / 4), k = i % (columns / 4);
+            *(floatx4 *)&xs[(t * chunks + k / (E / 4)) * XP + 4 * (k % (E / 4))] = v[j];
+        }
     }
     __syncthreads();
     const uint32_t step = gridDim.x * kDenseWaves * kRows;
@@ -139,14 +152,29 @@ __global__ void __launch_bounds__(64 * kDenseWaves) q5_0_gemv_kernel(const uint8
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t blocks = columns / 32;
     float *xsum = xs + TOK * blocks * kQ5Ld;
-    for (uint32_t i = threadIdx.x; i < TOK * columns / 4; i += 64 * kDenseWaves) {
-        const uint32_t blk = i / 8, q = i % 8;  // 8 float4s per block
-        *(floatx4 *)&xs[blk * kQ5Ld + 4 * q] = ((const floatx4 *)x)[i];
+    for (uint32_t i0 = 0; i0 < TOK * columns / 4; i0 += kXU * 64 * kDenseWaves) {
+        floatx4 v[kXU];
+#pragma unroll
+        for (uint32_t j = 0; j < kXU; j++) {
+            const uint32_t i = i0 + j * 64 * kDenseWaves + threadIdx.x;
+            v[j] = i < TOK * columns / 4 ? ((const floatx4 *)x)[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kXU; j++) {
+            const uint32_t i = i0 + j * 64 * kDenseWaves + threadIdx.x;
+            if (i >= TOK * columns / 4) break;
+            const uint32_t blk = i / 8, q = i % 8;  // 8 float4s per block
+            *(floatx4 *)&xs[blk * kQ5Ld + 4 * q] = v[j];
+        }
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < TOK * blocks; i += 64 * kDenseWaves) {
+        floatx4 q[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) q[e] = *(const floatx4 *)&xs[i * kQ5Ld + 4 * e];  // all reads before the sum
         float s = 0.0f;
-        for (int e = 0; e < 32; e++) s += xs[i * kQ5Ld + e];
+#pragma unroll
+        for (int e = 0; e < 32; e++) s += q[e / 4][e % 4];
         xsum[i] = s;
     }
     __syncthreads();

@@ -33,6 +33,32 @@
 
 namespace dm {
 
+// Host-to-HBM copy of one expert's two byte ranges (gate_up, then down) by a
+// kernel that reads the pinned source over PCIe: each thread keeps four
+// 16-byte loads in flight before it stores them.  Measured on MI355X with
+// 3 MB experts on two upload streams: 54-55 GB/s against 42.6 GB/s for
+// hipMemcpyAsync (the DMA engines), 16 to 32 workgroups per copy.
+constexpr uint32_t kUploadCopyGroups = 32;
+typedef uint32_t c16 __attribute__((ext_vector_type(4)));  // 16-byte aligned
+__global__ void __launch_bounds__(256) upload_copy_kernel(const c16 *__restrict__ a_src, c16 *__restrict__ a_dst,
+                                                          size_t a16, const c16 *__restrict__ b_src,
+                                                          c16 *__restrict__ b_dst, size_t b16) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x, n = a16 + b16;
+    auto at = [&](size_t i) -> const c16 & { return i < a16 ? a_src[i] : b_src[i - a16]; };
+    auto put = [&](size_t i, const c16 &v) {
+        if (i < a16) a_dst[i] = v; else b_dst[i - a16] = v;
+    };
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + 3 * stride < n; i += 4 * stride) {
+        const c16 v0 = at(i), v1 = at(i + stride), v2 = at(i + 2 * stride), v3 = at(i + 3 * stride);
+        put(i, v0);
+        put(i + stride, v1);
+        put(i + 2 * stride, v2);
+        put(i + 3 * stride, v3);
+    }
+    for (; i < n; i += stride) put(i, at(i));
+}
+
 __global__ void gather_rows_kernel(const float *__restrict__ x, const uint32_t *__restrict__ rows,
                                    uint32_t count, uint32_t width, float *__restrict__ out) {
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < (size_t)count * width;
@@ -119,6 +145,7 @@ struct TimedUpload {
 // One pinned host buffer of the file source's staging ring.
 struct Staging {
     uint8_t *host = nullptr;
+    uint8_t *host_dev = nullptr;  // its device address (pinned memory)
     hipEvent_t done = nullptr;  // end of the copies out of it
     bool busy = false;          // done has been recorded
 };
@@ -131,6 +158,9 @@ struct dmhip_expert_cache {
     // Memory source (fd < 0) or file source.
     const uint8_t *source = nullptr;
     size_t source_len = 0;
+    // The source's address on the device when it is pinned host memory
+    // (uploads then run as copy kernels), else null (hipMemcpyAsync).
+    const uint8_t *source_dev = nullptr;
     int fd = -1;
     std::vector<dm::Staging> staging;
     size_t next_staging = 0;
@@ -238,6 +268,17 @@ int upload_expert(dmhip_expert_cache *c, const dmhip_expert_layer_layout &L, siz
         gu_src = c->source + gu_off;
         dn_src = c->source + dn_off;
     }
+    // the source's device addresses, when the copy can run as a kernel
+    const uint8_t *gu_dev = nullptr, *dn_dev = nullptr;
+    if (entry && entry->host_dev) {
+        gu_dev = entry->host_dev;
+        dn_dev = entry->host_dev + gu_bytes;
+    } else if (!entry && c->source_dev) {
+        gu_dev = c->source_dev + gu_off;
+        dn_dev = c->source_dev + dn_off;
+    }
+    const bool by_kernel = gu_dev && ((uintptr_t)gu_dev % 16 | (uintptr_t)dn_dev % 16 | gu_bytes % 16 |
+                                      dn_bytes % 16 | (uintptr_t)s.gate_up % 16 | (uintptr_t)s.down % 16) == 0;
     // experts alternate between the two upload streams
     hipStream_t up = (c->ctx->upload_next++ & 1u) ? c->ctx->upload2 : c->ctx->upload;
     // The slot's last readers and its previous upload are waited for here,
@@ -254,8 +295,14 @@ int upload_expert(dmhip_expert_cache *c, const dmhip_expert_layer_layout &L, siz
         account_upload(c, *timer, true);  // the oldest pair of the ring
         DM_HIP(hipEventRecord(timer->start, up));
     }
-    DM_HIP(hipMemcpyAsync(s.gate_up, gu_src, gu_bytes, hipMemcpyHostToDevice, up));
-    DM_HIP(hipMemcpyAsync(s.down, dn_src, dn_bytes, hipMemcpyHostToDevice, up));
+    if (by_kernel) {
+        hipLaunchKernelGGL(upload_copy_kernel, dim3(kUploadCopyGroups), dim3(256), 0, up, (const c16 *)gu_dev,
+                           (c16 *)s.gate_up, gu_bytes / 16, (const c16 *)dn_dev, (c16 *)s.down, dn_bytes / 16);
+        DM_HIP(hipGetLastError());
+    } else {
+        DM_HIP(hipMemcpyAsync(s.gate_up, gu_src, gu_bytes, hipMemcpyHostToDevice, up));
+        DM_HIP(hipMemcpyAsync(s.down, dn_src, dn_bytes, hipMemcpyHostToDevice, up));
+    }
     DM_HIP(hipEventRecord(s.ready, up));
     s.uploaded = true;
     if (timer) {
@@ -511,6 +558,16 @@ int dmhip_expert_cache_new(dmhip_ctx *ctx, const void *source, size_t source_len
     dmhip_expert_cache *c = new dmhip_expert_cache();
     c->source = (const uint8_t *)source;
     c->source_len = source_len;
+    // Pinned host memory (hipHostMalloc, dmhip_host_alloc_pinned) has a
+    // device address: uploads from it run as copy kernels.
+    if (source_len) {
+        hipPointerAttribute_t attr;
+        void *dev = nullptr;
+        if (hipPointerGetAttributes(&attr, source) == hipSuccess && attr.type == hipMemoryTypeHost &&
+            hipHostGetDevicePointer(&dev, const_cast<void *>(source), 0) == hipSuccess)
+            c->source_dev = (const uint8_t *)dev;
+        (void)hipGetLastError();  // a pageable source leaves an error behind
+    }
     const int st = build_cache(ctx, layouts, layer_count, slots_per_layer, c);
     if (st != DMHIP_OK) {
         destroy(c);
@@ -553,6 +610,9 @@ int dmhip_expert_cache_new_file(dmhip_ctx *ctx, int fd, const dmhip_expert_layer
                 st = fail_alloc(entry_bytes);
                 break;
             }
+            void *dev = nullptr;
+            if (hipHostGetDevicePointer(&dev, e.host, 0) == hipSuccess) e.host_dev = (uint8_t *)dev;
+            (void)hipGetLastError();
             if (hipEventCreateWithFlags(&e.done, hipEventDisableTiming) != hipSuccess) {
                 e.done = nullptr;
                 st = fail(DMHIP_ERR_COMMAND, "could not create the staging events");

@@ -744,7 +744,7 @@ int dmhip_append_kv(dmhip_ctx *ctx, dmhip_kv_layer *layer, size_t position, cons
     DM_CHECK_STATUS(set_device(ctx));
     DM_CHECK_STATUS(append_copy(ctx, layer, position, key, value, hipMemcpyHostToDevice));
     // the host slices may be reused once this returns
-    DM_HIP(hipStreamSynchronize(ctx->stream));
+    DM_CHECK_STATUS(stream_wait(ctx));
     layer->position += 1;
     return DMHIP_OK;
 }
@@ -828,7 +828,7 @@ int dmhip_attention_result(dmhip_ctx *ctx) {
     DM_CHECK_STATUS(set_device(ctx));
     uint32_t flag = 0;
     DM_HIP(hipMemcpyAsync(&flag, ctx->flags + kAttnFlagWord, 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_HIP(hipStreamSynchronize(ctx->stream));
+    DM_CHECK_STATUS(stream_wait(ctx));
     ctx->attn_pending = false;
     if (flag == ctx->attn_mark) return fail_non_finite("softmax");
     return DMHIP_OK;

@@ -797,7 +797,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
                                    BadFlag{ctx->flags + kMoeFlagWord, 1}, sel_ids, sel_probs,
                                    batch <= kRouterTickets ? ctx->router_tickets : nullptr, sel_bad));
     }
-    DM_HIP(hipStreamSynchronize(ctx->stream));
+    DM_CHECK_STATUS(stream_wait(ctx));
     // top_k_softmax rejects non-finite logits (src/cpu.rs:240-245); nothing
     // has been acquired yet.
     for (size_t t = 0; t < batch; t++)
@@ -967,7 +967,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
                        ctx->stream, d_eo, grouped ? nullptr : d_pos, d_probs, (uint32_t)batch, (uint32_t)k,
                        (uint32_t)hidden, y, nullptr);
     DM_HIP(hipGetLastError());
-    DM_HIP(hipStreamSynchronize(ctx->stream));
+    DM_CHECK_STATUS(stream_wait(ctx));
     // a call whose experts were all resident lets the next one-token call
     // try the device-side lookup again
     if (c->stats.misses == misses_before) Lay.try_lookup = true;

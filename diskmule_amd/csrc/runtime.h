@@ -119,6 +119,11 @@ struct dmhip_ctx {
     bool router_pending = false;  // a dmhip_router_top_k_device awaits dmhip_router_result
     bool attn_pending = false;    // a dmhip_attention_cached_device awaits dmhip_attention_result
     uint32_t *argmax_user_index = nullptr;
+    // Pinned word the stream writes a call's sequence number into once the
+    // call's work is done (stream_wait), and its device address.
+    volatile uint32_t *done_word = nullptr;
+    void *done_word_dev = nullptr;
+    uint32_t done_seq = 0;
 };
 
 struct dmhip_buf {
@@ -143,6 +148,10 @@ int enqueue_matvec(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns, c
 int enqueue_matvec_argmax(dmhip_ctx *ctx, uint32_t type, size_t rows, size_t columns,
                           const void *w, const float *x, float *y, uint32_t *index_device);
 int set_device(dmhip_ctx *ctx);
+// Waits until the work enqueued so far on the context's stream is done: the
+// stream writes a sequence number into a pinned word, which the host polls
+// for a while before it falls back to hipStreamSynchronize.
+int stream_wait(dmhip_ctx *ctx);
 
 // The copies of one synchronous host-slice call.  begin(total) sizes the
 // call's inputs and outputs together: up to kHostBounceMax they are staged in

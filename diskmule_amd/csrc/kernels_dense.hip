@@ -196,8 +196,12 @@ __global__ void __launch_bounds__(64 * kDenseWaves) q5_0_gemv_kernel(const uint8
                     const uint32_t b = b0 + 64 * j + lane;
                     // rows past the end and blocks past the row read past W: zeros
                     const uint32_t at = r0 + r < rows && b < blocks ? (r0 + r) * row_bytes + 22 * b : w_bytes;
+                    const u32x4 lo = rsrc_load16(rs, at & ~3u);
+                    const u32x2 hi = rsrc_load8(rs, (at & ~3u) + 16);
 #pragma unroll
-                    for (int i = 0; i < 6; i++) d[r][j][i] = rsrc_load4(rs, (at & ~3u) + 4 * i);
+                    for (int i = 0; i < 4; i++) d[r][j][i] = lo[i];
+                    d[r][j][4] = hi[0];
+                    d[r][j][5] = hi[1];
                 }
 #pragma unroll
             for (uint32_t j = 0; j < kGroup; j++) {

@@ -828,7 +828,7 @@ int dmhip_attention_result(dmhip_ctx *ctx) {
     DM_CHECK_STATUS(set_device(ctx));
     uint32_t flag = 0;
     DM_HIP(hipMemcpyAsync(&flag, ctx->flags + kAttnFlagWord, 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_CHECK_STATUS(stream_wait(ctx));
+    DM_HIP(hipStreamSynchronize(ctx->stream));  // a copy into pageable memory precedes
     ctx->attn_pending = false;
     if (flag == ctx->attn_mark) return fail_non_finite("softmax");
     return DMHIP_OK;

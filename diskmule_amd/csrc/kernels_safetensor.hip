@@ -562,7 +562,7 @@ int dmhip_matvec_safetensor(dmhip_ctx *ctx, uint32_t dtype, size_t rows, size_t 
     DM_CHECK_STATUS(st_enqueue(ctx, fmt, rows, columns, dw, ds, scale_count, group, scale_columns,
                                (const float *)ctx->in.ptr, (float *)ctx->out.ptr));
     DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, rows * 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_CHECK_STATUS(stream_wait(ctx));
+    DM_HIP(hipStreamSynchronize(ctx->stream));  // a copy into pageable memory precedes
     return DMHIP_OK;
 }
 

@@ -172,6 +172,7 @@ struct HostCall {
         size_t n;
     } pending[2];
     int outs = 0;
+    bool pageable_out = false;  // an output copied straight into pageable memory
     explicit HostCall(dmhip_ctx *c) : ctx(c) {}
     ~HostCall();
     HostCall(const HostCall &) = delete;

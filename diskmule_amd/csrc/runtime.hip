@@ -204,6 +204,7 @@ int HostCall::begin(size_t total) {
     staged = total <= kHostBounceMax;
     used = 0;
     outs = 0;
+    pageable_out = false;
     open = true;
     // room for the 256-byte alignment of up to four pieces
     return staged ? ctx->bounce.ensure(total + 4 * 256) : DMHIP_OK;
@@ -226,6 +227,7 @@ int HostCall::out(void *host_dst, const void *device_src, size_t n) {
     if (n == 0) return DMHIP_OK;
     if (!staged) {
         DM_HIP(hipMemcpyAsync(host_dst, device_src, n, hipMemcpyDeviceToHost, ctx->stream));
+        pageable_out = true;
         return DMHIP_OK;
     }
     if (outs == 2) return fail(DMHIP_ERR_COMMAND, "a host-slice call stages at most two outputs");
@@ -264,7 +266,13 @@ int stream_wait(dmhip_ctx *ctx) {
 
 int HostCall::finish() {
     open = false;
-    DM_CHECK_STATUS(stream_wait(ctx));
+    // a copy into pageable memory is waited for by the blocking synchronisation
+    if (pageable_out) {
+        pageable_out = false;
+        DM_HIP(hipStreamSynchronize(ctx->stream));
+    } else {
+        DM_CHECK_STATUS(stream_wait(ctx));
+    }
     for (int i = 0; i < outs; i++) memcpy(pending[i].dst, pending[i].src, pending[i].n);
     outs = 0;
     return DMHIP_OK;
@@ -978,7 +986,7 @@ int dmhip_dequantize(dmhip_ctx *ctx, uint32_t type, const dmhip_buf *encoded, si
                              elements, (float *)ctx->out.ptr));
     DM_HIP(hipMemcpyAsync(output, ctx->out.ptr, elements * sizeof(float), hipMemcpyDeviceToHost,
                           ctx->stream));
-    DM_CHECK_STATUS(stream_wait(ctx));
+    DM_HIP(hipStreamSynchronize(ctx->stream));  // a copy into pageable memory precedes
     return DMHIP_OK;
 }
 
@@ -1072,7 +1080,7 @@ int dmhip_argmax_result(dmhip_ctx *ctx, size_t *index) {
     uint32_t result = 0;
     DM_HIP(hipMemcpyAsync(&state, ctx->argmax_state, sizeof state, hipMemcpyDeviceToHost, ctx->stream));
     DM_HIP(hipMemcpyAsync(&result, ctx->argmax_user_index, 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_CHECK_STATUS(stream_wait(ctx));
+    DM_HIP(hipStreamSynchronize(ctx->stream));  // a copy into pageable memory precedes
     ctx->argmax_pending = false;
     if (state.non_finite) return fail_non_finite("argmax");
     *index = result;
@@ -1191,7 +1199,7 @@ int dmhip_router_result(dmhip_ctx *ctx) {
     DM_CHECK(set_device(ctx));
     uint32_t flag = 0;
     DM_HIP(hipMemcpyAsync(&flag, ctx->flags, 4, hipMemcpyDeviceToHost, ctx->stream));
-    DM_CHECK_STATUS(stream_wait(ctx));
+    DM_HIP(hipStreamSynchronize(ctx->stream));  // a copy into pageable memory precedes
     ctx->router_pending = false;
     if (flag == ctx->router_mark) return fail_non_finite("top-k softmax");
     return DMHIP_OK;

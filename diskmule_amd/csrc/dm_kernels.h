@@ -103,7 +103,12 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
                                float *logits, uint32_t *ids, float *probabilities,
                                BadFlag non_finite, uint32_t *host_ids = nullptr,
                                float *host_probs = nullptr, uint32_t *tickets = nullptr,
-                               uint32_t *host_bad = nullptr, const ExpertLookup *lookup = nullptr);
+                               uint32_t *host_bad = nullptr, const ExpertLookup *lookup = nullptr,
+                               bool certified = false);
+// With `certified` (the MoE layer, whose logits stay internal) and tickets,
+// decode batches of up to 8192 columns take the certified router: the same
+// ids in the same order as the exact fold, probabilities from logits within
+// a proven bound of it; `logits` then holds 16 bytes per (token, expert).
 // True when launch_router_top_k takes a lookup for this router: one token,
 // and the router runs as one of the expert-parallel kernels whose token's
 // last workgroup makes the selection.

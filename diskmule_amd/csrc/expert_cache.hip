@@ -709,7 +709,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     // Workspace: logits | ids | probs | pos | pair tokens | xg | gate_up | act | expert_out
     const size_t pairs = batch * k;
     const size_t a_logits = 0;
-    const size_t a_ids = a_logits + ((batch * experts * 4 + 255) & ~(size_t)255);
+    const size_t a_ids = a_logits + ((batch * experts * 16 + 255) & ~(size_t)255);  // the certified router's (L, rho)
     const size_t a_probs = a_ids + ((pairs * 4 + 255) & ~(size_t)255);
     const size_t a_pos = a_probs + ((pairs * 4 + 255) & ~(size_t)255);
     const size_t a_tok = a_pos + ((pairs * 4 + 255) & ~(size_t)255);
@@ -739,7 +739,8 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
                          up_offset % (gate_up_type == 12 ? 16 : 4) == 0 &&  // 12: Q4_K
                          (uint64_t)pairs * (hidden > width ? hidden : width) < (1ull << 31);
 
-    // 1. Router logits (exact fold) and top-k softmax on the GPU.
+    // 1. Router logits and top-k softmax on the GPU (the certified router:
+    //    the exact fold's ids and order).
     uint32_t *sel_ids = (uint32_t *)c->host_selection;
     float *sel_probs = (float *)(c->host_selection + kSelectionPairs * 4);
     uint32_t *sel_bad = (uint32_t *)(c->host_selection + kSelectionPairs * 8);
@@ -770,7 +771,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
                               c->lookup_go, (uint32_t *)sel_go};
         DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts, (uint32_t)k,
                                    1, x, d_logits, d_ids, d_probs, BadFlag{ctx->flags + kMoeFlagWord, 1}, sel_ids,
-                                   sel_probs, ctx->router_tickets, sel_bad, &el));
+                                   sel_probs, ctx->router_tickets, sel_bad, &el, true));
         std::vector<QmvJob> gu_jobs(k), dn_jobs(k);
         for (size_t p = 0; p < k; p++) {
             gu_jobs[p] = QmvJob{nullptr, 1u, 0u, (uint32_t)(p * width), 0, 0};
@@ -795,7 +796,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
         DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts,
                                    (uint32_t)k, (uint32_t)batch, x, d_logits, d_ids, d_probs,
                                    BadFlag{ctx->flags + kMoeFlagWord, 1}, sel_ids, sel_probs,
-                                   batch <= kRouterTickets ? ctx->router_tickets : nullptr, sel_bad));
+                                   batch <= kRouterTickets ? ctx->router_tickets : nullptr, sel_bad, nullptr, true));
     }
     DM_CHECK_STATUS(stream_wait(ctx));
     // top_k_softmax rejects non-finite logits (src/cpu.rs:240-245); nothing

@@ -518,6 +518,21 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
     }
 }
 
+// Rank of a key among keys[0 .. n): the count of larger keys.  The loop
+// reads 16 keys at a time, so their LDS reads overlap.
+__device__ __forceinline__ uint32_t key_rank(const uint64_t *keys, uint32_t n, uint64_t mine) {
+    uint32_t rank = 0, j = 0;
+    for (; j + 16 <= n; j += 16) {
+        uint64_t w[16];
+#pragma unroll
+        for (uint32_t q = 0; q < 16; q++) w[q] = keys[j + q];
+#pragma unroll
+        for (uint32_t q = 0; q < 16; q++) rank += w[q] > mine ? 1u : 0u;
+    }
+    for (; j < n; j++) rank += keys[j] > mine ? 1u : 0u;
+    return rank;
+}
+
 // Exact router for decode with the rows staged in LDS as f32.  Workgroup
 // (g, t) of four waves first loads router rows R g .. R g + R - 1 and token
 // t's x with up to 16 loads per thread in flight at once (contiguous 16-byte
@@ -695,10 +710,17 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
     __shared__ uint32_t s_missing;
     if (tid == 0) s_missing = 0;
     const bool row_bad = __syncthreads_or((int)bad) != 0;
-    if (tid < experts) {
-        // keys are unique (value, then index), so ranks are 0 .. experts - 1
-        uint32_t rank = 0;
-        for (uint32_t j = 0; j < experts; j++) rank += s_keys[j] > mine ? 1u : 0u;
+    {
+        // keys are unique (value, then index), so ranks are 0 .. experts - 1;
+        // up to 128 experts two threads count a key's rank over half the keys
+        __shared__ uint32_t s_rank[256];
+        const uint32_t split = experts <= 128 ? 2u : 1u, span = (experts + split - 1) / split;
+        const uint32_t me = split == 2 ? tid & 127u : tid, begin = split == 2 ? (tid >> 7) * span : 0u;
+        s_rank[tid] = me < experts ? key_rank(s_keys + begin, span < experts - begin ? span : experts - begin,
+                                              s_keys[me])
+                                   : 0u;
+        __syncthreads();
+        const uint32_t rank = tid < experts ? s_rank[tid] + (split == 2 ? s_rank[tid + 128] : 0u) : experts;
         if (rank < k) s_sel[rank] = tid;
     }
     __syncthreads();
@@ -716,6 +738,344 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
         if (host_ids) host_ids[(size_t)token * k + tid] = index;
         if (lookup.go) {
             // the selected expert's slot (ExpertLookup)
+            const uint64_t gu = lookup.gate_up_of[index], dn = lookup.down_of[index];
+            lookup.gate_up_w[tid] = gu;
+            lookup.down_w[tid] = dn;
+            if (gu == 0 || dn == 0) s_missing = 1;  // every writer stores the same value
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (uint32_t j = 0; j < k; j++) sum += s_value[j];
+        s_sum = sum;
+    }
+    __syncthreads();
+    if (tid < k) {
+        const float p = s_value[tid] / s_sum;
+        tp[tid] = p;
+        if (host_ids) host_probs[(size_t)token * k + tid] = p;
+    }
+    if (tid == 0) {
+        if (host_ids) host_bad[token] = row_bad;
+        if (lookup.go) {
+            const uint32_t go = row_bad || s_missing ? 0u : 1u;
+            *lookup.go = go;
+            *lookup.host_go = go;
+        }
+        __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Certified router for the MoE layer: the top-k ids (and their order) of
+// the reference's sequential fold, from a parallel fold with a proven error
+// bound; the exact fold runs only for the experts the bound cannot order.
+//
+// The reference folds a logit in f32 from +0, one fma per column
+// (s^_{i+1} = fma(w_i, x_i, s^_i), src/cpu.rs:391-394 over widened bf16
+// rows).  With s_i the exact prefix sums and u = 2^-24 each fma rounds once:
+// |fl(r) - r| <= u |r| + 2^-150 (the second term for subnormal results), so
+// the error E_i = |s^_i - s_i| obeys E_i <= (1 + u) E_{i-1} + u |s_i| + 2^-150
+// and |s^_n - s_n| <= (1 + u)^n (u sum_i |s_i| + n 2^-150), as long as no
+// intermediate |s_i| + E_i reaches FLT_MAX (then the fold could overflow).
+// This kernel computes, per (token, expert) row, every product w_i x_i
+// exactly in double (8 + 24 significant bits), the prefix sums in double
+// (lane segments of 32 columns and one wave scan per 2048 columns), the
+// total L, A = sum |s_i|, M = max |s_i| and P = sum |w_i x_i|.  Each of these
+// double sums takes fewer than 128 roundings of at most 2^-53 P, so
+// D = 2^-46 P bounds the distance of every computed prefix sum (and of L)
+// from the exact one, and with n <= 8192 ((1 + u)^n < 1.0005):
+//   B = 1.001 (u (A + n D) + n 2^-150)     bounds |s^_n - s_n|
+//   rho = 1.001 (B + 2 D)                  bounds |s^_n - L|, with room for
+//                                          the rounding of L -+ rho
+// A row whose M + D + B is not below 3e38, or whose inputs are not finite,
+// gets rho = +inf.
+//
+// Workgroup (g, t): wave w takes row 4g + w of token t and publishes (L,
+// rho) with device-scope exchanges, then the workgroup takes the token's
+// ticket.  The last workgroup selects:
+//  * every rho finite: the top k by L (ties by index).  When the intervals
+//    [L - rho, L + rho] of consecutive selections are disjoint and every
+//    other row's interval lies below the k-th one's, the reference selects
+//    the same ids in the same order; the probabilities are then the
+//    reference's softmax over the f32 roundings of the selected L (within
+//    rho of the reference's logits).
+//  * otherwise C, the rows that can still be in the top k (every row whose
+//    L + rho reaches the smallest L - rho of the k candidates; any row
+//    outside C is below those k rows for certain), is ordered exactly: the
+//    members whose interval meets
+//    another member's (X: typically two rows) are folded exactly, the
+//    reference's way (staged in LDS, as router_lds_kernel folds), and
+//    compared by their exact logits (value, then index); every other pair
+//    of members has disjoint intervals, so L or an exact logit orders it.
+//    The selected members outside X take their f32-rounded L.
+//  * a non-finite L (a non-finite input of the row or of x, so a non-finite
+//    reference logit) fails the call; a row whose fold may overflow (rho
+//    infinite, finite L) makes every row a member of X, so the non-finite
+//    check is the reference's.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_max_f64(double v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmax(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+__global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__restrict__ router, uint32_t hidden,
+                                                          uint32_t experts, uint32_t k, const float *__restrict__ x,
+                                                          uint64_t *cert, uint32_t *tickets, uint32_t *ids,
+                                                          float *probabilities, BadFlag non_finite,
+                                                          uint32_t *host_ids, float *host_probs, uint32_t *host_bad,
+                                                          ExpertLookup lookup, uint32_t rf) {
+    extern __shared__ __attribute__((aligned(16))) v4a cert_lds[];  // exact folds: rf rows, then x (router_lds_bytes)
+    constexpr uint32_t nowhere = 0x80000000u;                      // every load from here reads zeros
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, token = blockIdx.y;
+    const uint32_t N8 = hidden / 8, e = blockIdx.x * 4 + wave;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(router, experts * hidden * 2);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)token * hidden, hidden * 4);
+    uint64_t *tc = cert + 2 * (size_t)token * experts;
+    {
+        // lane: pieces (8 columns) pc0 .. pc0 + 3 of each 256-piece round
+        double carry = 0.0, a = 0.0, sp = 0.0, m = 0.0;
+        for (uint32_t r = 0; r * 256 < N8; r++) {
+            const uint32_t pc0 = r * 256 + 4 * lane;
+            v4a wv[4], xv[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++)
+                wv[j] = __builtin_bit_cast(
+                    v4a, rsrc_load16(rw, e < experts && pc0 + j < N8 ? (e * N8 + pc0 + j) * 16 : nowhere));
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++)
+                xv[j] = __builtin_bit_cast(v4a, rsrc_load16(rx, pc0 + j / 2 < N8 ? (2 * pc0 + j) * 16 : nowhere));
+            double p[32], t = 0.0;
+#pragma unroll
+            for (uint32_t c = 0; c < 32; c++) {
+                const uint32_t d = wv[c / 8][(c % 8) / 2];
+                const float wf = __uint_as_float(c % 2 ? d & 0xffff0000u : d << 16);
+                p[c] = (double)wf * (double)__uint_as_float(xv[c / 4][c % 4]);
+                t += p[c];
+                sp += fabs(p[c]);
+            }
+            // exclusive scan of the lane totals
+            double incl = t;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const double o = __shfl_up(incl, off, 64);
+                if (lane >= (uint32_t)off) incl += o;
+            }
+            double s = __shfl_up(incl, 1, 64);
+            s = carry + (lane == 0 ? 0.0 : s);
+#pragma unroll
+            for (uint32_t c = 0; c < 32; c++) {
+                if (pc0 + c / 8 < N8) {
+                    s += p[c];
+                    a += fabs(s);
+                    m = fmax(m, fabs(s));
+                }
+            }
+            carry += __shfl(incl, 63, 64);
+        }
+        const double A = wave_sum_f64(a), P = wave_sum_f64(sp), M = wave_max_f64(m), n = (double)hidden;
+        const double D = P * 0x1p-46;
+        const double B = 1.001 * (0x1p-24 * (A + n * D) + n * 0x1p-150);
+        double rho = 1.001 * (B + 2.0 * D);
+        if (!(M + D + B < 3.0e38)) rho = __builtin_inf();
+        uint64_t o0 = 0, o1 = 0;
+        if (lane == 0 && e < experts) {
+            o0 = __hip_atomic_exchange(&tc[2 * e], __double_as_longlong(carry), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            o1 = __hip_atomic_exchange(&tc[2 * e + 1], __double_as_longlong(rho), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("" ::"v"(o0), "v"(o1) : "memory");  // the exchanges have completed
+    }
+    __shared__ uint32_t s_drawn;
+    __syncthreads();
+    if (tid == 0) s_drawn = atomicAdd(&tickets[token], 1u);
+    __syncthreads();
+    if (s_drawn != gridDim.x - 1) return;
+
+    // The token's last workgroup: thread i < experts owns row i.
+    __shared__ double c_l[256], c_lo[256], c_hi[256];
+    __shared__ double c_klo;
+    __shared__ double c_d[256];
+    __shared__ uint32_t c_sel[256], c_x[256], c_xn, c_c[256], c_cn, c_inx[256];
+    __shared__ uint64_t c_keys[256];
+    __shared__ uint32_t c_rank[256];
+    __shared__ float c_v[256], s_value[256];
+    __shared__ float s_sum;
+    __shared__ uint32_t s_missing;
+    const bool own = tid < experts;
+    double L = 0.0, lo = 0.0, hi = 0.0;
+    bool fin = true;
+    if (own) {
+        L = __longlong_as_double(__hip_atomic_load(&tc[2 * tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        const double rho =
+            __longlong_as_double(__hip_atomic_load(&tc[2 * tid + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        fin = __builtin_isfinite(rho);
+        lo = L - rho;
+        hi = L + rho;
+        c_l[tid] = L;
+        c_lo[tid] = lo;
+        c_hi[tid] = hi;
+    }
+    if (tid == 0) {
+        c_xn = 0;
+        c_cn = 0;
+        s_missing = 0;
+    }
+    const bool all_fin = __syncthreads_and((int)fin) != 0;
+    bool certified = false, member = own;
+    if (all_fin) {
+        // Candidate order: by (f32(L), index) keys.  Any order is sound (the
+        // test below proves the reference's order or fails); L values that
+        // round to one f32 lie within one ulp, inside their intervals, so
+        // they fail it whichever order they take.  Up to 128 experts, two
+        // threads count each key's rank over half of the keys.
+        if (own) c_keys[tid] = argmax_key((float)L, tid);
+        __syncthreads();
+        const uint32_t split = experts <= 128 ? 2u : 1u, span = (experts + split - 1) / split;
+        const uint32_t me = split == 2 ? tid & 127u : tid, begin = split == 2 ? (tid >> 7) * span : 0u;
+        c_rank[tid] = me < experts ? key_rank(c_keys + begin, span < experts - begin ? span : experts - begin, c_keys[me]) : 0u;
+        __syncthreads();
+        const uint32_t rank = own ? c_rank[tid] + (split == 2 ? c_rank[tid + 128] : 0u) : experts;
+        if (rank < k) c_sel[rank] = tid;
+        __syncthreads();
+        bool ok = true;
+        if (own) ok = rank < k ? rank == k - 1 || lo > c_hi[c_sel[rank + 1]] : hi < c_lo[c_sel[k - 1]];
+        certified = __syncthreads_and((int)ok) != 0;
+        if (certified) {
+            if (own) c_v[tid] = (float)L;
+        } else {
+            // every row whose interval lies below all k candidates' is below
+            // k rows for certain
+            if (tid == 0) {
+                double m = c_lo[c_sel[0]];
+                for (uint32_t j = 1; j < k; j++) m = fmin(m, c_lo[c_sel[j]]);
+                c_klo = m;
+            }
+            __syncthreads();
+            member = own && hi >= c_klo;
+        }
+    }
+    bool row_bad = false;
+    if (!certified) {
+        // A non-finite L comes from a non-finite input of its row or of x:
+        // the reference's logit is then NaN or infinite and the call fails,
+        // whatever the selection (the ids only stay in range for the lookup).
+        const bool nan_row = own && !__builtin_isfinite(L);
+        if (nan_row) *non_finite.word = non_finite.mark;  // every writer stores the same value
+        row_bad = __syncthreads_or((int)nan_row) != 0;
+        if (row_bad) {
+            if (tid < k) {
+                c_sel[tid] = tid;
+                c_v[tid] = 0.0f;
+            }
+        } else {
+            // X: the members of C whose interval meets another member's (every
+            // row when an interval is infinite: a fold that may overflow).  The
+            // other members' intervals are disjoint from every other member's,
+            // so their order follows from L.
+            if (member) c_c[atomicAdd(&c_cn, 1u)] = tid;
+            __syncthreads();
+            bool in_x = member && !all_fin;
+            if (member && all_fin)
+                for (uint32_t j = 0; j < c_cn; j++) {
+                    const uint32_t f = c_c[j];
+                    in_x |= f != tid && lo <= c_hi[f] && c_lo[f] <= hi;
+                }
+            c_inx[tid] = in_x ? 1u : 0u;
+            if (in_x) c_x[atomicAdd(&c_xn, 1u)] = tid;
+            // x into LDS as f32 pieces after the row area, zero past `hidden`
+            const uint32_t NS = router_lds_steps(hidden), RS = router_lds_row_pieces(hidden);
+            v4a *xs = cert_lds + rf * RS;
+            for (uint32_t p = tid; p < 2 * NS; p += 256)
+                xs[p] = __builtin_bit_cast(v4a, rsrc_load16(rx, p < 2 * N8 ? 16 * p : nowhere));
+            __syncthreads();
+            // The rows of X, rf at a time: widened to f32 into LDS (zero past
+            // `hidden`), then lane i < rf of wave 0 folds row i sequentially
+            // from column 0 with fma, as router_lds_kernel does.
+            for (uint32_t b0 = 0; b0 < c_xn; b0 += rf) {
+                const uint32_t nb = c_xn - b0 < rf ? c_xn - b0 : rf;
+                for (uint32_t p0 = 0; p0 < nb * NS; p0 += 4 * 256) {
+                    v4a wr[4];
+#pragma unroll
+                    for (uint32_t j = 0; j < 4; j++) {
+                        const uint32_t p = p0 + j * 256 + tid, rr = p / NS, col = p - rr * NS;
+                        const bool real = p < nb * NS && col < N8;
+                        wr[j] = __builtin_bit_cast(
+                            v4a, rsrc_load16(rw, real ? (c_x[b0 + rr] * N8 + col) * 16 : nowhere));
+                    }
+#pragma unroll
+                    for (uint32_t j = 0; j < 4; j++) {
+                        const uint32_t p = p0 + j * 256 + tid, rr = p / NS, col = p - rr * NS;
+                        if (p < nb * NS) {
+                            const v4a w = wr[j];
+                            cert_lds[rr * RS + 2 * col] =
+                                v4a{w[0] << 16, w[0] & 0xffff0000u, w[1] << 16, w[1] & 0xffff0000u};
+                            cert_lds[rr * RS + 2 * col + 1] =
+                                v4a{w[2] << 16, w[2] & 0xffff0000u, w[3] << 16, w[3] & 0xffff0000u};
+                        }
+                    }
+                }
+                __syncthreads();
+                if (tid < 64) {
+                    LdsChainState st;
+                    st.wrow = cert_lds + (tid % nb) * RS;
+                    st.xs = xs;
+                    lds_chain_read<0>(st, 0);
+                    lds_chain_read<1>(st, 1);
+                    lds_chain_read<2>(st, 2);
+                    static_assert(kRlAhead == 3, "the prologue reads kRlAhead steps");
+                    st.acc = 0.0f;
+                    constexpr auto ring = std::make_integer_sequence<uint32_t, kRlRing>{};
+                    uint32_t base = 0;
+#pragma unroll 1
+                    for (; base + kRlRing < NS; base += kRlRing) lds_chain_ring<kRlRing>(st, base, ring);
+                    lds_chain_ring<kRlRing - kRlAhead>(st, base, ring);
+                    if (tid < nb) c_v[c_x[b0 + tid]] = st.acc;
+                }
+                __syncthreads();
+            }
+            const bool bad = in_x && !__builtin_isfinite(c_v[tid]);
+            if (bad) *non_finite.word = non_finite.mark;  // every writer stores the same value
+            row_bad = __syncthreads_or((int)bad) != 0;
+            // Order C: two members of X by their exact logits (value, then
+            // index, as the reference sorts), any other pair by value (L, or a
+            // member of X's exact logit: their intervals are disjoint).
+            if (in_x) c_keys[tid] = argmax_key(c_v[tid], tid);
+            if (member) c_d[tid] = in_x ? (double)c_v[tid] : L;
+            __syncthreads();
+            if (member) {
+                uint32_t rank = 0;
+                for (uint32_t j = 0; j < c_cn; j++) {
+                    const uint32_t f = c_c[j];
+                    if (f != tid) rank += in_x && c_inx[f] ? (c_keys[f] > c_keys[tid] ? 1u : 0u)
+                                                           : (c_d[f] > c_d[tid] ? 1u : 0u);
+                }
+                if (rank < k) c_sel[rank] = tid;
+                if (!in_x) c_v[tid] = (float)L;
+            }
+        }
+    }
+    __syncthreads();  // the selection and its values (c_sel, c_v) are complete
+    // softmax_in_place over the selected logits (src/cpu.rs:195-230):
+    // maximum, exp(v - max), sequential sum, divide; selection s by thread s,
+    // the sum in selection order by thread 0.
+    uint32_t *ti = ids + (size_t)token * k;
+    float *tp = probabilities + (size_t)token * k;
+    if (tid < k) {
+        const uint32_t index = c_sel[tid];
+        float maximum = -__builtin_inff();
+        for (uint32_t j = 0; j < k; j++) maximum = fmaxf(maximum, c_v[c_sel[j]]);
+        s_value[tid] = expf(c_v[index] - maximum);
+        ti[tid] = index;
+        if (host_ids) host_ids[(size_t)token * k + tid] = index;
+        if (lookup.go) {
             const uint64_t gu = lookup.gate_up_of[index], dn = lookup.down_of[index];
             lookup.gate_up_w[tid] = gu;
             lookup.down_w[tid] = dn;
@@ -944,7 +1304,7 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
                                uint32_t experts, uint32_t k, uint32_t batch, const float *x,
                                float *logits, uint32_t *ids, float *probabilities,
                                BadFlag non_finite, uint32_t *host_ids, float *host_probs, uint32_t *tickets,
-                               uint32_t *host_bad, const ExpertLookup *lookup) {
+                               uint32_t *host_bad, const ExpertLookup *lookup, bool certified) {
     if (host_ids && (!host_probs || !host_bad)) return hipErrorInvalidValue;
     const bool staged = router_staged(hidden, experts, router, x);
     if (lookup && (!tickets || !router_takes_lookup(hidden, experts, batch, router, x)))
@@ -952,6 +1312,19 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
     const ExpertLookup no_lookup{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     const ExpertLookup L = lookup ? *lookup : no_lookup;
     // Decode batches: the expert-parallel fold, then the selection.
+    if (staged && experts >= 2 * RF_EXPERTS && certified && tickets && hidden <= 8192) {
+        // exact folds of the rows the bounds cannot order: two at a time up
+        // to 4096 columns (49 KB of LDS), one at a time above (up to 65 KB)
+        const uint32_t rf = hidden <= 4096 ? 2u : 1u;
+        const size_t lds = router_lds_bytes(hidden, rf);
+        static LdsLimit limit;
+        hipError_t e = limit.ensure((const void *)router_cert_kernel, lds);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(router_cert_kernel, dim3((experts + 3) / 4, batch), dim3(256), lds, s, router, hidden,
+                           experts, k, x, (uint64_t *)logits, tickets, ids, probabilities, non_finite, host_ids,
+                           host_probs, host_bad, L, rf);
+        return hipGetLastError();
+    }
     if (staged && experts >= 2 * RF_EXPERTS) {
         // as many rows per workgroup as fit in LDS beside x and the
         // kernel's own arrays (the rank selection's keys, ids, logits)

@@ -593,6 +593,11 @@ int dmhip_expert_release(dmhip_expert_cache *cache, size_t layer, size_t slot);
    order.  Expert gate_up rows are [gate; up] (2*width rows of `hidden`
    columns), down rows are `hidden` rows of `width` columns.  x and y are
    device [batch][hidden]; ids/probabilities receive host [batch][k].
+   The ids, and their order, are those of the reference's sequential router
+   fold; routers of up to 8192 columns and 256 experts compute the logits
+   in parallel with a proven bound on their distance from that fold (the
+   exact fold runs for the rows the bound cannot order), so the
+   probabilities can differ from the reference's in the last bits.
    Non-finite router logits return NonFinite before any expert is acquired.
    The call returns after the layer finished. */
 int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *cache, size_t layer, size_t batch,

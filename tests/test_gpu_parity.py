@@ -1170,6 +1170,142 @@ def test_moe_layer_resident_lookup_sequence(ctx, slots):
     src.free()
 
 
+# ---- the MoE layer's certified router: planted near-ties ------------------------
+
+def _moe_run_planted(ctx, router, x, hidden, width, experts, k, seed):
+    """One MoE layer call per token batch, twice (a cache with a slot per
+    expert: the second call of one token takes the device lookup), against
+    the oracle: ids exact and in order, weights within 1e-5, output within the
+    GEMV tolerance.  Returns the oracle's ids."""
+    batch = x.shape[0]
+    gu_bytes, dn_bytes = 2 * width * synth.row_bytes(Q4_K, hidden), hidden * synth.row_bytes(Q6_K, width)
+    gu = synth.quantized_matrix(Q4_K, experts * 2 * width, hidden, synth.weight_seed(seed, 1))
+    dn = synth.quantized_matrix(Q6_K, experts * hidden, width, synth.weight_seed(seed, 2))
+    cache = ExpertCache(ctx, np.concatenate([gu, dn]), [ExpertLayerLayout(experts, 0, gu_bytes, gu.size, dn_bytes)],
+                        experts)
+    sel, wts, want = capi.moe_layer(batch, hidden, width, experts, k, router, Q4_K, gu, Q6_K, dn, x)
+    rb, xb, yb = dev(ctx, router), dev(ctx, x), dev_out(ctx, batch * hidden * 4)
+    for step in range(2):
+        ids, probs = ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                                   xb.device_ptr, yb.device_ptr)
+        assert np.array_equal(ids, sel), f"call {step}: expert ids differ: {ids.tolist()} != {sel.tolist()}"
+        assert np.allclose(probs, wts, rtol=1e-5, atol=1e-7)
+        got = yb.read(0, batch * hidden * 4, np.float32).reshape(batch, hidden)
+        for t in range(batch):
+            assert_close(got[t], want[t], f"call {step} token {t}")
+    cache.free()
+    return sel
+
+
+def test_moe_router_planted_near_ties(ctx):
+    """Rows whose order under the reference's sequential f32 fold is the
+    reverse of their exact order, and two identical rows (an exact tie: the
+    lower index first), among the top k.  The certified router cannot order
+    either pair from its bounds and folds them exactly: the ids and their
+    order are the reference's (src/cpu.rs:232-260)."""
+    hidden, width, experts, k = 2048, 256, 128, 8
+    rng = np.random.default_rng(4601)
+    x = rng.standard_normal((3, hidden)).astype(np.float32)
+    # a and c lean towards every token, so their logits lead every selection
+    lean = x.sum(0)
+    a = synth.to_bf16_bits(np.float32(0.03) * lean + np.float32(0.01) * rng.standard_normal(hidden).astype(np.float32))
+    # b = a with weight i0 one bf16 step larger and weight j m steps away,
+    # so that exact(b) - exact(a) = delta (exact in double) is a fraction of
+    # an f32 ulp of the logit: find such a b whose fold over token 0 orders
+    # it against a the other way (a single changed weight cannot: rounding is
+    # monotone, so the two folds keep the order of their sums)
+    f64 = lambda v: synth.bf16_bits_to_f32(np.asarray(v, np.uint16)).astype(np.float64)
+    wa, x0 = f64(a), x[0].astype(np.float64)
+    fa = capi.matvec_bf16(1, hidden, a, x[0])[0]
+    b, delta = None, 0.0
+    for i0 in range(8):
+        d0 = (f64(a[i0] + np.uint16(1)) - wa[i0]) * x0[i0]
+        rows, deltas = [], []
+        for m in [v for v in range(-12, 13) if v]:
+            bj = (a.astype(np.int64) + m).astype(np.uint16)
+            dt = d0 + (f64(bj) - wa) * x0
+            ok = (np.sign(f64(bj)) == np.sign(wa)) & (np.arange(hidden) > 8) & (np.abs(dt) < 1.5e-6) & (dt != 0)
+            for j in np.nonzero(ok)[0]:
+                r = a.copy()
+                r[i0] += np.uint16(1)
+                r[j] = bj[j]
+                rows.append(r)
+                deltas.append(dt[j])
+        fb = capi.matvec_bf16(len(rows), hidden, np.stack(rows), x[0])
+        for r, d, fv in zip(rows, deltas, fb):
+            if (d > 0 and fv < fa) or (d < 0 and fv > fa):
+                b, delta = r, d
+                break
+        if b is not None:
+            break
+    assert b is not None, "no planted pair reverses the fold order"
+    router = synth.to_bf16_bits(rng.standard_normal((experts, hidden)).astype(np.float32) * np.float32(0.02))
+    router[17] = a
+    router[40] = b
+    c = synth.to_bf16_bits(np.float32(0.02) * lean + np.float32(0.01) * rng.standard_normal(hidden).astype(np.float32))
+    router[5] = c
+    router[90] = c
+    sel = _moe_run_planted(ctx, router.reshape(-1), x, hidden, width, experts, k, 46)
+    s0 = sel[0].tolist()
+    assert 17 in s0 and 40 in s0 and 5 in s0 and 90 in s0, s0
+    # the planted reversal: the reference orders the pair by its fold, not by
+    # the exact sums
+    exact_first = 40 if delta > 0 else 17
+    assert s0.index(exact_first) > s0.index(57 - exact_first), s0
+    for t in range(3):
+        assert sel[t].tolist().index(5) < sel[t].tolist().index(90)
+
+
+@pytest.mark.parametrize("hidden,experts,k", [(2048, 128, 8), (6144, 32, 4)])
+def test_moe_router_all_rows_equal(ctx, hidden, experts, k):
+    """Every router row the same: every logit ties, and the reference selects
+    rows 0 .. k - 1 in index order with equal weights; the certified router
+    folds every row exactly (two rows per LDS batch up to 4096 columns, one
+    above)."""
+    width = 256
+    rng = np.random.default_rng(4602)
+    row = synth.to_bf16_bits(rng.standard_normal(hidden).astype(np.float32) * np.float32(0.02))
+    router = np.tile(row, experts)
+    x = rng.standard_normal((2, hidden)).astype(np.float32)
+    sel = _moe_run_planted(ctx, router, x, hidden, width, experts, k, 47)
+    assert sel.tolist() == [list(range(k))] * 2
+
+
+def test_moe_router_odd_shapes(ctx):
+    """The certified router over a partial last round of columns (hidden 2816:
+    352 pieces of 8) and a partial last workgroup (202 experts)."""
+    hidden, width, experts, k = 2816, 256, 202, 6
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(48, 0), experts * hidden) * np.float32(0.02))
+    x = synth.normal(synth.activation_seed(48, 1), 3 * hidden).reshape(3, hidden)
+    _moe_run_planted(ctx, router, x, hidden, width, experts, k, 48)
+
+
+def test_moe_router_fold_overflow_is_non_finite(ctx):
+    """A row whose sequential f32 fold overflows (partial sums past FLT_MAX)
+    although its exact sum is 0: the reference's logit is infinite and
+    top_k_softmax rejects it (src/cpu.rs:240-245), so the layer returns
+    NonFinite and acquires nothing."""
+    hidden, width, experts, k = 2048, 256, 128, 8
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(49, 0), experts * hidden) * np.float32(0.02))
+    router = router.reshape(experts, hidden)
+    router[3, :hidden // 2] = synth.to_bf16_bits(np.ones(hidden // 2, np.float32))
+    router[3, hidden // 2:] = synth.to_bf16_bits(-np.ones(hidden // 2, np.float32))
+    x = np.full((1, hidden), 1e36, dtype=np.float32)
+    assert np.isinf(capi.matvec_bf16(experts, hidden, router, x[0])[3])
+    gu_bytes, dn_bytes = 2 * width * synth.row_bytes(Q4_K, hidden), hidden * synth.row_bytes(Q6_K, width)
+    gu = synth.quantized_matrix(Q4_K, experts * 2 * width, hidden, synth.weight_seed(49, 1))
+    dn = synth.quantized_matrix(Q6_K, experts * hidden, width, synth.weight_seed(49, 2))
+    cache = ExpertCache(ctx, np.concatenate([gu, dn]), [ExpertLayerLayout(experts, 0, gu_bytes, gu.size, dn_bytes)],
+                        experts)
+    rb, xb, yb = dev(ctx, router.reshape(-1)), dev(ctx, x), dev_out(ctx, hidden * 4)
+    with pytest.raises(HipError) as e:
+        ctx.moe_layer(cache, 0, 1, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K, xb.device_ptr,
+                      yb.device_ptr)
+    assert e.value.variant == "NonFinite"
+    assert cache.stats()["misses"] == 0 and cache.stats()["hits"] == 0
+    cache.free()
+
+
 # ---- config 5: prefill GEMM ----------------------------------------------------
 
 def _gemm_check(ctx, kind, m, n, k, seed, what):

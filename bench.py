@@ -147,22 +147,27 @@ def bench_c1(ctx, synth, steps, warmup):
                      "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     # Sustained: 8 distinct cold matrices sharing x in one grouped launch
     # (matvec_batch_device), so the ~2.4 us launch floor is paid once per 8
-    # matvecs.  Time and bytes are reported per matrix.
-    group = 8
-    yg = ctx.new_owned_buffer(group * rows * 4)
-    sets = [[b.device_ptr for b in wbs[j * group:(j + 1) * group]] for j in range(copies // group)]
-    for i in range(warmup + 1):
-        ctx.matvec_batch_device(Q4_K, rows, cols, sets[i % len(sets)], xb.device_ptr, 0, yg.device_ptr, rows)
-    n = max(steps, 2 * len(sets))
-    with Timed(ctx) as t:
-        for i in range(n):
+    # matvecs; and 16, a layer's same-input matvecs.  Time and bytes are
+    # reported per matrix.
+    for group, key in ((8, "sustained"), (16, "sustained_16")):
+        yg = ctx.new_owned_buffer(group * rows * 4)
+        sets = [[b.device_ptr for b in wbs[j * group:(j + 1) * group]] for j in range(copies // group)]
+        for i in range(warmup + 1):
             ctx.matvec_batch_device(Q4_K, rows, cols, sets[i % len(sets)], xb.device_ptr, 0, yg.device_ptr, rows)
-    ms = t.wall_ms / (n * group)
-    per = w.size + rows * 4 + cols * 4 / group
-    out["sustained"] = {"matrices_per_launch": group, "ms_per_matrix": ms, "bytes_per_matrix": per,
-                        "gbps": per / (ms * 1e-3) / 1e9, "frac_of_peak": per / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        n = max(steps, 2 * len(sets))
+        with Timed(ctx) as t:
+            for i in range(n):
+                ctx.matvec_batch_device(Q4_K, rows, cols, sets[i % len(sets)], xb.device_ptr, 0, yg.device_ptr,
+                                        rows)
+        ms = t.wall_ms / (n * group)
+        per = w.size + rows * 4 + cols * 4 / group
+        out[key] = {"matrices_per_launch": group, "ms_per_matrix": ms, "bytes_per_matrix": per,
+                    "gbps": per / (ms * 1e-3) / 1e9, "frac_of_peak": per / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        yg.free()
     log(f"C1: cold {out['cold']['ms_per_step'] * 1e3:.2f} us per launch ({out['cold']['gbps']:.0f} GB/s); "
-        f"sustained {ms * 1e3:.2f} us per matrix ({out['sustained']['gbps']:.0f} GB/s)")
+        f"sustained {out['sustained']['ms_per_matrix'] * 1e3:.2f} us per matrix ({out['sustained']['gbps']:.0f} GB/s), "
+        f"{out['sustained_16']['ms_per_matrix'] * 1e3:.2f} us with 16 per launch "
+        f"({out['sustained_16']['gbps']:.0f} GB/s)")
     out["floor"] = c1_floor(ctx, wbs, w.size, step_bytes, steps)
     return out
 

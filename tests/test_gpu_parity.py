@@ -1271,6 +1271,20 @@ def test_moe_router_all_rows_equal(ctx, hidden, experts, k):
     assert sel.tolist() == [list(range(k))] * 2
 
 
+@pytest.mark.parametrize("scale", [0.02, 3e-18])
+def test_moe_router_random_tokens(ctx, scale):
+    """64 random tokens (4 calls of 16) through the certified router: every
+    call's ids, in order, are the oracle's sequential fold's; at this data
+    about one token in fifty needs the exact fold of its near-tied rows.  The
+    tiny scale puts the logits near 1e-16, far from the unit scale."""
+    hidden, width, experts, k, batch = 2048, 256, 128, 8, 16
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(50, 0), experts * hidden) * np.float32(scale))
+    for call in range(4):
+        x = synth.normal(synth.activation_seed(50, call), batch * hidden).reshape(batch, hidden)
+        print(f"scale={scale} call {call}", flush=True)
+        _moe_run_planted(ctx, router, x, hidden, width, experts, k, 50)
+
+
 def test_moe_router_odd_shapes(ctx):
     """The certified router over a partial last round of columns (hidden 2816:
     352 pieces of 8) and a partial last workgroup (202 experts)."""

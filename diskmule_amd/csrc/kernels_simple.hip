@@ -794,21 +794,21 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
 // Workgroup (g, t): wave w takes row 4g + w of token t and publishes (L,
 // rho) with device-scope exchanges, then the workgroup takes the token's
 // ticket.  The last workgroup selects:
-//  * every rho finite: the top k by L (ties by index).  When the intervals
-//    [L - rho, L + rho] of consecutive selections are disjoint and every
-//    other row's interval lies below the k-th one's, the reference selects
-//    the same ids in the same order; the probabilities are then the
-//    reference's softmax over the f32 roundings of the selected L (within
-//    rho of the reference's logits).
+//  * every rho finite: k candidates, the top k by (f32(L), index).  When
+//    the intervals [L - rho, L + rho] of consecutive candidates are disjoint
+//    and every other row's interval lies below the k-th one's, the
+//    reference selects the same ids in the same order; the probabilities
+//    are then the reference's softmax over the f32 roundings of the
+//    selected L (within rho of the reference's logits).
 //  * otherwise C, the rows that can still be in the top k (every row whose
 //    L + rho reaches the smallest L - rho of the k candidates; any row
 //    outside C is below those k rows for certain), is ordered exactly: the
-//    members whose interval meets
-//    another member's (X: typically two rows) are folded exactly, the
-//    reference's way (staged in LDS, as router_lds_kernel folds), and
-//    compared by their exact logits (value, then index); every other pair
-//    of members has disjoint intervals, so L or an exact logit orders it.
-//    The selected members outside X take their f32-rounded L.
+//    members whose interval meets another member's (X: typically two rows)
+//    are folded exactly, the reference's way (staged in LDS, as
+//    router_lds_kernel folds), and compared by their exact logits (value,
+//    then index); every other pair of members has disjoint intervals, so L
+//    or an exact logit orders it.  The selected members outside X take
+//    their f32-rounded L.
 //  * a non-finite L (a non-finite input of the row or of x, so a non-finite
 //    reference logit) fails the call; a row whose fold may overflow (rho
 //    infinite, finite L) makes every row a member of X, so the non-finite

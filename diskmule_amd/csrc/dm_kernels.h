@@ -108,7 +108,7 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
 // With `certified` (the MoE layer, whose logits stay internal) and tickets,
 // decode batches of up to 8192 columns take the certified router: the same
 // ids in the same order as the exact fold, probabilities from logits within
-// a proven bound of it; `logits` then holds 16 bytes per (token, expert).
+// a proven bound of it; `logits` then holds 8 bytes per (token, expert).
 // True when launch_router_top_k takes a lookup for this router: one token,
 // and the router runs as one of the expert-parallel kernels whose token's
 // last workgroup makes the selection.

@@ -709,7 +709,7 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     // Workspace: logits | ids | probs | pos | pair tokens | xg | gate_up | act | expert_out
     const size_t pairs = batch * k;
     const size_t a_logits = 0;
-    const size_t a_ids = a_logits + ((batch * experts * 16 + 255) & ~(size_t)255);  // the certified router's (L, rho)
+    const size_t a_ids = a_logits + ((batch * experts * 8 + 255) & ~(size_t)255);  // the certified router's (L, rho)
     const size_t a_probs = a_ids + ((pairs * 4 + 255) & ~(size_t)255);
     const size_t a_pos = a_probs + ((pairs * 4 + 255) & ~(size_t)255);
     const size_t a_tok = a_pos + ((pairs * 4 + 255) & ~(size_t)255);

@@ -791,9 +791,11 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
 // A row whose M + D + B is not below 3e38, or whose inputs are not finite,
 // gets rho = +inf.
 //
-// Workgroup (g, t): wave w takes row 4g + w of token t and publishes (L,
-// rho) with device-scope exchanges, then the workgroup takes the token's
-// ticket.  The last workgroup selects:
+// Workgroup (g, t): wave w takes row 4g + w of token t and publishes f32(L)
+// and rho (widened by the rounding of L, rounded up to f32) as one word with
+// a device-scope exchange, then the workgroup takes the token's ticket.  The
+// rounding slack D covers L -+ rho formed in double from those floats.  The
+// last workgroup selects:
 //  * every rho finite: k candidates, the top k by (f32(L), index).  When
 //    the intervals [L - rho, L + rho] of consecutive candidates are disjoint
 //    and every other row's interval lies below the k-th one's, the
@@ -837,7 +839,7 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
     const uint32_t N8 = hidden / 8, e = blockIdx.x * 4 + wave;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(router, experts * hidden * 2);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)token * hidden, hidden * 4);
-    uint64_t *tc = cert + 2 * (size_t)token * experts;
+    uint64_t *tc = cert + (size_t)token * experts;
     {
         // lane: pieces (8 columns) pc0 .. pc0 + 3 of each 256-piece round
         double carry = 0.0, a = 0.0, sp = 0.0, m = 0.0;
@@ -884,14 +886,17 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
         const double B = 1.001 * (0x1p-24 * (A + n * D) + n * 0x1p-150);
         double rho = 1.001 * (B + 2.0 * D);
         if (!(M + D + B < 3.0e38)) rho = __builtin_inf();
-        uint64_t o0 = 0, o1 = 0;
-        if (lane == 0 && e < experts) {
-            o0 = __hip_atomic_exchange(&tc[2 * e], __double_as_longlong(carry), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            o1 = __hip_atomic_exchange(&tc[2 * e + 1], __double_as_longlong(rho), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-        }
-        asm volatile("" ::"v"(o0), "v"(o1) : "memory");  // the exchanges have completed
+        // One word per row: f32(L) and an f32 radius rounded up to cover rho
+        // and the rounding of L (non-finite stays non-finite).
+        const float lf = (float)carry;
+        const double rd = rho + fabs(carry - (double)lf);
+        float rf = (float)rd;
+        if ((double)rf < rd) rf = __uint_as_float(__float_as_uint(rf) + 1u);  // rd >= 0: the next float up
+        uint64_t o0 = 0;
+        if (lane == 0 && e < experts)
+            o0 = __hip_atomic_exchange(&tc[e], ((uint64_t)__float_as_uint(rf) << 32) | __float_as_uint(lf),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"(o0) : "memory");  // the exchange has completed
     }
     __shared__ uint32_t s_drawn;
     __syncthreads();
@@ -900,7 +905,7 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
     if (s_drawn != gridDim.x - 1) return;
 
     // The token's last workgroup: thread i < experts owns row i.
-    __shared__ double c_l[256], c_lo[256], c_hi[256];
+    __shared__ double c_lo[256], c_hi[256];
     __shared__ double c_klo;
     __shared__ double c_d[256];
     __shared__ uint32_t c_sel[256], c_x[256], c_xn, c_c[256], c_cn, c_inx[256];
@@ -913,13 +918,12 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
     double L = 0.0, lo = 0.0, hi = 0.0;
     bool fin = true;
     if (own) {
-        L = __longlong_as_double(__hip_atomic_load(&tc[2 * tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        const double rho =
-            __longlong_as_double(__hip_atomic_load(&tc[2 * tid + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        const uint64_t pk = __hip_atomic_load(&tc[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        L = (double)__uint_as_float((uint32_t)pk);
+        const double rho = (double)__uint_as_float((uint32_t)(pk >> 32));
         fin = __builtin_isfinite(rho);
         lo = L - rho;
         hi = L + rho;
-        c_l[tid] = L;
         c_lo[tid] = lo;
         c_hi[tid] = hi;
     }

@@ -88,11 +88,13 @@ struct BadFlag {
 hipError_t launch_top_k(hipStream_t s, const float *logits, uint32_t rows, uint32_t count,
                         uint32_t k, uint32_t *ids, float *probabilities, BadFlag non_finite);
 // The routed experts' slots looked up on the device, for a MoE layer call
-// of one token whose expert launches are queued behind the router: per
-// expert of the layer the device addresses of its slot's gate_up and down
-// bytes (0 when not resident); out, per selection, the addresses, and one
-// go word (device and pinned host copies): 1 when every selected expert is
-// resident and the token's logits are finite, else 0.
+// of up to kMaxLookupTokens tokens whose expert launches are queued behind
+// the router: per expert of the layer the device addresses of its slot's
+// gate_up and down bytes (0 when not resident); out, per selection s of
+// token t, the addresses at [t * k + s], and per token a go word (device and
+// pinned host copies): 1 when every selected expert of the token is resident
+// and its logits are finite, else 0.
+constexpr uint32_t kMaxLookupTokens = 8;
 struct ExpertLookup {
     const uint64_t *gate_up_of, *down_of;
     uint64_t *gate_up_w, *down_w;
@@ -109,9 +111,9 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
 // decode batches of up to 8192 columns take the certified router: the same
 // ids in the same order as the exact fold, probabilities from logits within
 // a proven bound of it; `logits` then holds 8 bytes per (token, expert).
-// True when launch_router_top_k takes a lookup for this router: one token,
-// and the router runs as one of the expert-parallel kernels whose token's
-// last workgroup makes the selection.
+// True when launch_router_top_k takes a lookup for this router: up to
+// kMaxLookupTokens tokens, and the router runs as one of the
+// expert-parallel kernels whose token's last workgroup makes the selection.
 bool router_takes_lookup(uint32_t hidden, uint32_t experts, uint32_t batch, const void *router, const float *x);
 // With host_ids, the selection and one word per token (nonzero when that
 // token's logits held a non-finite value; with the one-workgroup-per-token

@@ -66,25 +66,28 @@ bool qmv8_grouped_supported(uint32_t type, size_t rows, size_t columns, uint32_t
 // All jobs in one or a few launches.  gate_up == 0: y = W x.  gate_up == 1:
 // y = (g / (1 + exp(-g))) * u with g = gate . x, u = up . x, the routed-expert
 // activation of src/glm52/expert.rs:260-267.
-// The ordered combine of one token's experts fused into their down launch:
-// y_final[r] = sum over jobs p in order of fma(y[p * rows + r], p_[p], .),
-// with one zeroed ticket per row-tile workgroup (returned to zero).
+// The ordered combine of each token's experts fused into their down launch:
+// jobs t * k .. t * k + k - 1 are token t's selections, and
+// y_final[t * y_stride + r] = sum over them in order of
+// fma(y[p * rows + r], p_[p], .), with one zeroed ticket per token and
+// row-tile workgroup (returned to zero).
 struct QmvCombine {
     uint32_t *tickets;
     size_t tickets_count;
     const float *p;
     float *y;
+    uint32_t k, y_stride;
 };
 
 // With dev_w (one-token jobs, at most 64, one launch) the job addresses are
-// read on the device from dev_w[job] and the launch does nothing when *go is
-// 0: both written by a kernel earlier on the stream (ExpertLookup).  With
-// combine (one-token down jobs writing y + p * rows) the launch also makes
-// the ordered combine.
+// read on the device from dev_w[job] and the launch does nothing unless
+// go[0 .. go_count) are all 1: both written by a kernel earlier on the
+// stream (ExpertLookup).  With combine (one-token down jobs writing
+// y + p * rows) the launch also makes the ordered combine.
 hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, int gate_up,
                                uint64_t up_offset, const QmvJob *jobs, size_t count, const float *x, float *y,
                                const uint64_t *dev_w = nullptr, const uint32_t *go = nullptr,
-                               const QmvCombine *combine = nullptr);
+                               const QmvCombine *combine = nullptr, uint32_t go_count = 1);
 
 // True when the MFMA matvec takes this shape: Q4_K or Q6_K rows of whole
 // 256-value blocks, a weight base address aligned to 4 bytes (16 for Q4_K),

@@ -75,7 +75,10 @@ __global__ void moe_combine_pos_kernel(const float *__restrict__ expert_out,
                                        const uint32_t *__restrict__ pos, const float *__restrict__ p,
                                        uint32_t batch, uint32_t k, uint32_t hidden,
                                        float *__restrict__ y, const uint32_t *__restrict__ go) {
-    if (go && *go == 0) return;  // the device-side lookup found a slot missing
+    // the device-side lookup found a slot missing (go: one word per token)
+    if (go)
+        for (uint32_t t = 0; t < batch; t++)
+            if (go[t] == 0) return;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < (size_t)batch * hidden;
          e += (size_t)gridDim.x * blockDim.x) {
         uint32_t t = (uint32_t)(e / hidden), i = (uint32_t)(e - (size_t)t * hidden);
@@ -178,7 +181,7 @@ struct dmhip_expert_cache {
     std::vector<hipEvent_t> release_events;
     size_t next_release = 0;
     // Device memory: every layer's residency table, then the lookup's
-    // outputs (gate_up and down addresses per selection, the go word); the
+    // outputs (gate_up and down addresses per selection, a go word per token); the
     // tables' pinned host masters.
     uint64_t *tables = nullptr;
     uint64_t *host_tables = nullptr;
@@ -189,7 +192,7 @@ struct dmhip_expert_cache {
 
 namespace {
 constexpr size_t kSelectionPairs = 16 * dm::kMaxTopK;  // batch <= 16
-constexpr size_t kSelectionBytes = kSelectionPairs * 8 + 16 * 4 + 16;  // ids, probabilities, per-token flags, go
+constexpr size_t kSelectionBytes = kSelectionPairs * 8 + 16 * 4 + 16 * 4;  // ids, probabilities, per-token flags, go
 constexpr size_t kReleaseEvents = 64;
 constexpr size_t kCombineTickets = 4096;  // row-tile workgroups of a fused down + combine launch
 constexpr size_t kStagingEntries = 4;  // file source: experts in flight from storage
@@ -499,7 +502,7 @@ int build_cache(dmhip_ctx *ctx, const dmhip_expert_layer_layout *layouts, size_t
     // residency tables (all zero: nothing resident) and the lookup outputs
     size_t entries = 0;
     for (const Layer &layer : c->layers) entries += 2 * layer.layout.expert_count;
-    const size_t table_bytes = (entries + 2 * kMaxTopK + 1) * sizeof(uint64_t) + kCombineTickets * sizeof(uint32_t);
+    const size_t table_bytes = (entries + 2 * kMaxTopK + 8) * sizeof(uint64_t) + kCombineTickets * sizeof(uint32_t);
     if (hipMalloc((void **)&c->tables, table_bytes) != hipSuccess) {
         c->tables = nullptr;
         return fail_alloc(table_bytes);
@@ -519,8 +522,8 @@ int build_cache(dmhip_ctx *ctx, const dmhip_expert_layer_layout *layouts, size_t
     }
     c->lookup_gate_up = c->tables + at;
     c->lookup_down = c->lookup_gate_up + kMaxTopK;
-    c->lookup_go = (uint32_t *)(c->lookup_down + kMaxTopK);
-    c->combine_tickets = (uint32_t *)(c->lookup_down + kMaxTopK + 1);
+    c->lookup_go = (uint32_t *)(c->lookup_down + kMaxTopK);  // 16 words: one per token
+    c->combine_tickets = (uint32_t *)(c->lookup_down + kMaxTopK + 8);
     return DMHIP_OK;
 }
 
@@ -749,18 +752,19 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
     // per-token words can be cleared from here.
     memset(sel_bad, 0, 16 * 4);
     Layer &Lay = c->layers[layer];
-    // One token whose experts are likely resident: the router's last
-    // workgroup looks the selected experts up in the layer's residency table
-    // and the expert launches and the combine are queued right behind it,
-    // reading the slot addresses it found; when a slot is missing (or the
-    // logits are not finite) they do nothing and the host takes the path
-    // below with the selection in hand.  Every earlier upload is already
-    // waited for on the compute stream, before the table copy and the
-    // router.
-    const bool lookup = Lay.try_lookup && grouped && k <= kMaxGroupedJobs &&
+    // Up to kMaxLookupTokens tokens whose experts are likely resident: each
+    // token's last router workgroup looks its selected experts up in the
+    // layer's residency table, and the expert launches (one job per token
+    // and selection) and the combine are queued right behind the router,
+    // reading the slot addresses it found; when a slot is missing (or a
+    // token's logits are not finite) they do nothing and the host takes the
+    // path below with the selection in hand.  Every earlier upload is
+    // already waited for on the compute stream, before the table copy and
+    // the router.
+    const bool lookup = Lay.try_lookup && grouped && pairs <= kMaxGroupedJobs &&
                         router_takes_lookup((uint32_t)hidden, (uint32_t)experts, (uint32_t)batch, router_bf16, x);
     if (lookup) {
-        *sel_go = 0;
+        for (size_t t = 0; t < batch; t++) sel_go[t] = 0;
         DM_CHECK_STATUS(wait_all_ready(c, layer));  // none pending after a completed call
         if (Lay.table_dirty) {
             DM_HIP(hipMemcpyAsync(Lay.table, Lay.host_table, 2 * L.expert_count * sizeof(uint64_t),
@@ -770,25 +774,27 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
         const ExpertLookup el{Lay.table, Lay.table + L.expert_count, c->lookup_gate_up, c->lookup_down,
                               c->lookup_go, (uint32_t *)sel_go};
         DM_HIP(launch_router_top_k(ctx->stream, router_bf16, (uint32_t)hidden, (uint32_t)experts, (uint32_t)k,
-                                   1, x, d_logits, d_ids, d_probs, BadFlag{ctx->flags + kMoeFlagWord, 1}, sel_ids,
-                                   sel_probs, ctx->router_tickets, sel_bad, &el, true));
-        std::vector<QmvJob> gu_jobs(k), dn_jobs(k);
-        for (size_t p = 0; p < k; p++) {
-            gu_jobs[p] = QmvJob{nullptr, 1u, 0u, (uint32_t)(p * width), 0, 0};
+                                   (uint32_t)batch, x, d_logits, d_ids, d_probs, BadFlag{ctx->flags + kMoeFlagWord, 1},
+                                   sel_ids, sel_probs, ctx->router_tickets, sel_bad, &el, true));
+        // job p: selection p % k of token p / k
+        std::vector<QmvJob> gu_jobs(pairs), dn_jobs(pairs);
+        for (size_t p = 0; p < pairs; p++) {
+            gu_jobs[p] = QmvJob{nullptr, 1u, (uint32_t)(p / k * hidden), (uint32_t)(p * width), 0, 0};
             dn_jobs[p] = QmvJob{nullptr, 1u, (uint32_t)(p * width), (uint32_t)(p * hidden), 0, 0};
         }
+        const uint32_t tokens = (uint32_t)batch;
         DM_HIP(launch_qmv8_grouped(ctx, gate_up_type, (uint32_t)width, (uint32_t)hidden, 1, up_offset,
-                                   gu_jobs.data(), k, x, d_act, c->lookup_gate_up, c->lookup_go));
+                                   gu_jobs.data(), pairs, x, d_act, c->lookup_gate_up, c->lookup_go, nullptr, tokens));
         // the down launch also makes the ordered combine when its split
         // allows (every workgroup holds whole row tiles of every expert)
-        const QmvCombine cmb{c->combine_tickets, kCombineTickets, d_probs, y};
-        if (launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(), k, d_act,
-                                d_eo, c->lookup_down, c->lookup_go, &cmb) != hipSuccess) {
+        const QmvCombine cmb{c->combine_tickets, kCombineTickets, d_probs, y, (uint32_t)k, (uint32_t)hidden};
+        if (launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(), pairs,
+                                d_act, d_eo, c->lookup_down, c->lookup_go, &cmb, tokens) != hipSuccess) {
             (void)hipGetLastError();
-            DM_HIP(launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(), k,
-                                       d_act, d_eo, c->lookup_down, c->lookup_go));
-            hipLaunchKernelGGL(moe_combine_pos_kernel, dim3((uint32_t)((hidden + 255) / 256)), dim3(256), 0,
-                               ctx->stream, d_eo, nullptr, d_probs, 1u, (uint32_t)k, (uint32_t)hidden, y,
+            DM_HIP(launch_qmv8_grouped(ctx, down_type, (uint32_t)hidden, (uint32_t)width, 0, 0, dn_jobs.data(), pairs,
+                                       d_act, d_eo, c->lookup_down, c->lookup_go, nullptr, tokens));
+            hipLaunchKernelGGL(moe_combine_pos_kernel, dim3((uint32_t)((batch * hidden + 255) / 256)), dim3(256), 0,
+                               ctx->stream, d_eo, nullptr, d_probs, tokens, (uint32_t)k, (uint32_t)hidden, y,
                                c->lookup_go);
             DM_HIP(hipGetLastError());
         }
@@ -805,14 +811,17 @@ int dmhip_moe_layer(dmhip_ctx *ctx, dmhip_expert_cache *c, size_t layer, size_t 
         if (sel_bad[t]) return fail_non_finite("top-k softmax");
     memcpy(ids, sel_ids, pairs * 4);
     memcpy(probabilities, sel_probs, pairs * 4);
-    if (lookup && *sel_go) {
+    bool all_go = lookup;
+    for (size_t t = 0; all_go && t < batch; t++) all_go = sel_go[t] != 0;
+    if (all_go) {
         // Done on the device: the cache's bookkeeping is the reference's
-        // acquire sequence, every one a hit.  The work that read the slots
-        // has finished (the synchronisation above), so a later upload into
-        // them has nothing to wait for.
+        // acquire sequence (token by token, selection order), every one a
+        // hit.  The work that read the slots has finished (the
+        // synchronisation above), so a later upload into them has nothing to
+        // wait for.
         size_t slot;
-        for (size_t p = 0; p < k; p++) DM_CHECK_STATUS(acquire(c, layer, ids[p], &slot));
-        for (size_t p = 0; p < k; p++)
+        for (size_t p = 0; p < pairs; p++) DM_CHECK_STATUS(acquire(c, layer, ids[p], &slot));
+        for (size_t p = 0; p < pairs; p++)
             for (Slot &sl : Lay.slots)
                 if (sl.has && sl.expert == ids[p]) sl.released_recorded = false;
         return DMHIP_OK;

@@ -930,17 +930,18 @@ struct JobTable8 {
     Job8 job[kMaxJobs8];
 };
 
-// The ordered combine of one token's routed experts fused into their down
+// The ordered combine of each token's routed experts fused into their down
 // launch: y[r] = fma(out_k-1[r], p[k-1], ... fma(out_0[r], p[0], 0)) in
 // selection order, as the separate combine computes it
-// (src/gemma4/cpu.rs:608-611).  Every workgroup publishes its expert's rows
-// (PUB), then takes the ticket of its row tiles; the one that draws the
-// last (of gridDim.y = k) adds the k rows of those tiles and resets the
-// ticket.
+// (src/gemma4/cpu.rs:608-611).  Job j is selection j % k of token j / k.
+// Every workgroup publishes its expert's rows (PUB), then takes the ticket
+// of its token's row tiles; the one that draws the last (of k) adds the k
+// rows of those tiles and resets the ticket.
 struct Combine8 {
-    uint32_t *tickets;  // one per blockIdx.x, zero between launches
-    const float *p;     // the token's k probabilities
-    float *y;           // the token's output
+    uint32_t *tickets;  // one per (token, blockIdx.x), zero between launches
+    const float *p;     // k probabilities per token
+    float *y;           // token t's output at y + t * y_stride
+    uint32_t k, y_stride;
 };
 
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G, bool PUB = false>
@@ -948,10 +949,13 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     __attribute__((amdgpu_waves_per_eu(waves_per_eu8<TYPE, MODE, TOK, G>()))) qmv8_grouped_kernel(JobTable8 jobs, uint32_t rows, uint32_t columns, uint32_t row_bytes,
                         uint32_t total_bytes, uint64_t w2_offset, const float *__restrict__ x,
                         float *__restrict__ y, int glm, const uint64_t *__restrict__ dev_w,
-                        const uint32_t *__restrict__ go, Combine8 cb) {
+                        const uint32_t *__restrict__ go, uint32_t go_count, Combine8 cb) {
     // Jobs whose matrices a kernel earlier on the stream looked up: their
-    // addresses come from dev_w, and the launch does nothing when go is 0.
-    if (go && *go == 0) return;
+    // addresses come from dev_w, and the launch does nothing unless each of
+    // the go_count tokens' go words is 1.
+    if (go)
+        for (uint32_t t = 0; t < go_count; t++)
+            if (go[t] == 0) return;
     const Job8 j = jobs.job[blockIdx.y];
     const uint8_t *w = (const uint8_t *)(dev_w ? dev_w[blockIdx.y] : j.w);
     constexpr uint32_t WAVES = S > 8 ? S : 8;
@@ -962,21 +966,24 @@ __global__ void __launch_bounds__(64 * (S > 8 ? S : 8))
     if constexpr (PUB) {
         static_assert(MODE == 0 && TOK == 1 && S > 1, "the combine follows one-token split launches");
         __shared__ uint32_t s_last;
+        const uint32_t token = blockIdx.y / cb.k;
+        uint32_t *ticket = &cb.tickets[(size_t)token * gridDim.x + blockIdx.x];
         __syncthreads();  // every wave's rows are published
-        if (threadIdx.x == 0) s_last = atomicAdd(&cb.tickets[blockIdx.x], 1u) == gridDim.y - 1 ? 1u : 0u;
+        if (threadIdx.x == 0) s_last = atomicAdd(ticket, 1u) == cb.k - 1 ? 1u : 0u;
         __syncthreads();
         if (!s_last) return;
         // the rows of this workgroup's tiles (y_off of job p is p * rows)
         const uint32_t r0 = blockIdx.x * (WAVES / S) * 16, r1 = min(r0 + (WAVES / S) * 16, rows);
+        const uint32_t j0 = token * cb.k;
         for (uint32_t r = r0 + threadIdx.x; r < r1; r += blockDim.x) {
             float acc = 0.0f;
-            for (uint32_t p = 0; p < gridDim.y; p++)
+            for (uint32_t p = j0; p < j0 + cb.k; p++)
                 acc = __builtin_fmaf(__hip_atomic_load(&y[(size_t)p * rows + r], __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_AGENT),
                                      cb.p[p], acc);
-            cb.y[r] = acc;
+            cb.y[(size_t)token * cb.y_stride + r] = acc;
         }
-        if (threadIdx.x == 0) __hip_atomic_store(&cb.tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1184,7 +1191,8 @@ Plan8 plan8_grouped(uint32_t type, uint32_t rows, uint32_t columns, uint32_t bat
 struct DeviceJobs {
     const uint64_t *w;
     const uint32_t *go;
-    Combine8 cb;  // cb.tickets set: the fused combine (one-token down jobs)
+    uint32_t go_count;  // go words (tokens) a launch checks
+    Combine8 cb;        // cb.tickets set: the fused combine (one-token down jobs)
 };
 
 template <uint32_t TYPE, int S, int MODE, int TOK, uint32_t G>
@@ -1208,7 +1216,7 @@ hipError_t run8_grouped(dmhip_ctx *ctx, uint32_t rows, uint32_t columns, uint64_
         if (e != hipSuccess) return e;
     }
     return launch_kernel(ctx, kernel, dim3(grid, count), dim3(64 * WAVES), lds, table, rows, columns, row_bytes,
-                         row_bytes * rows, up_offset, x, y, MODE == 2 ? 1 : 0, dj.w, dj.go, dj.cb);
+                         row_bytes * rows, up_offset, x, y, MODE == 2 ? 1 : 0, dj.w, dj.go, dj.go_count, dj.cb);
 }
 
 template <uint32_t TYPE, int MODE, int TOK, uint32_t G>
@@ -1307,7 +1315,8 @@ bool qmv8_grouped_supported(uint32_t type, size_t rows, size_t columns, uint32_t
 
 hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uint32_t columns, int gate_up,
                                uint64_t up_offset, const QmvJob *jobs, size_t count, const float *x, float *y,
-                               const uint64_t *dev_w, const uint32_t *go, const QmvCombine *combine) {
+                               const uint64_t *dev_w, const uint32_t *go, const QmvCombine *combine,
+                               uint32_t go_count) {
     const uint32_t mats = gate_up ? 2u : 1u;
     // device-side addresses (and the fused combine): one launch of one-token
     // jobs, in order
@@ -1316,15 +1325,19 @@ hipError_t launch_qmv8_grouped(dmhip_ctx *ctx, uint32_t type, uint32_t rows, uin
         for (size_t i = 0; i < count; i++)
             if (jobs[i].tokens != 1) return hipErrorInvalidValue;
     }
-    DeviceJobs dj{dev_w, go, Combine8{nullptr, nullptr, nullptr}};
+    DeviceJobs dj{dev_w, go, go_count, Combine8{nullptr, nullptr, nullptr, 1u, 0u}};
     if (combine) {
         // the combine reads job p's rows at y + p * rows, and needs a split
-        // launch (one workgroup holds whole tiles of every job)
+        // launch (one workgroup holds whole tiles of every job) with a ticket
+        // per token and row-tile workgroup
         for (size_t i = 0; i < count; i++)
             if (jobs[i].y_off != i * rows) return hipErrorInvalidValue;
+        if (combine->k == 0 || count % combine->k != 0) return hipErrorInvalidValue;
         const Plan8 p = plan8_grouped(type, rows, columns, 1, mats, (uint32_t)count);
-        if (gate_up || p.s < 2 || (rows + 15) / 16 > combine->tickets_count * (8 / p.s)) return hipErrorInvalidValue;
-        dj.cb = Combine8{combine->tickets, combine->p, combine->y};
+        if (gate_up || p.s < 2) return hipErrorInvalidValue;
+        const size_t groups = ((size_t)(rows + 15) / 16 + 8 / p.s - 1) / (8 / p.s);
+        if (groups * (count / combine->k) > combine->tickets_count) return hipErrorInvalidValue;
+        dj.cb = Combine8{combine->tickets, combine->p, combine->y, combine->k, combine->y_stride};
     }
     // Jobs of one and of two tokens go to separate launches, kMaxJobs8 each.
     for (uint32_t tok = 1; tok <= 2; tok++) {

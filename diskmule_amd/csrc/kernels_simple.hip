@@ -361,19 +361,19 @@ __global__ void __launch_bounds__(256) router_staged_kernel(
     }
 }
 
-// The selected experts' slots (MoE layer call of one token): thread 0 of
-// the token's last workgroup looks each id up and publishes the addresses
-// and the go word (ExpertLookup).
-__device__ void expert_lookup(const ExpertLookup &L, const uint32_t *ids, uint32_t k, bool bad) {
+// The selected experts' slots (MoE layer call): thread 0 of the token's
+// last workgroup looks each id up and publishes the addresses and the
+// token's go word (ExpertLookup).
+__device__ void expert_lookup(const ExpertLookup &L, const uint32_t *ids, uint32_t k, uint32_t token, bool bad) {
     uint32_t go = bad ? 0u : 1u;
     for (uint32_t s = 0; s < k; s++) {
         const uint64_t gu = L.gate_up_of[ids[s]], dn = L.down_of[ids[s]];
         if (gu == 0 || dn == 0) go = 0;
-        L.gate_up_w[s] = gu;
-        L.down_w[s] = dn;
+        L.gate_up_w[(size_t)token * k + s] = gu;
+        L.down_w[(size_t)token * k + s] = dn;
     }
-    *L.go = go;
-    *L.host_go = go;
+    L.go[token] = go;
+    L.host_go[token] = go;
 }
 
 // Expert-parallel form of the exact router for decode: workgroup (g, t) is
@@ -513,7 +513,7 @@ __global__ void __launch_bounds__(64) router_fold_kernel(const uint16_t *__restr
             }
             host_bad[token] = bad;
         }
-        if (lookup.go) expert_lookup(lookup, ti, k, bad);
+        if (lookup.go) expert_lookup(lookup, ti, k, token, bad);
         __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -739,8 +739,8 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
         if (lookup.go) {
             // the selected expert's slot (ExpertLookup)
             const uint64_t gu = lookup.gate_up_of[index], dn = lookup.down_of[index];
-            lookup.gate_up_w[tid] = gu;
-            lookup.down_w[tid] = dn;
+            lookup.gate_up_w[(size_t)token * k + tid] = gu;
+            lookup.down_w[(size_t)token * k + tid] = dn;
             if (gu == 0 || dn == 0) s_missing = 1;  // every writer stores the same value
         }
     }
@@ -760,8 +760,8 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
         if (host_ids) host_bad[token] = row_bad;
         if (lookup.go) {
             const uint32_t go = row_bad || s_missing ? 0u : 1u;
-            *lookup.go = go;
-            *lookup.host_go = go;
+            lookup.go[token] = go;
+            lookup.host_go[token] = go;
         }
         __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1081,8 +1081,8 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
         if (host_ids) host_ids[(size_t)token * k + tid] = index;
         if (lookup.go) {
             const uint64_t gu = lookup.gate_up_of[index], dn = lookup.down_of[index];
-            lookup.gate_up_w[tid] = gu;
-            lookup.down_w[tid] = dn;
+            lookup.gate_up_w[(size_t)token * k + tid] = gu;
+            lookup.down_w[(size_t)token * k + tid] = dn;
             if (gu == 0 || dn == 0) s_missing = 1;  // every writer stores the same value
         }
     }
@@ -1102,8 +1102,8 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
         if (host_ids) host_bad[token] = row_bad;
         if (lookup.go) {
             const uint32_t go = row_bad || s_missing ? 0u : 1u;
-            *lookup.go = go;
-            *lookup.host_go = go;
+            lookup.go[token] = go;
+            lookup.host_go[token] = go;
         }
         __hip_atomic_store(&tickets[token], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1301,7 +1301,8 @@ bool router_staged(uint32_t hidden, uint32_t experts, const void *router, const 
 }  // namespace
 
 bool router_takes_lookup(uint32_t hidden, uint32_t experts, uint32_t batch, const void *router, const float *x) {
-    return batch == 1 && router_staged(hidden, experts, router, x) && experts >= 2 * RF_EXPERTS;
+    return batch >= 1 && batch <= kMaxLookupTokens && router_staged(hidden, experts, router, x) &&
+           experts >= 2 * RF_EXPERTS;
 }
 
 hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t hidden,

@@ -1170,6 +1170,77 @@ def test_moe_layer_resident_lookup_sequence(ctx, slots):
     src.free()
 
 
+@pytest.mark.parametrize("batch,slots", [(2, 24), (4, 128), (8, 128)])
+def test_moe_layer_resident_lookup_batches(ctx, batch, slots):
+    """Batches of 2-8 tokens take the device-side slot lookup once every
+    selected expert is resident (one job per token and selection, the
+    combine per token fused into the down launch), and the host path when a
+    slot is missing: batches a, a, a, b, b, a, a, a non-finite batch, a.
+    With 24 slots and 2 tokens, batch b evicts some of a's experts, so the
+    later calls of a find a slot missing at least once.  Every clean call
+    equals the oracle (ids, weights, output); calls of one batch on the
+    lookup path agree bit for bit; the cache counters equal the reference
+    LRU's for the same acquire sequence."""
+    hidden, width, experts, k = 2048, 256, 128, 8
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(51, 0), experts * hidden) * np.float32(0.02))
+    gu_bytes, dn_bytes = 2 * width * synth.row_bytes(Q4_K, hidden), hidden * synth.row_bytes(Q6_K, width)
+    gu = synth.quantized_matrix(Q4_K, experts * 2 * width, hidden, synth.weight_seed(51, 1))
+    dn = synth.quantized_matrix(Q6_K, experts * hidden, width, synth.weight_seed(51, 2))
+    src = PinnedHostBuffer(gu.size + dn.size)
+    src.array[:gu.size] = gu
+    src.array[gu.size:] = dn
+    cache = ExpertCache(ctx, src, [ExpertLayerLayout(experts, 0, gu_bytes, gu.size, dn_bytes)], slots)
+    xs = {name: synth.normal(synth.activation_seed(51, 10 * batch + i), batch * hidden).reshape(batch, hidden)
+          for i, name in enumerate("ab")}
+    want = {name: capi.moe_layer(batch, hidden, width, experts, k, router, Q4_K, gu, Q6_K, dn, x)
+            for name, x in xs.items()}
+    bad = xs["a"].copy()
+    bad[batch - 1, 7] = np.inf
+    rb, yb = dev(ctx, router), dev_out(ctx, batch * hidden * 4)
+    dx = {name: dev(ctx, x) for name, x in xs.items()}
+    lru = capi.Lru([experts], slots, gu_bytes, dn_bytes)
+    seen = {}
+    try_lookup = True  # the layer's state: a lookup is tried after a call whose experts were all resident
+    paths = []
+    for step, name in enumerate(["a", "a", "a", "b", "b", "a", "a", "bad", "a"]):
+        print(f"batch={batch} slots={slots} call {step}: {name}", flush=True)
+        if name == "bad":
+            before = cache.stats()
+            with pytest.raises(HipError) as e:
+                ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                              dev(ctx, bad).device_ptr, yb.device_ptr)
+            assert e.value.variant == "NonFinite"
+            after = cache.stats()
+            assert (after["hits"], after["misses"]) == (before["hits"], before["misses"])
+            continue
+        sel, wts, out = want[name]
+        misses = cache.stats()["misses"]
+        ids, probs = ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                                   dx[name].device_ptr, yb.device_ptr)
+        assert np.array_equal(ids, sel), f"call {step}: expert ids differ"
+        assert np.allclose(probs, wts, rtol=1e-5, atol=1e-7)
+        got = yb.read(0, batch * hidden * 4, np.float32).reshape(batch, hidden)
+        for t in range(batch):
+            assert_close(got[t], out[t], f"call {step} batch {name} token {t}")
+        hits_only = cache.stats()["misses"] == misses
+        path = "lookup" if try_lookup and hits_only else "host"
+        try_lookup = hits_only
+        paths.append(path)
+        # each path repeats its results bit for bit
+        if (name, path) in seen:
+            assert np.array_equal(bits(got), bits(seen[name, path])), f"call {step}: output differs"
+        seen.setdefault((name, path), got.copy())
+        for t in range(batch):
+            for e_id in sel[t]:
+                lru.acquire(0, int(e_id))
+    st, ref = cache.stats(), lru.stats()
+    for key in ("hits", "misses", "evictions", "reads", "bytes_read", "resident_bytes"):
+        assert st[key] == ref[key], key
+    assert "lookup" in paths, paths
+    cache.free()
+    src.free()
+
+
 # ---- the MoE layer's certified router: planted near-ties ------------------------
 
 def _moe_run_planted(ctx, router, x, hidden, width, experts, k, seed):

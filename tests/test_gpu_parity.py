@@ -1174,7 +1174,8 @@ def test_moe_layer_resident_lookup_sequence(ctx, slots):
 def test_moe_layer_resident_lookup_batches(ctx, batch, slots):
     """Batches of 2-8 tokens take the device-side slot lookup once every
     selected expert is resident (one job per token and selection, the
-    combine per token fused into the down launch), and the host path when a
+    combine per token fused into the down launch or run behind it), and the
+    host path when a
     slot is missing: batches a, a, a, b, b, a, a, a non-finite batch, a.
     With 24 slots and 2 tokens, batch b evicts some of a's experts, so the
     later calls of a find a slot missing at least once.  Every clean call

@@ -1242,6 +1242,44 @@ def test_moe_layer_resident_lookup_batches(ctx, batch, slots):
     src.free()
 
 
+def test_moe_layer_lookup_wide_router(ctx):
+    """Two tokens over a router wider than 8192 columns (the exact fold's
+    expert-parallel kernel, which writes the device-side lookup itself):
+    four calls of one batch, the host path until the experts are resident,
+    then the lookup; every call equals the oracle and each path repeats its
+    results bit for bit."""
+    hidden, width, experts, k, batch, slots = 8448, 256, 32, 4, 2, 32
+    router = synth.to_bf16_bits(synth.normal(synth.weight_seed(52, 0), experts * hidden) * np.float32(0.02))
+    gu_bytes, dn_bytes = 2 * width * synth.row_bytes(Q4_K, hidden), hidden * synth.row_bytes(Q6_K, width)
+    gu = synth.quantized_matrix(Q4_K, experts * 2 * width, hidden, synth.weight_seed(52, 1))
+    dn = synth.quantized_matrix(Q6_K, experts * hidden, width, synth.weight_seed(52, 2))
+    cache = ExpertCache(ctx, np.concatenate([gu, dn]), [ExpertLayerLayout(experts, 0, gu_bytes, gu.size, dn_bytes)],
+                        slots)
+    x = synth.normal(synth.activation_seed(52, 0), batch * hidden).reshape(batch, hidden)
+    sel, wts, want = capi.moe_layer(batch, hidden, width, experts, k, router, Q4_K, gu, Q6_K, dn, x)
+    rb, xb, yb = dev(ctx, router), dev(ctx, x), dev_out(ctx, batch * hidden * 4)
+    seen, try_lookup, paths = {}, True, []
+    for step in range(4):
+        misses = cache.stats()["misses"]
+        ids, probs = ctx.moe_layer(cache, 0, batch, hidden, width, experts, k, rb.device_ptr, Q4_K, Q6_K,
+                                   xb.device_ptr, yb.device_ptr)
+        assert np.array_equal(ids, sel), f"call {step}: expert ids differ"
+        assert np.allclose(probs, wts, rtol=1e-5, atol=1e-7)
+        got = yb.read(0, batch * hidden * 4, np.float32).reshape(batch, hidden)
+        for t in range(batch):
+            assert_close(got[t], want[t], f"call {step} token {t}")
+        hits_only = cache.stats()["misses"] == misses
+        path = "lookup" if try_lookup and hits_only else "host"
+        try_lookup = hits_only
+        paths.append(path)
+        if path in seen:
+            assert np.array_equal(bits(got), bits(seen[path])), f"call {step}: output differs"
+        seen.setdefault(path, got.copy())
+    print("paths", paths, flush=True)
+    assert "lookup" in paths, paths
+    cache.free()
+
+
 # ---- the MoE layer's certified router: planted near-ties ------------------------
 
 def _moe_run_planted(ctx, router, x, hidden, width, experts, k, seed):

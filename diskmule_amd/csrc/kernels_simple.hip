@@ -791,7 +791,7 @@ __global__ void __launch_bounds__(256) router_lds_kernel(const uint16_t *__restr
 // A row whose M + D + B is not below 3e38, or whose inputs are not finite,
 // gets rho = +inf.
 //
-// Workgroup (g, t): wave w takes row 4g + w of token t and publishes f32(L)
+// Workgroup (g, t) of W waves: wave w takes row W g + w of token t and publishes f32(L)
 // and rho (widened by the rounding of L, rounded up to f32) as one word with
 // a device-scope exchange, then the workgroup takes the token's ticket.  The
 // rounding slack D covers L -+ rho formed in double from those floats.  The
@@ -827,7 +827,8 @@ __device__ __forceinline__ double wave_max_f64(double v) {
     return v;
 }
 
-__global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__restrict__ router, uint32_t hidden,
+template <uint32_t W>
+__global__ void __launch_bounds__(64 * W) router_cert_kernel(const uint16_t *__restrict__ router, uint32_t hidden,
                                                           uint32_t experts, uint32_t k, const float *__restrict__ x,
                                                           uint64_t *cert, uint32_t *tickets, uint32_t *ids,
                                                           float *probabilities, BadFlag non_finite,
@@ -836,7 +837,8 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
     extern __shared__ __attribute__((aligned(16))) v4a cert_lds[];  // exact folds: rf rows, then x (router_lds_bytes)
     constexpr uint32_t nowhere = 0x80000000u;                      // every load from here reads zeros
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, token = blockIdx.y;
-    const uint32_t N8 = hidden / 8, e = blockIdx.x * 4 + wave;
+    constexpr uint32_t T = 64 * W;  // threads
+    const uint32_t N8 = hidden / 8, e = blockIdx.x * W + wave;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(router, experts * hidden * 2);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)token * hidden, hidden * 4);
     uint64_t *tc = cert + (size_t)token * experts;
@@ -910,7 +912,7 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
     __shared__ double c_d[256];
     __shared__ uint32_t c_sel[256], c_x[256], c_xn, c_c[256], c_cn, c_inx[256];
     __shared__ uint64_t c_keys[256];
-    __shared__ uint32_t c_rank[256];
+    __shared__ uint32_t c_rank[T];
     __shared__ float c_v[256], s_value[256];
     __shared__ float s_sum;
     __shared__ uint32_t s_missing;
@@ -938,15 +940,21 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
         // Candidate order: by (f32(L), index) keys.  Any order is sound (the
         // test below proves the reference's order or fails); L values that
         // round to one f32 lie within one ulp, inside their intervals, so
-        // they fail it whichever order they take.  Up to 128 experts, two
-        // threads count each key's rank over half of the keys.
+        // they fail it whichever order they take.  T / 128 threads (T / 256
+        // above 128 experts) count each key's rank over a part of the keys.
         if (own) c_keys[tid] = argmax_key((float)L, tid);
         __syncthreads();
-        const uint32_t split = experts <= 128 ? 2u : 1u, span = (experts + split - 1) / split;
-        const uint32_t me = split == 2 ? tid & 127u : tid, begin = split == 2 ? (tid >> 7) * span : 0u;
-        c_rank[tid] = me < experts ? key_rank(c_keys + begin, span < experts - begin ? span : experts - begin, c_keys[me]) : 0u;
+        const uint32_t per = experts <= 128 ? 128u : 256u, split = T / per;
+        const uint32_t span = (experts + split - 1) / split, me = tid % per, begin = tid / per * span;
+        c_rank[tid] = me < experts && begin < experts
+                          ? key_rank(c_keys + begin, span < experts - begin ? span : experts - begin, c_keys[me])
+                          : 0u;
         __syncthreads();
-        const uint32_t rank = own ? c_rank[tid] + (split == 2 ? c_rank[tid + 128] : 0u) : experts;
+        uint32_t rank = experts;
+        if (own) {
+            rank = 0;
+            for (uint32_t q = 0; q < split; q++) rank += c_rank[q * per + tid];
+        }
         if (rank < k) c_sel[rank] = tid;
         __syncthreads();
         bool ok = true;
@@ -992,12 +1000,12 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
                     const uint32_t f = c_c[j];
                     in_x |= f != tid && lo <= c_hi[f] && c_lo[f] <= hi;
                 }
-            c_inx[tid] = in_x ? 1u : 0u;
+            if (own) c_inx[tid] = in_x ? 1u : 0u;
             if (in_x) c_x[atomicAdd(&c_xn, 1u)] = tid;
             // x into LDS as f32 pieces after the row area, zero past `hidden`
             const uint32_t NS = router_lds_steps(hidden), RS = router_lds_row_pieces(hidden);
             v4a *xs = cert_lds + rf * RS;
-            for (uint32_t p = tid; p < 2 * NS; p += 256)
+            for (uint32_t p = tid; p < 2 * NS; p += T)
                 xs[p] = __builtin_bit_cast(v4a, rsrc_load16(rx, p < 2 * N8 ? 16 * p : nowhere));
             __syncthreads();
             // The rows of X, rf at a time: widened to f32 into LDS (zero past
@@ -1005,18 +1013,18 @@ __global__ void __launch_bounds__(256) router_cert_kernel(const uint16_t *__rest
             // from column 0 with fma, as router_lds_kernel does.
             for (uint32_t b0 = 0; b0 < c_xn; b0 += rf) {
                 const uint32_t nb = c_xn - b0 < rf ? c_xn - b0 : rf;
-                for (uint32_t p0 = 0; p0 < nb * NS; p0 += 4 * 256) {
+                for (uint32_t p0 = 0; p0 < nb * NS; p0 += 4 * T) {
                     v4a wr[4];
 #pragma unroll
                     for (uint32_t j = 0; j < 4; j++) {
-                        const uint32_t p = p0 + j * 256 + tid, rr = p / NS, col = p - rr * NS;
+                        const uint32_t p = p0 + j * T + tid, rr = p / NS, col = p - rr * NS;
                         const bool real = p < nb * NS && col < N8;
                         wr[j] = __builtin_bit_cast(
                             v4a, rsrc_load16(rw, real ? (c_x[b0 + rr] * N8 + col) * 16 : nowhere));
                     }
 #pragma unroll
                     for (uint32_t j = 0; j < 4; j++) {
-                        const uint32_t p = p0 + j * 256 + tid, rr = p / NS, col = p - rr * NS;
+                        const uint32_t p = p0 + j * T + tid, rr = p / NS, col = p - rr * NS;
                         if (p < nb * NS) {
                             const v4a w = wr[j];
                             cert_lds[rr * RS + 2 * col] =
@@ -1322,13 +1330,20 @@ hipError_t launch_router_top_k(hipStream_t s, const uint16_t *router, uint32_t h
         // to 4096 columns (49 KB of LDS), one at a time above (up to 65 KB)
         const uint32_t rf = hidden <= 4096 ? 2u : 1u;
         const size_t lds = router_lds_bytes(hidden, rf);
-        static LdsLimit limit;
-        hipError_t e = limit.ensure((const void *)router_cert_kernel, lds);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(router_cert_kernel, dim3((experts + 3) / 4, batch), dim3(256), lds, s, router, hidden,
-                           experts, k, x, (uint64_t *)logits, tickets, ids, probabilities, non_finite, host_ids,
-                           host_probs, host_bad, L, rf);
-        return hipGetLastError();
+        // Up to 8 tokens, 4 waves per workgroup (measured 1.2-1.7 us faster
+        // at 1 and 4 tokens); above, 8 waves (2.4 us faster at 16 tokens:
+        // half the workgroups take each token's ticket).
+        auto launch = [&](auto kernel, uint32_t waves, LdsLimit &limit) {
+            hipError_t e = limit.ensure((const void *)kernel, lds);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL(kernel, dim3((experts + waves - 1) / waves, batch), dim3(64 * waves), lds, s, router,
+                               hidden, experts, k, x, (uint64_t *)logits, tickets, ids, probabilities, non_finite,
+                               host_ids, host_probs, host_bad, L, rf);
+            return hipGetLastError();
+        };
+        static LdsLimit limit4, limit8;
+        return batch <= kMaxLookupTokens ? launch(router_cert_kernel<4>, 4, limit4)
+                                         : launch(router_cert_kernel<8>, 8, limit8);
     }
     if (staged && experts >= 2 * RF_EXPERTS) {
         // as many rows per workgroup as fit in LDS beside x and the

@@ -1366,19 +1366,19 @@ def test_moe_router_planted_near_ties(ctx):
         assert sel[t].tolist().index(5) < sel[t].tolist().index(90)
 
 
-@pytest.mark.parametrize("hidden,experts,k", [(2048, 128, 8), (6144, 32, 4)])
-def test_moe_router_all_rows_equal(ctx, hidden, experts, k):
+@pytest.mark.parametrize("hidden,experts,k,tokens", [(2048, 128, 8, 2), (6144, 32, 4, 2), (2048, 128, 8, 12)])
+def test_moe_router_all_rows_equal(ctx, hidden, experts, k, tokens):
     """Every router row the same: every logit ties, and the reference selects
     rows 0 .. k - 1 in index order with equal weights; the certified router
     folds every row exactly (two rows per LDS batch up to 4096 columns, one
-    above)."""
+    above).  Up to 8 tokens its workgroups have 4 waves, above 8."""
     width = 256
     rng = np.random.default_rng(4602)
     row = synth.to_bf16_bits(rng.standard_normal(hidden).astype(np.float32) * np.float32(0.02))
     router = np.tile(row, experts)
-    x = rng.standard_normal((2, hidden)).astype(np.float32)
+    x = rng.standard_normal((tokens, hidden)).astype(np.float32)
     sel = _moe_run_planted(ctx, router, x, hidden, width, experts, k, 47)
-    assert sel.tolist() == [list(range(k))] * 2
+    assert sel.tolist() == [list(range(k))] * tokens
 
 
 @pytest.mark.parametrize("scale", [0.02, 3e-18])
@@ -1395,12 +1395,14 @@ def test_moe_router_random_tokens(ctx, scale):
         _moe_run_planted(ctx, router, x, hidden, width, experts, k, 50)
 
 
-def test_moe_router_odd_shapes(ctx):
+@pytest.mark.parametrize("tokens", [3, 10])
+def test_moe_router_odd_shapes(ctx, tokens):
     """The certified router over a partial last round of columns (hidden 2816:
-    352 pieces of 8) and a partial last workgroup (202 experts)."""
+    352 pieces of 8) and a partial last workgroup (202 experts), with 4-wave
+    (3 tokens) and 8-wave (10 tokens) workgroups."""
     hidden, width, experts, k = 2816, 256, 202, 6
     router = synth.to_bf16_bits(synth.normal(synth.weight_seed(48, 0), experts * hidden) * np.float32(0.02))
-    x = synth.normal(synth.activation_seed(48, 1), 3 * hidden).reshape(3, hidden)
+    x = synth.normal(synth.activation_seed(48, 1), tokens * hidden).reshape(tokens, hidden)
     _moe_run_planted(ctx, router, x, hidden, width, experts, k, 48)
 
 
